@@ -1,0 +1,249 @@
+"""ctypes bindings of oracle/liboracle.so (the C restatement).
+
+TEST INFRASTRUCTURE ONLY: used by tests/, the smoke check and bench.py's
+cpu_baseline leg as the checker, never by the shipped library.
+"""
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+F32, F16, Q8_0, Q4_K, Q6_K = 0, 1, 8, 12, 14
+BLOCK_BYTES = {Q4_K: (256, 144), Q6_K: (256, 210), Q8_0: (32, 34), F32: (1, 4), F16: (1, 2)}
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = C.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+class Tensor(C.Structure):
+    _fields_ = [("type", C.c_int), ("data", C.c_void_p)]
+
+
+class Layer(C.Structure):
+    _fields_ = [(n, Tensor) for n in ("attn_norm", "wq", "wk", "wv", "wo", "q_norm", "k_norm",
+                                      "ffn_norm", "gate", "up", "down")]
+
+
+class Model(C.Structure):
+    _fields_ = [("n_layer", C.c_int), ("n_embd", C.c_int), ("n_head", C.c_int),
+                ("n_head_kv", C.c_int), ("head_dim", C.c_int), ("n_ff", C.c_int),
+                ("n_vocab", C.c_int), ("n_rot", C.c_int), ("eps", C.c_float),
+                ("rope_base", C.c_float), ("attn_scale", C.c_float), ("rope_neox", C.c_int),
+                ("rope_freqs", C.c_void_p), ("tok_embd", Tensor), ("output", Tensor),
+                ("output_norm", Tensor), ("layers", C.POINTER(Layer))]
+
+
+class Batch(C.Structure):
+    _fields_ = [("n_seq", C.c_int), ("max_blocks", C.c_int), ("block", C.c_int),
+                ("seq_n", C.c_void_p), ("seq_npast", C.c_void_p), ("block_tab", C.c_void_p),
+                ("ids", C.c_void_p), ("n_out", C.c_int), ("out_rows", C.c_void_p)]
+
+
+def _declare(L):
+    vp, i64, i32 = C.c_void_p, C.c_int64, C.c_int
+    L.orc_lcg_next.argtypes = [C.POINTER(C.c_uint64)]
+    L.orc_lcg_next.restype = C.c_double
+    L.orc_lcg_fill.argtypes = [C.POINTER(C.c_uint64), vp, i64, C.c_double, C.c_double]
+    L.orc_fill_normal.argtypes = [C.POINTER(C.c_uint64), vp, i64, C.c_double, C.c_double]
+    L.orc_fill_uniform.argtypes = [C.POINTER(C.c_uint64), vp, i64, C.c_double, C.c_double]
+    L.orc_f32_to_f16_row.argtypes = [vp, vp, i64]
+    L.orc_f16_to_f32_row.argtypes = [vp, vp, i64]
+    L.orc_row_size.argtypes = [i32, i64]
+    L.orc_row_size.restype = i64
+    L.orc_dequantize_row.argtypes = [i32, vp, vp, i64]
+    L.orc_quantize_row.argtypes = [i32, vp, vp, i64]
+    L.orc_quantize_row.restype = i64
+    L.orc_forward.argtypes = [C.POINTER(Model), vp, vp, i64, C.POINTER(Batch), vp, i32]
+    L.orc_paged_attention.argtypes = [vp, vp, vp, i32, i32, i32, C.c_float, C.POINTER(Batch),
+                                      vp, i32]
+    L.orc_set_rows_f16.argtypes = [vp, i64, i64, vp, vp, i64]
+    L.orc_mul_mat.argtypes = [i32, vp, i64, i64, vp, i64, vp, i32]
+    L.orc_argmax.argtypes = [vp, i64]
+    L.orc_argmax.restype = C.c_int32
+
+
+def _p(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+class Lcg:
+    """test/tiny.lua:16-22 seeded uniform numbers in [0, 1)."""
+
+    def __init__(self, seed):
+        self.state = C.c_uint64(seed & (2**64 - 1))
+
+    def next(self):
+        return lib().orc_lcg_next(C.byref(self.state))
+
+    def fill(self, n, lo, hi):
+        out = np.empty(n, np.float32)
+        lib().orc_lcg_fill(C.byref(self.state), _p(out), n, lo, hi)
+        return out
+
+
+def fill_normal(n, mean, sd, seed):
+    """src/lgml.c:3130-3136 tensor:fill("normal", mean, sd, seed)."""
+    s = C.c_uint64(seed & (2**64 - 1))
+    out = np.empty(n, np.float32)
+    lib().orc_fill_normal(C.byref(s), _p(out), n, mean, sd)
+    return out
+
+
+def fill_uniform(n, a, b, seed):
+    s = C.c_uint64(seed & (2**64 - 1))
+    out = np.empty(n, np.float32)
+    lib().orc_fill_uniform(C.byref(s), _p(out), n, a, b)
+    return out
+
+
+def f32_to_f16_bits(x):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_f16_row(_p(x), _p(y), x.size)
+    return y
+
+
+def f16_bits_to_f32(h):
+    h = np.ascontiguousarray(h, np.uint16)
+    y = np.empty(h.shape, np.float32)
+    lib().orc_f16_to_f32_row(_p(h), _p(y), h.size)
+    return y
+
+
+def row_size(t, n):
+    return lib().orc_row_size(t, n)
+
+
+def quantize(t, x):
+    """Quantize a (rows, K) f32 matrix row by row; returns uint8 (rows, row_size)."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, K = x.shape
+    rs = row_size(t, K)
+    out = np.zeros((rows, rs), np.uint8)
+    for r in range(rows):
+        if lib().orc_quantize_row(t, _p(x[r]), _p(out[r]), K) != rs:
+            raise ValueError("quantize failed")
+    return out
+
+
+def dequantize(t, q, K):
+    q = np.ascontiguousarray(q, np.uint8).reshape(-1, row_size(t, K))
+    out = np.empty((q.shape[0], K), np.float32)
+    for r in range(q.shape[0]):
+        if lib().orc_dequantize_row(t, _p(q[r]), _p(out[r]), K) != 0:
+            raise ValueError("dequantize failed")
+    return out
+
+
+def mul_mat(t, w, M, K, x, threads=8):
+    x = np.ascontiguousarray(x, np.float32)
+    N = x.shape[0]
+    y = np.empty((N, M), np.float32)
+    w = np.ascontiguousarray(w)
+    if lib().orc_mul_mat(t, _p(w), M, K, _p(x), N, _p(y), threads) != 0:
+        raise ValueError("mul_mat failed")
+    return y
+
+
+def argmax(v):
+    v = np.ascontiguousarray(v, np.float32)
+    return int(lib().orc_argmax(_p(v), v.size))
+
+
+class BatchDesc:
+    """Keeps the arrays of an orc_batch alive."""
+
+    def __init__(self, seq_n, seq_npast, block_tab, block, ids, out_rows):
+        self.seq_n = np.ascontiguousarray(seq_n, np.int32)
+        self.seq_npast = np.ascontiguousarray(seq_npast, np.int32)
+        bt = np.ascontiguousarray(block_tab, np.int32)
+        if bt.ndim == 1:
+            bt = bt.reshape(len(self.seq_n), -1)
+        self.block_tab = bt
+        self.ids = np.ascontiguousarray(ids, np.int32)
+        self.out_rows = np.ascontiguousarray(out_rows, np.int32)
+        self.c = Batch(len(self.seq_n), bt.shape[1], block, _p(self.seq_n), _p(self.seq_npast),
+                       _p(self.block_tab), _p(self.ids), len(self.out_rows), _p(self.out_rows))
+
+
+def paged_attention(q, kpool, vpool, H, Hkv, D, scale, batch, threads=8):
+    q = np.ascontiguousarray(q, np.float32)
+    out = np.empty_like(q)
+    rc = lib().orc_paged_attention(_p(q), _p(kpool), _p(vpool), H, Hkv, D, scale,
+                                   C.byref(batch.c), _p(out), threads)
+    if rc:
+        raise ValueError("paged_attention failed")
+    return out
+
+
+def set_rows_f16(dst, src, ids):
+    src = np.ascontiguousarray(src, np.float32)
+    ids = np.ascontiguousarray(ids, np.int64)
+    if lib().orc_set_rows_f16(_p(dst), dst.shape[0], dst.shape[1], _p(src), _p(ids),
+                              len(ids)) != 0:
+        raise ValueError("set_rows: id out of range")
+
+
+class OracleModel:
+    """Wraps a weights dict (see oracle.models) as an orc_model."""
+
+    def __init__(self, hp, w):
+        self.hp, self.w = hp, w
+        self._keep = []
+        L = hp["n_layer"]
+        self.layers = (Layer * L)()
+        for il in range(L):
+            lw = w["layers"][il]
+            for f, _ in Layer._fields_:
+                t = lw.get(f)
+                if t is not None:
+                    arr, ty = t
+                    arr = np.ascontiguousarray(arr)
+                    self._keep.append(arr)
+                    setattr(self.layers[il], f, Tensor(ty, _p(arr).value))
+        self.c = Model()
+        for k in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "n_ff", "n_vocab",
+                  "n_rot", "rope_neox"):
+            setattr(self.c, k, int(hp[k]))
+        self.c.eps, self.c.rope_base = hp["eps"], hp["rope_base"]
+        self.c.attn_scale = hp.get("attn_scale", 0.0)
+        rf = w.get("rope_freqs")
+        if rf is not None:
+            rf = np.ascontiguousarray(rf, np.float32)
+            self._keep.append(rf)
+            self.c.rope_freqs = _p(rf).value
+        for f in ("tok_embd", "output", "output_norm"):
+            arr, ty = w[f]
+            arr = np.ascontiguousarray(arr)
+            self._keep.append(arr)
+            setattr(self.c, f, Tensor(ty, _p(arr).value))
+        self.c.layers = self.layers
+
+    def forward(self, kpools, vpools, batch, threads=8):
+        """kpools/vpools: lists of (cap, Hkv*D) uint16 arrays (f16 bits), updated in place."""
+        L = self.hp["n_layer"]
+        kp = (C.c_void_p * L)(*[_p(a).value for a in kpools])
+        vp = (C.c_void_p * L)(*[_p(a).value for a in vpools])
+        cap = kpools[0].shape[0]
+        out = np.empty((len(batch.out_rows), self.hp["n_vocab"]), np.float32)
+        rc = lib().orc_forward(C.byref(self.c), kp, vp, cap, C.byref(batch.c), _p(out), threads)
+        if rc:
+            raise ValueError("orc_forward failed: %d" % rc)
+        return out

@@ -1,0 +1,168 @@
+"""Model weight builders for the oracle and the GPU path.
+
+TEST INFRASTRUCTURE: the tiny models regenerate the reference's test
+fixtures exactly, so the oracle can be pinned against its golden rows;
+the config builders make the seeded random-init models that the tests
+and bench.py feed to both the oracle and the GPU library.
+
+A weights dict: {"tok_embd": (arr, type), "output": ..., "output_norm":
+..., "rope_freqs": arr or None, "layers": [{name: (arr, type)}]} where a
+quantized arr is uint8 (rows, row_bytes) and an f32 arr is (rows, cols).
+"""
+import math
+
+import numpy as np
+
+from . import core
+
+LAYER_KEYS = ("attn_norm", "wq", "wk", "wv", "wo", "q_norm", "k_norm", "ffn_norm", "gate", "up",
+              "down")
+
+
+def ref_tiny(arch):
+    """The tiny llama / qwen3 of test/test_qwen_moe.lua:66-200 (build()).
+
+    Seed #arch * 7919 (:70); tensors drawn in the order build() lists them
+    (:140-195); w(): U(-s, s), s = gain * sqrt(3 / fan_in) (:88-91); norms
+    U(0.9, 1.1) (:92-94); llama rope_freqs U(1, 8) x D/2 (:143-147). All
+    stored as f32 (gguf.lua:41-50). Shapes: E=64, H=4, HKV=2, D=16,
+    FF=2E, 2 layers, vocab 259 (:41-64,66,96-104), eps 1e-6, base 1e6.
+    """
+    assert arch in ("llama", "qwen3")
+    E, H, HKV, D = 64, 4, 2, 16
+    nv = 256 + 3
+    r = core.Lcg(len(arch) * 7919)
+
+    def w(rows, cols, gain=1.0):
+        s = gain * math.sqrt(3.0 / cols)
+        return (r.fill(rows * cols, -s, s).reshape(rows, cols), core.F32)
+
+    def norm(d):
+        return (r.fill(d, 0.9, 1.1), core.F32)
+
+    out = {}
+    out["tok_embd"] = w(nv, E, 3.0)
+    out["output_norm"] = norm(E)
+    out["output"] = w(nv, E)
+    out["rope_freqs"] = None
+    if arch == "llama":
+        out["rope_freqs"] = r.fill(D // 2, 1.0, 8.0)
+    layers = []
+    for _ in range(2):
+        L = {}
+        L["attn_norm"] = norm(E)
+        L["wq"] = w(H * D, E)
+        L["wk"] = w(HKV * D, E)
+        L["wv"] = w(HKV * D, E)
+        L["wo"] = w(E, H * D)
+        if arch != "llama":
+            L["q_norm"] = norm(D)
+            L["k_norm"] = norm(D)
+        L["ffn_norm"] = norm(E)
+        L["gate"] = w(2 * E, E)
+        L["up"] = w(2 * E, E)
+        L["down"] = w(E, 2 * E)
+        layers.append(L)
+    out["layers"] = layers
+    hp = dict(arch=arch, n_layer=2, n_embd=E, n_head=H, n_head_kv=HKV, head_dim=D, n_ff=2 * E,
+              n_vocab=nv, n_rot=D, eps=1e-6, rope_base=1e6, rope_neox=0 if arch == "llama" else 1,
+              attn_scale=0.0)
+    return hp, out
+
+
+# Named model shapes of BASELINE.json's configs.
+SHAPES = {
+    # C1: tiny llama-style f32 model runnable on CPU.
+    "c1": dict(arch="llama", n_layer=2, n_embd=256, n_head=4, n_head_kv=2, head_dim=64, n_ff=688,
+               n_vocab=512, rope_base=1e4, eps=1e-6, wtype="f32"),
+    # C2: Llama-3-8B shape, Q4_K_M mix, f16 KV.
+    "c2": dict(arch="llama", n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128,
+               n_ff=14336, n_vocab=128256, rope_base=5e5, eps=1e-5, wtype="q4_K_M"),
+}
+
+
+def more_bits(i, n):
+    """lua/lgml/convert.lua:123-126: layers that get Q6_K in the _M mixes."""
+    return i < n // 8 or i >= 7 * n // 8 or (i - n // 8) % 3 == 2
+
+
+def weight_type(wtype, name, layer, n_layer):
+    """lua/lgml/convert.lua:128-165 policies: 1-D tensors stay f32; q4_K_M
+    gives output Q6_K and attn_v / ffn_down Q6_K on more_bits layers."""
+    if wtype == "f32":
+        return core.F32
+    if wtype == "q8_0":
+        return core.Q8_0
+    if wtype == "q4_K":
+        return core.Q4_K
+    if wtype == "q4_K_M":
+        if name == "output":
+            return core.Q6_K
+        if layer is not None and name in ("wv", "down") and more_bits(layer, n_layer):
+            return core.Q6_K
+        return core.Q4_K
+    raise ValueError(wtype)
+
+
+def build(shape, seed=1234, n_layer=None, init="uniform"):
+    """Seeded random-init weights for a named shape.
+
+    init "uniform": C1's U(-s, s), s = sqrt(3 / fan_in) (as tiny.lua:102-108),
+    norms U(0.9, 1.1), drawn from the reference LCG.
+    init "normal": N(0, 0.02) weights from the reference splitmix64 +
+    Box-Muller fill (src/lgml.c:3130-3136), one seed per tensor (seed + i),
+    norms 1.0; quantized per the shape's weight policy.
+    n_layer overrides the depth (reduced-depth parity runs keep the width).
+    """
+    hp = dict(SHAPES[shape]) if isinstance(shape, str) else dict(shape)
+    if n_layer is not None:
+        hp["n_layer"] = n_layer
+    hp.setdefault("n_rot", hp["head_dim"])
+    hp["rope_neox"] = 0 if hp["arch"] == "llama" else 1
+    hp["attn_scale"] = 0.0
+    E, H, Hkv, D, F, V = (hp[k] for k in ("n_embd", "n_head", "n_head_kv", "head_dim", "n_ff",
+                                          "n_vocab"))
+    nl = hp["n_layer"]
+    full_layers = SHAPES[shape]["n_layer"] if isinstance(shape, str) else nl
+    wt = hp["wtype"]
+    lcg = core.Lcg(seed)
+    counter = [0]
+
+    def mat(name, rows, cols, layer=None, gain=1.0):
+        ty = weight_type(wt, name, layer, full_layers)
+        if init == "uniform":
+            s = gain * math.sqrt(3.0 / cols)
+            x = lcg.fill(rows * cols, -s, s).reshape(rows, cols)
+        else:
+            counter[0] += 1
+            x = core.fill_normal(rows * cols, 0.0, 0.02, seed * 1000003 + counter[0])
+            x = x.reshape(rows, cols)
+        if ty == core.F32:
+            return (x, ty)
+        return (core.quantize(ty, x), ty)
+
+    def norm(d):
+        if init == "uniform":
+            return (lcg.fill(d, 0.9, 1.1), core.F32)
+        return (np.ones(d, np.float32), core.F32)
+
+    w = {}
+    w["tok_embd"] = mat("tok_embd", V, E)
+    w["output_norm"] = norm(E)
+    w["output"] = mat("output", V, E)
+    w["rope_freqs"] = None
+    layers = []
+    for il in range(nl):
+        L = {}
+        L["attn_norm"] = norm(E)
+        L["wq"] = mat("wq", H * D, E, il)
+        L["wk"] = mat("wk", Hkv * D, E, il)
+        L["wv"] = mat("wv", Hkv * D, E, il)
+        L["wo"] = mat("wo", E, H * D, il)
+        L["ffn_norm"] = norm(E)
+        L["gate"] = mat("gate", F, E, il)
+        L["up"] = mat("up", F, E, il)
+        L["down"] = mat("down", E, F, il)
+        layers.append(L)
+    w["layers"] = layers
+    return hp, w

@@ -1,0 +1,797 @@
+/*
+ * CPU oracle for the lgml ragged decode/prefill path.
+ *
+ * TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke()
+ * and the cpu_baseline leg of bench.py, as the checker. The shipped
+ * library never links or calls it.
+ *
+ * Everything here restates the reference's behaviour in plain C:
+ * fp32 values, f64 reductions, f16 KV storage (round to nearest even),
+ * closed-form Q4_K / Q6_K / Q8_0 dequantization. Reference citations are
+ * paths under the lgml tree; [ggml] marks the semantics of the
+ * un-vendored ggml op that the lgml wrapper calls (its public format or
+ * algorithm, restated here in our own code).
+ *
+ * Pinning (what checks each part):
+ *   orc_lcg_*, orc_fill_*        tests/test_oracle_golden.py regenerates the
+ *                                tiny models; REF logits then pin them.
+ *   f16 conversion               numpy astype(float16) on 2^32-sampled bits.
+ *   dequantize Q4_K/Q6_K/Q8_0    hand-built blocks with known values,
+ *                                quantize->dequantize error bounds
+ *                                (test_convert.lua:287-310 rmse bounds).
+ *   forward / attention          REF.llama / REF.qwen3 golden rows
+ *                                (test_qwen_moe.lua:210-241), TOL 2e-3 + argmax;
+ *                                attention also against numpy softmax on
+ *                                tiny cases; batched == lone equality.
+ *   mul_mat                      numpy matmul of the dequantized rows.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ---- random numbers ---------------------------------------------------- */
+
+/* test/tiny.lua:16-22, test/test_qwen_moe.lua:32-38 (Lua 5.4 integers wrap
+ * modulo 2^64 and >> is a logical shift). */
+double
+orc_lcg_next(uint64_t *state)
+{
+	*state = *state * 6364136223846793005ULL + 1442695040888963407ULL;
+	return (double)(*state >> 11) / 9007199254740992.0;
+}
+
+/* test/test_qwen_moe.lua:77-86: lo + (hi - lo) * r(), in double, then the
+ * f32 store of test/gguf.lua:41-50 (string.pack "<f"). */
+void
+orc_lcg_fill(uint64_t *state, float *out, int64_t n, double lo, double hi)
+{
+	for (int64_t i = 0; i < n; i++)
+		out[i] = (float)(lo + (hi - lo) * orc_lcg_next(state));
+}
+
+/* src/lgml.c:3064-3079 */
+static uint64_t
+splitmix64(uint64_t *x)
+{
+	uint64_t z = (*x += 0x9e3779b97f4a7c15ULL);
+
+	z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+	z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+	return z ^ (z >> 31);
+}
+
+static double
+unit01(uint64_t *x)
+{
+	return (double)(splitmix64(x) >> 11) * (1.0 / 9007199254740992.0);
+}
+
+/* src/lgml.c:3130-3136 ("normal": two draws, cos branch). */
+void
+orc_fill_normal(uint64_t *seed, float *out, int64_t n, double mean, double sd)
+{
+	for (int64_t i = 0; i < n; i++) {
+		double u1 = unit01(seed), u2 = unit01(seed);
+		out[i] = (float)(mean + sd * sqrt(-2.0 * log(u1 > 0 ? u1 : 1e-300)) *
+		    cos(6.283185307179586 * u2));
+	}
+}
+
+/* src/lgml.c:3128-3129 ("uniform"). */
+void
+orc_fill_uniform(uint64_t *seed, float *out, int64_t n, double a, double b)
+{
+	for (int64_t i = 0; i < n; i++)
+		out[i] = (float)(a + (b - a) * unit01(seed));
+}
+
+/* ---- f16 (IEEE binary16, round to nearest even) ---------------------------- */
+
+uint16_t
+orc_f32_to_f16(float f)
+{
+	uint32_t x;
+	memcpy(&x, &f, 4);
+	uint32_t sign = (x >> 16) & 0x8000u;
+	uint32_t ex = (x >> 23) & 0xffu;
+	uint32_t man = x & 0x7fffffu;
+
+	if (ex == 0xffu)
+		return (uint16_t)(sign | (man ? 0x7e00u : 0x7c00u));
+	int e = (int)ex - 127 + 15;
+	if (e >= 31)
+		return (uint16_t)(sign | 0x7c00u);
+	if (e <= 0) {
+		/* f16 subnormal: value = m * 2^-24, m = mant24 >> (14 - e). */
+		int shift = 14 - e;
+		if (ex == 0 || shift > 24)
+			return (uint16_t)sign;
+		uint32_t m24 = man | 0x800000u;
+		uint32_t h = m24 >> shift;
+		uint32_t rem = m24 & ((1u << shift) - 1u);
+		uint32_t half = 1u << (shift - 1);
+		if (rem > half || (rem == half && (h & 1u)))
+			h++;
+		return (uint16_t)(sign | h);
+	}
+	uint32_t h = ((uint32_t)e << 10) | (man >> 13);
+	uint32_t rem = man & 0x1fffu;
+	if (rem > 0x1000u || (rem == 0x1000u && (h & 1u)))
+		h++; /* a carry into the exponent is the correct rounding */
+	return (uint16_t)(sign | h);
+}
+
+float
+orc_f16_to_f32(uint16_t h)
+{
+	uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+	uint32_t ex = (h >> 10) & 0x1fu;
+	uint32_t man = h & 0x3ffu;
+	uint32_t x;
+
+	if (ex == 0) {
+		if (man == 0) {
+			x = sign;
+		} else {
+			/* subnormal: normalise */
+			int e = -1;
+			do {
+				man <<= 1;
+				e++;
+			} while (!(man & 0x400u));
+			man &= 0x3ffu;
+			x = sign | ((uint32_t)(127 - 15 - e) << 23) | (man << 13);
+		}
+	} else if (ex == 0x1fu) {
+		x = sign | 0x7f800000u | (man << 13);
+	} else {
+		x = sign | ((ex - 15 + 127) << 23) | (man << 13);
+	}
+	float f;
+	memcpy(&f, &x, 4);
+	return f;
+}
+
+void
+orc_f32_to_f16_row(const float *x, uint16_t *y, int64_t n)
+{
+	for (int64_t i = 0; i < n; i++)
+		y[i] = orc_f32_to_f16(x[i]);
+}
+
+void
+orc_f16_to_f32_row(const uint16_t *x, float *y, int64_t n)
+{
+	for (int64_t i = 0; i < n; i++)
+		y[i] = orc_f16_to_f32(x[i]);
+}
+
+/* ---- quantized block formats [ggml, public] --------------------------------
+ * Q4_K: 256 values, 144 B {f16 d; f16 dmin; u8 scales[12]; u8 qs[128]}
+ * Q6_K: 256 values, 210 B {u8 ql[128]; u8 qh[64]; i8 scales[16]; f16 d}
+ * Q8_0:  32 values,  34 B {f16 d; i8 qs[32]}
+ */
+#define QK_K 256
+#define Q4K_BYTES 144
+#define Q6K_BYTES 210
+#define Q8_0_BYTES 34
+
+int64_t
+orc_row_size(int type, int64_t n)
+{
+	switch (type) {
+	case ORC_F32:
+		return n * 4;
+	case ORC_F16:
+		return n * 2;
+	case ORC_Q8_0:
+		return n / 32 * Q8_0_BYTES;
+	case ORC_Q4_K:
+		return n / QK_K * Q4K_BYTES;
+	case ORC_Q6_K:
+		return n / QK_K * Q6K_BYTES;
+	}
+	return -1;
+}
+
+static uint16_t
+rd16(const uint8_t *p)
+{
+	return (uint16_t)(p[0] | (p[1] << 8));
+}
+
+static void
+wr16(uint8_t *p, uint16_t v)
+{
+	p[0] = (uint8_t)v;
+	p[1] = (uint8_t)(v >> 8);
+}
+
+/* 6-bit scale and min j (0..7) of a Q4_K super-block's 12 scale bytes. */
+static void
+q4k_scale_min(int j, const uint8_t *s, int *sc, int *mn)
+{
+	if (j < 4) {
+		*sc = s[j] & 63;
+		*mn = s[j + 4] & 63;
+	} else {
+		*sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
+		*mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+	}
+}
+
+/* Value v of a Q4_K super-block: group g = v / 32 has scale d * sc_g and
+ * min dmin * m_g; the 4-bit q of v sits in byte 32 * (v / 64) + v % 32,
+ * low nibble for v % 64 < 32, high nibble otherwise. The product d1 * q
+ * is exact in f32 (11 + 6 + 4 bits), so y is one rounding of the exact
+ * d1 * q - m1 with or without FMA contraction. */
+static void
+deq_q4k(const uint8_t *b, float *y)
+{
+	float d = orc_f16_to_f32(rd16(b));
+	float dmin = orc_f16_to_f32(rd16(b + 2));
+	const uint8_t *sc = b + 4, *qs = b + 16;
+
+	for (int g = 0; g < 8; g++) {
+		int s, m;
+		q4k_scale_min(g, sc, &s, &m);
+		float d1 = d * (float)s, m1 = dmin * (float)m;
+		const uint8_t *q = qs + 32 * (g / 2);
+		int hi = g & 1;
+		for (int l = 0; l < 32; l++) {
+			int qv = hi ? (q[l] >> 4) : (q[l] & 0xF);
+			y[32 * g + l] = d1 * (float)qv - m1;
+		}
+	}
+}
+
+/* Value v of a Q6_K super-block: half h = v / 128, r = v % 128, quarter
+ * t = r / 32, l = r % 32. Low 4 bits from ql[64h + l + 32 * (t & 1)]
+ * (low nibble for t < 2, high for t >= 2); high 2 bits from
+ * qh[32h + l] >> (2t). q = bits - 32; scale index v / 16.
+ * y = (d * sc) * q, evaluated left to right as the reference does. */
+static void
+deq_q6k(const uint8_t *b, float *y)
+{
+	const uint8_t *ql = b, *qh = b + 128;
+	const int8_t *sc = (const int8_t *)(b + 192);
+	float d = orc_f16_to_f32(rd16(b + 208));
+
+	for (int v = 0; v < QK_K; v++) {
+		int h = v / 128, r = v % 128, t = r / 32, l = r % 32;
+		int lo = ql[64 * h + l + 32 * (t & 1)];
+		lo = t < 2 ? (lo & 0xF) : (lo >> 4);
+		int hb = (qh[32 * h + l] >> (2 * t)) & 3;
+		int q = (lo | (hb << 4)) - 32;
+		y[v] = d * (float)sc[v / 16] * (float)q;
+	}
+}
+
+static void
+deq_q8_0(const uint8_t *b, float *y)
+{
+	float d = orc_f16_to_f32(rd16(b));
+	const int8_t *q = (const int8_t *)(b + 2);
+
+	for (int l = 0; l < 32; l++)
+		y[l] = d * (float)q[l];
+}
+
+int
+orc_dequantize_row(int type, const void *src, float *dst, int64_t n)
+{
+	const uint8_t *p = (const uint8_t *)src;
+
+	switch (type) {
+	case ORC_F32:
+		memcpy(dst, src, (size_t)n * 4);
+		return 0;
+	case ORC_F16:
+		orc_f16_to_f32_row((const uint16_t *)src, dst, n);
+		return 0;
+	case ORC_Q4_K:
+		if (n % QK_K)
+			return -1;
+		for (int64_t i = 0; i < n / QK_K; i++)
+			deq_q4k(p + i * Q4K_BYTES, dst + i * QK_K);
+		return 0;
+	case ORC_Q6_K:
+		if (n % QK_K)
+			return -1;
+		for (int64_t i = 0; i < n / QK_K; i++)
+			deq_q6k(p + i * Q6K_BYTES, dst + i * QK_K);
+		return 0;
+	case ORC_Q8_0:
+		if (n % 32)
+			return -1;
+		for (int64_t i = 0; i < n / 32; i++)
+			deq_q8_0(p + i * Q8_0_BYTES, dst + i * 32);
+		return 0;
+	}
+	return -1;
+}
+
+static int
+clampi(int v, int lo, int hi)
+{
+	return v < lo ? lo : v > hi ? hi : v;
+}
+
+/* Own Q4_K quantizer: per 32-group affine range [min(0, lo), hi], 6-bit
+ * scales and mins relative to the super-block maxima. */
+static void
+quant_q4k(const float *x, uint8_t *b)
+{
+	float scale[8], mins[8], ms = 0, mm = 0;
+
+	for (int g = 0; g < 8; g++) {
+		float lo = x[32 * g], hi = x[32 * g];
+		for (int l = 1; l < 32; l++) {
+			lo = fminf(lo, x[32 * g + l]);
+			hi = fmaxf(hi, x[32 * g + l]);
+		}
+		if (lo > 0)
+			lo = 0;
+		scale[g] = (hi - lo) / 15.0f;
+		mins[g] = -lo;
+		ms = fmaxf(ms, scale[g]);
+		mm = fmaxf(mm, mins[g]);
+	}
+	uint16_t hd = orc_f32_to_f16(ms / 63.0f), hm = orc_f32_to_f16(mm / 63.0f);
+	float d = orc_f16_to_f32(hd), dmin = orc_f16_to_f32(hm);
+	int sc[8], mn[8];
+	for (int g = 0; g < 8; g++) {
+		sc[g] = d > 0 ? clampi((int)lrintf(scale[g] / d), 0, 63) : 0;
+		mn[g] = dmin > 0 ? clampi((int)lrintf(mins[g] / dmin), 0, 63) : 0;
+	}
+	memset(b, 0, Q4K_BYTES);
+	wr16(b, hd);
+	wr16(b + 2, hm);
+	uint8_t *s = b + 4, *qs = b + 16;
+	for (int j = 0; j < 8; j++) {
+		if (j < 4) {
+			s[j] |= (uint8_t)sc[j];
+			s[j + 4] |= (uint8_t)mn[j];
+		} else {
+			s[j + 4] = (uint8_t)((sc[j] & 0xF) | ((mn[j] & 0xF) << 4));
+			s[j - 4] |= (uint8_t)((sc[j] >> 4) << 6);
+			s[j] |= (uint8_t)((mn[j] >> 4) << 6);
+		}
+	}
+	for (int g = 0; g < 8; g++) {
+		float d1 = d * (float)sc[g], m1 = dmin * (float)mn[g];
+		for (int l = 0; l < 32; l++) {
+			int q = d1 > 0 ? clampi((int)lrintf((x[32 * g + l] + m1) / d1), 0, 15) : 0;
+			int byte = 32 * (g / 2) + l;
+			qs[byte] |= (uint8_t)(g & 1 ? q << 4 : q);
+		}
+	}
+}
+
+/* Own Q6_K quantizer: symmetric 16-groups, 8-bit signed scales. */
+static void
+quant_q6k(const float *x, uint8_t *b)
+{
+	float gs[16], ms = 0;
+
+	for (int g = 0; g < 16; g++) {
+		float a = 0;
+		for (int l = 0; l < 16; l++)
+			a = fmaxf(a, fabsf(x[16 * g + l]));
+		gs[g] = a / 31.0f;
+		ms = fmaxf(ms, gs[g]);
+	}
+	uint16_t hd = orc_f32_to_f16(ms / 127.0f);
+	float d = orc_f16_to_f32(hd);
+	memset(b, 0, Q6K_BYTES);
+	int8_t *sc = (int8_t *)(b + 192);
+	for (int g = 0; g < 16; g++)
+		sc[g] = (int8_t)(d > 0 ? clampi((int)lrintf(gs[g] / d), -128, 127) : 0);
+	uint8_t *ql = b, *qh = b + 128;
+	for (int v = 0; v < QK_K; v++) {
+		float s = d * (float)sc[v / 16];
+		int q = s > 0 ? clampi((int)lrintf(x[v] / s), -32, 31) : 0;
+		int u = q + 32;
+		int h = v / 128, r = v % 128, t = r / 32, l = r % 32;
+		int idx = 64 * h + l + 32 * (t & 1);
+		ql[idx] |= (uint8_t)(t < 2 ? (u & 0xF) : ((u & 0xF) << 4));
+		qh[32 * h + l] |= (uint8_t)(((u >> 4) & 3) << (2 * t));
+	}
+	wr16(b + 208, hd);
+}
+
+static void
+quant_q8_0(const float *x, uint8_t *b)
+{
+	float a = 0;
+
+	for (int l = 0; l < 32; l++)
+		a = fmaxf(a, fabsf(x[l]));
+	float d = a / 127.0f;
+	uint16_t hd = orc_f32_to_f16(d);
+	float id = d > 0 ? 1.0f / d : 0.0f;
+	wr16(b, hd);
+	for (int l = 0; l < 32; l++)
+		((int8_t *)(b + 2))[l] = (int8_t)clampi((int)lrintf(x[l] * id), -127, 127);
+}
+
+int64_t
+orc_quantize_row(int type, const float *src, void *dst, int64_t n)
+{
+	uint8_t *p = (uint8_t *)dst;
+
+	switch (type) {
+	case ORC_F32:
+		memcpy(dst, src, (size_t)n * 4);
+		return n * 4;
+	case ORC_F16:
+		orc_f32_to_f16_row(src, (uint16_t *)dst, n);
+		return n * 2;
+	case ORC_Q4_K:
+		if (n % QK_K)
+			return -1;
+		for (int64_t i = 0; i < n / QK_K; i++)
+			quant_q4k(src + i * QK_K, p + i * Q4K_BYTES);
+		return n / QK_K * Q4K_BYTES;
+	case ORC_Q6_K:
+		if (n % QK_K)
+			return -1;
+		for (int64_t i = 0; i < n / QK_K; i++)
+			quant_q6k(src + i * QK_K, p + i * Q6K_BYTES);
+		return n / QK_K * Q6K_BYTES;
+	case ORC_Q8_0:
+		if (n % 32)
+			return -1;
+		for (int64_t i = 0; i < n / 32; i++)
+			quant_q8_0(src + i * 32, p + i * Q8_0_BYTES);
+		return n / 32 * Q8_0_BYTES;
+	}
+	return -1;
+}
+
+/* ---- ops ----------------------------------------------------------------- */
+
+static int
+nthreads(int n)
+{
+	return n > 0 ? n : 1;
+}
+
+/* ggml_mul_mat via graph:mul_mat (src/lgml.c:1811-1839): y[n][m] =
+ * sum_k w[m][k] * x[n][k]. Each weight row is dequantized once. */
+int
+orc_mul_mat(int type, const void *w, int64_t M, int64_t K, const float *x, int64_t N,
+    float *y, int n_threads)
+{
+	int64_t rs = orc_row_size(type, K);
+	int bad = 0;
+
+	if (rs <= 0)
+		return -1;
+#pragma omp parallel num_threads(nthreads(n_threads))
+	{
+		float *row = malloc((size_t)K * sizeof(float));
+		if (!row) {
+#pragma omp atomic write
+			bad = 1;
+		}
+#pragma omp for schedule(static)
+		for (int64_t m = 0; m < M; m++) {
+			if (!row)
+				continue;
+			orc_dequantize_row(type, (const uint8_t *)w + m * rs, row, K);
+			for (int64_t n = 0; n < N; n++) {
+				const float *xn = x + n * K;
+				double acc = 0;
+				for (int64_t k = 0; k < K; k++)
+					acc += (double)row[k] * (double)xn[k];
+				y[n * M + m] = (float)acc;
+			}
+		}
+		free(row);
+	}
+	return bad ? -1 : 0;
+}
+
+/* ggml_rms_norm [ggml] via graph:rms_norm (src/lgml.c:1633): sum of
+ * squares in f64, mean rounded to f32, scale = 1/sqrtf(mean + eps). */
+static void
+rms_norm_row(const float *x, float *y, int64_t n, float eps, const float *w)
+{
+	double s = 0;
+	for (int64_t i = 0; i < n; i++)
+		s += (double)x[i] * (double)x[i];
+	float mean = (float)(s / (double)n);
+	float scale = 1.0f / sqrtf(mean + eps);
+	for (int64_t i = 0; i < n; i++) {
+		float v = x[i] * scale;
+		y[i] = w ? v * w[i] : v;
+	}
+}
+
+/* ggml_rope_ext [ggml] as graph:rope calls it (src/lgml.c:2004-2081),
+ * ext_factor 0, freq_scale 1, attn_factor 1: theta_0 = pos, theta_{i+1} =
+ * theta_i * base^(-2/n_rot) in f32; pair i rotates by theta_i / ff_i.
+ * normal mode pairs (2i, 2i+1); neox pairs (i, i + n_rot/2). */
+static void
+rope_row(float *x, int n_heads, int D, int n_rot, int neox, float base, const float *ff,
+    int pos)
+{
+	float theta_scale = powf(base, -2.0f / (float)n_rot);
+	float cs[512], sn[512];
+	float theta = (float)pos;
+
+	for (int i = 0; i < n_rot / 2; i++) {
+		float t = theta / (ff ? ff[i] : 1.0f);
+		cs[i] = cosf(t);
+		sn[i] = sinf(t);
+		theta *= theta_scale;
+	}
+	for (int h = 0; h < n_heads; h++) {
+		float *v = x + (int64_t)h * D;
+		for (int i = 0; i < n_rot / 2; i++) {
+			int a = neox ? i : 2 * i, b = neox ? i + n_rot / 2 : 2 * i + 1;
+			double x0 = v[a], x1 = v[b];
+			v[a] = (float)(x0 * cs[i] - x1 * sn[i]);
+			v[b] = (float)(x0 * sn[i] + x1 * cs[i]);
+		}
+	}
+}
+
+static int64_t
+cell_of(const orc_batch *b, int s, int p)
+{
+	return (int64_t)b->block_tab[(int64_t)s * b->max_blocks + p / b->block] * b->block +
+	    p % b->block;
+}
+
+int
+orc_set_rows_f16(uint16_t *dst, int64_t dst_rows, int64_t row, const float *src,
+    const int64_t *ids, int64_t n)
+{
+	for (int64_t j = 0; j < n; j++) {
+		if (ids[j] < 0 || ids[j] >= dst_rows)
+			return -1;
+		orc_f32_to_f16_row(src + j * row, dst + ids[j] * row, row);
+	}
+	return 0;
+}
+
+/* The per-sequence softmax(q k^T * scale + mask) v of
+ * transformer.lua:1803-1817 (M.attend) under the fill_blocks mask of
+ * src/lgml.c:2936-3017: query j of sequence s (position npast + j) sees
+ * the cells of positions 0..npast+j; other cells are -inf and drop out.
+ * GQA: query head h reads kv head h / (H / Hkv) (src/lgml.c:1805-1809).
+ * Scores and sums in f64, K and V read from f16 storage. */
+int
+orc_paged_attention(const float *q, const uint16_t *kpool, const uint16_t *vpool, int H,
+    int Hkv, int D, float scale, const orc_batch *b, float *out, int n_threads)
+{
+	int64_t N = 0;
+	int64_t *off = malloc(sizeof(int64_t) * (size_t)(b->n_seq + 1));
+	if (!off)
+		return -1;
+	for (int s = 0; s < b->n_seq; s++) {
+		off[s] = N;
+		N += b->seq_n[s];
+	}
+	off[b->n_seq] = N;
+	int64_t row = (int64_t)Hkv * D;
+	int G = H / Hkv;
+	int bad = 0;
+
+#pragma omp parallel num_threads(nthreads(n_threads))
+	{
+		int maxp = 0;
+		for (int s = 0; s < b->n_seq; s++)
+			if (b->seq_npast[s] + b->seq_n[s] > maxp)
+				maxp = b->seq_npast[s] + b->seq_n[s];
+		double *sc = malloc(sizeof(double) * (size_t)(maxp + 1));
+		double *acc = malloc(sizeof(double) * (size_t)D);
+		if (!sc || !acc) {
+#pragma omp atomic write
+			bad = 1;
+		}
+#pragma omp for schedule(dynamic, 1) collapse(2)
+		for (int64_t t = 0; t < N; t++) {
+			for (int h = 0; h < H; h++) {
+				if (!sc || !acc)
+					continue;
+				int s = 0;
+				while (off[s + 1] <= t)
+					s++;
+				int p = b->seq_npast[s] + (int)(t - off[s]);
+				int kh = h / G;
+				const float *qh = q + (t * H + h) * D;
+				double mx = -INFINITY;
+				for (int j = 0; j <= p; j++) {
+					const uint16_t *kr = kpool + cell_of(b, s, j) * row + (int64_t)kh * D;
+					double a = 0;
+					for (int d = 0; d < D; d++)
+						a += (double)qh[d] * (double)orc_f16_to_f32(kr[d]);
+					sc[j] = a * scale;
+					if (sc[j] > mx)
+						mx = sc[j];
+				}
+				double sum = 0;
+				for (int j = 0; j <= p; j++) {
+					sc[j] = exp(sc[j] - mx);
+					sum += sc[j];
+				}
+				for (int d = 0; d < D; d++)
+					acc[d] = 0;
+				for (int j = 0; j <= p; j++) {
+					const uint16_t *vr = vpool + cell_of(b, s, j) * row + (int64_t)kh * D;
+					double w = sc[j] / sum;
+					for (int d = 0; d < D; d++)
+						acc[d] += w * (double)orc_f16_to_f32(vr[d]);
+				}
+				float *o = out + (t * H + h) * D;
+				for (int d = 0; d < D; d++)
+					o[d] = (float)acc[d];
+			}
+		}
+		free(sc);
+		free(acc);
+	}
+	free(off);
+	return bad ? -1 : 0;
+}
+
+int32_t
+orc_argmax(const float *v, int64_t n)
+{
+	int64_t best = 0;
+	float m = v[0];
+
+	for (int64_t i = 1; i < n; i++) {
+		if (v[i] > m) {
+			m = v[i];
+			best = i;
+		}
+	}
+	return (int32_t)best;
+}
+
+static void
+embed_rows(const orc_tensor *t, int64_t E, const int32_t *ids, int64_t N, float *x)
+{
+	int64_t rs = orc_row_size(t->type, E);
+	for (int64_t i = 0; i < N; i++)
+		orc_dequantize_row(t->type, (const uint8_t *)t->data + ids[i] * rs, x + i * E, E);
+}
+
+static int
+mm(const orc_tensor *w, int64_t M, int64_t K, const float *x, int64_t N, float *y, int nt)
+{
+	return orc_mul_mat(w->type, w->data, M, K, x, N, y, nt);
+}
+
+/* transformer.lua:2285-2365 (forward) with qkv (:1754-1789), the batched
+ * attention (:2389-2416: set_rows into the pool, then attend per
+ * sequence), attn_out (:1859-1872), ffn (:2042-2080, SwiGLU), and head
+ * (:2094-2104) on the rows of logit_rows (:2349-2350). Dense llama / qwen3
+ * layers; every matrix is an f32 or quantized weight. */
+int
+orc_forward(const orc_model *m, uint16_t *const *kpool, uint16_t *const *vpool,
+    int64_t cap, const orc_batch *b, float *logits, int nt)
+{
+	const int64_t E = m->n_embd, H = m->n_head, Hkv = m->n_head_kv, D = m->head_dim;
+	const int64_t F = m->n_ff, V = m->n_vocab;
+	int64_t N = 0;
+	int rc = 0;
+
+	for (int s = 0; s < b->n_seq; s++)
+		N += b->seq_n[s];
+	if (N == 0)
+		return 0;
+	float *x = malloc(sizeof(float) * (size_t)(N * E));
+	float *cur = malloc(sizeof(float) * (size_t)(N * E));
+	float *q = malloc(sizeof(float) * (size_t)(N * H * D));
+	float *k = malloc(sizeof(float) * (size_t)(N * Hkv * D));
+	float *v = malloc(sizeof(float) * (size_t)(N * Hkv * D));
+	float *o = malloc(sizeof(float) * (size_t)(N * H * D));
+	float *tmp = malloc(sizeof(float) * (size_t)(N * (E > H * D ? E : H * D)));
+	float *g = malloc(sizeof(float) * (size_t)(N * F));
+	float *u = malloc(sizeof(float) * (size_t)(N * F));
+	int32_t *pos = malloc(sizeof(int32_t) * (size_t)N);
+	int64_t *cells = malloc(sizeof(int64_t) * (size_t)N);
+	if (!x || !cur || !q || !k || !v || !o || !tmp || !g || !u || !pos || !cells) {
+		rc = -1;
+		goto done;
+	}
+	for (int s = 0, t = 0; s < b->n_seq; s++) {
+		for (int j = 0; j < b->seq_n[s]; j++, t++) {
+			pos[t] = b->seq_npast[s] + j;
+			cells[t] = cell_of(b, s, pos[t]);
+			if (cells[t] < 0 || cells[t] >= cap) {
+				rc = -2;
+				goto done;
+			}
+		}
+	}
+	embed_rows(&m->tok_embd, E, b->ids, N, x);
+	float scale = m->attn_scale > 0 ? m->attn_scale : 1.0f / sqrtf((float)D);
+	for (int il = 0; il < m->n_layer; il++) {
+		const orc_layer *L = &m->layers[il];
+		for (int64_t t = 0; t < N; t++)
+			rms_norm_row(x + t * E, cur + t * E, E, m->eps, (const float *)L->attn_norm.data);
+		if (mm(&L->wq, H * D, E, cur, N, q, nt) || mm(&L->wk, Hkv * D, E, cur, N, k, nt) ||
+		    mm(&L->wv, Hkv * D, E, cur, N, v, nt)) {
+			rc = -3;
+			goto done;
+		}
+		for (int64_t t = 0; t < N; t++) {
+			if (L->q_norm.data)
+				for (int h = 0; h < H; h++)
+					rms_norm_row(q + (t * H + h) * D, q + (t * H + h) * D, D, m->eps,
+					    (const float *)L->q_norm.data);
+			if (L->k_norm.data)
+				for (int h = 0; h < Hkv; h++)
+					rms_norm_row(k + (t * Hkv + h) * D, k + (t * Hkv + h) * D, D, m->eps,
+					    (const float *)L->k_norm.data);
+			rope_row(q + t * H * D, (int)H, (int)D, m->n_rot, m->rope_neox, m->rope_base,
+			    m->rope_freqs, pos[t]);
+			rope_row(k + t * Hkv * D, (int)Hkv, (int)D, m->n_rot, m->rope_neox, m->rope_base,
+			    m->rope_freqs, pos[t]);
+		}
+		orc_set_rows_f16(kpool[il], cap, Hkv * D, k, cells, N);
+		orc_set_rows_f16(vpool[il], cap, Hkv * D, v, cells, N);
+		if (orc_paged_attention(q, kpool[il], vpool[il], (int)H, (int)Hkv, (int)D, scale, b, o,
+		    nt)) {
+			rc = -4;
+			goto done;
+		}
+		if (mm(&L->wo, E, H * D, o, N, tmp, nt)) {
+			rc = -3;
+			goto done;
+		}
+		for (int64_t i = 0; i < N * E; i++)
+			x[i] = tmp[i] + x[i];
+		for (int64_t t = 0; t < N; t++)
+			rms_norm_row(x + t * E, cur + t * E, E, m->eps, (const float *)L->ffn_norm.data);
+		if (mm(&L->gate, F, E, cur, N, g, nt) || mm(&L->up, F, E, cur, N, u, nt)) {
+			rc = -3;
+			goto done;
+		}
+		for (int64_t i = 0; i < N * F; i++) {
+			double gv = g[i];
+			g[i] = (float)(gv / (1.0 + exp(-gv)) * (double)u[i]);
+		}
+		if (mm(&L->down, E, F, g, N, tmp, nt)) {
+			rc = -3;
+			goto done;
+		}
+		for (int64_t i = 0; i < N * E; i++)
+			x[i] = tmp[i] + x[i];
+	}
+	for (int r = 0; r < b->n_out; r++) {
+		if (b->out_rows[r] < 0 || b->out_rows[r] >= N) {
+			rc = -5;
+			goto done;
+		}
+		rms_norm_row(x + (int64_t)b->out_rows[r] * E, cur + (int64_t)r * E, E, m->eps,
+		    (const float *)m->output_norm.data);
+	}
+	if (mm(&m->output, V, E, cur, b->n_out, logits, nt))
+		rc = -3;
+done:
+	free(x);
+	free(cur);
+	free(q);
+	free(k);
+	free(v);
+	free(o);
+	free(tmp);
+	free(g);
+	free(u);
+	free(pos);
+	free(cells);
+	return rc;
+}

@@ -1,0 +1,111 @@
+/*
+ * CPU oracle for the lgml ragged decode/prefill path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Nothing in the shipped library (lgml_amd/)
+ * links, loads or calls this code. Only tests/, the smoke check in
+ * __graft_entry__.py and the cpu_baseline leg of bench.py use it, and
+ * only as the checker or the CPU baseline, never as the thing measured.
+ *
+ * Semantics: fp32 values, f64 reductions, f16 (round to nearest even)
+ * KV storage, closed-form Q4_K / Q6_K / Q8_0 dequantization, no
+ * activation quantization. Each function cites the reference file:line
+ * whose behaviour it restates (paths under the lgml tree).
+ */
+#ifndef LGML_ORACLE_H
+#define LGML_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids of the weight formats the path uses. */
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q6_K = 14 };
+
+/* ---- random numbers ---------------------------------------------------- */
+/* test/tiny.lua:16-22: x <- x*6364136223846793005 + 1442695040888963407,
+ * u = (x >> 11) / 2^53. state is advanced in place. */
+double orc_lcg_next(uint64_t *state);
+/* Fill n floats with lo + (hi - lo) * u, computed in double and rounded
+ * to f32, as test_qwen_moe.lua:77-86 and gguf.lua:41-50 store them. */
+void orc_lcg_fill(uint64_t *state, float *out, int64_t n, double lo, double hi);
+/* src/lgml.c:3064-3079,3130-3136: splitmix64 unit numbers and the
+ * Box-Muller "normal" fill (two draws per value, cos branch). */
+void orc_fill_normal(uint64_t *seed, float *out, int64_t n, double mean, double sd);
+void orc_fill_uniform(uint64_t *seed, float *out, int64_t n, double a, double b);
+
+/* ---- f16 ----------------------------------------------------------------- */
+uint16_t orc_f32_to_f16(float f);
+float orc_f16_to_f32(uint16_t h);
+void orc_f32_to_f16_row(const float *x, uint16_t *y, int64_t n);
+void orc_f16_to_f32_row(const uint16_t *x, float *y, int64_t n);
+
+/* ---- quantized formats --------------------------------------------------- */
+int64_t orc_row_size(int type, int64_t n);
+/* Dequantize n values (a multiple of the block size) of one row. */
+int orc_dequantize_row(int type, const void *src, float *dst, int64_t n);
+/* The oracle's own deterministic quantizer (format-exact, not ggml's
+ * search). Returns bytes written. */
+int64_t orc_quantize_row(int type, const float *src, void *dst, int64_t n);
+
+/* ---- dense model --------------------------------------------------------- */
+typedef struct {
+	int type;           /* ORC_* */
+	const void *data;   /* rows of `cols` values in `type` */
+} orc_tensor;
+
+typedef struct {
+	orc_tensor attn_norm, wq, wk, wv, wo, q_norm, k_norm, ffn_norm, gate, up, down;
+} orc_layer;
+
+typedef struct {
+	int n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab, n_rot;
+	float eps, rope_base, attn_scale; /* attn_scale 0 means 1/sqrt(head_dim) */
+	int rope_neox;                    /* 0 normal (llama), 1 neox (qwen3, gemma) */
+	const float *rope_freqs;          /* n_rot/2 factors or NULL */
+	orc_tensor tok_embd, output, output_norm;
+	const orc_layer *layers;
+} orc_model;
+
+/* One ubatch over a paged pool. Sequence s owns tokens
+ * [off_s, off_s + seq_n[s]) of ids (off_s = sum of earlier seq_n), at
+ * positions seq_npast[s] + j. Position p of sequence s lives in pool cell
+ * block_tab[s * max_blocks + p / block] * block + p % block.
+ * kpool[l], vpool[l] are (cap, n_head_kv * head_dim) f16 rows.
+ * logits gets one row per out_rows entry (token indices into the ubatch).
+ * hidden_out, when not NULL, gets the final-normed rows (n_out, n_embd). */
+typedef struct {
+	int n_seq, max_blocks, block;
+	const int32_t *seq_n, *seq_npast, *block_tab;
+	const int32_t *ids;
+	int n_out;
+	const int32_t *out_rows;
+} orc_batch;
+
+int orc_forward(const orc_model *m, uint16_t *const *kpool, uint16_t *const *vpool,
+    int64_t cap, const orc_batch *b, float *logits, int n_threads);
+
+/* Paged attention alone (the flash_attn / fill_blocks pair, per sequence).
+ * q: (N, H, D) f32 in ubatch order. out: (N, H, D) f32. Causal over the
+ * sequence's own positions 0..npast+j. */
+int orc_paged_attention(const float *q, const uint16_t *kpool, const uint16_t *vpool,
+    int H, int Hkv, int D, float scale, const orc_batch *b, float *out, int n_threads);
+
+/* ggml_set_rows (src/lgml.c:1937-1969): dst[ids[j]] = f16(src[j]). */
+int orc_set_rows_f16(uint16_t *dst, int64_t dst_rows, int64_t row, const float *src,
+    const int64_t *ids, int64_t n);
+
+/* Y (N, M) = X (N, K) W^T, W rows in `type` (ggml mul_mat convention,
+ * src/lgml.c:1811-1839). f64 accumulation. */
+int orc_mul_mat(int type, const void *w, int64_t M, int64_t K, const float *x, int64_t N,
+    float *y, int n_threads);
+
+/* Greedy first-max argmax (src/sample.c:914-925). */
+int32_t orc_argmax(const float *v, int64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
