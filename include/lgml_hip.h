@@ -1,0 +1,241 @@
+/*
+ * lgml_hip: MI355X (gfx950) kernels for lgml's ragged continuous-batching
+ * decode/prefill path, behind a plain C ABI.
+ *
+ * Every entry point takes plain pointers and sizes, returns an int status
+ * (LGMLH_OK = 0, negative on error, text in lgmlh_last_error()), never
+ * longjmps, and never allocates device or host memory: callers pass
+ * buffers and workspaces whose sizes the *_bytes / *_workspace functions
+ * report. Device pointers are HIP device addresses; `stream` is a
+ * hipStream_t (NULL = the null stream). Calls on one stream are ordered;
+ * calls on different streams that share a workspace race.
+ *
+ * Reference citations are paths under the lgml tree (mischief/lgml).
+ */
+#ifndef LGML_HIP_H
+#define LGML_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LGMLH_ABI_VERSION 1
+
+enum {
+	LGMLH_OK = 0,
+	LGMLH_EINVAL = -1, /* bad argument or shape (luaL_error "... shape mismatch") */
+	LGMLH_ENOMEM = -2, /* workspace or buffer too small */
+	LGMLH_EHIP = -3,   /* a HIP runtime call failed */
+	LGMLH_EFULL = -4,  /* kv pool full (transformer.lua:975, "kv pool full") */
+	LGMLH_ERANGE = -5  /* an index (cell, id, position) out of range */
+};
+
+/* Weight / element types, numbered as ggml's type ids. */
+enum { LGMLH_F32 = 0, LGMLH_F16 = 1, LGMLH_Q8_0 = 8, LGMLH_Q4_K = 12, LGMLH_Q6_K = 14 };
+
+/* Text of the last error on this thread (never NULL). */
+const char *lgmlh_last_error(void);
+int lgmlh_abi_version(void);
+
+/* Bytes of one row of n values in `type` (src/lgml.c:3603-3619 row_size). */
+int64_t lgmlh_row_size(int type, int64_t n);
+
+/* ===================================================================== *
+ * Paged KV pool.
+ *
+ * Replaces the pool tensors pool.k[il] / pool.v[il] of M:pool
+ * (lua/lgml/transformer.lua:678-705), (cap, Hkv*D) f16 rows, with an
+ * MI355X layout of 64-cell blocks (BLOCK, transformer.lua:30):
+ *   K: [block][kv_head][cell % 64][D]   (a 64 x D tile per block and head)
+ *   V: [block][kv_head][D][cell % 64]   (the same tile, transposed)
+ * Cell c of the reference lives in block c / 64 at offset c % 64, so the
+ * reference's cell ids (seq_cells, transformer.lua:1126-1133) are used
+ * unchanged. One layer's K (or V) takes lgmlh_kv_layer_bytes bytes.
+ * ===================================================================== */
+int64_t lgmlh_kv_layer_bytes(int64_t n_cells, int n_head_kv, int head_dim);
+
+/* The KV scatter of attention_batch (transformer.lua:2403-2409): two
+ * graph:set_rows (src/lgml.c:1937-1969) into the pool. k_src, v_src are
+ * (n, Hkv*D) f32 rows, stored as f16 (round to nearest even) at cells[j].
+ * Errors: LGMLH_ERANGE (checked on the host) if a cell id is outside
+ * [0, n_cells) -- the host copy h_cells is required for that check. */
+int lgmlh_kv_store(void *kpool, void *vpool, int64_t n_cells, int n_head_kv, int head_dim,
+    const float *k_src, const float *v_src, const int64_t *cells, const int64_t *h_cells,
+    int64_t n, void *stream);
+
+/* Read cells back as (n, Hkv*D) f16 rows in the reference row layout
+ * (which = 0: K, 1: V). For tests, snapshots and host spill. */
+int lgmlh_kv_gather(const void *pool, int which, int64_t n_cells, int n_head_kv, int head_dim,
+    const int64_t *cells, int64_t n, uint16_t *out, void *stream);
+
+/* Copy the first n cells of block src to block dst in one layer's K and V
+ * (M.copy_block, transformer.lua:989-1007, without the host round trip). */
+int lgmlh_kv_copy_block(void *kpool, void *vpool, int64_t n_cells, int n_head_kv, int head_dim,
+    int32_t src, int32_t dst, int n, void *stream);
+
+/* Plain ggml_set_rows on a row-major f16 tensor: dst[ids[j]] = f16(src[j])
+ * (src/lgml.c:1937-1969). h_ids is the host copy for the range check. */
+int lgmlh_set_rows_f16(uint16_t *dst, int64_t dst_rows, int64_t row, const float *src,
+    const int64_t *ids, const int64_t *h_ids, int64_t n, void *stream);
+
+/* ===================================================================== *
+ * Ubatch plan: the packing of fill_batch / batch_inputs
+ * (transformer.lua:2433-2551) plus the attention work list.
+ *
+ * A pass runs n_seq sequences; sequence s has seq_n[s] tokens at positions
+ * seq_npast[s] + j and a block table of max_blocks entries
+ * (block_tab[s * max_blocks + i] = block of positions [64 i, 64 i + 64)).
+ * lgmlh_plan fills one host buffer that the caller copies to the device
+ * unchanged; lgmlh_plan_bind turns a device copy into the device views.
+ * ===================================================================== */
+typedef struct {
+	int32_t n_seq, n_tokens, max_blocks, block;
+	int32_t n_items, n_merge, rows, n_head_kv; /* attention work sizes */
+	int64_t bytes;                             /* bytes of the plan buffer */
+	/* byte offsets of the arrays inside the plan buffer */
+	int64_t off_ids, off_pos, off_cells, off_seq_off, off_npast, off_block_tab, off_logit_rows,
+	    off_items, off_merge;
+} lgmlh_plan_info;
+
+typedef struct {
+	int32_t n_seq, n_tokens, max_blocks, block;
+	int32_t n_items, n_merge, rows, n_head_kv;
+	const int32_t *ids;        /* [n_tokens] token ids, sequences in pass order */
+	const int32_t *pos;        /* [n_tokens] n_past + j (fill_batch :2446-2451) */
+	const int64_t *cells;      /* [n_tokens] pool cells (seq_cells) */
+	const int32_t *seq_off;    /* [n_seq + 1] first token of each sequence */
+	const int32_t *seq_npast;  /* [n_seq] */
+	const int32_t *block_tab;  /* [n_seq * max_blocks] */
+	const int32_t *logit_rows; /* [n_seq] off + n - 1 (batch_inputs :2540-2545) */
+	const int32_t *items;      /* [n_items * 4] attention work items */
+	const int32_t *merge;      /* [n_merge * 4] split-merge items */
+} lgmlh_ubatch;
+
+/* Plan a pass. G = n_head / n_head_kv; blocks_per_split bounds the KV
+ * blocks one work item reads (0 = choose). With buf NULL only info is
+ * filled (sizes); otherwise buf must hold info->bytes. Errors:
+ * LGMLH_ERANGE when a block id that a position needs is outside
+ * [0, pool_blocks) (the fill_blocks "position ... is in no column" error,
+ * src/lgml.c:3003-3008), or a position passes 65535 blocks. */
+int lgmlh_plan(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
+    const int32_t *block_tab, int max_blocks, int64_t pool_blocks, const int32_t *ids,
+    int n_head, int n_head_kv, int blocks_per_split, void *buf, size_t buf_bytes,
+    lgmlh_plan_info *info);
+/* Device views of a plan buffer at dev (a device copy of buf). */
+int lgmlh_plan_bind(const lgmlh_plan_info *info, const void *dev, lgmlh_ubatch *ub);
+
+/* ===================================================================== *
+ * Paged GQA attention: the per-sequence graph:flash_attn
+ * (src/lgml.c:2121-2170) over the fill_blocks mask (src/lgml.c:2936-3017)
+ * of attention_batch (transformer.lua:2389-2416), for all sequences of a
+ * pass in one launch. Query row t (sequence s, position npast + j) sees
+ * exactly the cells of positions 0..npast+j of s, read through its block
+ * table; other cells are never read (the mask made them -inf).
+ * q: (n_tokens, H, D) f32; out: (n_tokens, H, D) f32 written in place in
+ * pass order (the concat chain of :2413 is not needed). K/V from the pool
+ * layout above. scale: 1/sqrt(D) for llama (transformer.lua:1845).
+ * D in {64, 128, 256}; H a multiple of Hkv with H/Hkv in {1, 2, 4, 8, 16}.
+ * ===================================================================== */
+size_t lgmlh_attention_workspace(const lgmlh_plan_info *info, int head_dim);
+int lgmlh_paged_attention(const float *q, int n_head, int n_head_kv, int head_dim, float scale,
+    const void *kpool, const void *vpool, const lgmlh_ubatch *ub, float *out, void *workspace,
+    size_t workspace_bytes, void *stream);
+
+/* ===================================================================== *
+ * Weight matrix products: graph:mul_mat (src/lgml.c:1811-1839), ggml
+ * convention: W (M, K) rows of `type`, X (N, K) -> Y (N, M) f32.
+ * Quantized weights are first repacked (once, at load) from the ggml
+ * block layout into row tiles of 16 rows (as ggml's CPU backend repacks
+ * into interleaved buffers); the values are the same bytes, permuted.
+ * F32 weights are used in place (no repack).
+ * ===================================================================== */
+int64_t lgmlh_repacked_bytes(int type, int64_t M, int64_t K);
+int lgmlh_repack(int type, int64_t M, int64_t K, const void *src, void *dst, void *stream);
+
+/* Dequantize rows [0, M) of a ggml-layout matrix to f32 (M, K); the
+ * closed form of the block format, bit-exact with the CPU reference. */
+int lgmlh_dequantize(int type, const void *src, int64_t M, int64_t K, float *out, void *stream);
+
+enum { LGMLH_EPI_NONE = 0, LGMLH_EPI_ADD = 1 };
+
+/* Workspace of a call: split-K partial sums and per-tile counters. It must
+ * be zero-filled once before its first use; every call leaves the counter
+ * words at zero again, so one workspace serves any number of calls on one
+ * stream (calls on two streams need two workspaces). */
+size_t lgmlh_mul_mat_workspace(int type, int64_t M, int64_t K, int64_t N);
+/* y = X W^T (+ residual when epi == LGMLH_EPI_ADD; residual may alias y).
+ * x is f32 or f16 (xtype). Quantized types take the repacked w. The
+ * result of an output element does not depend on N or on the other rows
+ * of X (fixed summation order), so a row gives the same bits alone or in
+ * any batch. */
+int lgmlh_mul_mat(int type, const void *w, int64_t M, int64_t K, const void *x, int xtype,
+    int64_t N, float *y, int epi, const float *residual, void *workspace, size_t ws_bytes,
+    void *stream);
+
+/* ===================================================================== *
+ * Dense-layer ops around the hot ops (transformer.lua:1754-1789,
+ * 1859-1872, 2042-2104).
+ * ===================================================================== */
+/* get_rows of a (rows, n_cols) table in `type` (ggml layout): out f32. */
+int lgmlh_get_rows(int type, const void *table, int64_t n_rows, int64_t n_cols,
+    const int32_t *ids, const int32_t *h_ids, int64_t n, float *out, void *stream);
+/* rms_norm(x) * w per row (graph:rms_norm, src/lgml.c:1633); out f32 or f16. */
+int lgmlh_rms_norm(const float *x, int64_t n_rows, int64_t n, float eps, const float *w,
+    void *out, int out_type, void *stream);
+/* The qkv tail (transformer.lua:1776-1788): optional per-head rms_norm with
+ * q_norm / k_norm, rope (graph:rope, src/lgml.c:2004-2081: mode normal or
+ * neox, freq factors), then the KV store of k and v at cells. q is roped
+ * in place. qkv is (n, (H + 2 Hkv) * D) f32 with [q | k | v] per row. */
+int lgmlh_qkv_rope_store(float *qkv, int64_t n, int n_head, int n_head_kv, int head_dim,
+    int n_rot, int neox, float freq_base, const float *freq_factors, const float *q_norm,
+    const float *k_norm, float eps, const int32_t *pos, void *kpool, void *vpool,
+    int64_t n_cells, const int64_t *cells, float *q_out, void *stream);
+/* silu(g) * u (transformer.lua:2048) for gu = (n, 2F) rows [g | u]; out f32 or f16. */
+int lgmlh_swiglu(const float *gu, int64_t n, int64_t F, void *out, int out_type, void *stream);
+/* Greedy id of each row: the first index of the maximum (src/sample.c:914-925). */
+int lgmlh_argmax(const float *x, int64_t n_rows, int64_t n_cols, int32_t *out, void *stream);
+
+/* ===================================================================== *
+ * One forward pass of a dense llama / qwen3 model over a planned ubatch:
+ * transformer.lua forward (:2285-2365) with the batched attention of
+ * attention_batch (:2389-2416), for every sequence of the pass at once.
+ * Weights are device pointers: quantized matrices repacked, f32 in place.
+ * wqkv holds the rows of [wq | wk | wv] (or [wq | wk] with wv separate
+ * when its type differs, as in the Q4_K_M mix); wgu holds [gate | up].
+ * ===================================================================== */
+typedef struct {
+	const float *attn_norm, *ffn_norm, *q_norm, *k_norm; /* q/k_norm may be NULL */
+	int wqkv_type, wv_type, wo_type, wgu_type, wdown_type;
+	int64_t wqkv_rows;       /* rows of wqkv: (H + 2 Hkv) D, or (H + Hkv) D */
+	const void *wqkv, *wv, *wo, *wgu, *wdown; /* wv NULL when inside wqkv */
+	void *kpool, *vpool;     /* this layer's pool tensors */
+} lgmlh_layer;
+
+typedef struct {
+	int n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab, n_rot, rope_neox;
+	float eps, rope_base, attn_scale; /* attn_scale 0: 1 / sqrt(head_dim) */
+	const float *rope_freqs;          /* n_rot / 2 factors or NULL */
+	int tok_embd_type, output_type;
+	const void *tok_embd;             /* ggml row layout (get_rows) */
+	const void *output;               /* repacked (or f32) */
+	const float *output_norm;
+	int64_t n_cells;                  /* pool cells per layer */
+	const lgmlh_layer *layers;        /* host array of n_layer */
+} lgmlh_model;
+
+/* Workspace bytes of lgmlh_forward for a plan and n_out logit rows. Zero-
+ * fill it once before its first use (split-K counters). */
+size_t lgmlh_forward_workspace(const lgmlh_model *m, const lgmlh_plan_info *info, int n_out);
+/* Run the pass: logits (n_out, n_vocab) f32 for the ubatch rows out_rows
+ * (device; NULL = ub->logit_rows with n_out = n_seq). ids must be in range
+ * (checked by the caller's plan, h_ids) -- the kernel reads them unchecked. */
+int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub, const int32_t *out_rows,
+    int n_out, float *logits, void *workspace, size_t ws_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

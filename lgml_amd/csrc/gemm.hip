@@ -1,0 +1,488 @@
+// Weight products Y (N, M) = X (N, K) W^T for f32 / Q4_K / Q6_K / Q8_0 W
+// (graph:mul_mat, src/lgml.c:1811-1839) on gfx950.
+//
+// Quantized W is repacked once into row tiles of 16 rows. For row tile rt
+// and K step sb (256 values) one chunk holds the tile's block headers and
+// then, for each of the 64 lanes of a wavefront (lane = r + 16 c: row r,
+// 8-value k chunk c of every 32-value group), exactly the bytes that lane
+// dequantizes into its MFMA A fragment. A wave streams its chunks with
+// 16-byte loads, dequantizes in registers (closed forms of quant.h, one
+// rounding to f16), and multiplies with 16x16x32 f16 MFMAs against X
+// staged in LDS as f16. Every output element is the same f32 sum over K in
+// the same order for any N, so a row gives the same bits alone or batched.
+// K is split over workgroups when M alone gives too few; the splits are
+// added in a fixed order by the last workgroup of each tile.
+#include "common.h"
+#include "quant.h"
+
+namespace lgmlh {
+
+constexpr int GEMM_WAVES = 4;      // waves per workgroup
+constexpr int RT_PER_WAVE = 4;     // 16-row tiles per wave
+constexpr int WG_ROWS = GEMM_WAVES * RT_PER_WAVE * 16;  // 256
+constexpr int WG_COLS = 64;        // N columns per workgroup (4 tiles)
+constexpr int X_STRIDE = 264;      // f16 per LDS row of X (256 + pad)
+
+// Bytes of one repacked chunk (16 rows x 256 values).
+__host__ __device__ constexpr int chunk_bytes(int type) {
+  return type == LGMLH_Q4_K ? 16 * Q4K_BYTES
+       : type == LGMLH_Q6_K ? 16 * Q6K_BYTES
+       : type == LGMLH_Q8_0 ? 16 * 8 * Q8_0_BYTES : 0;
+}
+// Bytes of the header part of a chunk.
+__host__ __device__ constexpr int chunk_hdr(int type) {
+  return type == LGMLH_Q4_K ? 256 : type == LGMLH_Q6_K ? 288 : type == LGMLH_Q8_0 ? 256 : 0;
+}
+// Bytes of one lane's data in a chunk.
+__host__ __device__ constexpr int lane_bytes(int type) {
+  return type == LGMLH_Q4_K ? 32 : type == LGMLH_Q6_K ? 48 : type == LGMLH_Q8_0 ? 64 : 0;
+}
+
+// ---- repack: ggml row blocks -> row-tile chunks ------------------------------
+// One thread per (row tile, sb, lane): copies the lane's bytes and, for
+// c == 0, the row's header.
+template <int TYPE>
+__global__ void repack_kernel(const uint8_t *__restrict__ src, int64_t M, int64_t NSB,
+                              uint8_t *__restrict__ dst) {
+  int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  int64_t MT = (M + 15) / 16;
+  if (gid >= MT * NSB * 64) return;
+  int lane = (int)(gid % 64);
+  int64_t sb = (gid / 64) % NSB, rt = gid / 64 / NSB;
+  int r = lane % 16, c = lane / 16;
+  int64_t m = rt * 16 + r;
+  uint8_t *ch = dst + (rt * NSB + sb) * chunk_bytes(TYPE);
+  uint8_t *ld = ch + chunk_hdr(TYPE) + lane * lane_bytes(TYPE);
+  if (m >= M) {  // padding rows: zero bytes dequantize to 0
+    for (int i = 0; i < lane_bytes(TYPE); i++) ld[i] = 0;
+    if (c == 0)
+      for (int i = 0; i < chunk_hdr(TYPE) / 16; i++) ch[r * (chunk_hdr(TYPE) / 16) + i] = 0;
+    return;
+  }
+  if (TYPE == LGMLH_Q4_K) {
+    const uint8_t *b = src + (m * NSB + sb) * Q4K_BYTES;
+    if (c == 0)
+      for (int i = 0; i < 16; i++) ch[r * 16 + i] = b[i];
+    for (int j = 0; j < 4; j++)
+      for (int e = 0; e < 8; e++) ld[8 * j + e] = b[16 + 32 * j + 8 * c + e];
+  } else if (TYPE == LGMLH_Q6_K) {
+    const uint8_t *b = src + (m * NSB + sb) * Q6K_BYTES;
+    if (c == 0) {
+      ch[r * 18 + 0] = b[208];
+      ch[r * 18 + 1] = b[209];
+      for (int i = 0; i < 16; i++) ch[r * 18 + 2 + i] = b[192 + i];
+    }
+    // ql pieces (h, tb): ql[64h + 32tb + 8c .. +7]; then qh pieces h: qh[32h + 8c .. +7]
+    for (int h = 0; h < 2; h++)
+      for (int tb = 0; tb < 2; tb++)
+        for (int e = 0; e < 8; e++) ld[8 * (2 * h + tb) + e] = b[64 * h + 32 * tb + 8 * c + e];
+    for (int h = 0; h < 2; h++)
+      for (int e = 0; e < 8; e++) ld[32 + 8 * h + e] = b[128 + 32 * h + 8 * c + e];
+  } else {  // Q8_0: 8 blocks of 32 per 256 values
+    const uint8_t *b = src + (m * NSB * 8 + sb * 8) * Q8_0_BYTES;
+    if (c == 0)
+      for (int g = 0; g < 8; g++) {
+        ch[r * 16 + 2 * g] = b[g * Q8_0_BYTES];
+        ch[r * 16 + 2 * g + 1] = b[g * Q8_0_BYTES + 1];
+      }
+    for (int g = 0; g < 8; g++)
+      for (int e = 0; e < 8; e++) ld[8 * g + e] = b[g * Q8_0_BYTES + 2 + 8 * c + e];
+  }
+}
+
+// ---- per-lane weight data of one chunk --------------------------------------
+template <int TYPE>
+struct WFrag;
+
+template <>
+struct WFrag<LGMLH_Q4_K> {
+  u32x4 hdr;       // d | dmin << 16, scales[0..3], scales[4..7], scales[8..11]
+  u32x4 qs[2];     // 4 pieces of 8 bytes
+  __device__ void load(const uint8_t *ch, int lane) {
+    hdr = *(const u32x4 *)(ch + (lane & 15) * 16);
+    const u32x4 *p = (const u32x4 *)(ch + 256 + lane * 32);
+    qs[0] = p[0];
+    qs[1] = p[1];
+  }
+  __device__ __forceinline__ uint8_t sbyte(int i) const {
+    uint32_t w = hdr[1 + (i >> 2)];
+    return (uint8_t)(w >> (8 * (i & 3)));
+  }
+  // A fragment of 32-value group g (k = 32g + 8c + e).
+  __device__ __forceinline__ f16x8 frag(int g) const {
+    float d = h2f((uint16_t)hdr[0]), dmin = h2f((uint16_t)(hdr[0] >> 16));
+    int sc, m;
+    if (g < 4) {
+      sc = sbyte(g) & 63;
+      m = sbyte(g + 4) & 63;
+    } else {
+      sc = (sbyte(g + 4) & 0xF) | ((sbyte(g - 4) >> 6) << 4);
+      m = (sbyte(g + 4) >> 4) | ((sbyte(g) >> 6) << 4);
+    }
+    float d1 = d * (float)sc, m1 = dmin * (float)m;
+    int j = g >> 1;
+    uint32_t lo = qs[j >> 1][2 * (j & 1)], hi = qs[j >> 1][2 * (j & 1) + 1];
+    int sh = (g & 1) * 4;
+    f16x8 r;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      r[e] = (f16)(d1 * (float)((lo >> (8 * e + sh)) & 15) - m1);
+      r[4 + e] = (f16)(d1 * (float)((hi >> (8 * e + sh)) & 15) - m1);
+    }
+    return r;
+  }
+};
+
+template <>
+struct WFrag<LGMLH_Q6_K> {
+  uint32_t hdr[5];  // d (16 bits) + 16 int8 scales, 18 bytes from row r's header
+  u32x4 ql[2];      // pieces (h, tb) of 8 bytes: index 2h + tb
+  u32x4 qh;         // pieces h of 8 bytes
+  __device__ void load(const uint8_t *ch, int lane) {
+    const uint16_t *h = (const uint16_t *)(ch + (lane & 15) * 18);
+#pragma unroll
+    for (int i = 0; i < 4; i++) hdr[i] = (uint32_t)h[2 * i] | ((uint32_t)h[2 * i + 1] << 16);
+    hdr[4] = h[8];
+    const u32x4 *p = (const u32x4 *)(ch + 288 + lane * 48);
+    ql[0] = p[0];
+    ql[1] = p[1];
+    qh = p[2];
+  }
+  __device__ __forceinline__ f16x8 frag(int g, int c) const {
+    // bytes of hdr: [0..1] d, [2..17] scales
+    float d = h2f((uint16_t)hdr[0]);
+    int si = 2 * g + (c >> 1);  // scale of values 32g + 8c .. : (32g + 8c) / 16
+    int sb = 2 + si;
+    int8_t scv = (int8_t)(hdr[sb >> 2] >> (8 * (sb & 3)));
+    float dsc = d * (float)scv;
+    int h = g >> 2, t = g & 3;
+    int piece = 2 * h + (t & 1);
+    uint32_t lo = ql[piece >> 1][2 * (piece & 1)], hi = ql[piece >> 1][2 * (piece & 1) + 1];
+    uint32_t hlo = qh[2 * h], hhi = qh[2 * h + 1];
+    int nsh = t < 2 ? 0 : 4;
+    f16x8 r;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      int q0 = (int)(((lo >> (8 * e + nsh)) & 15) | (((hlo >> (8 * e + 2 * t)) & 3) << 4)) - 32;
+      int q1 = (int)(((hi >> (8 * e + nsh)) & 15) | (((hhi >> (8 * e + 2 * t)) & 3) << 4)) - 32;
+      r[e] = (f16)(dsc * (float)q0);
+      r[4 + e] = (f16)(dsc * (float)q1);
+    }
+    return r;
+  }
+};
+
+template <>
+struct WFrag<LGMLH_Q8_0> {
+  u32x4 hdr;           // 8 f16 scales of row r
+  const uint8_t *qs;   // the lane's 8 blocks x 8 int8, read per group
+  __device__ void load(const uint8_t *ch, int lane) {
+    hdr = *(const u32x4 *)(ch + (lane & 15) * 16);
+    qs = ch + 256 + lane * 64;
+  }
+  __device__ __forceinline__ f16x8 frag(int g) const {
+    float d = h2f((uint16_t)(hdr[g >> 1] >> (16 * (g & 1))));
+    u32x2 q = *(const u32x2 *)(qs + 8 * g);
+    f16x8 r;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      r[e] = (f16)(d * (float)(int8_t)(q[0] >> (8 * e)));
+      r[4 + e] = (f16)(d * (float)(int8_t)(q[1] >> (8 * e)));
+    }
+    return r;
+  }
+};
+
+template <int TYPE>
+__device__ __forceinline__ f16x8 wfrag(const WFrag<TYPE> &w, int g, int c) {
+  if constexpr (TYPE == LGMLH_Q6_K)
+    return w.frag(g, c);
+  else
+    return w.frag(g);
+}
+
+// ---- the quantized GEMM --------------------------------------------------------
+// grid: (ceil(N / 64), ceil(M / 256), splits). blockIdx.x (N tiles) varies
+// fastest so the workgroups that share a weight tile run together.
+template <int TYPE, bool XF32>
+__global__ void __launch_bounds__(256, 2)
+qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__restrict__ xv,
+             int64_t N, float *__restrict__ y, int64_t ldy, const float *__restrict__ residual,
+             int splits, int sb_per_split, float *__restrict__ part,
+             int32_t *__restrict__ counters) {
+  __shared__ __align__(16) f16 xs[WG_COLS * X_STRIDE];
+  __shared__ int last_flag;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t NSB = K / QK_K;
+  const int64_t MT = (M + 15) / 16;
+  const int64_t n0 = (int64_t)blockIdx.x * WG_COLS;
+  const int64_t rt0 = (int64_t)blockIdx.y * (WG_ROWS / 16) + wave * RT_PER_WAVE;
+  const int z = blockIdx.z;
+  const int64_t sb_lo = (int64_t)z * sb_per_split;
+  const int64_t sb_hi = sb_lo + sb_per_split < NSB ? sb_lo + sb_per_split : NSB;
+  const int c = lane >> 4;
+
+  f32x4 acc[RT_PER_WAVE][4];
+#pragma unroll
+  for (int a = 0; a < RT_PER_WAVE; a++)
+#pragma unroll
+    for (int b = 0; b < 4; b++) acc[a][b] = f32x4{0, 0, 0, 0};
+
+  for (int64_t sb = sb_lo; sb < sb_hi; sb++) {
+    // Stage X[n0 .. n0+64][sb*256 .. +256] in LDS as f16 (zeros past N).
+    __syncthreads();
+    if constexpr (XF32) {
+      const float *x = (const float *)xv;
+      for (int i = tid; i < WG_COLS * 64; i += 256) {  // 64 pieces of 4 floats per row
+        int r = i >> 6, p = i & 63;
+        int64_t n = n0 + r;
+        f32x4 v = f32x4{0, 0, 0, 0};
+        if (n < N) v = *(const f32x4 *)(x + n * K + sb * QK_K + p * 4);
+        f16x4 h = f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+        *(f16x4 *)(xs + r * X_STRIDE + p * 4) = h;
+      }
+    } else {
+      const f16 *x = (const f16 *)xv;
+      for (int i = tid; i < WG_COLS * 32; i += 256) {  // 32 pieces of 8 f16 per row
+        int r = i >> 5, p = i & 31;
+        int64_t n = n0 + r;
+        u32x4 v = u32x4{0, 0, 0, 0};
+        if (n < N) v = *(const u32x4 *)(x + n * K + sb * QK_K + p * 8);
+        *(u32x4 *)(xs + r * X_STRIDE + p * 8) = v;
+      }
+    }
+    __syncthreads();
+
+    WFrag<TYPE> wf[RT_PER_WAVE];
+#pragma unroll
+    for (int a = 0; a < RT_PER_WAVE; a++) {
+      int64_t rt = rt0 + a;
+      if (rt < MT) wf[a].load(w + (rt * NSB + sb) * chunk_bytes(TYPE), lane);
+    }
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+      f16x8 bx[4];
+#pragma unroll
+      for (int ct = 0; ct < 4; ct++)
+        bx[ct] = *(const f16x8 *)(xs + (ct * 16 + (lane & 15)) * X_STRIDE + g * 32 + c * 8);
+#pragma unroll
+      for (int a = 0; a < RT_PER_WAVE; a++) {
+        if (rt0 + a >= MT) continue;
+        f16x8 af = wfrag<TYPE>(wf[a], g, c);
+#pragma unroll
+        for (int ct = 0; ct < 4; ct++)
+          acc[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bx[ct], acc[a][ct], 0, 0, 0);
+      }
+    }
+  }
+
+  // acc[a][ct][i] = Y[n0 + ct*16 + lane%16][(rt0+a)*16 + 4*(lane/16) + i]
+  if (splits == 1) {
+#pragma unroll
+    for (int a = 0; a < RT_PER_WAVE; a++)
+#pragma unroll
+      for (int ct = 0; ct < 4; ct++) {
+        int64_t n = n0 + ct * 16 + (lane & 15);
+        int64_t m = (rt0 + a) * 16 + 4 * c;
+        if (n >= N) continue;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (m + i < M) {
+            float v = acc[a][ct][i];
+            if (residual) v += residual[n * ldy + m + i];
+            y[n * ldy + m + i] = v;
+          }
+      }
+    return;
+  }
+  // Split K: write this split's tile, then the last workgroup of the tile
+  // adds all splits in order 0..splits-1.
+  float *pz = part + (int64_t)z * N * M;
+#pragma unroll
+  for (int a = 0; a < RT_PER_WAVE; a++)
+#pragma unroll
+    for (int ct = 0; ct < 4; ct++) {
+      int64_t n = n0 + ct * 16 + (lane & 15);
+      int64_t m = (rt0 + a) * 16 + 4 * c;
+      if (n >= N) continue;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        if (m + i < M) pz[n * M + m + i] = acc[a][ct][i];
+    }
+  __threadfence();
+  __syncthreads();
+  int32_t *cnt = counters + (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+  if (tid == 0) last_flag = atomicAdd(cnt, 1) == splits - 1;
+  __syncthreads();
+  if (!last_flag) return;
+  __threadfence();
+  const int64_t mlo = (int64_t)blockIdx.y * WG_ROWS;
+  const int64_t ncols = N - n0 < WG_COLS ? N - n0 : WG_COLS;
+  const int64_t mrows = M - mlo < WG_ROWS ? M - mlo : WG_ROWS;
+  for (int64_t e = tid; e < ncols * mrows; e += 256) {
+    int64_t n = n0 + e / mrows, m = mlo + e % mrows;
+    float v = 0.0f;
+    for (int zz = 0; zz < splits; zz++) v += __builtin_nontemporal_load(part + ((int64_t)zz * N + n) * M + m);
+    if (residual) v += residual[n * ldy + m];
+    y[n * ldy + m] = v;
+  }
+  if (tid == 0) *cnt = 0;  // ready for the next call
+}
+
+// ---- f32 weights: LDS-tiled VALU GEMM, sequential k order ----------------------
+__global__ void __launch_bounds__(256)
+f32gemm_kernel(const float *__restrict__ w, int64_t M, int64_t K, const float *__restrict__ x,
+               int64_t N, float *__restrict__ y, int64_t ldy, const float *__restrict__ residual) {
+  __shared__ float ws_[16][17], xs_[16][17];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int64_t m = (int64_t)blockIdx.x * 16 + tx, n = (int64_t)blockIdx.y * 16 + ty;
+  float acc = 0.0f;
+  for (int64_t k0 = 0; k0 < K; k0 += 16) {
+    int64_t wm = (int64_t)blockIdx.x * 16 + ty, xn = (int64_t)blockIdx.y * 16 + ty;
+    ws_[ty][tx] = (wm < M && k0 + tx < K) ? w[wm * K + k0 + tx] : 0.0f;
+    xs_[ty][tx] = (xn < N && k0 + tx < K) ? x[xn * K + k0 + tx] : 0.0f;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; k++) acc = fmaf(xs_[ty][k], ws_[tx][k], acc);
+    __syncthreads();
+  }
+  if (m < M && n < N) {
+    float v = acc;
+    if (residual) v += residual[n * ldy + m];
+    y[n * ldy + m] = v;
+  }
+}
+
+// K splits depend on M and K only, never on N: each output element is then
+// the same sum in the same order for any batch size.
+int splits_for(int64_t M, int64_t K, int64_t N) {
+  (void)N;
+  int64_t NSB = K / QK_K;
+  int64_t tiles = (M + WG_ROWS - 1) / WG_ROWS;
+  // Aim for ~512 workgroups (two per CU) at 64 columns, at least 2 K steps
+  // per split.
+  int64_t want = (512 + tiles - 1) / tiles;
+  int64_t maxs = NSB / 2 > 1 ? NSB / 2 : 1;
+  if (want > maxs) want = maxs;
+  if (want < 1) want = 1;
+  return (int)want;
+}
+
+size_t workspace_for(int type, int64_t M, int64_t K, int64_t N) {
+  if (type == LGMLH_F32) return 0;
+  int s = splits_for(M, K, N);
+  if (s == 1) return 0;
+  int64_t tiles = ((M + WG_ROWS - 1) / WG_ROWS) * ((N + WG_COLS - 1) / WG_COLS);
+  return (size_t)s * N * M * 4 + (size_t)tiles * 4 + 256;
+}
+
+template <int TYPE>
+static void launch_q(const void *w, int64_t M, int64_t K, const void *x, int xtype, int64_t N,
+                     float *y, int64_t ldy, const float *res, int splits, void *ws,
+                     hipStream_t st) {
+  int64_t NSB = K / QK_K;
+  int spb = (int)((NSB + splits - 1) / splits);
+  splits = (int)((NSB + spb - 1) / spb);
+  dim3 grid((unsigned)((N + WG_COLS - 1) / WG_COLS), (unsigned)((M + WG_ROWS - 1) / WG_ROWS),
+            (unsigned)splits);
+  float *part = (float *)ws;
+  int32_t *cnt = splits > 1 ? (int32_t *)((char *)ws + (size_t)splits * N * M * 4) : nullptr;
+  if (xtype == LGMLH_F32)
+    hipLaunchKernelGGL((qgemm_kernel<TYPE, true>), grid, dim3(256), 0, st, (const uint8_t *)w, M,
+                       K, x, N, y, ldy, res, splits, spb, part, cnt);
+  else
+    hipLaunchKernelGGL((qgemm_kernel<TYPE, false>), grid, dim3(256), 0, st, (const uint8_t *)w,
+                       M, K, x, N, y, ldy, res, splits, spb, part, cnt);
+}
+
+// Internal entry with an output row stride (the executor writes [q|k|v]
+// and [gate|up] rows from separate weights into one buffer).
+int mul_mat_ldy(int type, const void *w, int64_t M, int64_t K, const void *x, int xtype,
+                int64_t N, float *y, int64_t ldy, const float *residual, void *ws,
+                size_t ws_bytes, hipStream_t st) {
+  if (!w || !x || !y || M <= 0 || K <= 0 || N < 0 || ldy < M ||
+      (xtype != LGMLH_F32 && xtype != LGMLH_F16)) {
+    set_error("mul_mat: bad arguments");
+    return LGMLH_EINVAL;
+  }
+  if (N == 0) return LGMLH_OK;
+  if (type == LGMLH_F32) {
+    if (xtype != LGMLH_F32) {
+      set_error("mul_mat: f32 weights take f32 x");
+      return LGMLH_EINVAL;
+    }
+    dim3 grid((unsigned)((M + 15) / 16), (unsigned)((N + 15) / 16));
+    hipLaunchKernelGGL(f32gemm_kernel, grid, dim3(256), 0, st, (const float *)w, M, K,
+                       (const float *)x, N, y, ldy, residual);
+    return hip_check(hipGetLastError(), "mul_mat");
+  }
+  if (K % QK_K) {
+    set_error("mul_mat: K = %lld is not a multiple of 256", (long long)K);
+    return LGMLH_EINVAL;
+  }
+  int splits = splits_for(M, K, N);
+  if (splits > 1 && ws_bytes < workspace_for(type, M, K, N)) {
+    set_error("mul_mat: workspace of %zu bytes, need %zu", ws_bytes,
+              workspace_for(type, M, K, N));
+    return LGMLH_ENOMEM;
+  }
+  switch (type) {
+    case LGMLH_Q4_K: launch_q<LGMLH_Q4_K>(w, M, K, x, xtype, N, y, ldy, residual, splits, ws, st); break;
+    case LGMLH_Q6_K: launch_q<LGMLH_Q6_K>(w, M, K, x, xtype, N, y, ldy, residual, splits, ws, st); break;
+    case LGMLH_Q8_0: launch_q<LGMLH_Q8_0>(w, M, K, x, xtype, N, y, ldy, residual, splits, ws, st); break;
+    default:
+      set_error("mul_mat: type %d not supported", type);
+      return LGMLH_EINVAL;
+  }
+  return hip_check(hipGetLastError(), "mul_mat");
+}
+
+}  // namespace lgmlh
+
+using namespace lgmlh;
+
+extern "C" int64_t lgmlh_repacked_bytes(int type, int64_t M, int64_t K) {
+  if (M <= 0 || K <= 0) return -1;
+  if (type == LGMLH_F32) return M * K * 4;
+  if (chunk_bytes(type) == 0 || K % QK_K) return -1;
+  return ((M + 15) / 16) * (K / QK_K) * chunk_bytes(type);
+}
+
+extern "C" int lgmlh_repack(int type, int64_t M, int64_t K, const void *src, void *dst,
+                            void *stream) {
+  if (!src || !dst || lgmlh_repacked_bytes(type, M, K) < 0) {
+    set_error("repack: bad arguments (type %d, M %lld, K %lld)", type, (long long)M, (long long)K);
+    return LGMLH_EINVAL;
+  }
+  hipStream_t st = as_stream(stream);
+  if (type == LGMLH_F32)
+    return hip_check(hipMemcpyAsync(dst, src, (size_t)(M * K * 4), hipMemcpyDeviceToDevice, st),
+                     "repack");
+  int64_t NSB = K / QK_K, total = ((M + 15) / 16) * NSB * 64;
+  unsigned blocks = (unsigned)((total + 255) / 256);
+  switch (type) {
+    case LGMLH_Q4_K: hipLaunchKernelGGL(repack_kernel<LGMLH_Q4_K>, dim3(blocks), dim3(256), 0, st, (const uint8_t *)src, M, NSB, (uint8_t *)dst); break;
+    case LGMLH_Q6_K: hipLaunchKernelGGL(repack_kernel<LGMLH_Q6_K>, dim3(blocks), dim3(256), 0, st, (const uint8_t *)src, M, NSB, (uint8_t *)dst); break;
+    case LGMLH_Q8_0: hipLaunchKernelGGL(repack_kernel<LGMLH_Q8_0>, dim3(blocks), dim3(256), 0, st, (const uint8_t *)src, M, NSB, (uint8_t *)dst); break;
+  }
+  return hip_check(hipGetLastError(), "repack");
+}
+
+extern "C" size_t lgmlh_mul_mat_workspace(int type, int64_t M, int64_t K, int64_t N) {
+  return workspace_for(type, M, K, N);
+}
+
+extern "C" int lgmlh_mul_mat(int type, const void *w, int64_t M, int64_t K, const void *x,
+                             int xtype, int64_t N, float *y, int epi, const float *residual,
+                             void *workspace, size_t ws_bytes, void *stream) {
+  if (epi != LGMLH_EPI_NONE && epi != LGMLH_EPI_ADD) {
+    set_error("mul_mat: bad epilogue");
+    return LGMLH_EINVAL;
+  }
+  if (epi == LGMLH_EPI_ADD && !residual) {
+    set_error("mul_mat: the add epilogue needs a residual");
+    return LGMLH_EINVAL;
+  }
+  return mul_mat_ldy(type, w, M, K, x, xtype, N, y, M, epi == LGMLH_EPI_ADD ? residual : nullptr,
+                     workspace, ws_bytes, as_stream(stream));
+}

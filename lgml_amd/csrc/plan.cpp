@@ -1,0 +1,168 @@
+// Ubatch packing and the attention work list (host side).
+//
+// Packs what fill_batch / batch_inputs (lua/lgml/transformer.lua:2433-2551)
+// put in the graph leaves -- ids, positions n_past + j, the pool cell of
+// every token (seq_cells, :1126-1133), the block tables, the logit rows
+// off + n - 1 -- into one buffer for a single host-to-device copy, and adds
+// the work list of the paged attention kernel: for every sequence, groups
+// of 16 / G query tokens, each split into runs of at most blocks_per_split
+// KV blocks, plus one merge item per group with more than one split.
+#include <string.h>
+
+#include <vector>
+
+#include "common.h"
+
+namespace lgmlh {
+static int64_t align16(int64_t x) { return (x + 15) & ~int64_t(15); }
+}  // namespace lgmlh
+
+using namespace lgmlh;
+
+extern "C" int lgmlh_plan(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
+                          const int32_t *block_tab, int max_blocks, int64_t pool_blocks,
+                          const int32_t *ids, int n_head, int n_head_kv, int blocks_per_split,
+                          void *buf, size_t buf_bytes, lgmlh_plan_info *info) {
+  if (n_seq < 0 || !seq_n || !seq_npast || !block_tab || max_blocks <= 0 || !info ||
+      n_head_kv <= 0 || n_head % n_head_kv || n_head / n_head_kv > 16 ||
+      16 % (n_head / n_head_kv) || blocks_per_split < 0) {
+    set_error("plan: bad arguments");
+    return LGMLH_EINVAL;
+  }
+  const int G = n_head / n_head_kv, T = 16 / G, B = KV_BLOCK;
+  int64_t N = 0, total_blocks = 0;
+  for (int s = 0; s < n_seq; s++) {
+    if (seq_n[s] < 0 || seq_npast[s] < 0) {
+      set_error("plan: negative count");
+      return LGMLH_EINVAL;
+    }
+    int64_t n_kv = (int64_t)seq_npast[s] + seq_n[s];
+    int64_t nb = (n_kv + B - 1) / B;
+    if (nb > max_blocks || nb > 0xffff) {
+      set_error("plan: sequence %d needs %lld blocks (table has %d)", s, (long long)nb,
+                max_blocks);
+      return LGMLH_ERANGE;
+    }
+    for (int64_t i = 0; i < nb; i++) {
+      int32_t b = block_tab[(int64_t)s * max_blocks + i];
+      if (b < 0 || b >= pool_blocks) {
+        set_error("plan: position %lld of sequence %d is in no block (block %d, pool of %lld)",
+                  (long long)(i * B), s, b, (long long)pool_blocks);
+        return LGMLH_ERANGE;
+      }
+    }
+    N += seq_n[s];
+    for (int g0 = 0; g0 < seq_n[s]; g0 += T) {
+      int ge = g0 + T < seq_n[s] ? g0 + T : seq_n[s];
+      total_blocks += ((int64_t)seq_npast[s] + ge - 1) / B + 1;
+    }
+  }
+  if (N > INT32_MAX / 2) {
+    set_error("plan: too many tokens");
+    return LGMLH_EINVAL;
+  }
+  int bps = blocks_per_split;
+  if (bps == 0) {
+    // About 4096 waves in flight over the KV heads, at least 2 blocks each.
+    int64_t want = (total_blocks * n_head_kv + 4095) / 4096;
+    bps = (int)(want < 2 ? 2 : want > 64 ? 64 : want);
+  }
+  std::vector<int32_t> items, merge;
+  for (int s = 0, off = 0; s < n_seq; off += seq_n[s], s++) {
+    for (int g0 = 0; g0 < seq_n[s]; g0 += T) {
+      int ge = g0 + T < seq_n[s] ? g0 + T : seq_n[s];
+      int nbg = (int)(((int64_t)seq_npast[s] + ge - 1) / B + 1);
+      int ns = (nbg + bps - 1) / bps;
+      int first = (int)(items.size() / 4);
+      for (int j = 0; j < ns; j++) {
+        int lo = j * bps, hi = (j + 1) * bps < nbg ? (j + 1) * bps : nbg;
+        items.push_back(s);
+        items.push_back(off + g0);
+        items.push_back((ge - g0) | (ns == 1 ? 1 << 16 : 0));
+        items.push_back(lo | (hi << 16));
+      }
+      if (ns > 1) {
+        merge.push_back(first);
+        merge.push_back(ns);
+        merge.push_back(off + g0);
+        merge.push_back(ge - g0);
+      }
+    }
+  }
+  lgmlh_plan_info in;
+  memset(&in, 0, sizeof in);
+  in.n_seq = n_seq;
+  in.n_tokens = (int32_t)N;
+  in.max_blocks = max_blocks;
+  in.block = B;
+  in.n_items = (int32_t)(items.size() / 4);
+  in.n_merge = (int32_t)(merge.size() / 4);
+  in.rows = 16;
+  in.n_head_kv = n_head_kv;
+  int64_t o = 0;
+  in.off_ids = o;          o = align16(o + 4 * N);
+  in.off_pos = o;          o = align16(o + 4 * N);
+  in.off_cells = o;        o = align16(o + 8 * N);
+  in.off_seq_off = o;      o = align16(o + 4 * ((int64_t)n_seq + 1));
+  in.off_npast = o;        o = align16(o + 4 * (int64_t)n_seq);
+  in.off_block_tab = o;    o = align16(o + 4 * (int64_t)n_seq * max_blocks);
+  in.off_logit_rows = o;   o = align16(o + 4 * (int64_t)n_seq);
+  in.off_items = o;        o = align16(o + 4 * (int64_t)items.size());
+  in.off_merge = o;        o = align16(o + 4 * (int64_t)merge.size());
+  in.bytes = o;
+  *info = in;
+  if (!buf) return LGMLH_OK;
+  if (buf_bytes < (size_t)in.bytes) {
+    set_error("plan: buffer of %zu bytes, need %lld", buf_bytes, (long long)in.bytes);
+    return LGMLH_ENOMEM;
+  }
+  char *b = (char *)buf;
+  memset(b, 0, (size_t)in.bytes);
+  int32_t *pid = (int32_t *)(b + in.off_ids), *ppos = (int32_t *)(b + in.off_pos);
+  int64_t *pcell = (int64_t *)(b + in.off_cells);
+  int32_t *psoff = (int32_t *)(b + in.off_seq_off), *pnp = (int32_t *)(b + in.off_npast);
+  int32_t *plr = (int32_t *)(b + in.off_logit_rows);
+  int64_t t = 0;
+  for (int s = 0; s < n_seq; s++) {
+    psoff[s] = (int32_t)t;
+    pnp[s] = seq_npast[s];
+    for (int j = 0; j < seq_n[s]; j++, t++) {
+      int p = seq_npast[s] + j;
+      if (ids) pid[t] = ids[t];
+      ppos[t] = p;
+      pcell[t] = (int64_t)block_tab[(int64_t)s * max_blocks + p / B] * B + p % B;
+    }
+    plr[s] = (int32_t)t - 1;
+  }
+  psoff[n_seq] = (int32_t)t;
+  memcpy(b + in.off_block_tab, block_tab, 4 * (size_t)n_seq * max_blocks);
+  if (!items.empty()) memcpy(b + in.off_items, items.data(), 4 * items.size());
+  if (!merge.empty()) memcpy(b + in.off_merge, merge.data(), 4 * merge.size());
+  return LGMLH_OK;
+}
+
+extern "C" int lgmlh_plan_bind(const lgmlh_plan_info *info, const void *dev, lgmlh_ubatch *ub) {
+  if (!info || !dev || !ub) {
+    set_error("plan_bind: bad arguments");
+    return LGMLH_EINVAL;
+  }
+  const char *b = (const char *)dev;
+  ub->n_seq = info->n_seq;
+  ub->n_tokens = info->n_tokens;
+  ub->max_blocks = info->max_blocks;
+  ub->block = info->block;
+  ub->n_items = info->n_items;
+  ub->n_merge = info->n_merge;
+  ub->rows = info->rows;
+  ub->n_head_kv = info->n_head_kv;
+  ub->ids = (const int32_t *)(b + info->off_ids);
+  ub->pos = (const int32_t *)(b + info->off_pos);
+  ub->cells = (const int64_t *)(b + info->off_cells);
+  ub->seq_off = (const int32_t *)(b + info->off_seq_off);
+  ub->seq_npast = (const int32_t *)(b + info->off_npast);
+  ub->block_tab = (const int32_t *)(b + info->off_block_tab);
+  ub->logit_rows = (const int32_t *)(b + info->off_logit_rows);
+  ub->items = (const int32_t *)(b + info->off_items);
+  ub->merge = (const int32_t *)(b + info->off_merge);
+  return LGMLH_OK;
+}

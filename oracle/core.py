@@ -63,6 +63,9 @@ def _declare(L):
     L.orc_lcg_fill.argtypes = [C.POINTER(C.c_uint64), vp, i64, C.c_double, C.c_double]
     L.orc_fill_normal.argtypes = [C.POINTER(C.c_uint64), vp, i64, C.c_double, C.c_double]
     L.orc_fill_uniform.argtypes = [C.POINTER(C.c_uint64), vp, i64, C.c_double, C.c_double]
+    L.orc_gen_normal.argtypes = [C.c_uint64, vp, i64, C.c_double, C.c_double, i32]
+    L.orc_gen_normal_quant.argtypes = [C.c_uint64, i32, i64, i64, C.c_double, C.c_double, vp, i32]
+    L.orc_gen_normal_quant.restype = i64
     L.orc_f32_to_f16_row.argtypes = [vp, vp, i64]
     L.orc_f16_to_f32_row.argtypes = [vp, vp, i64]
     L.orc_row_size.argtypes = [i32, i64]
@@ -103,6 +106,27 @@ def fill_normal(n, mean, sd, seed):
     s = C.c_uint64(seed & (2**64 - 1))
     out = np.empty(n, np.float32)
     lib().orc_fill_normal(C.byref(s), _p(out), n, mean, sd)
+    return out
+
+
+def threads():
+    """OpenMP threads for the oracle: OMP_NUM_THREADS, else up to 16 cores."""
+    return int(os.environ.get("OMP_NUM_THREADS") or min(16, os.cpu_count() or 1))
+
+
+def gen_normal(n, mean, sd, seed):
+    """fill_normal's values (same seed), generated in parallel."""
+    out = np.empty(n, np.float32)
+    lib().orc_gen_normal(seed & (2**64 - 1), _p(out), n, mean, sd, threads())
+    return out
+
+
+def gen_normal_quant(t, rows, cols, mean, sd, seed):
+    """gen_normal(rows * cols) quantized row by row; uint8 (rows, row_size)."""
+    out = np.empty((rows, row_size(t, cols)), np.uint8)
+    if lib().orc_gen_normal_quant(seed & (2**64 - 1), t, rows, cols, mean, sd, _p(out),
+                                  threads()) < 0:
+        raise ValueError("gen_normal_quant failed")
     return out
 
 
@@ -152,12 +176,12 @@ def dequantize(t, q, K):
     return out
 
 
-def mul_mat(t, w, M, K, x, threads=8):
+def mul_mat(t, w, M, K, x, nthreads=None):
     x = np.ascontiguousarray(x, np.float32)
     N = x.shape[0]
     y = np.empty((N, M), np.float32)
     w = np.ascontiguousarray(w)
-    if lib().orc_mul_mat(t, _p(w), M, K, _p(x), N, _p(y), threads) != 0:
+    if lib().orc_mul_mat(t, _p(w), M, K, _p(x), N, _p(y), nthreads or threads()) != 0:
         raise ValueError("mul_mat failed")
     return y
 
@@ -183,11 +207,11 @@ class BatchDesc:
                        _p(self.block_tab), _p(self.ids), len(self.out_rows), _p(self.out_rows))
 
 
-def paged_attention(q, kpool, vpool, H, Hkv, D, scale, batch, threads=8):
+def paged_attention(q, kpool, vpool, H, Hkv, D, scale, batch, nthreads=None):
     q = np.ascontiguousarray(q, np.float32)
     out = np.empty_like(q)
     rc = lib().orc_paged_attention(_p(q), _p(kpool), _p(vpool), H, Hkv, D, scale,
-                                   C.byref(batch.c), _p(out), threads)
+                                   C.byref(batch.c), _p(out), nthreads or threads())
     if rc:
         raise ValueError("paged_attention failed")
     return out
@@ -236,14 +260,15 @@ class OracleModel:
             setattr(self.c, f, Tensor(ty, _p(arr).value))
         self.c.layers = self.layers
 
-    def forward(self, kpools, vpools, batch, threads=8):
+    def forward(self, kpools, vpools, batch, nthreads=None):
         """kpools/vpools: lists of (cap, Hkv*D) uint16 arrays (f16 bits), updated in place."""
         L = self.hp["n_layer"]
         kp = (C.c_void_p * L)(*[_p(a).value for a in kpools])
         vp = (C.c_void_p * L)(*[_p(a).value for a in vpools])
         cap = kpools[0].shape[0]
         out = np.empty((len(batch.out_rows), self.hp["n_vocab"]), np.float32)
-        rc = lib().orc_forward(C.byref(self.c), kp, vp, cap, C.byref(batch.c), _p(out), threads)
+        rc = lib().orc_forward(C.byref(self.c), kp, vp, cap, C.byref(batch.c), _p(out),
+                               nthreads or threads())
         if rc:
             raise ValueError("orc_forward failed: %d" % rc)
         return out

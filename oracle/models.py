@@ -135,8 +135,10 @@ def build(shape, seed=1234, n_layer=None, init="uniform"):
             x = lcg.fill(rows * cols, -s, s).reshape(rows, cols)
         else:
             counter[0] += 1
-            x = core.fill_normal(rows * cols, 0.0, 0.02, seed * 1000003 + counter[0])
-            x = x.reshape(rows, cols)
+            tseed = seed * 1000003 + counter[0]
+            if ty == core.F32:
+                return (core.gen_normal(rows * cols, 0.0, 0.02, tseed).reshape(rows, cols), ty)
+            return (core.gen_normal_quant(ty, rows, cols, 0.0, 0.02, tseed), ty)
         if ty == core.F32:
             return (x, ty)
         return (core.quantize(ty, x), ty)

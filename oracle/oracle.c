@@ -83,6 +83,61 @@ orc_fill_normal(uint64_t *seed, float *out, int64_t n, double mean, double sd)
 	}
 }
 
+/* The same values as orc_fill_normal(seed, out, n, ...), computed in
+ * parallel: splitmix64's state after j draws is seed + j * gamma, so value
+ * i (draws 2i+1, 2i+2) needs no sequential pass. */
+static float
+normal_at(uint64_t seed, int64_t i, double mean, double sd)
+{
+	uint64_t a = seed + (uint64_t)(2 * i) * 0x9e3779b97f4a7c15ULL;
+	uint64_t b = a + 0x9e3779b97f4a7c15ULL;
+	double u1 = unit01(&a), u2 = unit01(&b);
+	return (float)(mean + sd * sqrt(-2.0 * log(u1 > 0 ? u1 : 1e-300)) *
+	    cos(6.283185307179586 * u2));
+}
+
+void
+orc_gen_normal(uint64_t seed, float *out, int64_t n, double mean, double sd, int n_threads)
+{
+#pragma omp parallel for schedule(static) num_threads(n_threads > 0 ? n_threads : 1)
+	for (int64_t i = 0; i < n; i++)
+		out[i] = normal_at(seed, i, mean, sd);
+}
+
+/* rows x cols normal values (as orc_gen_normal) quantized row by row into
+ * type. Returns the bytes written or -1. */
+int64_t
+orc_gen_normal_quant(uint64_t seed, int type, int64_t rows, int64_t cols, double mean, double sd,
+    void *out, int n_threads)
+{
+	int64_t rs = orc_row_size(type, cols);
+	int bad = 0;
+
+	if (rs <= 0)
+		return -1;
+#pragma omp parallel num_threads(n_threads > 0 ? n_threads : 1)
+	{
+		float *row = malloc(sizeof(float) * (size_t)cols);
+		if (!row) {
+#pragma omp atomic write
+			bad = 1;
+		}
+#pragma omp for schedule(static)
+		for (int64_t r = 0; r < rows; r++) {
+			if (!row)
+				continue;
+			for (int64_t c = 0; c < cols; c++)
+				row[c] = normal_at(seed, r * cols + c, mean, sd);
+			if (orc_quantize_row(type, row, (uint8_t *)out + r * rs, cols) != rs) {
+#pragma omp atomic write
+				bad = 1;
+			}
+		}
+		free(row);
+	}
+	return bad ? -1 : rows * rs;
+}
+
 /* src/lgml.c:3128-3129 ("uniform"). */
 void
 orc_fill_uniform(uint64_t *seed, float *out, int64_t n, double a, double b)

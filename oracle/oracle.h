@@ -35,6 +35,11 @@ void orc_lcg_fill(uint64_t *state, float *out, int64_t n, double lo, double hi);
  * Box-Muller "normal" fill (two draws per value, cos branch). */
 void orc_fill_normal(uint64_t *seed, float *out, int64_t n, double mean, double sd);
 void orc_fill_uniform(uint64_t *seed, float *out, int64_t n, double a, double b);
+/* orc_fill_normal's values for a fresh seed, in parallel; and the same
+ * values quantized row by row (rows x cols) into `type`. */
+void orc_gen_normal(uint64_t seed, float *out, int64_t n, double mean, double sd, int n_threads);
+int64_t orc_gen_normal_quant(uint64_t seed, int type, int64_t rows, int64_t cols, double mean,
+    double sd, void *out, int n_threads);
 
 /* ---- f16 ----------------------------------------------------------------- */
 uint16_t orc_f32_to_f16(float f);

@@ -1,0 +1,124 @@
+"""CPU checks of the C ABI: the library loads, exports every function that
+include/lgml_hip.h declares, and its host-only entry points (sizes, the
+ubatch plan) behave; no GPU compute is called here."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+from oracle import kvpool as kp
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared():
+    text = open(os.path.join(ROOT, "include", "lgml_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lgmlh_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def hip():
+    from lgml_amd import build, hip
+    if not os.path.exists(hip.LIB_PATH):
+        build.build()
+    hip.lib()
+    return hip
+
+
+def test_exports_every_declared_symbol(hip):
+    names = declared()
+    assert len(names) >= 20
+    L = hip.lib()
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing
+    assert sorted(hip.SYMBOLS) == names
+    assert L.lgmlh_abi_version() == 1
+
+
+def test_sizes(hip):
+    L = hip.lib()
+    assert L.lgmlh_row_size(hip.Q4_K, 4096) == 16 * 144
+    assert L.lgmlh_row_size(hip.Q6_K, 4096) == 16 * 210
+    assert L.lgmlh_row_size(hip.Q8_0, 4096) == 128 * 34
+    assert L.lgmlh_row_size(hip.Q4_K, 100) == -1
+    assert L.lgmlh_kv_layer_bytes(4096, 8, 128) == 4096 * 8 * 128 * 2
+    assert L.lgmlh_kv_layer_bytes(100, 8, 128) == -1
+    assert L.lgmlh_repacked_bytes(hip.Q4_K, 4096, 4096) == 4096 * 16 * 144
+    assert L.lgmlh_repacked_bytes(hip.Q6_K, 1000, 4096) == 63 * 16 * 16 * 210
+    # split-K workspace does not depend on the batch size beyond the rows it holds
+    a = L.lgmlh_mul_mat_workspace(hip.Q4_K, 4096, 4096, 64)
+    b = L.lgmlh_mul_mat_workspace(hip.Q4_K, 4096, 4096, 128)
+    assert a > 0 and b > a
+
+
+def plan(hip, seq_n, npast, bt, ids, H, Hkv, pool_blocks, bps=0):
+    L = hip.lib()
+    info = hip.PlanInfo()
+    bt = np.ascontiguousarray(bt, np.int32)
+    args = (len(seq_n), np.ascontiguousarray(seq_n, np.int32).ctypes.data,
+            np.ascontiguousarray(npast, np.int32).ctypes.data, bt.ctypes.data, bt.shape[1],
+            pool_blocks, np.ascontiguousarray(ids, np.int32).ctypes.data, H, Hkv, bps)
+    keep = [np.ascontiguousarray(seq_n, np.int32), np.ascontiguousarray(npast, np.int32),
+            np.ascontiguousarray(ids, np.int32)]
+    args = (len(seq_n), keep[0].ctypes.data, keep[1].ctypes.data, bt.ctypes.data, bt.shape[1],
+            pool_blocks, keep[2].ctypes.data, H, Hkv, bps)
+    rc = L.lgmlh_plan(*args, None, 0, C.byref(info))
+    if rc:
+        return rc, None, None
+    buf = np.zeros(info.bytes, np.uint8)
+    rc = L.lgmlh_plan(*args, buf.ctypes.data, buf.nbytes, C.byref(info))
+    return rc, info, buf
+
+
+def arr(buf, off, n, dt):
+    return buf[off:off + n * np.dtype(dt).itemsize].view(dt)
+
+
+def test_plan_packs_like_fill_batch(hip):
+    # Two interleaved sequences (blocks from the pool restatement), one
+    # decode token and one 70-token chunk.
+    p = kp.Pool(64, 64)
+    a, b = kp.Seq(p), kp.Seq(p)
+    for n in (50, 100, 150):
+        kp.reserve(a, n)
+        kp.reserve(b, n)
+    kp.reserve(a, 151)
+    kp.reserve(b, 220)
+    bt = np.full((2, 4), -1, np.int32)
+    bt[0, :len(a.blocks)] = a.blocks
+    bt[1, :len(b.blocks)] = b.blocks
+    ids = np.arange(71, dtype=np.int32) + 7
+    rc, info, buf = plan(hip, [1, 70], [150, 150], bt, ids, 32, 8, 64, bps=2)
+    assert rc == 0 and info.n_tokens == 71 and info.n_seq == 2
+    assert list(arr(buf, info.off_ids, 71, np.int32)) == list(ids)
+    assert list(arr(buf, info.off_pos, 71, np.int32)) == [150] + list(range(150, 220))
+    want = kp.seq_cells(a.blocks, 64, 150, 1) + kp.seq_cells(b.blocks, 64, 150, 70)
+    assert list(arr(buf, info.off_cells, 71, np.int64)) == want
+    assert list(arr(buf, info.off_logit_rows, 2, np.int32)) == [0, 70]
+    assert list(arr(buf, info.off_seq_off, 3, np.int32)) == [0, 1, 71]
+    items = arr(buf, info.off_items, 4 * info.n_items, np.int32).reshape(-1, 4)
+    # every (token group, block) pair up to the group's last position is covered once
+    seen = {}
+    for s, tok0, nt, blk in items:
+        lo, hi = blk & 0xffff, blk >> 16
+        key = (int(s), int(tok0))
+        seen.setdefault(key, []).append((lo, hi))
+        assert hi - lo <= 2
+    for (s, tok0), runs in seen.items():
+        runs.sort()
+        assert runs[0][0] == 0 and all(runs[i][1] == runs[i + 1][0] for i in range(len(runs) - 1))
+    assert info.n_merge == sum(1 for r in seen.values() if len(r) > 1)
+
+
+def test_plan_errors(hip):
+    bt = np.array([[3, -1]], np.int32)
+    rc, _, _ = plan(hip, [1], [64], bt, [0], 4, 2, 16)  # position 64 needs block table[1]
+    assert rc == hip.ERANGE
+    rc, _, _ = plan(hip, [1], [0], np.array([[16]], np.int32), [0], 4, 2, 16)  # block 16 >= pool
+    assert rc == hip.ERANGE
+    rc, _, _ = plan(hip, [1], [0], np.array([[1]], np.int32), [0], 6, 4, 16)  # H % Hkv
+    assert rc == hip.EINVAL
+    assert "plan" in hip.last_error()

@@ -1,0 +1,101 @@
+"""End-to-end GPU parity of whole passes against the CPU oracle.
+
+C1: tiny llama-style f32 model, 4 slots with
+prompts 17/64/129/300 prefilled in one ragged pass, then 32 greedy decode
+steps batched over the 4 slots. Greedy tokens must be identical; logits
+within 2e-3 max relative error. C2-shaped passes at reduced depth (2 layers,
+full width, Q4_K_M mix) on ragged decode batches, same bar. Batched passes
+equal lone passes bit for bit.
+"""
+import numpy as np
+import pytest
+
+from oracle import core, models
+from tests.gpu_util import Schedule, lcg_ints, oracle_pools, rel_err
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def run_both(hp, w, n_cells, prompts, steps, seed=99):
+    from lgml_amd import runtime
+    gm = runtime.DeviceModel(hp, w, n_cells)
+    om = core.OracleModel(hp, w)
+    kp, vp = oracle_pools(hp, n_cells)
+    sch = Schedule(n_cells // 64, len(prompts))
+    which = list(range(len(prompts)))
+    npast = [0] * len(prompts)
+    cur = [list(p) for p in prompts]
+    errs, same = [], True
+    toks_g, toks_o = [[] for _ in prompts], [[] for _ in prompts]
+    for step in range(steps + 1):
+        for s in which:
+            sch.grow(s, npast[s] + len(cur[s]))
+        bt = sch.table(which)
+        seq_n = [len(cur[s]) for s in which]
+        ids = np.concatenate([np.array(cur[s], np.int32) for s in which])
+        plan = gm.plan(seq_n, [npast[s] for s in which], bt, ids)
+        lg = gm.forward(plan).cpu().numpy()
+        b = core.BatchDesc(seq_n, [npast[s] for s in which], bt, 64, ids, plan.logit_rows)
+        lo = om.forward(kp, vp, b)
+        errs.append(rel_err(lg, lo))
+        for i, s in enumerate(which):
+            g, o = int(np.argmax(lg[i])), core.argmax(lo[i])
+            toks_g[s].append(g)
+            toks_o[s].append(o)
+            same = same and g == o
+            npast[s] += len(cur[s])
+            cur[s] = [o]  # both sides continue on the oracle's token
+    return errs, same, toks_g, toks_o, gm, om, kp, vp, sch
+
+
+def test_c1_prefill_and_32_greedy_steps():
+    hp, w = models.build("c1", seed=1)
+    lens = [17, 64, 129, 300]
+    prompts = [lcg_ints(1000 + i, n, 0, hp["n_vocab"]) for i, n in enumerate(lens)]
+    errs, same, tg, to, gm, om, kp, vp, sch = run_both(hp, w, 4096, prompts, 32)
+    assert max(errs) < 2e-3, errs
+    assert same, (tg, to)
+    # the KV the GPU wrote is the oracle's, up to the f32 rounding of k and v
+    cells = np.concatenate([np.array(sch.seqs[s].blocks) for s in range(4)]) * 64
+    cells = (cells[:, None] + np.arange(64)).reshape(-1)
+    kg = core.f16_bits_to_f32(gm.gather_kv(1, cells, 0))
+    ko = core.f16_bits_to_f32(kp[1][cells])
+    assert rel_err(kg, ko) < 2e-3
+
+
+@pytest.mark.parametrize("n_layer", [2])
+def test_c2_shape_reduced_depth_ragged_decode(n_layer):
+    hp, w = models.build("c2", seed=2, n_layer=n_layer, init="normal")
+    # 6 ragged sequences, short prompts prefilled, then 4 decode steps
+    lens = [5, 70, 1, 130, 33, 64]
+    prompts = [lcg_ints(2000 + i, n, 0, hp["n_vocab"]) for i, n in enumerate(lens)]
+    errs, same, tg, to, *_ = run_both(hp, w, 4096, prompts, 4)
+    assert max(errs) < 2e-3, errs
+    assert same, (tg, to)
+
+
+def test_batched_pass_equals_lone_pass():
+    """test_batch.lua:40-81 / test_qwen_moe.lua:466-509: a sequence decoded in
+    a batch gives the same logits as decoded alone (here bit for bit)."""
+    from lgml_amd import runtime
+    hp, w = models.build("c2", seed=3, n_layer=2, init="normal")
+    gm_b = runtime.DeviceModel(hp, w, 2048)
+    gm_a = runtime.DeviceModel(hp, w, 2048)
+    prompts = [lcg_ints(3000 + i, n, 0, hp["n_vocab"]) for i, n in enumerate([9, 40, 3])]
+    sch = Schedule(32, 3)
+    for s, p in enumerate(prompts):
+        sch.grow(s, len(p) + 1)
+    bt = sch.table([0, 1, 2])
+    ids = np.concatenate([np.array(p, np.int32) for p in prompts])
+    lb = gm_b.forward(gm_b.plan([9, 40, 3], [0, 0, 0], bt, ids)).cpu().numpy()
+    for s, p in enumerate(prompts):
+        la = gm_a.forward(gm_a.plan([len(p)], [0], bt[s:s + 1], np.array(p, np.int32)))
+        assert np.array_equal(la.cpu().numpy()[0].view(np.uint32), lb[s].view(np.uint32))
+    nxt = [int(np.argmax(lb[s])) for s in range(3)]
+    lb2 = gm_b.forward(gm_b.plan([1, 1, 1], [9, 40, 3], bt, np.array(nxt, np.int32))).cpu().numpy()
+    for s in range(3):
+        la2 = gm_a.forward(gm_a.plan([1], [len(prompts[s])], bt[s:s + 1],
+                                     np.array([nxt[s]], np.int32))).cpu().numpy()
+        assert np.array_equal(la2[0].view(np.uint32), lb2[s].view(np.uint32))
