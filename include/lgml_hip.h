@@ -161,10 +161,10 @@ int lgmlh_dequantize(int type, const void *src, int64_t M, int64_t K, float *out
 
 enum { LGMLH_EPI_NONE = 0, LGMLH_EPI_ADD = 1 };
 
-/* Workspace of a call: split-K partial sums and per-tile counters. It must
- * be zero-filled once before its first use; every call leaves the counter
- * words at zero again, so one workspace serves any number of calls on one
- * stream (calls on two streams need two workspaces). */
+/* Workspace of a call: per-tile counters, then split-K partial sums (0
+ * bytes when K is not split). Zero-fill it before its first use; a call
+ * leaves its counter words at zero again, so one workspace serves any
+ * number of calls with the same M and N on one stream. */
 size_t lgmlh_mul_mat_workspace(int type, int64_t M, int64_t K, int64_t N);
 /* y = X W^T (+ residual when epi == LGMLH_EPI_ADD; residual may alias y).
  * x is f32 or f16 (xtype). Quantized types take the repacked w. The
@@ -227,7 +227,9 @@ typedef struct {
 } lgmlh_model;
 
 /* Workspace bytes of lgmlh_forward for a plan and n_out logit rows. Zero-
- * fill it once before its first use (split-K counters). */
+ * fill it once before its first use: its first 256 KB hold split-K tile
+ * counters that every call leaves at zero, so one workspace (grown when a
+ * larger pass needs more) serves passes of any size on one stream. */
 size_t lgmlh_forward_workspace(const lgmlh_model *m, const lgmlh_plan_info *info, int n_out);
 /* Run the pass: logits (n_out, n_vocab) f32 for the ubatch rows out_rows
  * (device; NULL = ub->logit_rows with n_out = n_seq). ids must be in range

@@ -10,7 +10,8 @@
 // (K rows straight from the [cell][D] tile), an online softmax per row in
 // f32 (each lane owns one row; reductions over 4 lanes with shuffles), and
 // O^T += V^T P^T (V columns straight from the transposed [D][cell] tile, P
-// through 2.3 KB of LDS). Splits of one token group are merged in a fixed
+// through 4.6 KB of LDS). K and V are exact f16; Q and P enter the MFMAs as
+// f16 hi + lo pairs, so every product is f32-accurate. Splits of one token group are merged in a fixed
 // order by lgmlh_merge_kernel, so results are deterministic and the same
 // for a sequence alone or in any batch.
 #include <math.h>
@@ -46,7 +47,8 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
                   int max_blocks, float *__restrict__ out, float *__restrict__ part) {
   constexpr int KS = D / 32;   // MFMA k-steps over D
   constexpr int DT = D / 16;   // d tiles of the output
-  __shared__ __align__(16) uint16_t pl[ROWS * P_STRIDE];
+  __shared__ __align__(16) uint16_t plh[ROWS * P_STRIDE];  // P as f16 hi
+  __shared__ __align__(16) uint16_t pll[ROWS * P_STRIDE];  // and lo
 
   const int lane = threadIdx.x;
   const int item = blockIdx.x;
@@ -67,22 +69,27 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
   const int p_first = seq_npast[s] + (tok0 - seq_off[s]);
   const int p_row = p_first + rtok;  // last visible position of the row
 
-  // Q fragments (B operand): Q[row][ks*32 + quad*8 .. +7] as f16.
-  f16x8 qf[KS];
+  // Q fragments (B operand): Q[row][ks*32 + quad*8 .. +7] as f16 hi + lo
+  // (q = hi + lo to 22 bits; K is exact f16, so S^T is f32-accurate).
+  f16x8 qh[KS], ql[KS];
   {
     const float *qr = q + ((int64_t)(tok0 + rtok) * H + rhead) * D;
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
-      f16x8 v;
+      f16x8 h = f16x8{0, 0, 0, 0, 0, 0, 0, 0}, lo = h;
       if (rvalid) {
         const f32x4 *p4 = (const f32x4 *)(qr + ks * 32 + quad * 8);
         f32x4 a = p4[0], b = p4[1];
-        v = f16x8{(f16)a[0], (f16)a[1], (f16)a[2], (f16)a[3],
-                  (f16)b[0], (f16)b[1], (f16)b[2], (f16)b[3]};
-      } else {
-        v = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          h[e] = (f16)a[e];
+          lo[e] = (f16)(a[e] - (float)h[e]);
+          h[4 + e] = (f16)b[e];
+          lo[4 + e] = (f16)(b[e] - (float)h[4 + e]);
+        }
       }
-      qf[ks] = v;
+      qh[ks] = h;
+      ql[ks] = lo;
     }
   }
 
@@ -113,7 +120,8 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
 #pragma unroll
       for (int ks = 0; ks < KS; ks++) {
         f16x8 kf = load_f16x8(kt + (ct * 16 + row) * D + ks * 32 + quad * 8);
-        acc = mfma16(kf, qf[ks], acc);
+        acc = mfma16(kf, qh[ks], acc);
+        acc = mfma16(kf, ql[ks], acc);
       }
       st[ct] = acc;
     }
@@ -138,16 +146,21 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
     float rs = 0.0f;
 #pragma unroll
     for (int ct = 0; ct < 4; ct++) {
-      uint16_t ph[4];
+      uint16_t ph[4], pq[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         float pv = exp2f(st[ct][i] - m_use);
         rs += pv;
-        ph[i] = f2h(pv);
+        f16 hv = (f16)pv;
+        ph[i] = __builtin_bit_cast(uint16_t, hv);
+        pq[i] = f2h(pv - (float)hv);
       }
-      u32x2 w = u32x2{(uint32_t)ph[0] | ((uint32_t)ph[1] << 16),
-                      (uint32_t)ph[2] | ((uint32_t)ph[3] << 16)};
-      *(u32x2 *)(pl + row * P_STRIDE + ct * 16 + quad * 4) = w;
+      u32x2 wh = u32x2{(uint32_t)ph[0] | ((uint32_t)ph[1] << 16),
+                       (uint32_t)ph[2] | ((uint32_t)ph[3] << 16)};
+      u32x2 wl = u32x2{(uint32_t)pq[0] | ((uint32_t)pq[1] << 16),
+                       (uint32_t)pq[2] | ((uint32_t)pq[3] << 16)};
+      *(u32x2 *)(plh + row * P_STRIDE + ct * 16 + quad * 4) = wh;
+      *(u32x2 *)(pll + row * P_STRIDE + ct * 16 + quad * 4) = wl;
     }
     rs += __shfl_xor(rs, 16);
     rs += __shfl_xor(rs, 32);
@@ -156,13 +169,19 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) o[dt] *= alpha;
     __syncthreads();  // one wave per workgroup: orders the P writes before the reads
-    f16x8 pf[2];
+    f16x8 pfh[2], pfl[2];
 #pragma unroll
-    for (int kc = 0; kc < 2; kc++) pf[kc] = load_f16x8(pl + row * P_STRIDE + kc * 32 + quad * 8);
+    for (int kc = 0; kc < 2; kc++) {
+      pfh[kc] = load_f16x8(plh + row * P_STRIDE + kc * 32 + quad * 8);
+      pfl[kc] = load_f16x8(pll + row * P_STRIDE + kc * 32 + quad * 8);
+    }
 #pragma unroll
     for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-      for (int kc = 0; kc < 2; kc++) o[dt] = mfma16(vf[dt][kc], pf[kc], o[dt]);
+      for (int kc = 0; kc < 2; kc++) {
+        o[dt] = mfma16(vf[dt][kc], pfh[kc], o[dt]);
+        o[dt] = mfma16(vf[dt][kc], pfl[kc], o[dt]);
+      }
     __syncthreads();  // P reads done before the next block's writes
   }
 

@@ -17,8 +17,9 @@
 
 namespace lgmlh {
 
-constexpr int GEMM_WAVES = 4;      // waves per workgroup
-constexpr int RT_PER_WAVE = 4;     // 16-row tiles per wave
+constexpr int GEMM_WAVES = 8;      // waves per workgroup
+constexpr int GEMM_THREADS = GEMM_WAVES * 64;
+constexpr int RT_PER_WAVE = 2;     // 16-row tiles per wave
 constexpr int WG_ROWS = GEMM_WAVES * RT_PER_WAVE * 16;  // 256
 constexpr int WG_COLS = 64;        // N columns per workgroup (4 tiles)
 constexpr int X_STRIDE = 264;      // f16 per LDS row of X (256 + pad)
@@ -91,8 +92,19 @@ __global__ void repack_kernel(const uint8_t *__restrict__ src, int64_t M, int64_
 }
 
 // ---- per-lane weight data of one chunk --------------------------------------
+// A fragments hold exact small integers in f16 -- the group scale times the
+// quant (Q4_K: sc * q <= 945; Q6_K: sc * q split as 16 * s_hi * q + s_lo * q,
+// both exact; Q8_0: q) -- so the MFMA sees the weights without rounding; the
+// f16 super-block scales d (and dmin) are applied in f32 when a chunk is
+// flushed into the accumulator.
 template <int TYPE>
 struct WFrag;
+
+__device__ __forceinline__ f16x2 u16pair_to_f16(uint32_t lo16_hi16) {
+  // two small non-negative integers (< 1024) in the 16-bit halves -> exact f16
+  uint32_t m = lo16_hi16 | 0x64006400u;  // 1024 + v
+  return __builtin_bit_cast(f16x2, m) - f16x2{(f16)1024.0f, (f16)1024.0f};
+}
 
 template <>
 struct WFrag<LGMLH_Q4_K> {
@@ -104,14 +116,10 @@ struct WFrag<LGMLH_Q4_K> {
     qs[0] = p[0];
     qs[1] = p[1];
   }
-  __device__ __forceinline__ uint8_t sbyte(int i) const {
-    uint32_t w = hdr[1 + (i >> 2)];
-    return (uint8_t)(w >> (8 * (i & 3)));
+  __device__ __forceinline__ uint32_t sbyte(int i) const {
+    return (hdr[1 + (i >> 2)] >> (8 * (i & 3))) & 0xffu;
   }
-  // A fragment of 32-value group g (k = 32g + 8c + e).
-  __device__ __forceinline__ f16x8 frag(int g) const {
-    float d = h2f((uint16_t)hdr[0]), dmin = h2f((uint16_t)(hdr[0] >> 16));
-    int sc, m;
+  __device__ __forceinline__ void scale_min(int g, int &sc, int &m) const {
     if (g < 4) {
       sc = sbyte(g) & 63;
       m = sbyte(g + 4) & 63;
@@ -119,15 +127,33 @@ struct WFrag<LGMLH_Q4_K> {
       sc = (sbyte(g + 4) & 0xF) | ((sbyte(g - 4) >> 6) << 4);
       m = (sbyte(g + 4) >> 4) | ((sbyte(g) >> 6) << 4);
     }
-    float d1 = d * (float)sc, m1 = dmin * (float)m;
+  }
+  // sc_g * q for k = 32g + 8c + e, e = 0..7.
+  __device__ __forceinline__ f16x8 frag(int g) const {
+    int sc, m;
+    scale_min(g, sc, m);
     int j = g >> 1;
     uint32_t lo = qs[j >> 1][2 * (j & 1)], hi = qs[j >> 1][2 * (j & 1) + 1];
     int sh = (g & 1) * 4;
-    f16x8 r;
+    uint32_t a = (lo >> sh) & 0x0F0F0F0Fu, b = (hi >> sh) & 0x0F0F0F0Fu;
+    f16x2 s2 = f16x2{(f16)(float)sc, (f16)(float)sc};
+    f16x2 p0 = u16pair_to_f16((a & 0xffu) | ((a & 0xff00u) << 8)) * s2;
+    f16x2 p1 = u16pair_to_f16(((a >> 16) & 0xffu) | ((a >> 8) & 0xff0000u)) * s2;
+    f16x2 p2 = u16pair_to_f16((b & 0xffu) | ((b & 0xff00u) << 8)) * s2;
+    f16x2 p3 = u16pair_to_f16(((b >> 16) & 0xffu) | ((b >> 8) & 0xff0000u)) * s2;
+    return f16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+  }
+  // The 16x16x16 A fragment of the mins: row lane%16, k = groups 4c..4c+3
+  // (zero for c >= 2).
+  __device__ __forceinline__ f16x4 mins(int c) const {
+    f16x4 r = f16x4{0, 0, 0, 0};
+    if (c < 2) {
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      r[e] = (f16)(d1 * (float)((lo >> (8 * e + sh)) & 15) - m1);
-      r[4 + e] = (f16)(d1 * (float)((hi >> (8 * e + sh)) & 15) - m1);
+      for (int i = 0; i < 4; i++) {
+        int sc, m;
+        scale_min(4 * c + i, sc, m);
+        r[i] = (f16)(float)m;
+      }
     }
     return r;
   }
@@ -148,69 +174,62 @@ struct WFrag<LGMLH_Q6_K> {
     ql[1] = p[1];
     qh = p[2];
   }
-  __device__ __forceinline__ f16x8 frag(int g, int c) const {
-    // bytes of hdr: [0..1] d, [2..17] scales
-    float d = h2f((uint16_t)hdr[0]);
-    int si = 2 * g + (c >> 1);  // scale of values 32g + 8c .. : (32g + 8c) / 16
-    int sb = 2 + si;
-    int8_t scv = (int8_t)(hdr[sb >> 2] >> (8 * (sb & 3)));
-    float dsc = d * (float)scv;
+  // Two fragments whose sum is sc * q (scale index (32g + 8c) / 16):
+  // a1 = 16 * (sc >> 4) * q, a2 = (sc & 15) * q, both exact in f16.
+  __device__ __forceinline__ void frag(int g, int c, f16x8 &a1, f16x8 &a2) const {
+    int si = 2 + 2 * g + (c >> 1);
+    int sc = (int)(int8_t)(hdr[si >> 2] >> (8 * (si & 3)));
+    int s_hi = sc >> 4, s_lo = sc & 15;
     int h = g >> 2, t = g & 3;
     int piece = 2 * h + (t & 1);
     uint32_t lo = ql[piece >> 1][2 * (piece & 1)], hi = ql[piece >> 1][2 * (piece & 1) + 1];
     uint32_t hlo = qh[2 * h], hhi = qh[2 * h + 1];
     int nsh = t < 2 ? 0 : 4;
-    f16x8 r;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
       int q0 = (int)(((lo >> (8 * e + nsh)) & 15) | (((hlo >> (8 * e + 2 * t)) & 3) << 4)) - 32;
       int q1 = (int)(((hi >> (8 * e + nsh)) & 15) | (((hhi >> (8 * e + 2 * t)) & 3) << 4)) - 32;
-      r[e] = (f16)(dsc * (float)q0);
-      r[4 + e] = (f16)(dsc * (float)q1);
+      a1[e] = (f16)(float)(16 * s_hi * q0);
+      a1[4 + e] = (f16)(float)(16 * s_hi * q1);
+      a2[e] = (f16)(float)(s_lo * q0);
+      a2[4 + e] = (f16)(float)(s_lo * q1);
     }
-    return r;
   }
 };
 
 template <>
 struct WFrag<LGMLH_Q8_0> {
-  u32x4 hdr;           // 8 f16 scales of row r
   const uint8_t *qs;   // the lane's 8 blocks x 8 int8, read per group
-  __device__ void load(const uint8_t *ch, int lane) {
-    hdr = *(const u32x4 *)(ch + (lane & 15) * 16);
-    qs = ch + 256 + lane * 64;
-  }
+  __device__ void load(const uint8_t *ch, int lane) { qs = ch + 256 + lane * 64; }
   __device__ __forceinline__ f16x8 frag(int g) const {
-    float d = h2f((uint16_t)(hdr[g >> 1] >> (16 * (g & 1))));
     u32x2 q = *(const u32x2 *)(qs + 8 * g);
     f16x8 r;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-      r[e] = (f16)(d * (float)(int8_t)(q[0] >> (8 * e)));
-      r[4 + e] = (f16)(d * (float)(int8_t)(q[1] >> (8 * e)));
+      r[e] = (f16)(float)(int8_t)(q[0] >> (8 * e));
+      r[4 + e] = (f16)(float)(int8_t)(q[1] >> (8 * e));
     }
     return r;
   }
 };
 
-template <int TYPE>
-__device__ __forceinline__ f16x8 wfrag(const WFrag<TYPE> &w, int g, int c) {
-  if constexpr (TYPE == LGMLH_Q6_K)
-    return w.frag(g, c);
-  else
-    return w.frag(g);
-}
-
 // ---- the quantized GEMM --------------------------------------------------------
-// grid: (ceil(N / 64), ceil(M / 256), splits). blockIdx.x (N tiles) varies
+// grid: (ceil(N / 64), ceil(M / WG_ROWS), splits); blockIdx.x (N tiles) varies
 // fastest so the workgroups that share a weight tile run together.
+//
+// X is staged per K step as f16 hi and lo planes (x = hi + lo to 22 bits)
+// plus the 32-value group sums (Q4_K min term); each product is the MFMA
+// of the exact integer weights with hi, then with lo, summed in f32.
 template <int TYPE, bool XF32>
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(GEMM_THREADS)
 qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__restrict__ xv,
              int64_t N, float *__restrict__ y, int64_t ldy, const float *__restrict__ residual,
              int splits, int sb_per_split, float *__restrict__ part,
              int32_t *__restrict__ counters) {
-  __shared__ __align__(16) f16 xs[WG_COLS * X_STRIDE];
+  __shared__ __align__(16) f16 xh[WG_COLS * X_STRIDE];
+  __shared__ __align__(16) f16 xl[WG_COLS * X_STRIDE];
+  __shared__ __align__(16) f16 gsh[WG_COLS * 8];  // group sums, hi
+  __shared__ __align__(16) f16 gsl[WG_COLS * 8];  // group sums, lo
   __shared__ int last_flag;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t NSB = K / QK_K;
@@ -220,7 +239,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__
   const int z = blockIdx.z;
   const int64_t sb_lo = (int64_t)z * sb_per_split;
   const int64_t sb_hi = sb_lo + sb_per_split < NSB ? sb_lo + sb_per_split : NSB;
-  const int c = lane >> 4;
+  const int c = lane >> 4, r16 = lane & 15;
 
   f32x4 acc[RT_PER_WAVE][4];
 #pragma unroll
@@ -229,26 +248,43 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__
     for (int b = 0; b < 4; b++) acc[a][b] = f32x4{0, 0, 0, 0};
 
   for (int64_t sb = sb_lo; sb < sb_hi; sb++) {
-    // Stage X[n0 .. n0+64][sb*256 .. +256] in LDS as f16 (zeros past N).
     __syncthreads();
-    if constexpr (XF32) {
-      const float *x = (const float *)xv;
-      for (int i = tid; i < WG_COLS * 64; i += 256) {  // 64 pieces of 4 floats per row
-        int r = i >> 6, p = i & 63;
-        int64_t n = n0 + r;
-        f32x4 v = f32x4{0, 0, 0, 0};
-        if (n < N) v = *(const f32x4 *)(x + n * K + sb * QK_K + p * 4);
-        f16x4 h = f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
-        *(f16x4 *)(xs + r * X_STRIDE + p * 4) = h;
+    // Stage X[n0 .. n0+64][sb*256 .. +256]: 64 pieces of 4 values per row.
+    for (int i = tid; i < WG_COLS * 64; i += GEMM_THREADS) {
+      int r = i >> 6, p = i & 63;
+      int64_t n = n0 + r;
+      f32x4 v = f32x4{0, 0, 0, 0};
+      f16x4 h, l;
+      if constexpr (XF32) {
+        if (n < N) v = *(const f32x4 *)((const float *)xv + n * K + sb * QK_K + p * 4);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          h[e] = (f16)v[e];
+          l[e] = (f16)(v[e] - (float)h[e]);
+        }
+      } else {
+        u32x2 hv = u32x2{0, 0};
+        if (n < N) hv = *(const u32x2 *)((const f16 *)xv + n * K + sb * QK_K + p * 4);
+        h = __builtin_bit_cast(f16x4, hv);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          v[e] = (float)h[e];
+          l[e] = (f16)0.0f;
+        }
       }
-    } else {
-      const f16 *x = (const f16 *)xv;
-      for (int i = tid; i < WG_COLS * 32; i += 256) {  // 32 pieces of 8 f16 per row
-        int r = i >> 5, p = i & 31;
-        int64_t n = n0 + r;
-        u32x4 v = u32x4{0, 0, 0, 0};
-        if (n < N) v = *(const u32x4 *)(x + n * K + sb * QK_K + p * 8);
-        *(u32x4 *)(xs + r * X_STRIDE + p * 8) = v;
+      *(f16x4 *)(xh + r * X_STRIDE + p * 4) = h;
+      *(f16x4 *)(xl + r * X_STRIDE + p * 4) = l;
+      if constexpr (TYPE == LGMLH_Q4_K) {
+        // group sum over the 8 pieces (8 consecutive threads) of a group
+        float gs = (v[0] + v[1]) + (v[2] + v[3]);
+        gs += __shfl_xor(gs, 1);
+        gs += __shfl_xor(gs, 2);
+        gs += __shfl_xor(gs, 4);
+        if ((p & 7) == 0) {
+          f16 gh = (f16)gs;
+          gsh[r * 8 + (p >> 3)] = gh;
+          gsl[r * 8 + (p >> 3)] = (f16)(gs - (float)gh);
+        }
       }
     }
     __syncthreads();
@@ -256,22 +292,109 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__
     WFrag<TYPE> wf[RT_PER_WAVE];
 #pragma unroll
     for (int a = 0; a < RT_PER_WAVE; a++) {
-      int64_t rt = rt0 + a;
-      if (rt < MT) wf[a].load(w + (rt * NSB + sb) * chunk_bytes(TYPE), lane);
+      int64_t rt = rt0 + a < MT ? rt0 + a : MT - 1;  // clamp: rows past M are never stored
+      wf[a].load(w + (rt * NSB + sb) * chunk_bytes(TYPE), lane);
     }
+    f32x4 cm[RT_PER_WAVE][4];
+#pragma unroll
+    for (int a = 0; a < RT_PER_WAVE; a++)
+#pragma unroll
+      for (int b = 0; b < 4; b++) cm[a][b] = f32x4{0, 0, 0, 0};
 #pragma unroll
     for (int g = 0; g < 8; g++) {
-      f16x8 bx[4];
+      f16x8 bh[4], bl[4];
 #pragma unroll
-      for (int ct = 0; ct < 4; ct++)
-        bx[ct] = *(const f16x8 *)(xs + (ct * 16 + (lane & 15)) * X_STRIDE + g * 32 + c * 8);
+      for (int ct = 0; ct < 4; ct++) {
+        const int off = (ct * 16 + r16) * X_STRIDE + g * 32 + c * 8;
+        bh[ct] = *(const f16x8 *)(xh + off);
+        if constexpr (XF32) bl[ct] = *(const f16x8 *)(xl + off);
+      }
 #pragma unroll
       for (int a = 0; a < RT_PER_WAVE; a++) {
-        if (rt0 + a >= MT) continue;
-        f16x8 af = wfrag<TYPE>(wf[a], g, c);
+        if constexpr (TYPE == LGMLH_Q6_K) {
+          f16x8 a1, a2;
+          wf[a].frag(g, c, a1, a2);
 #pragma unroll
-        for (int ct = 0; ct < 4; ct++)
-          acc[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bx[ct], acc[a][ct], 0, 0, 0);
+          for (int ct = 0; ct < 4; ct++) {
+            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bh[ct], cm[a][ct], 0, 0, 0);
+            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bh[ct], cm[a][ct], 0, 0, 0);
+            if constexpr (XF32) {
+              cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bl[ct], cm[a][ct], 0, 0, 0);
+              cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bl[ct], cm[a][ct], 0, 0, 0);
+            }
+          }
+        } else {
+          f16x8 af = wf[a].frag(g);
+#pragma unroll
+          for (int ct = 0; ct < 4; ct++) {
+            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bh[ct], cm[a][ct], 0, 0, 0);
+            if constexpr (XF32)
+              cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bl[ct], cm[a][ct], 0, 0, 0);
+          }
+        }
+      }
+      if constexpr (TYPE == LGMLH_Q8_0) {
+        // Q8_0: one scale per 32-value block: flush every group.
+#pragma unroll
+        for (int a = 0; a < RT_PER_WAVE; a++) {
+          int64_t rt = rt0 + a < MT ? rt0 + a : MT - 1;
+          const uint8_t *hd = w + (rt * NSB + sb) * chunk_bytes(TYPE);
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            float d = h2f(*(const uint16_t *)(hd + (4 * c + i) * 16 + 2 * g));
+#pragma unroll
+            for (int ct = 0; ct < 4; ct++) {
+              acc[a][ct][i] += d * cm[a][ct][i];
+              cm[a][ct][i] = 0.0f;
+            }
+          }
+        }
+      }
+    }
+    if constexpr (TYPE == LGMLH_Q4_K) {
+      // min term: sum_g m_g * S_g[n] as one 16x16x16 MFMA over the 8 groups.
+      f16x4 sh4[4], sl4[4];
+#pragma unroll
+      for (int ct = 0; ct < 4; ct++) {
+        if (c < 2) {
+          sh4[ct] = *(const f16x4 *)(gsh + (ct * 16 + r16) * 8 + 4 * c);
+          sl4[ct] = *(const f16x4 *)(gsl + (ct * 16 + r16) * 8 + 4 * c);
+        } else {
+          sh4[ct] = f16x4{0, 0, 0, 0};
+          sl4[ct] = f16x4{0, 0, 0, 0};
+        }
+      }
+#pragma unroll
+      for (int a = 0; a < RT_PER_WAVE; a++) {
+        f16x4 am = wf[a].mins(c);
+        int64_t rt = rt0 + a < MT ? rt0 + a : MT - 1;
+        const uint8_t *hd = w + (rt * NSB + sb) * chunk_bytes(TYPE);
+        float dd[4], dm[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          uint32_t h = *(const uint32_t *)(hd + (4 * c + i) * 16);
+          dd[i] = h2f((uint16_t)h);
+          dm[i] = h2f((uint16_t)(h >> 16));
+        }
+#pragma unroll
+        for (int ct = 0; ct < 4; ct++) {
+          f32x4 mn = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sh4[ct], f32x4{0, 0, 0, 0}, 0, 0, 0);
+          mn = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sl4[ct], mn, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; i++) acc[a][ct][i] += dd[i] * cm[a][ct][i] - dm[i] * mn[i];
+        }
+      }
+    } else if constexpr (TYPE == LGMLH_Q6_K) {
+#pragma unroll
+      for (int a = 0; a < RT_PER_WAVE; a++) {
+        int64_t rt = rt0 + a < MT ? rt0 + a : MT - 1;
+        const uint8_t *hd = w + (rt * NSB + sb) * chunk_bytes(TYPE);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          float d = h2f(*(const uint16_t *)(hd + (4 * c + i) * 18));
+#pragma unroll
+          for (int ct = 0; ct < 4; ct++) acc[a][ct][i] += d * cm[a][ct][i];
+        }
       }
     }
   }
@@ -282,7 +405,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__
     for (int a = 0; a < RT_PER_WAVE; a++)
 #pragma unroll
       for (int ct = 0; ct < 4; ct++) {
-        int64_t n = n0 + ct * 16 + (lane & 15);
+        int64_t n = n0 + ct * 16 + r16;
         int64_t m = (rt0 + a) * 16 + 4 * c;
         if (n >= N) continue;
 #pragma unroll
@@ -302,7 +425,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__
   for (int a = 0; a < RT_PER_WAVE; a++)
 #pragma unroll
     for (int ct = 0; ct < 4; ct++) {
-      int64_t n = n0 + ct * 16 + (lane & 15);
+      int64_t n = n0 + ct * 16 + r16;
       int64_t m = (rt0 + a) * 16 + 4 * c;
       if (n >= N) continue;
 #pragma unroll
@@ -319,10 +442,11 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__
   const int64_t mlo = (int64_t)blockIdx.y * WG_ROWS;
   const int64_t ncols = N - n0 < WG_COLS ? N - n0 : WG_COLS;
   const int64_t mrows = M - mlo < WG_ROWS ? M - mlo : WG_ROWS;
-  for (int64_t e = tid; e < ncols * mrows; e += 256) {
+  for (int64_t e = tid; e < ncols * mrows; e += GEMM_THREADS) {
     int64_t n = n0 + e / mrows, m = mlo + e % mrows;
     float v = 0.0f;
-    for (int zz = 0; zz < splits; zz++) v += __builtin_nontemporal_load(part + ((int64_t)zz * N + n) * M + m);
+    for (int zz = 0; zz < splits; zz++)
+      v += __builtin_nontemporal_load(part + ((int64_t)zz * N + n) * M + m);
     if (residual) v += residual[n * ldy + m];
     y[n * ldy + m] = v;
   }
@@ -368,38 +492,48 @@ int splits_for(int64_t M, int64_t K, int64_t N) {
   return (int)want;
 }
 
-size_t workspace_for(int type, int64_t M, int64_t K, int64_t N) {
+int64_t counter_words(int64_t M, int64_t N) {
+  return ((M + WG_ROWS - 1) / WG_ROWS) * ((N + WG_COLS - 1) / WG_COLS);
+}
+
+// Split-K partial sums of a call (0 when K is not split).
+size_t partial_bytes(int type, int64_t M, int64_t K, int64_t N) {
   if (type == LGMLH_F32) return 0;
   int s = splits_for(M, K, N);
-  if (s == 1) return 0;
-  int64_t tiles = ((M + WG_ROWS - 1) / WG_ROWS) * ((N + WG_COLS - 1) / WG_COLS);
-  return (size_t)s * N * M * 4 + (size_t)tiles * 4 + 256;
+  return s == 1 ? 0 : (size_t)s * N * M * 4;
+}
+
+// Public workspace: [tile counters, 256-byte aligned][partial sums].
+size_t workspace_for(int type, int64_t M, int64_t K, int64_t N) {
+  size_t p = partial_bytes(type, M, K, N);
+  if (p == 0) return 0;
+  return (((size_t)counter_words(M, N) * 4 + 255) & ~size_t(255)) + p;
 }
 
 template <int TYPE>
 static void launch_q(const void *w, int64_t M, int64_t K, const void *x, int xtype, int64_t N,
-                     float *y, int64_t ldy, const float *res, int splits, void *ws,
-                     hipStream_t st) {
+                     float *y, int64_t ldy, const float *res, int splits, float *part,
+                     int32_t *cnt, hipStream_t st) {
   int64_t NSB = K / QK_K;
   int spb = (int)((NSB + splits - 1) / splits);
   splits = (int)((NSB + spb - 1) / spb);
   dim3 grid((unsigned)((N + WG_COLS - 1) / WG_COLS), (unsigned)((M + WG_ROWS - 1) / WG_ROWS),
             (unsigned)splits);
-  float *part = (float *)ws;
-  int32_t *cnt = splits > 1 ? (int32_t *)((char *)ws + (size_t)splits * N * M * 4) : nullptr;
   if (xtype == LGMLH_F32)
-    hipLaunchKernelGGL((qgemm_kernel<TYPE, true>), grid, dim3(256), 0, st, (const uint8_t *)w, M,
+    hipLaunchKernelGGL((qgemm_kernel<TYPE, true>), grid, dim3(GEMM_THREADS), 0, st, (const uint8_t *)w, M,
                        K, x, N, y, ldy, res, splits, spb, part, cnt);
   else
-    hipLaunchKernelGGL((qgemm_kernel<TYPE, false>), grid, dim3(256), 0, st, (const uint8_t *)w,
+    hipLaunchKernelGGL((qgemm_kernel<TYPE, false>), grid, dim3(GEMM_THREADS), 0, st, (const uint8_t *)w,
                        M, K, x, N, y, ldy, res, splits, spb, part, cnt);
 }
 
 // Internal entry with an output row stride (the executor writes [q|k|v]
-// and [gate|up] rows from separate weights into one buffer).
+// and [gate|up] rows from separate weights into one buffer) and separate
+// partial / counter regions: counters stay at one place for every call
+// that shares them, zero between calls.
 int mul_mat_ldy(int type, const void *w, int64_t M, int64_t K, const void *x, int xtype,
-                int64_t N, float *y, int64_t ldy, const float *residual, void *ws,
-                size_t ws_bytes, hipStream_t st) {
+                int64_t N, float *y, int64_t ldy, const float *residual, float *part,
+                size_t part_bytes, int32_t *counters, int64_t n_counters, hipStream_t st) {
   if (!w || !x || !y || M <= 0 || K <= 0 || N < 0 || ldy < M ||
       (xtype != LGMLH_F32 && xtype != LGMLH_F16)) {
     set_error("mul_mat: bad arguments");
@@ -421,15 +555,15 @@ int mul_mat_ldy(int type, const void *w, int64_t M, int64_t K, const void *x, in
     return LGMLH_EINVAL;
   }
   int splits = splits_for(M, K, N);
-  if (splits > 1 && ws_bytes < workspace_for(type, M, K, N)) {
-    set_error("mul_mat: workspace of %zu bytes, need %zu", ws_bytes,
-              workspace_for(type, M, K, N));
+  if (splits > 1 && (part_bytes < partial_bytes(type, M, K, N) || !counters ||
+                     n_counters < counter_words(M, N))) {
+    set_error("mul_mat: workspace too small for %d K splits", splits);
     return LGMLH_ENOMEM;
   }
   switch (type) {
-    case LGMLH_Q4_K: launch_q<LGMLH_Q4_K>(w, M, K, x, xtype, N, y, ldy, residual, splits, ws, st); break;
-    case LGMLH_Q6_K: launch_q<LGMLH_Q6_K>(w, M, K, x, xtype, N, y, ldy, residual, splits, ws, st); break;
-    case LGMLH_Q8_0: launch_q<LGMLH_Q8_0>(w, M, K, x, xtype, N, y, ldy, residual, splits, ws, st); break;
+    case LGMLH_Q4_K: launch_q<LGMLH_Q4_K>(w, M, K, x, xtype, N, y, ldy, residual, splits, part, counters, st); break;
+    case LGMLH_Q6_K: launch_q<LGMLH_Q6_K>(w, M, K, x, xtype, N, y, ldy, residual, splits, part, counters, st); break;
+    case LGMLH_Q8_0: launch_q<LGMLH_Q8_0>(w, M, K, x, xtype, N, y, ldy, residual, splits, part, counters, st); break;
     default:
       set_error("mul_mat: type %d not supported", type);
       return LGMLH_EINVAL;
@@ -483,6 +617,15 @@ extern "C" int lgmlh_mul_mat(int type, const void *w, int64_t M, int64_t K, cons
     set_error("mul_mat: the add epilogue needs a residual");
     return LGMLH_EINVAL;
   }
+  size_t need = workspace_for(type, M, K, N);
+  if (need > 0 && (!workspace || ws_bytes < need)) {
+    set_error("mul_mat: workspace of %zu bytes, need %zu", ws_bytes, need);
+    return LGMLH_ENOMEM;
+  }
+  int64_t nc = counter_words(M, N);
+  size_t cb = ((size_t)nc * 4 + 255) & ~size_t(255);
+  int32_t *cnt = need ? (int32_t *)workspace : nullptr;
+  float *part = need ? (float *)((char *)workspace + cb) : nullptr;
   return mul_mat_ldy(type, w, M, K, x, xtype, N, y, M, epi == LGMLH_EPI_ADD ? residual : nullptr,
-                     workspace, ws_bytes, as_stream(stream));
+                     part, need ? need - cb : 0, cnt, nc, as_stream(stream));
 }

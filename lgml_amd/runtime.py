@@ -164,13 +164,18 @@ class DeviceModel:
         return self.n_cells // 64
 
     def plan(self, seq_n, seq_npast, block_tab, ids, blocks_per_split=0):
+        ids = np.ascontiguousarray(ids, np.int32)
+        if len(ids) and (ids.min() < 0 or ids.max() >= self.hp["n_vocab"]):
+            raise ValueError("token id out of range [0, %d)" % self.hp["n_vocab"])
         return Plan(seq_n, seq_npast, block_tab, ids, self.hp["n_head"], self.hp["n_head_kv"],
                     self.pool_blocks, blocks_per_split)
 
     def workspace(self, plan, n_out):
         need = hip.lib().lgmlh_forward_workspace(C.byref(self.m), C.byref(plan.info), n_out)
         if need > self.ws_bytes:
-            self.ws = _zeros(need)  # zero once: split-K counters start at 0
+            # zero-filled when (re)allocated: the split-K counters start at 0
+            # and every pass leaves them at 0
+            self.ws = _zeros(need)
             self.ws_bytes = need
         return self.ws
 

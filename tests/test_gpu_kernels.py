@@ -1,11 +1,11 @@
 """GPU parity of the single kernels against the CPU oracle, through the C ABI.
 
 Bit-exact: KV store (f32 -> f16 RNE), gather, block copy, dequantization,
-plan cells. Tolerance: attention and weight products (f16 operands, f32
-accumulation) within 2e-3 max relative error of the oracle's f64 result
-and within 1e-5 of the oracle run on the same
-f16-rounded operands. Batch invariance: a row alone and in a batch give the
-same bits.
+plan cells. Tolerance: attention and weight products within 2e-3 max
+relative error of the oracle's f64 result; the
+kernels keep weights exact and split f32 activations into f16 hi + lo, so
+they also meet 1e-5 (products) and 1e-4 (attention). Batch invariance: a
+row alone and in a batch give the same bits.
 """
 import ctypes as C
 
@@ -37,7 +37,7 @@ def st():
 
 def test_kv_store_gather_bit_exact(L):
     from lgml_amd import hip
-    Hkv, D, cells_n = 8, 128, 1024
+    Hkv, D, cells_n = 8, 128, 4096
     rng = np.random.default_rng(1)
     n = 200
     k = rng.standard_normal((n, Hkv * D)).astype(np.float32) * 3
@@ -47,7 +47,7 @@ def test_kv_store_gather_bit_exact(L):
                      1.000732421875, -0.0, 5.96e-8], np.float32)
     k[0, :len(edge)] = edge
     v[1, :len(edge)] = edge
-    cells = rng.choice(cells_n, n, replace=False).astype(np.int64)
+    cells = rng.choice(cells_n // 2, n, replace=False).astype(np.int64)
     kb = L.lgmlh_kv_layer_bytes(cells_n, Hkv, D)
     kp, vp = torch.zeros(kb, dtype=torch.uint8, device="cuda"), torch.zeros(kb, dtype=torch.uint8, device="cuda")
     dk, dv, dc = dev(k), dev(v), dev(cells)
@@ -119,7 +119,7 @@ def run_mul_mat(L, ty, w, M, K, x, xtype=None):
     ws_n = L.lgmlh_mul_mat_workspace(ty, M, K, N)
     ws = torch.zeros(max(ws_n, 1), dtype=torch.uint8, device="cuda")
     y = torch.empty((N, M), dtype=torch.float32, device="cuda")
-    xt = xtype if xtype is not None else (hip.F16 if ty != core.F32 else hip.F32)
+    xt = xtype if xtype is not None else hip.F32
     xd = dev(x.astype(np.float16) if xt == hip.F16 else x)
     hip.check(L.lgmlh_mul_mat(ty, rp.data_ptr(), M, K, xd.data_ptr(), xt, N, y.data_ptr(),
                               hip.EPI_NONE, None, ws.data_ptr(), ws_n, st()))
@@ -140,12 +140,7 @@ def test_mul_mat_parity_and_batch_invariance(L, ty, MK):
         y = run_mul_mat(L, ty, w, M, K, x[:N])
         want = core.mul_mat(core.F32, deq, M, K, x[:N])
         assert rel_err(y, want) < 2e-3, (N, rel_err(y, want))
-        if ty != core.F32:
-            # same f16-rounded operands: only the summation order differs
-            xh = x[:N].astype(np.float16).astype(np.float32)
-            wh = deq.astype(np.float16).astype(np.float32)
-            tight = core.mul_mat(core.F32, wh, M, K, xh)
-            assert rel_err(y, tight) < 1e-5, (N, rel_err(y, tight))
+        assert rel_err(y, want) < 1e-5, (N, rel_err(y, want))
         if N == 130:
             for j in (0, 63, 64, 129):
                 alone = run_mul_mat(L, ty, w, M, K, x[j:j + 1])
@@ -158,9 +153,10 @@ def test_mul_mat_f32_input_and_residual(L):
     wf = core.fill_normal(M * K, 0, 0.02, 9).reshape(M, K)
     w = core.quantize(core.Q4_K, wf)
     x = core.fill_normal(N * K, 0, 1, 10).reshape(N, K)
+    x = x.astype(np.float16).astype(np.float32)  # values an f16 input can hold
     y16 = run_mul_mat(L, core.Q4_K, w, M, K, x, hip.F16)
     y32 = run_mul_mat(L, core.Q4_K, w, M, K, x, hip.F32)
-    assert np.array_equal(y16, y32)  # f32 x is rounded to f16 on the way in
+    assert np.array_equal(y16, y32)  # an f16 x is the f32 x with a zero lo part
     nb = L.lgmlh_repacked_bytes(core.Q4_K, M, K)
     rp = torch.empty(nb, dtype=torch.uint8, device="cuda")
     hip.check(L.lgmlh_repack(core.Q4_K, M, K, dev(w).data_ptr(), rp.data_ptr(), st()))
@@ -231,7 +227,8 @@ def test_paged_attention_parity(L, H, Hkv, D):
                            np.zeros(len(q), np.int32), [])
         want = core.paged_attention(q, kpool, vpool, H, Hkv, D, 1.0 / np.sqrt(D), b)
         assert np.isfinite(got).all()
-        assert rel_err(got.reshape(len(q) * H, D), want.reshape(len(q) * H, D)) < 2e-3, bps
+        e = rel_err(got.reshape(len(q) * H, D), want.reshape(len(q) * H, D))
+        assert e < 2e-3 and e < 1e-4, (bps, e)
 
 
 def test_paged_attention_alone_equals_batched(L):
