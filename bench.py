@@ -1,0 +1,238 @@
+#!/usr/bin/env python3
+"""Decode throughput of lgml's ragged continuous-batching path on one MI355X.
+
+Workload ("C2"): a Llama-3-8B-shaped model
+(32 layers, d 4096, 32 / 8 heads, head 128, FFN 14336, vocab 128256) with
+N(0, 0.02) weights quantized Q4_K_M (output and attn_v / ffn_down of the
+more_bits layers Q6_K), f16 KV in 64-cell blocks; 64 slots with prompt
+lengths U[128, 4096]; continuous batching: every request has a decode budget
+U[64, 2048]; a finished request's slot is taken by a new one whose prompt
+(U[128, 4096]) is prefilled in 512-token chunks mixed into the decode passes.
+The initial 64 contexts are filled with synthetic KV (the attention reads
+cost the same whatever the values); joining prompts run the real prefill.
+One step = one pass of the engine (E:flush): the next token of every
+decoding slot plus the prompt chunks of joining slots.
+
+value = decoded tokens / wall seconds of the K timed steps (inputs resident
+in HBM; the per-step host plan upload and the 64 sampled ids read back are
+inside). roofline = the paged attention kernel (the dominant kernel: ~80% of
+the step's bytes): its algorithmic bytes (K + V of every visible cell, q
+in, out) per launch over its HIP-event-timed duration on its own stream,
+against 8 TB/s. cpu_baseline = the C oracle (oracle/) timed on a bounded
+sample of the same step on the host cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--seed", type=int, default=20261201)
+    ap.add_argument("--slots", type=int, default=64)
+    ap.add_argument("--bps", type=int, default=0, help="KV blocks per attention work item (0 = auto)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--quiet", action="store_true")
+    return ap.parse_args()
+
+
+HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s
+
+
+def log(args, *a):
+    if not args.quiet:
+        print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(hp, contexts, seed, args):
+    """The C oracle on one decode step of the workload's shape: 1 of the 32
+    layers plus the output head, 64 sequences at the workload's contexts
+    (synthetic KV), timed on the host cores; scaled to a 32-layer step."""
+    import numpy as np
+
+    from oracle import core, models
+
+    E, V = hp["n_embd"], hp["n_vocab"]
+    threads = core.threads()
+    ohp, w = models.build("c2", seed=seed, n_layer=1, init="normal")
+    om = core.OracleModel(ohp, w)
+    S = len(contexts)
+    B = 64
+    nbs = [(c + 1 + B - 1) // B for c in contexts]
+    n_cells = sum(nbs) * B
+    row = hp["n_head_kv"] * hp["head_dim"]
+    rng = np.random.default_rng(seed)
+    kp = [rng.integers(0x3000, 0x3c00, size=(n_cells, row), dtype=np.uint16)]
+    vp = [rng.integers(0x3000, 0x3c00, size=(n_cells, row), dtype=np.uint16)]
+    bt = np.full((S, max(nbs)), -1, np.int32)
+    o = 0
+    for i, nb in enumerate(nbs):
+        bt[i, :nb] = np.arange(o, o + nb)
+        o += nb
+    ids = rng.integers(0, V, size=S).astype(np.int32)
+    b = core.BatchDesc([1] * S, contexts, bt, B, ids, list(range(S)))
+    t0 = time.time()
+    om.forward(kp, vp, b)
+    t_one = time.time() - t0
+    x = rng.standard_normal((S, E)).astype(np.float32)
+    t0 = time.time()
+    core.mul_mat(w["output"][1], w["output"][0], V, E, x)
+    t_head = time.time() - t0
+    t_layer = max(t_one - t_head, 1e-9)
+    t_step = t_head + hp["n_layer"] * t_layer
+    return {"value": S / t_step, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": "oracle/ (C, OpenMP) one decode step of the C2 shape at %d sequences "
+                      "(contexts as the GPU run, synthetic KV): 1 layer + output head timed "
+                      "(%.1f s + %.1f s), scaled to 32 layers" % (S, t_layer, t_head)}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: every GPU box here has one, and the multi-GPU "
+              "sharding of this path is design only (see DESIGN.md); run with --gpus 1",
+              file=sys.stderr)
+        return 2
+    import numpy as np
+    import torch
+
+    from lgml_amd import engine, hip, runtime, workload
+
+    hp = dict(workload.SHAPES["c2"])
+    ty = workload.policy(hp["wtype"], hp["n_layer"])
+    rng = workload.Lcg(args.seed)
+    S = args.slots
+    max_ctx = 4096 + 2048 + 64
+    n_cells = ((S * max_ctx + 63) // 64) * 64
+    log(args, "building the model on the device ...")
+    t0 = time.time()
+    model = runtime.DeviceModel(hp, runtime.generated_weights(hp, args.seed, ty), n_cells)
+    torch.cuda.synchronize()
+    log(args, "model ready in %.1f s; pool %d cells (%.1f GB KV)" % (
+        time.time() - t0, n_cells, n_cells * 2 * 2 * hp["n_head_kv"] * hp["head_dim"] *
+        hp["n_layer"] / 1e9))
+    # Synthetic KV for the initial contexts: small f16 values in every cell.
+    g = torch.Generator(device="cuda")
+    g.manual_seed(args.seed)
+    for t in model.kpools + model.vpools:
+        t.view(torch.float16).uniform_(-1.0, 1.0, generator=g)
+
+    trace = runtime.EventTrace(args.steps * hp["n_layer"] * 8 + 64,
+                               hip.TRACE_ATTN | hip.TRACE_GEMM)
+    eng = engine.Engine(model, S, blocks_per_split=args.bps)
+
+    def new_request(prefilled):
+        n = rng.int(128, 4096)
+        prompt = [rng.int(0, hp["n_vocab"] - 1) for _ in range(n)]
+        r = engine.Request(prompt, rng.int(64, 2048))
+        eng.submit(r)
+        if prefilled:
+            eng.seqs.reserve(r.seq, n)
+            r.seq.n_past = n
+            r.fed = n
+            r.out = [prompt[-1]]
+            r.max_new += 1
+        return r
+
+    for _ in range(S):
+        new_request(True)
+    contexts0 = [r.seq.n_past for r in eng.active]
+    joins = [0]
+
+    def step(record):
+        eng.trace = trace if record else None
+        got = eng.step()
+        while len(eng.active) < S:
+            new_request(False)
+            joins[0] += 1
+        return got
+
+    for _ in range(args.warmup):
+        step(False)
+    torch.cuda.synchronize()
+    trace.reset()
+    decoded = prefill_tok = 0
+    attn_bytes = []
+    step_bytes = []
+    wbytes = workload.weight_bytes(hp)
+    kvb = 2 * hp["n_layer"] * hp["n_head_kv"] * hp["head_dim"] * 2  # K+V bytes per cell, all layers
+    joins[0] = 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        got = step(True)
+        plan = eng.last_plan
+        seq_n = plan.seq_n
+        npast = plan.seq_npast
+        n_kv = (npast.astype(np.int64) + seq_n)
+        N = int(seq_n.sum())
+        decoded += len(got)
+        prefill_tok += int(seq_n[seq_n > 1].sum())
+        per_layer_kv = int(n_kv.sum()) * kvb // hp["n_layer"]
+        qo = N * hp["n_head"] * hp["head_dim"] * 4 * 2
+        attn_bytes.append(per_layer_kv + qo)
+        step_bytes.append(wbytes + int(n_kv.sum()) * kvb + N * kvb)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    at = trace.times_ms(hip.TRACE_ATTN)
+    gt = trace.times_ms(hip.TRACE_GEMM)
+    L = hp["n_layer"]
+    # attention launches are recorded in step order, L per step
+    n_att = len(at)
+    tot_bytes = sum(attn_bytes[i // L] for i in range(n_att))
+    attn_gbs = tot_bytes / (sum(at) / 1e3) if at else 0.0
+    avg_attn_ms = sum(at) / max(n_att, 1)
+    gemm_ms = sum(gt) / args.steps
+    ms_step = wall * 1e3 / args.steps
+    step_gbs = sum(step_bytes) / wall
+    result = {
+        "metric": "decode tok/s, 64 ragged seqs, Llama-3-8B-shape Q4_K; paged-attn HBM GB/s %",
+        "value": decoded / wall,
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_K_M weights, f16 KV, f32 accumulate",
+        "data": "synthetic (seeded random-init weights, LCG prompts, synthetic initial KV)",
+        "config": {
+            "workload": "C2: Llama-3-8B shape, Q4_K_M, f16 KV, 64 ragged slots, prompts "
+                        "U[128,4096], continuous batching (budgets U[64,2048], joins prefilled "
+                        "in 512-token chunks)",
+            "slots": S, "seed": args.seed, "decoded_tokens": decoded,
+            "prefill_tokens": prefill_tok, "joins": joins[0],
+            "mean_context": float(np.mean(contexts0)),
+        },
+        "roofline": {
+            "bound": "hbm", "kernel": "paged_attn_kernel + merge_kernel (per layer)",
+            "achieved": attn_gbs / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+            "frac": attn_gbs / HBM_PEAK, "traffic": None,
+            "avg_launch_ms": avg_attn_ms, "launches": n_att,
+        },
+        "step_roofline": {
+            "bytes_per_step": sum(step_bytes) / len(step_bytes),
+            "achieved_GBps": step_gbs / 1e9, "frac": step_gbs / HBM_PEAK,
+            "gemm_ms_per_step": gemm_ms, "attn_ms_per_step": sum(at) / args.steps,
+            "gemm_GBps": wbytes / (gemm_ms / 1e3) / 1e9 if gemm_ms else None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        log(args, "timing the CPU oracle sample ...")
+        try:
+            result["cpu_baseline"] = cpu_baseline(hp, contexts0, args.seed, args)
+        except Exception as e:  # report, do not hide the GPU number
+            result["cpu_baseline"] = {"error": repr(e)}
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

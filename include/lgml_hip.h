@@ -82,6 +82,48 @@ int lgmlh_set_rows_f16(uint16_t *dst, int64_t dst_rows, int64_t row, const float
     const int64_t *ids, const int64_t *h_ids, int64_t n, void *stream);
 
 /* ===================================================================== *
+ * Pool bookkeeping (host): lua/lgml/kvpool.lua in C. All state lives in
+ * one caller buffer of lgmlh_kvpool_bytes(blocks, size) bytes. Block ids
+ * count from 0; priorities are LOW 0, NORMAL 1, HIGH 2 (kvpool.lua:25).
+ * Lua's pairs() order leaves exact ties of evict / longest_kid open; here
+ * they go to the lowest block id.
+ * ===================================================================== */
+size_t lgmlh_kvpool_bytes(int32_t blocks, int32_t size);
+/* M.new (kvpool.lua:65-72): blocks of size cells, cap usable. */
+int lgmlh_kvpool_init(void *mem, size_t bytes, int32_t blocks, int32_t size, int32_t cap);
+/* P:take (kvpool.lua:102-116): the lowest free block from min up, else the
+ * lowest one; -1 when none is free below cap. */
+int32_t lgmlh_kvpool_take(void *pool, int32_t min);
+/* P:evict (kvpool.lua:139-160): the cached block of the lowest priority,
+ * least recently used, deepest; it loses its key. -1 when none. */
+int32_t lgmlh_kvpool_evict(void *pool);
+/* P:ref / P:unref / P:refs_of (kvpool.lua:165-205). */
+int lgmlh_kvpool_ref(void *pool, int32_t b, int prio);
+int lgmlh_kvpool_unref(void *pool, int32_t b);
+int32_t lgmlh_kvpool_refs_of(void *pool, int32_t b);
+/* P:publish (kvpool.lua:217-226): 1 when b got the key, 0 when b or the
+ * key already had one. P:publish_part (:239-249) likewise. */
+int lgmlh_kvpool_publish(void *pool, int32_t b, const char *key, const char *parent,
+    int32_t depth, const int32_t *tokens, int32_t n, int prio);
+int lgmlh_kvpool_publish_part(void *pool, int32_t b, const char *parent, int32_t depth,
+    const int32_t *tokens, int32_t n, int prio);
+/* P:key_of (kvpool.lua:254-256): 0 none, 1 a key (64 hex digits + NUL to
+ * out), 2 the partial-block marker. */
+int lgmlh_kvpool_key_of(void *pool, int32_t b, char *out);
+/* P:lookup (kvpool.lua:261-263): the block with key, or -1. */
+int32_t lgmlh_kvpool_lookup(void *pool, const char *key);
+/* P:longest_kid (kvpool.lua:273-285) on tokens[0..max): block or -1, and
+ * the shared token count in *shared. */
+int32_t lgmlh_kvpool_longest_kid(void *pool, const char *parent, const int32_t *tokens,
+    int32_t max, int32_t *shared);
+/* P:set_cap (kvpool.lua:289-293). */
+int lgmlh_kvpool_set_cap(void *pool, int32_t cap);
+/* out[8]: n, size, cap, used, low, cached, tick, evicted. */
+int lgmlh_kvpool_stats(void *pool, int64_t *out);
+/* M.key (kvpool.lua:51-59): sha256 hex of parent "," t0 "," t1 ... (65 bytes). */
+int lgmlh_block_key(const char *parent, const int32_t *tokens, int32_t n, char *out);
+
+/* ===================================================================== *
  * Ubatch plan: the packing of fill_batch / batch_inputs
  * (transformer.lua:2433-2551) plus the attention work list.
  *
@@ -161,10 +203,8 @@ int lgmlh_dequantize(int type, const void *src, int64_t M, int64_t K, float *out
 
 enum { LGMLH_EPI_NONE = 0, LGMLH_EPI_ADD = 1 };
 
-/* Workspace of a call: per-tile counters, then split-K partial sums (0
- * bytes when K is not split). Zero-fill it before its first use; a call
- * leaves its counter words at zero again, so one workspace serves any
- * number of calls with the same M and N on one stream. */
+/* Workspace of a call: the split-K partial sums (0 bytes when K is not
+ * split). Its contents need no initialisation. */
 size_t lgmlh_mul_mat_workspace(int type, int64_t M, int64_t K, int64_t N);
 /* y = X W^T (+ residual when epi == LGMLH_EPI_ADD; residual may alias y).
  * x is f32 or f16 (xtype). Quantized types take the repacked w. The
@@ -198,6 +238,14 @@ int lgmlh_swiglu(const float *gu, int64_t n, int64_t F, void *out, int out_type,
 /* Greedy id of each row: the first index of the maximum (src/sample.c:914-925). */
 int lgmlh_argmax(const float *x, int64_t n_rows, int64_t n_cols, int32_t *out, void *stream);
 
+/* Seeded random-init weights in a ggml layout (rows x cols of `type`,
+ * F32 / Q4_K / Q6_K / Q8_0): N(mean, sd) values of tensor:fill("normal")
+ * (src/lgml.c:3130-3136, splitmix64 + Box-Muller, value i from draws
+ * 2i+1 and 2i+2 after seed) quantized by this library's own quantizer
+ * (the role of lgml.quantize, src/quant.c:107). */
+int lgmlh_gen_normal(uint64_t seed, int type, int64_t rows, int64_t cols, double mean, double sd,
+    void *out, void *stream);
+
 /* ===================================================================== *
  * One forward pass of a dense llama / qwen3 model over a planned ubatch:
  * transformer.lua forward (:2285-2365) with the batched attention of
@@ -226,16 +274,29 @@ typedef struct {
 	const lgmlh_layer *layers;        /* host array of n_layer */
 } lgmlh_model;
 
-/* Workspace bytes of lgmlh_forward for a plan and n_out logit rows. Zero-
- * fill it once before its first use: its first 256 KB hold split-K tile
- * counters that every call leaves at zero, so one workspace (grown when a
- * larger pass needs more) serves passes of any size on one stream. */
+/* Workspace bytes of lgmlh_forward for a plan and n_out logit rows. Its
+ * contents need no initialisation; one workspace (grown when a larger pass
+ * needs more) serves passes of any size on one stream. */
 size_t lgmlh_forward_workspace(const lgmlh_model *m, const lgmlh_plan_info *info, int n_out);
+/* Optional timing: hipEvent_t handles (created by the caller), two per
+ * slot, recorded on the pass's stream right before and after each traced
+ * launch group. kinds: LGMLH_TRACE_ATTN (paged attention + merge, one slot
+ * per layer), LGMLH_TRACE_GEMM (each weight product). used counts slots;
+ * a pass stops recording when capacity runs out. */
+enum { LGMLH_TRACE_ATTN = 1, LGMLH_TRACE_GEMM = 2 };
+typedef struct {
+	void *const *events; /* 2 * capacity hipEvent_t */
+	int32_t capacity, used, kinds;
+	int32_t *kind;       /* per slot: the kind recorded (may be NULL) */
+} lgmlh_trace;
+
 /* Run the pass: logits (n_out, n_vocab) f32 for the ubatch rows out_rows
  * (device; NULL = ub->logit_rows with n_out = n_seq). ids must be in range
- * (checked by the caller's plan, h_ids) -- the kernel reads them unchecked. */
+ * (checked by the caller's plan, h_ids) -- the kernel reads them unchecked.
+ * trace may be NULL. */
 int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub, const int32_t *out_rows,
-    int n_out, float *logits, void *workspace, size_t ws_bytes, void *stream);
+    int n_out, float *logits, void *workspace, size_t ws_bytes, lgmlh_trace *trace,
+    void *stream);
 
 #ifdef __cplusplus
 }

@@ -220,17 +220,22 @@ struct WFrag<LGMLH_Q8_0> {
 // X is staged per K step as f16 hi and lo planes (x = hi + lo to 22 bits)
 // plus the 32-value group sums (Q4_K min term); each product is the MFMA
 // of the exact integer weights with hi, then with lo, summed in f32.
+//
+// Pipeline: the weight fragments and X pieces of K step sb + 1 load into
+// registers while sb computes (two register sets, two LDS X buffers, one
+// barrier per step). A split writes its partial sums; a second kernel adds
+// the splits in order (no inter-workgroup sync).
 template <int TYPE, bool XF32>
 __global__ void __launch_bounds__(GEMM_THREADS)
 qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__restrict__ xv,
              int64_t N, float *__restrict__ y, int64_t ldy, const float *__restrict__ residual,
-             int splits, int sb_per_split, float *__restrict__ part,
-             int32_t *__restrict__ counters) {
-  __shared__ __align__(16) f16 xh[WG_COLS * X_STRIDE];
-  __shared__ __align__(16) f16 xl[WG_COLS * X_STRIDE];
-  __shared__ __align__(16) f16 gsh[WG_COLS * 8];  // group sums, hi
-  __shared__ __align__(16) f16 gsl[WG_COLS * 8];  // group sums, lo
-  __shared__ int last_flag;
+             int splits, int sb_per_split, float *__restrict__ part) {
+  // Two X buffers: step sb computes from buffer sb & 1 while the pieces of
+  // sb + 1 are staged into the other one (one barrier per step).
+  __shared__ __align__(16) f16 xh_[2][WG_COLS * X_STRIDE];
+  __shared__ __align__(16) f16 xl_[2][WG_COLS * X_STRIDE];
+  __shared__ __align__(16) f16 gsh_[2][WG_COLS * 8];  // group sums, hi
+  __shared__ __align__(16) f16 gsl_[2][WG_COLS * 8];  // group sums, lo
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t NSB = K / QK_K;
   const int64_t MT = (M + 15) / 16;
@@ -247,54 +252,67 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__
 #pragma unroll
     for (int b = 0; b < 4; b++) acc[a][b] = f32x4{0, 0, 0, 0};
 
-  for (int64_t sb = sb_lo; sb < sb_hi; sb++) {
-    __syncthreads();
-    // Stage X[n0 .. n0+64][sb*256 .. +256]: 64 pieces of 4 values per row.
-    for (int i = tid; i < WG_COLS * 64; i += GEMM_THREADS) {
-      int r = i >> 6, p = i & 63;
-      int64_t n = n0 + r;
+  // Thread tid stages pieces p = tid % 64 of X rows tid / 64 + 8 j: one
+  // wave per row, so a 32-value group is 8 consecutive lanes.
+  constexpr int XP = WG_COLS * 64 / GEMM_THREADS;  // pieces of 4 values per thread
+  const int xp = tid & 63, xr0 = tid >> 6;
+  f32x4 xreg[XP];
+  auto load_x = [&](int64_t sbk) {
+#pragma unroll
+    for (int j = 0; j < XP; j++) {
+      int64_t n = n0 + xr0 + 8 * j;
       f32x4 v = f32x4{0, 0, 0, 0};
-      f16x4 h, l;
-      if constexpr (XF32) {
-        if (n < N) v = *(const f32x4 *)((const float *)xv + n * K + sb * QK_K + p * 4);
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          h[e] = (f16)v[e];
-          l[e] = (f16)(v[e] - (float)h[e]);
-        }
-      } else {
-        u32x2 hv = u32x2{0, 0};
-        if (n < N) hv = *(const u32x2 *)((const f16 *)xv + n * K + sb * QK_K + p * 4);
-        h = __builtin_bit_cast(f16x4, hv);
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          v[e] = (float)h[e];
-          l[e] = (f16)0.0f;
+      if (n < N) {
+        if constexpr (XF32) {
+          v = *(const f32x4 *)((const float *)xv + n * K + sbk * QK_K + xp * 4);
+        } else {
+          u32x2 hv = *(const u32x2 *)((const f16 *)xv + n * K + sbk * QK_K + xp * 4);
+          f16x4 h = __builtin_bit_cast(f16x4, hv);
+          v = f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
         }
       }
-      *(f16x4 *)(xh + r * X_STRIDE + p * 4) = h;
-      *(f16x4 *)(xl + r * X_STRIDE + p * 4) = l;
+      xreg[j] = v;
+    }
+  };
+  auto stage_x = [&](int buf) {
+    f16 *xh = xh_[buf], *xl = xl_[buf], *gsh = gsh_[buf], *gsl = gsl_[buf];
+#pragma unroll
+    for (int j = 0; j < XP; j++) {
+      const int r = xr0 + 8 * j;
+      f32x4 v = xreg[j];
+      f16x4 h, l;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        h[e] = (f16)v[e];
+        l[e] = (f16)(v[e] - (float)h[e]);
+      }
+      *(f16x4 *)(xh + r * X_STRIDE + xp * 4) = h;
+      *(f16x4 *)(xl + r * X_STRIDE + xp * 4) = l;
       if constexpr (TYPE == LGMLH_Q4_K) {
-        // group sum over the 8 pieces (8 consecutive threads) of a group
         float gs = (v[0] + v[1]) + (v[2] + v[3]);
         gs += __shfl_xor(gs, 1);
         gs += __shfl_xor(gs, 2);
         gs += __shfl_xor(gs, 4);
-        if ((p & 7) == 0) {
+        if ((xp & 7) == 0) {
           f16 gh = (f16)gs;
-          gsh[r * 8 + (p >> 3)] = gh;
-          gsl[r * 8 + (p >> 3)] = (f16)(gs - (float)gh);
+          gsh[r * 8 + (xp >> 3)] = gh;
+          gsl[r * 8 + (xp >> 3)] = (f16)(gs - (float)gh);
         }
       }
     }
-    __syncthreads();
-
-    WFrag<TYPE> wf[RT_PER_WAVE];
+  };
+  auto chunk_of = [&](int a, int64_t sbk) {
+    int64_t rt = rt0 + a < MT ? rt0 + a : MT - 1;  // clamp: rows past M are never stored
+    return w + (rt * NSB + sbk) * chunk_bytes(TYPE);
+  };
+  auto load_w = [&](WFrag<TYPE>(&dst)[RT_PER_WAVE], int64_t sbk) {
 #pragma unroll
-    for (int a = 0; a < RT_PER_WAVE; a++) {
-      int64_t rt = rt0 + a < MT ? rt0 + a : MT - 1;  // clamp: rows past M are never stored
-      wf[a].load(w + (rt * NSB + sb) * chunk_bytes(TYPE), lane);
-    }
+    for (int a = 0; a < RT_PER_WAVE; a++) dst[a].load(chunk_of(a, sbk), lane);
+  };
+
+  // One K step on the staged X with the weight fragments cur.
+  auto compute = [&](int64_t sb, const WFrag<TYPE>(&cur)[RT_PER_WAVE], int buf) {
+    const f16 *xh = xh_[buf], *xl = xl_[buf], *gsh = gsh_[buf], *gsl = gsl_[buf];
     f32x4 cm[RT_PER_WAVE][4];
 #pragma unroll
     for (int a = 0; a < RT_PER_WAVE; a++)
@@ -302,34 +320,29 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__
       for (int b = 0; b < 4; b++) cm[a][b] = f32x4{0, 0, 0, 0};
 #pragma unroll
     for (int g = 0; g < 8; g++) {
-      f16x8 bh[4], bl[4];
+      f16x8 af[RT_PER_WAVE], af2[RT_PER_WAVE];
+#pragma unroll
+      for (int a = 0; a < RT_PER_WAVE; a++) {
+        if constexpr (TYPE == LGMLH_Q6_K)
+          cur[a].frag(g, c, af[a], af2[a]);
+        else
+          af[a] = cur[a].frag(g);
+      }
 #pragma unroll
       for (int ct = 0; ct < 4; ct++) {
         const int off = (ct * 16 + r16) * X_STRIDE + g * 32 + c * 8;
-        bh[ct] = *(const f16x8 *)(xh + off);
-        if constexpr (XF32) bl[ct] = *(const f16x8 *)(xl + off);
-      }
+        f16x8 bh = *(const f16x8 *)(xh + off);
+        f16x8 bl;
+        if constexpr (XF32) bl = *(const f16x8 *)(xl + off);
 #pragma unroll
-      for (int a = 0; a < RT_PER_WAVE; a++) {
-        if constexpr (TYPE == LGMLH_Q6_K) {
-          f16x8 a1, a2;
-          wf[a].frag(g, c, a1, a2);
-#pragma unroll
-          for (int ct = 0; ct < 4; ct++) {
-            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bh[ct], cm[a][ct], 0, 0, 0);
-            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bh[ct], cm[a][ct], 0, 0, 0);
-            if constexpr (XF32) {
-              cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bl[ct], cm[a][ct], 0, 0, 0);
-              cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bl[ct], cm[a][ct], 0, 0, 0);
-            }
-          }
-        } else {
-          f16x8 af = wf[a].frag(g);
-#pragma unroll
-          for (int ct = 0; ct < 4; ct++) {
-            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bh[ct], cm[a][ct], 0, 0, 0);
-            if constexpr (XF32)
-              cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bl[ct], cm[a][ct], 0, 0, 0);
+        for (int a = 0; a < RT_PER_WAVE; a++) {
+          cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bh, cm[a][ct], 0, 0, 0);
+          if constexpr (TYPE == LGMLH_Q6_K)
+            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af2[a], bh, cm[a][ct], 0, 0, 0);
+          if constexpr (XF32) {
+            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bl, cm[a][ct], 0, 0, 0);
+            if constexpr (TYPE == LGMLH_Q6_K)
+              cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af2[a], bl, cm[a][ct], 0, 0, 0);
           }
         }
       }
@@ -337,8 +350,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__
         // Q8_0: one scale per 32-value block: flush every group.
 #pragma unroll
         for (int a = 0; a < RT_PER_WAVE; a++) {
-          int64_t rt = rt0 + a < MT ? rt0 + a : MT - 1;
-          const uint8_t *hd = w + (rt * NSB + sb) * chunk_bytes(TYPE);
+          const uint8_t *hd = chunk_of(a, sb);
 #pragma unroll
           for (int i = 0; i < 4; i++) {
             float d = h2f(*(const uint16_t *)(hd + (4 * c + i) * 16 + 2 * g));
@@ -353,22 +365,10 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__
     }
     if constexpr (TYPE == LGMLH_Q4_K) {
       // min term: sum_g m_g * S_g[n] as one 16x16x16 MFMA over the 8 groups.
-      f16x4 sh4[4], sl4[4];
-#pragma unroll
-      for (int ct = 0; ct < 4; ct++) {
-        if (c < 2) {
-          sh4[ct] = *(const f16x4 *)(gsh + (ct * 16 + r16) * 8 + 4 * c);
-          sl4[ct] = *(const f16x4 *)(gsl + (ct * 16 + r16) * 8 + 4 * c);
-        } else {
-          sh4[ct] = f16x4{0, 0, 0, 0};
-          sl4[ct] = f16x4{0, 0, 0, 0};
-        }
-      }
 #pragma unroll
       for (int a = 0; a < RT_PER_WAVE; a++) {
-        f16x4 am = wf[a].mins(c);
-        int64_t rt = rt0 + a < MT ? rt0 + a : MT - 1;
-        const uint8_t *hd = w + (rt * NSB + sb) * chunk_bytes(TYPE);
+        f16x4 am = cur[a].mins(c);
+        const uint8_t *hd = chunk_of(a, sb);
         float dd[4], dm[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -378,8 +378,13 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__
         }
 #pragma unroll
         for (int ct = 0; ct < 4; ct++) {
-          f32x4 mn = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sh4[ct], f32x4{0, 0, 0, 0}, 0, 0, 0);
-          mn = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sl4[ct], mn, 0, 0, 0);
+          f16x4 sh4 = f16x4{0, 0, 0, 0}, sl4 = sh4;
+          if (c < 2) {
+            sh4 = *(const f16x4 *)(gsh + (ct * 16 + r16) * 8 + 4 * c);
+            sl4 = *(const f16x4 *)(gsl + (ct * 16 + r16) * 8 + 4 * c);
+          }
+          f32x4 mn = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sh4, f32x4{0, 0, 0, 0}, 0, 0, 0);
+          mn = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sl4, mn, 0, 0, 0);
 #pragma unroll
           for (int i = 0; i < 4; i++) acc[a][ct][i] += dd[i] * cm[a][ct][i] - dm[i] * mn[i];
         }
@@ -387,8 +392,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__
     } else if constexpr (TYPE == LGMLH_Q6_K) {
 #pragma unroll
       for (int a = 0; a < RT_PER_WAVE; a++) {
-        int64_t rt = rt0 + a < MT ? rt0 + a : MT - 1;
-        const uint8_t *hd = w + (rt * NSB + sb) * chunk_bytes(TYPE);
+        const uint8_t *hd = chunk_of(a, sb);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           float d = h2f(*(const uint16_t *)(hd + (4 * c + i) * 18));
@@ -397,30 +401,37 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__
         }
       }
     }
+  };
+
+  // Step sb: the loads of sb + 1 (weights into the other register set, X
+  // pieces into xreg) go out first, compute runs on sb, then the X of sb + 1
+  // is staged into the free LDS buffer and one barrier publishes it.
+  WFrag<TYPE> w0[RT_PER_WAVE], w1[RT_PER_WAVE];
+  auto step = [&](int64_t sb, const WFrag<TYPE>(&cur)[RT_PER_WAVE],
+                  WFrag<TYPE>(&nxt)[RT_PER_WAVE]) {
+    const bool more = sb + 1 < sb_hi;
+    if (more) {
+      load_w(nxt, sb + 1);
+      load_x(sb + 1);
+    }
+    compute(sb, cur, (int)((sb - sb_lo) & 1));
+    if (more) stage_x((int)((sb + 1 - sb_lo) & 1));
+    __syncthreads();
+  };
+  if (sb_lo < sb_hi) {
+    load_w(w0, sb_lo);
+    load_x(sb_lo);
+    stage_x(0);
+    __syncthreads();
+  }
+  for (int64_t sb = sb_lo; sb < sb_hi; sb += 2) {
+    step(sb, w0, w1);
+    if (sb + 1 < sb_hi) step(sb + 1, w1, w0);
   }
 
   // acc[a][ct][i] = Y[n0 + ct*16 + lane%16][(rt0+a)*16 + 4*(lane/16) + i]
-  if (splits == 1) {
-#pragma unroll
-    for (int a = 0; a < RT_PER_WAVE; a++)
-#pragma unroll
-      for (int ct = 0; ct < 4; ct++) {
-        int64_t n = n0 + ct * 16 + r16;
-        int64_t m = (rt0 + a) * 16 + 4 * c;
-        if (n >= N) continue;
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-          if (m + i < M) {
-            float v = acc[a][ct][i];
-            if (residual) v += residual[n * ldy + m + i];
-            y[n * ldy + m + i] = v;
-          }
-      }
-    return;
-  }
-  // Split K: write this split's tile, then the last workgroup of the tile
-  // adds all splits in order 0..splits-1.
-  float *pz = part + (int64_t)z * N * M;
+  float *dst = splits == 1 ? y : part + (int64_t)z * N * M;
+  const int64_t ld = splits == 1 ? ldy : M;
 #pragma unroll
   for (int a = 0; a < RT_PER_WAVE; a++)
 #pragma unroll
@@ -430,27 +441,27 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__
       if (n >= N) continue;
 #pragma unroll
       for (int i = 0; i < 4; i++)
-        if (m + i < M) pz[n * M + m + i] = acc[a][ct][i];
+        if (m + i < M) {
+          float v = acc[a][ct][i];
+          if (splits == 1 && residual) v += residual[n * ldy + m + i];
+          dst[n * ld + m + i] = v;
+        }
     }
-  __threadfence();
-  __syncthreads();
-  int32_t *cnt = counters + (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
-  if (tid == 0) last_flag = atomicAdd(cnt, 1) == splits - 1;
-  __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
-  const int64_t mlo = (int64_t)blockIdx.y * WG_ROWS;
-  const int64_t ncols = N - n0 < WG_COLS ? N - n0 : WG_COLS;
-  const int64_t mrows = M - mlo < WG_ROWS ? M - mlo : WG_ROWS;
-  for (int64_t e = tid; e < ncols * mrows; e += GEMM_THREADS) {
-    int64_t n = n0 + e / mrows, m = mlo + e % mrows;
+}
+
+// The splits of a split-K product, added in order 0..splits-1.
+__global__ void splitk_reduce_kernel(const float *__restrict__ part, int splits, int64_t N,
+                                     int64_t M, float *__restrict__ y, int64_t ldy,
+                                     const float *__restrict__ residual) {
+  int64_t total = N * M;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    int64_t n = e / M, m = e % M;
     float v = 0.0f;
-    for (int zz = 0; zz < splits; zz++)
-      v += __builtin_nontemporal_load(part + ((int64_t)zz * N + n) * M + m);
+    for (int zz = 0; zz < splits; zz++) v += part[(int64_t)zz * total + e];
     if (residual) v += residual[n * ldy + m];
     y[n * ldy + m] = v;
   }
-  if (tid == 0) *cnt = 0;  // ready for the next call
 }
 
 // ---- f32 weights: LDS-tiled VALU GEMM, sequential k order ----------------------
@@ -483,17 +494,13 @@ int splits_for(int64_t M, int64_t K, int64_t N) {
   (void)N;
   int64_t NSB = K / QK_K;
   int64_t tiles = (M + WG_ROWS - 1) / WG_ROWS;
-  // Aim for ~512 workgroups (two per CU) at 64 columns, at least 2 K steps
-  // per split.
-  int64_t want = (512 + tiles - 1) / tiles;
+  // About one workgroup per CU (256) at 64 columns, at least 2 K steps per
+  // split so the pipeline has a step to overlap.
+  int64_t want = (256 + tiles / 2) / tiles;
   int64_t maxs = NSB / 2 > 1 ? NSB / 2 : 1;
   if (want > maxs) want = maxs;
   if (want < 1) want = 1;
   return (int)want;
-}
-
-int64_t counter_words(int64_t M, int64_t N) {
-  return ((M + WG_ROWS - 1) / WG_ROWS) * ((N + WG_COLS - 1) / WG_COLS);
 }
 
 // Split-K partial sums of a call (0 when K is not split).
@@ -503,37 +510,39 @@ size_t partial_bytes(int type, int64_t M, int64_t K, int64_t N) {
   return s == 1 ? 0 : (size_t)s * N * M * 4;
 }
 
-// Public workspace: [tile counters, 256-byte aligned][partial sums].
 size_t workspace_for(int type, int64_t M, int64_t K, int64_t N) {
-  size_t p = partial_bytes(type, M, K, N);
-  if (p == 0) return 0;
-  return (((size_t)counter_words(M, N) * 4 + 255) & ~size_t(255)) + p;
+  return partial_bytes(type, M, K, N);
 }
 
 template <int TYPE>
 static void launch_q(const void *w, int64_t M, int64_t K, const void *x, int xtype, int64_t N,
                      float *y, int64_t ldy, const float *res, int splits, float *part,
-                     int32_t *cnt, hipStream_t st) {
+                     hipStream_t st) {
   int64_t NSB = K / QK_K;
   int spb = (int)((NSB + splits - 1) / splits);
   splits = (int)((NSB + spb - 1) / spb);
   dim3 grid((unsigned)((N + WG_COLS - 1) / WG_COLS), (unsigned)((M + WG_ROWS - 1) / WG_ROWS),
             (unsigned)splits);
   if (xtype == LGMLH_F32)
-    hipLaunchKernelGGL((qgemm_kernel<TYPE, true>), grid, dim3(GEMM_THREADS), 0, st, (const uint8_t *)w, M,
-                       K, x, N, y, ldy, res, splits, spb, part, cnt);
+    hipLaunchKernelGGL((qgemm_kernel<TYPE, true>), grid, dim3(GEMM_THREADS), 0, st,
+                       (const uint8_t *)w, M, K, x, N, y, ldy, res, splits, spb, part);
   else
-    hipLaunchKernelGGL((qgemm_kernel<TYPE, false>), grid, dim3(GEMM_THREADS), 0, st, (const uint8_t *)w,
-                       M, K, x, N, y, ldy, res, splits, spb, part, cnt);
+    hipLaunchKernelGGL((qgemm_kernel<TYPE, false>), grid, dim3(GEMM_THREADS), 0, st,
+                       (const uint8_t *)w, M, K, x, N, y, ldy, res, splits, spb, part);
+  if (splits > 1) {
+    int64_t total = N * M;
+    unsigned blocks = (unsigned)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, st, part, splits, N, M,
+                       y, ldy, res);
+  }
 }
 
 // Internal entry with an output row stride (the executor writes [q|k|v]
-// and [gate|up] rows from separate weights into one buffer) and separate
-// partial / counter regions: counters stay at one place for every call
-// that shares them, zero between calls.
+// and [gate|up] rows from separate weights into one buffer) and a partial-
+// sum region for split K.
 int mul_mat_ldy(int type, const void *w, int64_t M, int64_t K, const void *x, int xtype,
                 int64_t N, float *y, int64_t ldy, const float *residual, float *part,
-                size_t part_bytes, int32_t *counters, int64_t n_counters, hipStream_t st) {
+                size_t part_bytes, hipStream_t st) {
   if (!w || !x || !y || M <= 0 || K <= 0 || N < 0 || ldy < M ||
       (xtype != LGMLH_F32 && xtype != LGMLH_F16)) {
     set_error("mul_mat: bad arguments");
@@ -555,15 +564,14 @@ int mul_mat_ldy(int type, const void *w, int64_t M, int64_t K, const void *x, in
     return LGMLH_EINVAL;
   }
   int splits = splits_for(M, K, N);
-  if (splits > 1 && (part_bytes < partial_bytes(type, M, K, N) || !counters ||
-                     n_counters < counter_words(M, N))) {
+  if (splits > 1 && (!part || part_bytes < partial_bytes(type, M, K, N))) {
     set_error("mul_mat: workspace too small for %d K splits", splits);
     return LGMLH_ENOMEM;
   }
   switch (type) {
-    case LGMLH_Q4_K: launch_q<LGMLH_Q4_K>(w, M, K, x, xtype, N, y, ldy, residual, splits, part, counters, st); break;
-    case LGMLH_Q6_K: launch_q<LGMLH_Q6_K>(w, M, K, x, xtype, N, y, ldy, residual, splits, part, counters, st); break;
-    case LGMLH_Q8_0: launch_q<LGMLH_Q8_0>(w, M, K, x, xtype, N, y, ldy, residual, splits, part, counters, st); break;
+    case LGMLH_Q4_K: launch_q<LGMLH_Q4_K>(w, M, K, x, xtype, N, y, ldy, residual, splits, part, st); break;
+    case LGMLH_Q6_K: launch_q<LGMLH_Q6_K>(w, M, K, x, xtype, N, y, ldy, residual, splits, part, st); break;
+    case LGMLH_Q8_0: launch_q<LGMLH_Q8_0>(w, M, K, x, xtype, N, y, ldy, residual, splits, part, st); break;
     default:
       set_error("mul_mat: type %d not supported", type);
       return LGMLH_EINVAL;
@@ -622,10 +630,6 @@ extern "C" int lgmlh_mul_mat(int type, const void *w, int64_t M, int64_t K, cons
     set_error("mul_mat: workspace of %zu bytes, need %zu", ws_bytes, need);
     return LGMLH_ENOMEM;
   }
-  int64_t nc = counter_words(M, N);
-  size_t cb = ((size_t)nc * 4 + 255) & ~size_t(255);
-  int32_t *cnt = need ? (int32_t *)workspace : nullptr;
-  float *part = need ? (float *)((char *)workspace + cb) : nullptr;
   return mul_mat_ldy(type, w, M, K, x, xtype, N, y, M, epi == LGMLH_EPI_ADD ? residual : nullptr,
-                     part, need ? need - cb : 0, cnt, nc, as_stream(stream));
+                     (float *)workspace, ws_bytes, as_stream(stream));
 }

@@ -12,9 +12,8 @@ namespace lgmlh {
 
 int mul_mat_ldy(int type, const void *w, int64_t M, int64_t K, const void *x, int xtype,
                 int64_t N, float *y, int64_t ldy, const float *residual, float *part,
-                size_t part_bytes, int32_t *counters, int64_t n_counters, hipStream_t st);
+                size_t part_bytes, hipStream_t st);
 size_t partial_bytes(int type, int64_t M, int64_t K, int64_t N);
-int64_t counter_words(int64_t M, int64_t N);
 int get_rows_dev(int type, const void *table, int64_t n_cols, const int32_t *ids, int64_t n,
                  float *out, hipStream_t st);
 
@@ -62,7 +61,6 @@ struct Carve {
 struct Sizes {
   int64_t N, E, H, Hkv, D, F, V, W, n_out;
   size_t gemm_ws, attn_ws;
-  int64_t counters;
 };
 
 static Sizes sizes_of(const lgmlh_model *m, int64_t n_tokens, int64_t n_items, int n_out) {
@@ -77,11 +75,9 @@ static Sizes sizes_of(const lgmlh_model *m, int64_t n_tokens, int64_t n_items, i
   z.W = (z.H + 2 * z.Hkv) * z.D;
   z.n_out = n_out;
   size_t g = 0;
-  int64_t c = 0;
   auto upd = [&](int t, int64_t M, int64_t K, int64_t N) {
     size_t w = partial_bytes(t, M, K, N);
     if (w > g) g = w;
-    if (counter_words(M, N) > c) c = counter_words(M, N);
   };
   for (int il = 0; il < m->n_layer; il++) {
     const lgmlh_layer &L = m->layers[il];
@@ -93,20 +89,13 @@ static Sizes sizes_of(const lgmlh_model *m, int64_t n_tokens, int64_t n_items, i
   }
   upd(m->output_type, z.V, z.E, n_out);
   z.gemm_ws = g;
-  z.counters = c;
   z.attn_ws = (size_t)n_items * z.Hkv * (16 * z.D + 32) * sizeof(float);
   return z;
 }
 
-// Split-K tile counters live at the start of the workspace, in a region of
-// fixed size that nothing else writes: every GEMM leaves its counters at
-// zero, so passes of any size can share one workspace.
-constexpr int64_t MAX_COUNTERS = 65536;
-
 static size_t ws_bytes_of(const Sizes &z) {
   size_t b = 0;
   auto add = [&](size_t x) { b += (x + 255) & ~size_t(255); };
-  add(MAX_COUNTERS * 4);     // split-K tile counters (fixed place)
   add(z.N * z.E * 4);        // x (residual stream)
   add(z.N * z.E * 4);        // normed x (f16 or f32)
   add(z.N * z.W * 4);        // [q | k | v]
@@ -130,9 +119,27 @@ extern "C" size_t lgmlh_forward_workspace(const lgmlh_model *m, const lgmlh_plan
   return ws_bytes_of(sizes_of(m, info->n_tokens, info->n_items, n_out));
 }
 
+namespace {
+// Records an event pair around a launch group when the trace asks for it.
+struct Span {
+  lgmlh_trace *t;
+  hipStream_t st;
+  int slot;
+  Span(lgmlh_trace *tr, int kind, hipStream_t s) : t(tr), st(s), slot(-1) {
+    if (!t || !(t->kinds & kind) || t->used >= t->capacity) return;
+    slot = t->used++;
+    if (t->kind) t->kind[slot] = kind;
+    (void)hipEventRecord((hipEvent_t)t->events[2 * slot], st);
+  }
+  ~Span() {
+    if (slot >= 0) (void)hipEventRecord((hipEvent_t)t->events[2 * slot + 1], st);
+  }
+};
+}  // namespace
+
 extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
                              const int32_t *out_rows, int n_out, float *logits, void *workspace,
-                             size_t ws_bytes, void *stream) {
+                             size_t ws_bytes, lgmlh_trace *trace, void *stream) {
   if (!m || !ub || !logits || !workspace || !m->layers || m->n_layer <= 0 ||
       m->n_head_kv != ub->n_head_kv) {
     set_error("forward: bad arguments");
@@ -150,13 +157,8 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
     return LGMLH_ENOMEM;
   }
   if (z.N == 0) return LGMLH_OK;
-  if (z.counters > MAX_COUNTERS) {
-    set_error("forward: %lld split-K tiles (pass too large)", (long long)z.counters);
-    return LGMLH_EINVAL;
-  }
   uintptr_t base = ((uintptr_t)workspace + 255) & ~uintptr_t(255);
   Carve cv{(char *)base, ws_bytes - (size_t)(base - (uintptr_t)workspace), true};
-  int32_t *cnt = (int32_t *)cv.take(MAX_COUNTERS * 4);
   float *x = (float *)cv.take(z.N * z.E * 4);
   void *xn = cv.take(z.N * z.E * 4);
   float *qkv = (float *)cv.take(z.N * z.W * 4);
@@ -173,6 +175,11 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
   }
   const float scale = m->attn_scale > 0 ? m->attn_scale : 1.0f / sqrtf((float)z.D);
 
+#define GEMM(...)                                  \
+  do {                                             \
+    Span sp_(trace, LGMLH_TRACE_GEMM, st);         \
+    LGMLH_TRY(mul_mat_ldy(__VA_ARGS__));           \
+  } while (0)
   // token embeddings (get_rows, transformer.lua:2309); the ids were range
   // checked when the plan was made.
   LGMLH_TRY(get_rows_dev(m->tok_embd_type, m->tok_embd, z.E, ub->ids, z.N, x, st));
@@ -181,28 +188,31 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
     // Activations stay f32: the GEMM splits them into f16 hi + lo itself.
     const int at = LGMLH_F32;
     LGMLH_TRY(lgmlh_rms_norm(x, z.N, z.E, m->eps, L.attn_norm, xn, at, st));
-    LGMLH_TRY(mul_mat_ldy(L.wqkv_type, L.wqkv, L.wqkv_rows, z.E, xn, at, z.N, qkv, z.W, nullptr,
-                          gws, z.gemm_ws, cnt, z.counters, st));
+    GEMM(L.wqkv_type, L.wqkv, L.wqkv_rows, z.E, xn, at, z.N, qkv, z.W, nullptr,
+                          gws, z.gemm_ws, st);
     if (L.wv) {
-      LGMLH_TRY(mul_mat_ldy(L.wv_type, L.wv, z.W - L.wqkv_rows, z.E, xn, at, z.N,
-                            qkv + L.wqkv_rows, z.W, nullptr, gws, z.gemm_ws, cnt, z.counters, st));
+      GEMM(L.wv_type, L.wv, z.W - L.wqkv_rows, z.E, xn, at, z.N,
+                            qkv + L.wqkv_rows, z.W, nullptr, gws, z.gemm_ws, st);
     }
     LGMLH_TRY(lgmlh_qkv_rope_store(qkv, z.N, (int)z.H, (int)z.Hkv, (int)z.D, m->n_rot,
                                    m->rope_neox, m->rope_base, m->rope_freqs, L.q_norm, L.k_norm,
                                    m->eps, ub->pos, L.kpool, L.vpool, m->n_cells, ub->cells, q,
                                    st));
-    LGMLH_TRY(lgmlh_paged_attention(q, (int)z.H, (int)z.Hkv, (int)z.D, scale, L.kpool, L.vpool,
-                                    ub, att, aws, z.attn_ws, st));
-    LGMLH_TRY(mul_mat_ldy(L.wo_type, L.wo, z.E, z.H * z.D, att, LGMLH_F32, z.N, x, z.E, x, gws,
-                          z.gemm_ws, cnt, z.counters, st));
+    {
+      Span sp(trace, LGMLH_TRACE_ATTN, st);
+      LGMLH_TRY(lgmlh_paged_attention(q, (int)z.H, (int)z.Hkv, (int)z.D, scale, L.kpool,
+                                      L.vpool, ub, att, aws, z.attn_ws, st));
+    }
+    GEMM(L.wo_type, L.wo, z.E, z.H * z.D, att, LGMLH_F32, z.N, x, z.E, x, gws,
+                          z.gemm_ws, st);
     const int ft = LGMLH_F32;
     LGMLH_TRY(lgmlh_rms_norm(x, z.N, z.E, m->eps, L.ffn_norm, xn, ft, st));
-    LGMLH_TRY(mul_mat_ldy(L.wgu_type, L.wgu, 2 * z.F, z.E, xn, ft, z.N, gu, 2 * z.F, nullptr,
-                          gws, z.gemm_ws, cnt, z.counters, st));
+    GEMM(L.wgu_type, L.wgu, 2 * z.F, z.E, xn, ft, z.N, gu, 2 * z.F, nullptr,
+                          gws, z.gemm_ws, st);
     const int dt = LGMLH_F32;
     LGMLH_TRY(lgmlh_swiglu(gu, z.N, z.F, act, dt, st));
-    LGMLH_TRY(mul_mat_ldy(L.wdown_type, L.wdown, z.E, z.F, act, dt, z.N, x, z.E, x, gws,
-                          z.gemm_ws, cnt, z.counters, st));
+    GEMM(L.wdown_type, L.wdown, z.E, z.F, act, dt, z.N, x, z.E, x, gws,
+                          z.gemm_ws, st);
   }
   // head (transformer.lua:2094-2104) on the logit rows (:2349-2350)
   const int ot = LGMLH_F32;
@@ -214,8 +224,9 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
       hipLaunchKernelGGL(rms_norm_rows_kernel<float>, dim3(n_out), dim3(256), 0, st, x, out_rows,
                          z.E, m->eps, m->output_norm, (float *)xo);
     LGMLH_TRY(hip_check(hipGetLastError(), "forward: head norm"));
-    LGMLH_TRY(mul_mat_ldy(m->output_type, m->output, z.V, z.E, xo, ot, n_out, logits, z.V,
-                          nullptr, gws, z.gemm_ws, cnt, z.counters, st));
+    GEMM(m->output_type, m->output, z.V, z.E, xo, ot, n_out, logits, z.V,
+                          nullptr, gws, z.gemm_ws, st);
   }
+#undef GEMM
   return LGMLH_OK;
 }

@@ -1,0 +1,209 @@
+"""Pool sequences and the continuous-batching scheduler of the HIP path.
+
+Sequences over one paged pool follow lua/lgml/transformer.lua's pool
+helpers -- new_block (:934-958), reserve (:963-981), truncate (:1084-1108,
+copy-on-write of a shared partial block, here a device block copy),
+share (:1116-1123), seq_cells (:1126-1133) -- over the native pool
+bookkeeping (lgml_amd.kvpool). Engine.flush restates E:flush
+(lua/lgml/engine.lua:1423-1506): the pending decode steps and prompt
+chunks of all slots run as one pass, blocks are taken for each entry in
+arrival order first, and an entry that gets no block fails alone with
+"kv pool full". Prompts go in chunks of at most ubatch tokens
+(E:prefill_batched, :2213-2255, ubatch 512, :57). Greedy sampling is the
+first maximum (src/sample.c:914-925) on the device.
+"""
+import ctypes as C
+
+import numpy as np
+import torch
+
+from . import hip, kvpool
+from .hip import check, stream
+
+UBATCH = 512  # lua/lgml/engine.lua:57
+BLOCK = 64    # lua/lgml/transformer.lua:30
+
+
+class PoolFull(RuntimeError):
+    pass
+
+
+class Seq:
+    """A sequence on the pool (M:seq, transformer.lua:716-725)."""
+
+    def __init__(self, pool, prio=kvpool.NORMAL):
+        self.pool, self.blocks, self.keys, self.n_past, self.prio = pool, [], [], 0, prio
+
+
+class PoolSeqs:
+    """Block tables of the sequences on one device model's pool."""
+
+    def __init__(self, model, pressure=None):
+        self.model = model
+        self.alloc = kvpool.Pool(model.pool_blocks, BLOCK)
+        self.pressure = pressure
+
+    def new_block(self, c, min_):
+        """transformer.lua:934-958 (the pool is allocated whole up front, so
+        the grow branch never runs): a free block, else a cached one, else
+        one that pressure frees for c."""
+        b = self.alloc.take(min_)
+        if b is not None:
+            return b
+        b = self.alloc.evict()
+        if b is None and self.pressure is not None:
+            self.pressure(self, c)
+            b = self.alloc.take(min_)
+            if b is None:
+                b = self.alloc.evict()
+        return b
+
+    def reserve(self, c, n):
+        """transformer.lua:963-981: blocks for positions [0, n); the new
+        blocks of one call go in cell order."""
+        first = len(c.blocks)
+        while len(c.blocks) * BLOCK < n:
+            last = c.blocks[-1] if c.blocks else None
+            b = self.new_block(c, None if last is None else last + 1)
+            if b is None:
+                raise PoolFull("kv pool full: %d of %d cells in use" % (
+                    self.alloc.used * BLOCK, self.model.n_cells))
+            c.blocks.append(b)
+        if len(c.blocks) - first > 1:
+            c.blocks[first:] = sorted(c.blocks[first:])
+
+    def copy_block(self, src, dst, n):
+        """M.copy_block (transformer.lua:989-1007) on the device, every layer."""
+        hp = self.model.hp
+        for kp, vp in zip(self.model.kpools, self.model.vpools):
+            check(hip.lib().lgmlh_kv_copy_block(kp.data_ptr(), vp.data_ptr(), self.model.n_cells,
+                                                hp["n_head_kv"], hp["head_dim"], src, dst, n,
+                                                stream()))
+
+    def truncate(self, c, n):
+        """transformer.lua:1084-1108."""
+        keep = (n + BLOCK - 1) // BLOCK
+        while len(c.blocks) > keep:
+            self.alloc.unref(c.blocks.pop())
+        del c.keys[n // BLOCK:]
+        last = c.blocks[keep - 1] if keep >= 1 and len(c.blocks) >= keep else None
+        if n % BLOCK and last is not None and (self.alloc.refs_of(last) > 1 or
+                                               self.alloc.key_of(last)):
+            prev = c.blocks[keep - 2] if keep >= 2 else None
+            b = self.new_block(c, None if prev is None else prev + 1)
+            if b is None:
+                raise PoolFull("kv pool full")
+            self.copy_block(last, b, n % BLOCK)
+            c.blocks[keep - 1] = b
+            self.alloc.unref(last)
+        c.n_past = min(c.n_past, n)
+
+    def share(self, c, blocks, keys):
+        """transformer.lua:1116-1123."""
+        assert not c.blocks, "share: the sequence has blocks"
+        for b, k in zip(blocks, keys):
+            self.alloc.ref(b, c.prio)
+            c.blocks.append(b)
+            c.keys.append(k)
+        c.n_past = len(blocks) * BLOCK
+
+    def free(self, c):
+        """M:free_seq (transformer.lua:784-803): give the blocks back."""
+        self.truncate(c, 0)
+
+
+def seq_cells(c, frm, n):
+    """transformer.lua:1126-1133."""
+    return [c.blocks[p // BLOCK] * BLOCK + p % BLOCK for p in range(frm, frm + n)]
+
+
+class Request:
+    def __init__(self, prompt, max_new, prio=kvpool.NORMAL):
+        self.prompt = list(prompt)
+        self.max_new = max_new
+        self.prio = prio
+        self.out = []
+        self.seq = None
+        self.fed = 0       # prompt tokens run so far
+        self.err = None
+        self.done = False
+
+    def pending(self, ubatch):
+        """The ids of this request's next pass: a prompt chunk or one token."""
+        if self.fed < len(self.prompt):
+            return self.prompt[self.fed:self.fed + ubatch]
+        return [self.out[-1]]
+
+
+class Engine:
+    """Slots over one pool; step() runs one batched pass (E:flush)."""
+
+    def __init__(self, model, n_slots, ubatch=UBATCH, blocks_per_split=0, trace=None):
+        self.model = model
+        self.seqs = PoolSeqs(model)
+        self.n_slots = n_slots
+        self.ubatch = ubatch
+        self.bps = blocks_per_split
+        self.active = []   # requests in arrival order
+        self.trace = trace
+        self.passes = self.rows = self.tokens = 0
+        self.last_plan = None
+        self._ids = torch.empty(0, dtype=torch.int32, device="cuda")
+
+    def submit(self, req):
+        if len(self.active) >= self.n_slots:
+            raise RuntimeError("no free slot")
+        req.seq = Seq(self.seqs, req.prio)
+        self.active.append(req)
+        return req
+
+    def finish(self, req):
+        self.seqs.free(req.seq)
+        req.done = True
+        self.active.remove(req)
+
+    def step(self):
+        """One pass over every active request; returns the requests that got
+        a token. Requests whose budget is spent finish."""
+        entries = []
+        for r in list(self.active):
+            ids = r.pending(self.ubatch)
+            try:
+                self.seqs.reserve(r.seq, r.seq.n_past + len(ids))
+            except PoolFull as e:
+                r.err = str(e)
+                self.finish(r)
+                continue
+            entries.append((r, ids))
+        if not entries:
+            return []
+        seq_n = [len(ids) for _, ids in entries]
+        npast = [r.seq.n_past for r, _ in entries]
+        mb = max(len(r.seq.blocks) for r, _ in entries)
+        bt = np.full((len(entries), mb), -1, np.int32)
+        for i, (r, _) in enumerate(entries):
+            bt[i, :len(r.seq.blocks)] = r.seq.blocks
+        ids = np.concatenate([np.asarray(x, np.int32) for _, x in entries])
+        plan = self.model.plan(seq_n, npast, bt, ids, self.bps)
+        self.last_plan = plan
+        logits = self.model.forward(plan, trace=self.trace)
+        if self._ids.numel() < len(entries):
+            self._ids = torch.empty(len(entries), dtype=torch.int32, device="cuda")
+        check(hip.lib().lgmlh_argmax(logits.data_ptr(), len(entries), self.model.hp["n_vocab"],
+                                     self._ids.data_ptr(), stream()))
+        nxt = self._ids[:len(entries)].cpu().numpy()
+        self.passes += 1
+        self.rows += len(entries)
+        self.tokens += int(sum(seq_n))
+        got = []
+        for (r, x), tok in zip(entries, nxt):
+            r.seq.n_past += len(x)
+            if r.fed < len(r.prompt):
+                r.fed += len(x)
+                if r.fed < len(r.prompt):
+                    continue  # mid-prompt chunk: its logits are not sampled
+            r.out.append(int(tok))
+            got.append(r)
+            if len(r.out) >= r.max_new:
+                self.finish(r)
+        return got

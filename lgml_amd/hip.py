@@ -23,7 +23,13 @@ SYMBOLS = (
     "lgmlh_repacked_bytes", "lgmlh_repack", "lgmlh_dequantize", "lgmlh_mul_mat_workspace",
     "lgmlh_mul_mat", "lgmlh_get_rows", "lgmlh_rms_norm", "lgmlh_qkv_rope_store",
     "lgmlh_swiglu", "lgmlh_argmax", "lgmlh_forward_workspace", "lgmlh_forward",
+    "lgmlh_kvpool_bytes", "lgmlh_kvpool_init", "lgmlh_kvpool_take", "lgmlh_kvpool_evict",
+    "lgmlh_kvpool_ref", "lgmlh_kvpool_unref", "lgmlh_kvpool_refs_of", "lgmlh_kvpool_publish",
+    "lgmlh_kvpool_publish_part", "lgmlh_kvpool_key_of", "lgmlh_kvpool_lookup",
+    "lgmlh_kvpool_longest_kid", "lgmlh_kvpool_set_cap", "lgmlh_kvpool_stats", "lgmlh_block_key",
+    "lgmlh_gen_normal",
 )
+TRACE_ATTN, TRACE_GEMM = 1, 2
 
 
 class LgmlhError(RuntimeError):
@@ -56,6 +62,11 @@ class Layer(C.Structure):
                 ("kpool", C.c_void_p), ("vpool", C.c_void_p)]
 
 
+class Trace(C.Structure):
+    _fields_ = [("events", C.POINTER(C.c_void_p)), ("capacity", C.c_int32), ("used", C.c_int32),
+                ("kinds", C.c_int32), ("kind", C.POINTER(C.c_int32))]
+
+
 class Model(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim",
                                        "n_ff", "n_vocab", "n_rot", "rope_neox")] + \
@@ -72,6 +83,9 @@ def lib():
     """The loaded library; raises if it was not built (no CPU fallback)."""
     global _lib
     if _lib is None:
+        # torch first: its HIP runtime (soname libamdhip64.so.7) is then the
+        # one this library binds to, so one runtime serves the process.
+        import torch  # noqa: F401
         if not os.path.exists(LIB_PATH):
             raise RuntimeError("lgml_amd: %s is missing; run `python -m lgml_amd.build`" % LIB_PATH)
         L = C.CDLL(LIB_PATH)
@@ -109,7 +123,27 @@ def _declare(L):
         "lgmlh_swiglu": ([vp, i64, i64, vp, i32, vp], i32),
         "lgmlh_argmax": ([vp, i64, i64, vp, vp], i32),
         "lgmlh_forward_workspace": ([C.POINTER(Model), C.POINTER(PlanInfo), i32], sz),
-        "lgmlh_forward": ([C.POINTER(Model), C.POINTER(Ubatch), vp, i32, vp, vp, sz, vp], i32),
+        "lgmlh_forward": ([C.POINTER(Model), C.POINTER(Ubatch), vp, i32, vp, vp, sz,
+                           C.POINTER(Trace), vp], i32),
+        "lgmlh_kvpool_bytes": ([C.c_int32, C.c_int32], sz),
+        "lgmlh_kvpool_init": ([vp, sz, C.c_int32, C.c_int32, C.c_int32], i32),
+        "lgmlh_kvpool_take": ([vp, C.c_int32], C.c_int32),
+        "lgmlh_kvpool_evict": ([vp], C.c_int32),
+        "lgmlh_kvpool_ref": ([vp, C.c_int32, i32], i32),
+        "lgmlh_kvpool_unref": ([vp, C.c_int32], i32),
+        "lgmlh_kvpool_refs_of": ([vp, C.c_int32], C.c_int32),
+        "lgmlh_kvpool_publish": ([vp, C.c_int32, C.c_char_p, C.c_char_p, C.c_int32, vp, C.c_int32,
+                                  i32], i32),
+        "lgmlh_kvpool_publish_part": ([vp, C.c_int32, C.c_char_p, C.c_int32, vp, C.c_int32, i32],
+                                      i32),
+        "lgmlh_kvpool_key_of": ([vp, C.c_int32, vp], i32),
+        "lgmlh_kvpool_lookup": ([vp, C.c_char_p], C.c_int32),
+        "lgmlh_kvpool_longest_kid": ([vp, C.c_char_p, vp, C.c_int32, C.POINTER(C.c_int32)],
+                                     C.c_int32),
+        "lgmlh_kvpool_set_cap": ([vp, C.c_int32], i32),
+        "lgmlh_kvpool_stats": ([vp, vp], i32),
+        "lgmlh_block_key": ([C.c_char_p, vp, C.c_int32, vp], i32),
+        "lgmlh_gen_normal": ([C.c_uint64, i32, i64, i64, C.c_double, C.c_double, vp, vp], i32),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)

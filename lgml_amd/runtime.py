@@ -36,27 +36,53 @@ def _zeros(nbytes):
 
 
 def repack_concat(parts, K):
-    """Repack weight matrices of one type (each (rows, row_bytes) in ggml
-    layout, rows a multiple of 16) into one device matrix [p0 | p1 | ...]."""
+    """Repack weight matrices of one type into one device matrix
+    [p0 | p1 | ...]. Each part is (arr, type) with arr a numpy array (ggml
+    layout: uint8 (rows, row_bytes), or f32 (rows, K)) or (dev, type, rows)
+    with dev a device uint8 tensor in the same layout. Rows of fused parts
+    come in multiples of 16 (whole row tiles)."""
     ty = parts[0][1]
     assert all(p[1] == ty for p in parts)
-    rows = [p[0].shape[0] for p in parts]
+    rows = [p[2] if len(p) > 2 else p[0].shape[0] for p in parts]
     M = sum(rows)
     L = hip.lib()
+
+    def on_dev(p):
+        return p[0] if len(p) > 2 else _dev(p[0])
+
     if ty == hip.F32:
-        return _dev(np.concatenate([np.ascontiguousarray(p[0], np.float32) for p in parts])), ty, M
+        return torch.cat([on_dev(p) for p in parts]), ty, M
     total = L.lgmlh_repacked_bytes(ty, M, K)
     if total < 0:
         raise ValueError("cannot repack type %d (%d x %d)" % (ty, M, K))
     out = _empty(total)
     off = 0
-    for (arr, _), r in zip(parts, rows):
-        assert r % 16 == 0, "fused matrices need rows in multiples of 16"
-        src = _dev(arr)
+    for p, r in zip(parts, rows):
+        assert r % 16 == 0 or len(parts) == 1, "fused matrices need rows in multiples of 16"
+        src = on_dev(p)
         nb = L.lgmlh_repacked_bytes(ty, r, K)
         check(L.lgmlh_repack(ty, r, K, ptr(src), out.data_ptr() + off, stream()))
         off += nb
+    torch.cuda.current_stream().synchronize()  # sources may go
     return out, ty, M
+
+
+def generated_weights(hp, seed, policy):
+    """A weights source for DeviceModel that makes each matrix on the device
+    with lgmlh_gen_normal: N(0, 0.02), one seed per tensor in draw order;
+    norms are 1. policy(name, layer) gives the weight type."""
+    counter = [0]
+
+    def get(name, layer, rows, cols):
+        ty = policy(name, layer)
+        counter[0] += 1
+        nb = hip.lib().lgmlh_row_size(ty, cols) * rows
+        t = _empty(nb)
+        check(hip.lib().lgmlh_gen_normal(seed * 1000003 + counter[0], ty, rows, cols, 0.0, 0.02,
+                                         t.data_ptr(), stream()))
+        return (t, ty, rows)
+
+    return get
 
 
 class Plan:
@@ -95,10 +121,39 @@ class Plan:
         return self.host_array(self.info.off_logit_rows, self.info.n_seq, np.int32)
 
 
+class EventTrace:
+    """HIP events (torch.cuda.Event handles) that lgmlh_forward records around
+    the launch groups of the kinds asked for, on the pass's own stream."""
+
+    def __init__(self, capacity, kinds=hip.TRACE_ATTN):
+        self.events = [torch.cuda.Event(enable_timing=True) for _ in range(2 * capacity)]
+        for e in self.events:  # torch creates the HIP event on first record
+            e.record()
+        torch.cuda.synchronize()
+        self.handles = (C.c_void_p * (2 * capacity))(*[e.cuda_event for e in self.events])
+        self.kinds_arr = (C.c_int32 * capacity)()
+        self.c = hip.Trace(self.handles, capacity, 0, kinds, self.kinds_arr)
+
+    def reset(self):
+        self.c.used = 0
+
+    def times_ms(self, kind):
+        """Elapsed ms of every recorded slot of one kind (synchronizes)."""
+        torch.cuda.synchronize()
+        out = []
+        for i in range(self.c.used):
+            if self.kinds_arr[i] == kind:
+                out.append(self.events[2 * i].elapsed_time(self.events[2 * i + 1]))
+        return out
+
+
 class DeviceModel:
     """A dense llama / qwen3 model on the device with its paged KV pool."""
 
     def __init__(self, hp, w, n_cells):
+        """w: a weights dict of numpy arrays, or a callable source
+        w(name, layer, rows, cols) -> (device tensor, type, rows) such as
+        generated_weights()."""
         L = hip.lib()
         self.hp = hp
         E, H, Hkv, D = hp["n_embd"], hp["n_head"], hp["n_head_kv"], hp["head_dim"]
@@ -106,35 +161,49 @@ class DeviceModel:
         self.n_cells = int(n_cells)
         assert self.n_cells % 64 == 0
         self._keep = []
+        gen = callable(w)
 
         def keep(t):
             self._keep.append(t)
             return t
 
+        def mat(name, layer, rows, cols):
+            if gen:
+                return w(name, layer, rows, cols)
+            return w["layers"][layer][name] if layer is not None else w[name]
+
+        def vec(name, layer, n):
+            if gen:
+                return keep(torch.ones(n, dtype=torch.float32, device=DEV)).data_ptr()
+            arr = w["layers"][layer][name][0] if layer is not None else w[name][0]
+            return keep(_dev(np.asarray(arr, np.float32))).data_ptr()
+
         kvb = L.lgmlh_kv_layer_bytes(self.n_cells, Hkv, D)
         self.kpools, self.vpools = [], []
         self.layers = (hip.Layer * hp["n_layer"])()
-        for il, lw in enumerate(w["layers"]):
+        for il in range(hp["n_layer"]):
             Ly = self.layers[il]
-            Ly.attn_norm = keep(_dev(np.asarray(lw["attn_norm"][0], np.float32))).data_ptr()
-            Ly.ffn_norm = keep(_dev(np.asarray(lw["ffn_norm"][0], np.float32))).data_ptr()
-            for nm in ("q_norm", "k_norm"):
-                if lw.get(nm) is not None:
-                    setattr(Ly, nm, keep(_dev(np.asarray(lw[nm][0], np.float32))).data_ptr())
-            qk = [lw["wq"], lw["wk"]]
-            if lw["wv"][1] == lw["wq"][1] == lw["wk"][1]:
-                t, ty, M = repack_concat(qk + [lw["wv"]], E)
+            Ly.attn_norm = vec("attn_norm", il, E)
+            Ly.ffn_norm = vec("ffn_norm", il, E)
+            if not gen:
+                for nm in ("q_norm", "k_norm"):
+                    if w["layers"][il].get(nm) is not None:
+                        setattr(Ly, nm, vec(nm, il, D))
+            wq, wk, wv = mat("wq", il, H * D, E), mat("wk", il, Hkv * D, E), mat("wv", il, Hkv * D, E)
+            if wv[1] == wq[1] == wk[1]:
+                t, ty, M = repack_concat([wq, wk, wv], E)
                 Ly.wv = None
             else:
-                t, ty, M = repack_concat(qk, E)
-                tv, tyv, _ = repack_concat([lw["wv"]], E)
+                t, ty, M = repack_concat([wq, wk], E)
+                tv, tyv, _ = repack_concat([wv], E)
                 Ly.wv, Ly.wv_type = keep(tv).data_ptr(), tyv
             Ly.wqkv, Ly.wqkv_type, Ly.wqkv_rows = keep(t).data_ptr(), ty, M
-            t, ty, _ = repack_concat([lw["wo"]], H * D)
+            del wq, wk, wv
+            t, ty, _ = repack_concat([mat("wo", il, E, H * D)], H * D)
             Ly.wo, Ly.wo_type = keep(t).data_ptr(), ty
-            t, ty, _ = repack_concat([lw["gate"], lw["up"]], E)
+            t, ty, _ = repack_concat([mat("gate", il, F, E), mat("up", il, F, E)], E)
             Ly.wgu, Ly.wgu_type = keep(t).data_ptr(), ty
-            t, ty, _ = repack_concat([lw["down"]], F)
+            t, ty, _ = repack_concat([mat("down", il, E, F)], F)
             Ly.wdown, Ly.wdown_type = keep(t).data_ptr(), ty
             kp, vp = keep(_zeros(kvb)), keep(_zeros(kvb))
             self.kpools.append(kp)
@@ -146,13 +215,16 @@ class DeviceModel:
             setattr(m, k, int(hp[k]))
         m.eps, m.rope_base = hp["eps"], hp["rope_base"]
         m.attn_scale = hp.get("attn_scale", 0.0)
-        if w.get("rope_freqs") is not None:
+        if not gen and w.get("rope_freqs") is not None:
             m.rope_freqs = keep(_dev(np.asarray(w["rope_freqs"], np.float32))).data_ptr()
-        arr, ty = w["tok_embd"]
-        m.tok_embd, m.tok_embd_type = keep(_dev(arr)).data_ptr(), ty
-        t, ty, _ = repack_concat([w["output"]], E)
+        te = mat("tok_embd", None, V, E)
+        if gen:
+            m.tok_embd, m.tok_embd_type = keep(te[0]).data_ptr(), te[1]
+        else:
+            m.tok_embd, m.tok_embd_type = keep(_dev(te[0])).data_ptr(), te[1]
+        t, ty, _ = repack_concat([mat("output", None, V, E)], E)
         m.output, m.output_type = keep(t).data_ptr(), ty
-        m.output_norm = keep(_dev(np.asarray(w["output_norm"][0], np.float32))).data_ptr()
+        m.output_norm = vec("output_norm", None, E)
         m.n_cells = self.n_cells
         m.layers = self.layers
         self.m = m
@@ -173,15 +245,14 @@ class DeviceModel:
     def workspace(self, plan, n_out):
         need = hip.lib().lgmlh_forward_workspace(C.byref(self.m), C.byref(plan.info), n_out)
         if need > self.ws_bytes:
-            # zero-filled when (re)allocated: the split-K counters start at 0
-            # and every pass leaves them at 0
-            self.ws = _zeros(need)
+            self.ws = _empty(need)
             self.ws_bytes = need
         return self.ws
 
-    def forward(self, plan, out_rows=None, logits=None):
+    def forward(self, plan, out_rows=None, logits=None, trace=None):
         """Logits (n_out, vocab) f32 on the device for out_rows (ubatch token
-        indices; default the last token of each sequence)."""
+        indices; default the last token of each sequence). trace: an
+        EventTrace to time launch groups with HIP events."""
         if out_rows is None:
             n_out, rows = plan.info.n_seq, None
         else:
@@ -191,7 +262,8 @@ class DeviceModel:
         if logits is None:
             logits = torch.empty((n_out, self.hp["n_vocab"]), dtype=torch.float32, device=DEV)
         check(hip.lib().lgmlh_forward(C.byref(self.m), C.byref(plan.ub), ptr(rows), n_out,
-                                      logits.data_ptr(), ws.data_ptr(), self.ws_bytes, stream()))
+                                      logits.data_ptr(), ws.data_ptr(), self.ws_bytes,
+                                      C.byref(trace.c) if trace is not None else None, stream()))
         return logits
 
     def gather_kv(self, layer, cells, which=0):

@@ -1,0 +1,70 @@
+"""Model shapes, weight-type policy and synthetic workloads of the benchmark
+configurations (seeds recorded with each result).
+
+Integers (lengths, ids, budgets) come from the reference's test LCG
+(test/tiny.lua:16-22); weights from lgmlh_gen_normal (tensor:fill
+"normal", src/lgml.c:3130-3136)."""
+
+SHAPES = {
+    # C2: Llama-3-8B shape, Q4_K_M mix, f16 KV.
+    "c2": dict(arch="llama", n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128,
+               n_ff=14336, n_vocab=128256, rope_base=5e5, eps=1e-5, n_rot=128, rope_neox=0,
+               attn_scale=0.0, wtype="q4_K_M"),
+}
+
+F32, Q8_0, Q4_K, Q6_K = 0, 8, 12, 14
+
+
+def more_bits(i, n):
+    """lua/lgml/convert.lua:123-126: layers that get Q6_K in the _M mixes."""
+    return i < n // 8 or i >= 7 * n // 8 or (i - n // 8) % 3 == 2
+
+
+def policy(wtype, n_layer):
+    """lua/lgml/convert.lua:128-165: weight type of matrix `name` of `layer`
+    (None for the embeddings / output)."""
+    def ty(name, layer):
+        if wtype == "f32":
+            return F32
+        if wtype == "q8_0":
+            return Q8_0
+        if wtype == "q4_K":
+            return Q4_K
+        if name == "output":
+            return Q6_K
+        if layer is not None and name in ("wv", "down") and more_bits(layer, n_layer):
+            return Q6_K
+        return Q4_K
+    return ty
+
+
+class Lcg:
+    """test/tiny.lua:16-22: x <- x * 6364136223846793005 + 1442695040888963407
+    (mod 2^64), u = (x >> 11) / 2^53."""
+
+    def __init__(self, seed):
+        self.x = seed % 2**64
+
+    def next(self):
+        self.x = (self.x * 6364136223846793005 + 1442695040888963407) % 2**64
+        return (self.x >> 11) / 2.0**53
+
+    def int(self, lo, hi):
+        """U[lo, hi] inclusive."""
+        return lo + int(self.next() * (hi - lo + 1))
+
+
+def weight_bytes(hp):
+    """Bytes of the weights a decode step reads (all layer matrices and the
+    output head; the embedding table is read only at the ubatch's ids)."""
+    E, H, Hkv, D, F, V, L = (hp[k] for k in ("n_embd", "n_head", "n_head_kv", "head_dim", "n_ff",
+                                             "n_vocab", "n_layer"))
+    ty = policy(hp["wtype"], L)
+    size = {F32: 4.0, Q8_0: 34 / 32, Q4_K: 144 / 256, Q6_K: 210 / 256}
+    b = size[ty("output", None)] * V * E
+    for il in range(L):
+        b += size[ty("wq", il)] * H * D * E + size[ty("wk", il)] * Hkv * D * E
+        b += size[ty("wv", il)] * Hkv * D * E + size[ty("wo", il)] * E * H * D
+        b += size[ty("gate", il)] * F * E + size[ty("up", il)] * F * E
+        b += size[ty("down", il)] * E * F
+    return int(b)
