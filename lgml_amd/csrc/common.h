@@ -26,6 +26,47 @@ int hip_check(hipError_t e, const char *what);
 
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Split-K partial sums of a product not yet reduced: part[z][n][m] for
+// z < splits, n < rows, m < cols (cols = the product's M). The consumer
+// adds them in order z = 0, 1, ... (then the residual, if any).
+struct Pending {
+  const float *part = nullptr;
+  int splits = 0;
+  int64_t rows = 0, cols = 0;
+  __device__ __forceinline__ float sum(int64_t n, int64_t m) const {
+    float v = 0.0f;
+    for (int z = 0; z < splits; z++) v += part[((int64_t)z * rows + n) * cols + m];
+    return v;
+  }
+  // The sums at (n, m0 .. m0 + 7), m0 % 4 == 0 and cols % 4 == 0: 16-byte
+  // loads, four splits in flight, added in split order.
+  __device__ __forceinline__ void sum8(int64_t n, int64_t m0, float (&v)[8]) const {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    f4 a = {0.0f, 0.0f, 0.0f, 0.0f}, b = a;
+    const float *p = part + n * cols + m0;
+    const int64_t zs = rows * cols;
+    int z = 0;
+    for (; z + 4 <= splits; z += 4, p += 4 * zs) {
+      const f4 a0 = *(const f4 *)p, b0 = *(const f4 *)(p + 4);
+      const f4 a1 = *(const f4 *)(p + zs), b1 = *(const f4 *)(p + zs + 4);
+      const f4 a2 = *(const f4 *)(p + 2 * zs), b2 = *(const f4 *)(p + 2 * zs + 4);
+      const f4 a3 = *(const f4 *)(p + 3 * zs), b3 = *(const f4 *)(p + 3 * zs + 4);
+      a += a0; b += b0;
+      a += a1; b += b1;
+      a += a2; b += b2;
+      a += a3; b += b3;
+    }
+    for (; z < splits; z++, p += zs) {
+      a += *(const f4 *)p;
+      b += *(const f4 *)(p + 4);
+    }
+    for (int e = 0; e < 4; e++) {
+      v[e] = a[e];
+      v[4 + e] = b[e];
+    }
+  }
+};
+
 // Cells per KV block; the pool layout and the attention tiles assume it.
 constexpr int KV_BLOCK = 64;
 

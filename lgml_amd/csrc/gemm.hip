@@ -5,15 +5,25 @@
 // and K step sb (256 values) one chunk holds the tile's block headers and
 // then, for each of the 64 lanes of a wavefront (lane = r + 16 c: row r,
 // 8-value k chunk c of every 32-value group), exactly the bytes that lane
-// dequantizes into its MFMA A fragment. A wave streams its chunks with
-// 16-byte loads, dequantizes in registers (closed forms of quant.h, one
-// rounding to f16), and multiplies with 16x16x32 f16 MFMAs against X
-// staged in LDS as f16. Every output element is the same f32 sum over K in
-// the same order for any N, so a row gives the same bits alone or batched.
-// K is split over workgroups when M alone gives too few; the splits are
-// added in a fixed order by the last workgroup of each tile.
+// turns into its MFMA A fragment. The headers are laid out so that a lane
+// finds the scales of its row, and the super-block scales of the four
+// output rows it accumulates, in one load each.
+//
+// X arrives split (split.h): f16 hi and lo planes and the 32-value group
+// sums. A wave streams its chunks with 16-byte loads and builds exact
+// integer A fragments with byte permutes and one packed f16 FMA per pair
+// (Q4_K: sc * q; Q6_K: sc * q / 4 as two exact parts; Q8_0: q); each
+// 16x16x32 f16 MFMA takes A against hi and against lo, so a product is
+// f32-accurate. Super-block scales (d, dmin) are applied in f32 per K step
+// (Q8_0: per 32-value block).
+//
+// Every output element is the same f32 sum over K in the same order for any
+// N, so a row gives the same bits alone or batched. K is split over
+// workgroups when M alone gives too few (split count from M and K only);
+// the splits are added in a fixed order by a second kernel.
 #include "common.h"
 #include "quant.h"
+#include "split.h"
 
 namespace lgmlh {
 
@@ -30,7 +40,10 @@ __host__ __device__ constexpr int chunk_bytes(int type) {
        : type == LGMLH_Q6_K ? 16 * Q6K_BYTES
        : type == LGMLH_Q8_0 ? 16 * 8 * Q8_0_BYTES : 0;
 }
-// Bytes of the header part of a chunk.
+// Bytes of the header part of a chunk:
+//   Q4_K: [16 rows: u32 d | dmin << 16] [16 rows: 12 scale bytes]
+//   Q6_K: [16 rows: f16 d] [16 rows: 16 int8 scales]
+//   Q8_0: [4 c][8 blocks g][4 i] f16 d of row 4c + i, block g
 __host__ __device__ constexpr int chunk_hdr(int type) {
   return type == LGMLH_Q4_K ? 256 : type == LGMLH_Q6_K ? 288 : type == LGMLH_Q8_0 ? 256 : 0;
 }
@@ -41,7 +54,7 @@ __host__ __device__ constexpr int lane_bytes(int type) {
 
 // ---- repack: ggml row blocks -> row-tile chunks ------------------------------
 // One thread per (row tile, sb, lane): copies the lane's bytes and, for
-// c == 0, the row's header.
+// c == 0, the row's header fields.
 template <int TYPE>
 __global__ void repack_kernel(const uint8_t *__restrict__ src, int64_t M, int64_t NSB,
                               uint8_t *__restrict__ dst) {
@@ -54,189 +67,215 @@ __global__ void repack_kernel(const uint8_t *__restrict__ src, int64_t M, int64_
   int64_t m = rt * 16 + r;
   uint8_t *ch = dst + (rt * NSB + sb) * chunk_bytes(TYPE);
   uint8_t *ld = ch + chunk_hdr(TYPE) + lane * lane_bytes(TYPE);
-  if (m >= M) {  // padding rows: zero bytes dequantize to 0
-    for (int i = 0; i < lane_bytes(TYPE); i++) ld[i] = 0;
-    if (c == 0)
-      for (int i = 0; i < chunk_hdr(TYPE) / 16; i++) ch[r * (chunk_hdr(TYPE) / 16) + i] = 0;
-    return;
-  }
+  const bool pad = m >= M;  // padding rows: zero bytes give zero weights
   if (TYPE == LGMLH_Q4_K) {
     const uint8_t *b = src + (m * NSB + sb) * Q4K_BYTES;
-    if (c == 0)
-      for (int i = 0; i < 16; i++) ch[r * 16 + i] = b[i];
+    if (c == 0) {
+      for (int i = 0; i < 4; i++) ch[4 * r + i] = pad ? 0 : b[i];
+      for (int i = 0; i < 12; i++) ch[64 + 12 * r + i] = pad ? 0 : b[4 + i];
+    }
+    // piece j: qs[32j + 8c .. +7] (low nibbles group 2j, high nibbles 2j + 1)
     for (int j = 0; j < 4; j++)
-      for (int e = 0; e < 8; e++) ld[8 * j + e] = b[16 + 32 * j + 8 * c + e];
+      for (int e = 0; e < 8; e++) ld[8 * j + e] = pad ? 0 : b[16 + 32 * j + 8 * c + e];
   } else if (TYPE == LGMLH_Q6_K) {
     const uint8_t *b = src + (m * NSB + sb) * Q6K_BYTES;
     if (c == 0) {
-      ch[r * 18 + 0] = b[208];
-      ch[r * 18 + 1] = b[209];
-      for (int i = 0; i < 16; i++) ch[r * 18 + 2 + i] = b[192 + i];
+      ch[2 * r] = pad ? 0 : b[208];
+      ch[2 * r + 1] = pad ? 0 : b[209];
+      for (int i = 0; i < 16; i++) ch[32 + 16 * r + i] = pad ? 0 : b[192 + i];
     }
     // ql pieces (h, tb): ql[64h + 32tb + 8c .. +7]; then qh pieces h: qh[32h + 8c .. +7]
     for (int h = 0; h < 2; h++)
       for (int tb = 0; tb < 2; tb++)
-        for (int e = 0; e < 8; e++) ld[8 * (2 * h + tb) + e] = b[64 * h + 32 * tb + 8 * c + e];
+        for (int e = 0; e < 8; e++)
+          ld[8 * (2 * h + tb) + e] = pad ? 0 : b[64 * h + 32 * tb + 8 * c + e];
     for (int h = 0; h < 2; h++)
-      for (int e = 0; e < 8; e++) ld[32 + 8 * h + e] = b[128 + 32 * h + 8 * c + e];
+      for (int e = 0; e < 8; e++) ld[32 + 8 * h + e] = pad ? 0 : b[128 + 32 * h + 8 * c + e];
   } else {  // Q8_0: 8 blocks of 32 per 256 values
     const uint8_t *b = src + (m * NSB * 8 + sb * 8) * Q8_0_BYTES;
     if (c == 0)
       for (int g = 0; g < 8; g++) {
-        ch[r * 16 + 2 * g] = b[g * Q8_0_BYTES];
-        ch[r * 16 + 2 * g + 1] = b[g * Q8_0_BYTES + 1];
+        uint8_t *d = ch + 64 * (r >> 2) + 8 * g + 2 * (r & 3);
+        d[0] = pad ? 0 : b[g * Q8_0_BYTES];
+        d[1] = pad ? 0 : b[g * Q8_0_BYTES + 1];
       }
     for (int g = 0; g < 8; g++)
-      for (int e = 0; e < 8; e++) ld[8 * g + e] = b[g * Q8_0_BYTES + 2 + 8 * c + e];
+      for (int e = 0; e < 8; e++) ld[8 * g + e] = pad ? 0 : b[g * Q8_0_BYTES + 2 + 8 * c + e];
   }
 }
 
-// ---- per-lane weight data of one chunk --------------------------------------
-// A fragments hold exact small integers in f16 -- the group scale times the
-// quant (Q4_K: sc * q <= 945; Q6_K: sc * q split as 16 * s_hi * q + s_lo * q,
-// both exact; Q8_0: q) -- so the MFMA sees the weights without rounding; the
-// f16 super-block scales d (and dmin) are applied in f32 when a chunk is
-// flushed into the accumulator.
+// ---- A fragments -----------------------------------------------------------
+// biased(bytes, SEL_*): two bytes b of `bytes` as the f16 pair 1024 + b
+// (0x64 in the high byte, b in the mantissa); SEL_01 takes bytes 0, 1 and
+// SEL_23 bytes 2, 3. An FMA with (s, -1024 s) then gives s * b exactly
+// whenever the result fits 11 significant bits.
+constexpr uint32_t SEL_01 = 0x04010400u, SEL_23 = 0x04030402u;
+// hbiased(bytes, HSEL_*): the f16 pair whose high bytes are bytes 0, 1 (or
+// 2, 3) and whose low bytes are zero.
+constexpr uint32_t HSEL_01 = 0x050c040cu, HSEL_23 = 0x070c060cu;
+
+__device__ __forceinline__ f16x2 biased(uint32_t bytes, uint32_t sel) {
+  return __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, bytes, sel));
+}
+__device__ __forceinline__ f16x2 hbiased(uint32_t bytes, uint32_t sel) {
+  return __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(bytes, 0u, sel));
+}
+__device__ __forceinline__ f16x2 fma2(f16x2 a, f16 s, f16 c) {
+  return __builtin_elementwise_fma(a, f16x2{s, s}, f16x2{c, c});
+}
+__device__ __forceinline__ f16x8 cat4(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
+  return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+__device__ __forceinline__ f16 byte_f16(uint32_t w, int k) {
+  return (f16)(float)((w >> (8 * k)) & 0xffu);
+}
+
 template <int TYPE>
 struct WFrag;
 
-__device__ __forceinline__ f16x2 u16pair_to_f16(uint32_t lo16_hi16) {
-  // two small non-negative integers (< 1024) in the 16-bit halves -> exact f16
-  uint32_t m = lo16_hi16 | 0x64006400u;  // 1024 + v
-  return __builtin_bit_cast(f16x2, m) - f16x2{(f16)1024.0f, (f16)1024.0f};
-}
-
 template <>
 struct WFrag<LGMLH_Q4_K> {
-  u32x4 hdr;       // d | dmin << 16, scales[0..3], scales[4..7], scales[8..11]
-  u32x4 qs[2];     // 4 pieces of 8 bytes
-  __device__ void load(const uint8_t *ch, int lane) {
-    hdr = *(const u32x4 *)(ch + (lane & 15) * 16);
+  u32x4 dm;               // d | dmin << 16 of rows 4c + i, i = 0..3
+  uint32_t s0, s1, s2;    // the 12 scale bytes of row r
+  u32x4 qs[2];            // 4 pieces of 8 bytes
+  __device__ __forceinline__ void load(const uint8_t *ch, int lane) {
+    dm = *(const u32x4 *)(ch + 16 * (lane >> 4));
+    const uint32_t *sp = (const uint32_t *)(ch + 64 + 12 * (lane & 15));
+    s0 = sp[0];
+    s1 = sp[1];
+    s2 = sp[2];
     const u32x4 *p = (const u32x4 *)(ch + 256 + lane * 32);
     qs[0] = p[0];
     qs[1] = p[1];
   }
-  __device__ __forceinline__ uint32_t sbyte(int i) const {
-    return (hdr[1 + (i >> 2)] >> (8 * (i & 3))) & 0xffu;
+  // 6-bit scales (sc) and mins (m) of groups 0..3 / 4..7, one per byte
+  // (get_scale_min_k4 of the block format).
+  __device__ __forceinline__ uint32_t sc03() const { return s0 & 0x3F3F3F3Fu; }
+  __device__ __forceinline__ uint32_t sc47() const {
+    return (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
   }
-  __device__ __forceinline__ void scale_min(int g, int &sc, int &m) const {
-    if (g < 4) {
-      sc = sbyte(g) & 63;
-      m = sbyte(g + 4) & 63;
+  __device__ __forceinline__ uint32_t m03() const { return s1 & 0x3F3F3F3Fu; }
+  __device__ __forceinline__ uint32_t m47() const {
+    return ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+  }
+  // sc_g * q for k = 32g + 8c + e, e = 0..7 (<= 945, exact). scb holds the
+  // scales of g's half (sc03 or sc47). Low nibbles: (1024 + q) sc - 1024 sc;
+  // high nibbles kept in place: (1024 + 16 q) sc / 16 - 64 sc.
+  __device__ __forceinline__ f16x8 frag(int g, uint32_t scb) const {
+    const int j = g >> 1;
+    const uint32_t w0 = qs[j >> 1][2 * (j & 1)], w1 = qs[j >> 1][2 * (j & 1) + 1];
+    const f16 scf = byte_f16(scb, g & 3);
+    uint32_t n0, n1;
+    f16 s, cc;
+    if (g & 1) {
+      n0 = w0 & 0xF0F0F0F0u;
+      n1 = w1 & 0xF0F0F0F0u;
+      s = scf * (f16)0.0625f;
+      cc = scf * (f16)-64.0f;
     } else {
-      sc = (sbyte(g + 4) & 0xF) | ((sbyte(g - 4) >> 6) << 4);
-      m = (sbyte(g + 4) >> 4) | ((sbyte(g) >> 6) << 4);
+      n0 = w0 & 0x0F0F0F0Fu;
+      n1 = w1 & 0x0F0F0F0Fu;
+      s = scf;
+      cc = scf * (f16)-1024.0f;
     }
+    return cat4(fma2(biased(n0, SEL_01), s, cc), fma2(biased(n0, SEL_23), s, cc),
+                fma2(biased(n1, SEL_01), s, cc), fma2(biased(n1, SEL_23), s, cc));
   }
-  // sc_g * q for k = 32g + 8c + e, e = 0..7.
-  __device__ __forceinline__ f16x8 frag(int g) const {
-    int sc, m;
-    scale_min(g, sc, m);
-    int j = g >> 1;
-    uint32_t lo = qs[j >> 1][2 * (j & 1)], hi = qs[j >> 1][2 * (j & 1) + 1];
-    int sh = (g & 1) * 4;
-    uint32_t a = (lo >> sh) & 0x0F0F0F0Fu, b = (hi >> sh) & 0x0F0F0F0Fu;
-    f16x2 s2 = f16x2{(f16)(float)sc, (f16)(float)sc};
-    f16x2 p0 = u16pair_to_f16((a & 0xffu) | ((a & 0xff00u) << 8)) * s2;
-    f16x2 p1 = u16pair_to_f16(((a >> 16) & 0xffu) | ((a >> 8) & 0xff0000u)) * s2;
-    f16x2 p2 = u16pair_to_f16((b & 0xffu) | ((b & 0xff00u) << 8)) * s2;
-    f16x2 p3 = u16pair_to_f16(((b >> 16) & 0xffu) | ((b >> 8) & 0xff0000u)) * s2;
-    return f16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-  }
-  // The 16x16x16 A fragment of the mins: row lane%16, k = groups 4c..4c+3
+  // The 16x16x16 A fragment of the mins: row r, k = groups 4c .. 4c + 3
   // (zero for c >= 2).
   __device__ __forceinline__ f16x4 mins(int c) const {
-    f16x4 r = f16x4{0, 0, 0, 0};
-    if (c < 2) {
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        int sc, m;
-        scale_min(4 * c + i, sc, m);
-        r[i] = (f16)(float)m;
-      }
-    }
-    return r;
+    const uint32_t mb = c == 0 ? m03() : m47();
+    const f16x2 k = f16x2{(f16)1024.0f, (f16)1024.0f};
+    const f16x2 a = biased(mb, SEL_01) - k, b = biased(mb, SEL_23) - k;
+    return c < 2 ? f16x4{a[0], a[1], b[0], b[1]} : f16x4{0, 0, 0, 0};
   }
 };
 
 template <>
 struct WFrag<LGMLH_Q6_K> {
-  uint32_t hdr[5];  // d (16 bits) + 16 int8 scales, 18 bytes from row r's header
-  u32x4 ql[2];      // pieces (h, tb) of 8 bytes: index 2h + tb
-  u32x4 qh;         // pieces h of 8 bytes
-  __device__ void load(const uint8_t *ch, int lane) {
-    const uint16_t *h = (const uint16_t *)(ch + (lane & 15) * 18);
-#pragma unroll
-    for (int i = 0; i < 4; i++) hdr[i] = (uint32_t)h[2 * i] | ((uint32_t)h[2 * i + 1] << 16);
-    hdr[4] = h[8];
+  u32x2 d4;        // f16 d of rows 4c + i, i = 0..3
+  u32x4 scl;       // the 16 int8 scales of row r
+  u32x4 ql[2];     // ql pieces (h, tb), index 2h + tb
+  u32x4 qh;        // qh pieces h
+  __device__ __forceinline__ void load(const uint8_t *ch, int lane) {
+    d4 = *(const u32x2 *)(ch + 8 * (lane >> 4));
+    scl = *(const u32x4 *)(ch + 32 + 16 * (lane & 15));
     const u32x4 *p = (const u32x4 *)(ch + 288 + lane * 48);
     ql[0] = p[0];
     ql[1] = p[1];
     qh = p[2];
   }
-  // Two fragments whose sum is sc * q (scale index (32g + 8c) / 16):
-  // a1 = 16 * (sc >> 4) * q, a2 = (sc & 15) * q, both exact in f16.
-  __device__ __forceinline__ void frag(int g, int c, f16x8 &a1, f16x8 &a2) const {
-    int si = 2 + 2 * g + (c >> 1);
-    int sc = (int)(int8_t)(hdr[si >> 2] >> (8 * (si & 3)));
-    int s_hi = sc >> 4, s_lo = sc & 15;
-    int h = g >> 2, t = g & 3;
-    int piece = 2 * h + (t & 1);
-    uint32_t lo = ql[piece >> 1][2 * (piece & 1)], hi = ql[piece >> 1][2 * (piece & 1) + 1];
-    uint32_t hlo = qh[2 * h], hhi = qh[2 * h + 1];
-    int nsh = t < 2 ? 0 : 4;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      int q0 = (int)(((lo >> (8 * e + nsh)) & 15) | (((hlo >> (8 * e + 2 * t)) & 3) << 4)) - 32;
-      int q1 = (int)(((hi >> (8 * e + nsh)) & 15) | (((hhi >> (8 * e + 2 * t)) & 3) << 4)) - 32;
-      a1[e] = (f16)(float)(16 * s_hi * q0);
-      a1[4 + e] = (f16)(float)(16 * s_hi * q1);
-      a2[e] = (f16)(float)(s_lo * q0);
-      a2[4 + e] = (f16)(float)(s_lo * q1);
+  // sc * q / 4 for k = 32g + 8c + e, with q = u - 32, u = u_lo + 16 u_hi:
+  //   a1 = sc u_lo / 4       = (1024 + u_lo) (sc / 4) - 256 sc      exact
+  //   a2 = 4 sc (u_hi - 2)   = (1 + u_hi / 4) (16 sc) - 24 sc        exact
+  //   ar = f16(a1 + a2)      rounded, for the product with x lo.
+  // sh = 8 * (c >> 1): the lane's scale (16-value block 2g + c / 2).
+  __device__ __forceinline__ void frag(int g, uint32_t sh, f16x8 &a1, f16x8 &a2, f16x8 &ar) const {
+    const int hh = g >> 2, t = g & 3, piece = 2 * hh + (t & 1);
+    const uint32_t lq0 = ql[piece >> 1][2 * (piece & 1)], lq1 = ql[piece >> 1][2 * (piece & 1) + 1];
+    const uint32_t hq0 = qh[2 * hh], hq1 = qh[2 * hh + 1];
+    uint32_t n0, n1;
+    if (t < 2) {
+      n0 = lq0 & 0x0F0F0F0Fu;
+      n1 = lq1 & 0x0F0F0F0Fu;
+    } else {
+      n0 = (lq0 >> 4) & 0x0F0F0F0Fu;
+      n1 = (lq1 >> 4) & 0x0F0F0F0Fu;
     }
+    const uint32_t b0 = ((hq0 >> (2 * t)) & 0x03030303u) | 0x3C3C3C3Cu;
+    const uint32_t b1 = ((hq1 >> (2 * t)) & 0x03030303u) | 0x3C3C3C3Cu;
+    const int sc = (int)(int8_t)(scl[g >> 1] >> (16 * (g & 1) + sh));
+    const f16 scf = (f16)(float)sc;
+    const f16 s1 = scf * (f16)0.25f, c1 = scf * (f16)-256.0f;
+    const f16 s2 = scf * (f16)16.0f, c2 = scf * (f16)-24.0f;
+    a1 = cat4(fma2(biased(n0, SEL_01), s1, c1), fma2(biased(n0, SEL_23), s1, c1),
+              fma2(biased(n1, SEL_01), s1, c1), fma2(biased(n1, SEL_23), s1, c1));
+    a2 = cat4(fma2(hbiased(b0, HSEL_01), s2, c2), fma2(hbiased(b0, HSEL_23), s2, c2),
+              fma2(hbiased(b1, HSEL_01), s2, c2), fma2(hbiased(b1, HSEL_23), s2, c2));
+    ar = a1 + a2;
   }
 };
 
 template <>
 struct WFrag<LGMLH_Q8_0> {
-  const uint8_t *qs;   // the lane's 8 blocks x 8 int8, read per group
-  __device__ void load(const uint8_t *ch, int lane) { qs = ch + 256 + lane * 64; }
-  __device__ __forceinline__ f16x8 frag(int g) const {
-    u32x2 q = *(const u32x2 *)(qs + 8 * g);
-    f16x8 r;
+  u32x4 qs[4];           // 8 blocks x 8 int8
+  const uint8_t *hd;     // header: d of rows 4c + i, block g at hd + 8g
+  __device__ __forceinline__ void load(const uint8_t *ch, int lane) {
+    const u32x4 *p = (const u32x4 *)(ch + 256 + lane * 64);
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      r[e] = (f16)(float)(int8_t)(q[0] >> (8 * e));
-      r[4 + e] = (f16)(float)(int8_t)(q[1] >> (8 * e));
-    }
-    return r;
+    for (int i = 0; i < 4; i++) qs[i] = p[i];
+    hd = ch + 64 * (lane >> 4);
+  }
+  // q for k = 32g + 8c + e: (1024 + (q + 128)) - 1152, exact.
+  __device__ __forceinline__ f16x8 frag(int g) const {
+    const uint32_t w0 = qs[g >> 1][2 * (g & 1)] ^ 0x80808080u;
+    const uint32_t w1 = qs[g >> 1][2 * (g & 1) + 1] ^ 0x80808080u;
+    const f16x2 k = f16x2{(f16)1152.0f, (f16)1152.0f};
+    return cat4(biased(w0, SEL_01) - k, biased(w0, SEL_23) - k, biased(w1, SEL_01) - k,
+                biased(w1, SEL_23) - k);
   }
 };
 
 // ---- the quantized GEMM --------------------------------------------------------
-// grid: (ceil(N / 64), ceil(M / WG_ROWS), splits); blockIdx.x (N tiles) varies
+// grid: (Npad / 64, ceil(M / WG_ROWS), splits); blockIdx.x (N tiles) varies
 // fastest so the workgroups that share a weight tile run together.
-//
-// X is staged per K step as f16 hi and lo planes (x = hi + lo to 22 bits)
-// plus the 32-value group sums (Q4_K min term); each product is the MFMA
-// of the exact integer weights with hi, then with lo, summed in f32.
 //
 // Pipeline: the weight fragments and X pieces of K step sb + 1 load into
 // registers while sb computes (two register sets, two LDS X buffers, one
 // barrier per step). A split writes its partial sums; a second kernel adds
 // the splits in order (no inter-workgroup sync).
-template <int TYPE, bool XF32>
+template <int TYPE>
 __global__ void __launch_bounds__(GEMM_THREADS)
-qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__restrict__ xv,
-             int64_t N, float *__restrict__ y, int64_t ldy, const float *__restrict__ residual,
-             int splits, int sb_per_split, float *__restrict__ part) {
-  // Two X buffers: step sb computes from buffer sb & 1 while the pieces of
-  // sb + 1 are staged into the other one (one barrier per step).
+qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__restrict__ xs,
+             int64_t Npad, int64_t N, float *__restrict__ y, int64_t ldy,
+             const float *__restrict__ residual, int splits, int sb_per_split,
+             float *__restrict__ part) {
   __shared__ __align__(16) f16 xh_[2][WG_COLS * X_STRIDE];
   __shared__ __align__(16) f16 xl_[2][WG_COLS * X_STRIDE];
-  __shared__ __align__(16) f16 gsh_[2][WG_COLS * 8];  // group sums, hi
-  __shared__ __align__(16) f16 gsl_[2][WG_COLS * 8];  // group sums, lo
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ __align__(16) f16 gh_[2][WG_COLS * 8];  // group sums, hi
+  __shared__ __align__(16) f16 gl_[2][WG_COLS * 8];  // group sums, lo
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int64_t NSB = K / QK_K;
   const int64_t MT = (M + 15) / 16;
   const int64_t n0 = (int64_t)blockIdx.x * WG_COLS;
@@ -252,139 +291,139 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__
 #pragma unroll
     for (int b = 0; b < 4; b++) acc[a][b] = f32x4{0, 0, 0, 0};
 
-  // Thread tid stages pieces p = tid % 64 of X rows tid / 64 + 8 j: one
-  // wave per row, so a 32-value group is 8 consecutive lanes.
-  constexpr int XP = WG_COLS * 64 / GEMM_THREADS;  // pieces of 4 values per thread
-  const int xp = tid & 63, xr0 = tid >> 6;
-  f32x4 xreg[XP];
-  auto load_x = [&](int64_t sbk) {
+  // Staging: the 64 x 256 slice of each plane is 2048 pieces of 8 f16;
+  // thread tid moves pieces tid + 512 j (row i / 32, piece i % 32), so a
+  // wave reads two contiguous 512-byte row segments per load. Offsets are
+  // 32-bit element offsets from the wave-uniform plane bases.
+  constexpr int XP = WG_COLS * 32 / GEMM_THREADS;  // 4
+  const f16 *xhi = xs + n0 * K + sb_lo * QK_K, *xlo = xhi + Npad * K;
+  const f16 *ghi = xs + 2 * Npad * K + n0 * (K / 32) + sb_lo * 8, *glo = ghi + Npad * (K / 32);
+  const uint32_t xoff = (uint32_t)((tid >> 5) * K + (tid & 31) * 8);
+  const uint32_t xrow16 = (uint32_t)(16 * K);
+  const uint32_t goff = (uint32_t)((tid & 63) * (K / 32));
+  u32x4 xrh[XP], xrl[XP], xrg;
+  auto load_x = [&](uint32_t kstep) {  // kstep = sb - sb_lo
+    const uint32_t o = xoff + kstep * QK_K;
 #pragma unroll
     for (int j = 0; j < XP; j++) {
-      int64_t n = n0 + xr0 + 8 * j;
-      f32x4 v = f32x4{0, 0, 0, 0};
-      if (n < N) {
-        if constexpr (XF32) {
-          v = *(const f32x4 *)((const float *)xv + n * K + sbk * QK_K + xp * 4);
-        } else {
-          u32x2 hv = *(const u32x2 *)((const f16 *)xv + n * K + sbk * QK_K + xp * 4);
-          f16x4 h = __builtin_bit_cast(f16x4, hv);
-          v = f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
-        }
-      }
-      xreg[j] = v;
+      xrh[j] = *(const u32x4 *)(xhi + (o + j * xrow16));
+      xrl[j] = *(const u32x4 *)(xlo + (o + j * xrow16));
+    }
+    if constexpr (TYPE == LGMLH_Q4_K) {
+      if (tid < 2 * WG_COLS) xrg = *(const u32x4 *)((tid < WG_COLS ? ghi : glo) + (goff + kstep * 8));
     }
   };
   auto stage_x = [&](int buf) {
-    f16 *xh = xh_[buf], *xl = xl_[buf], *gsh = gsh_[buf], *gsl = gsl_[buf];
 #pragma unroll
     for (int j = 0; j < XP; j++) {
-      const int r = xr0 + 8 * j;
-      f32x4 v = xreg[j];
-      f16x4 h, l;
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        h[e] = (f16)v[e];
-        l[e] = (f16)(v[e] - (float)h[e]);
-      }
-      *(f16x4 *)(xh + r * X_STRIDE + xp * 4) = h;
-      *(f16x4 *)(xl + r * X_STRIDE + xp * 4) = l;
-      if constexpr (TYPE == LGMLH_Q4_K) {
-        float gs = (v[0] + v[1]) + (v[2] + v[3]);
-        gs += __shfl_xor(gs, 1);
-        gs += __shfl_xor(gs, 2);
-        gs += __shfl_xor(gs, 4);
-        if ((xp & 7) == 0) {
-          f16 gh = (f16)gs;
-          gsh[r * 8 + (xp >> 3)] = gh;
-          gsl[r * 8 + (xp >> 3)] = (f16)(gs - (float)gh);
-        }
-      }
+      const int i = tid + GEMM_THREADS * j;
+      const int o = (i >> 5) * X_STRIDE + (i & 31) * 8;
+      *(u32x4 *)(xh_[buf] + o) = xrh[j];
+      *(u32x4 *)(xl_[buf] + o) = xrl[j];
+    }
+    if constexpr (TYPE == LGMLH_Q4_K) {
+      if (tid < 2 * WG_COLS) *(u32x4 *)((tid < WG_COLS ? gh_[buf] : gl_[buf]) + (tid & 63) * 8) = xrg;
     }
   };
-  auto chunk_of = [&](int a, int64_t sbk) {
-    int64_t rt = rt0 + a < MT ? rt0 + a : MT - 1;  // clamp: rows past M are never stored
-    return w + (rt * NSB + sbk) * chunk_bytes(TYPE);
-  };
-  auto load_w = [&](WFrag<TYPE>(&dst)[RT_PER_WAVE], int64_t sbk) {
+  // Chunk of tile a at K step sb_lo + kstep: a wave-uniform address (rows
+  // past M clamp to the last tile; they are computed but never stored).
+  const uint8_t *wt[RT_PER_WAVE];
 #pragma unroll
-    for (int a = 0; a < RT_PER_WAVE; a++) dst[a].load(chunk_of(a, sbk), lane);
+  for (int a = 0; a < RT_PER_WAVE; a++) {
+    const int64_t rt = rt0 + a < MT ? rt0 + a : MT - 1;
+    wt[a] = w + (rt * NSB + sb_lo) * chunk_bytes(TYPE);
+  }
+  auto load_w = [&](WFrag<TYPE>(&dst)[RT_PER_WAVE], uint32_t kstep) {
+#pragma unroll
+    for (int a = 0; a < RT_PER_WAVE; a++) dst[a].load(wt[a] + kstep * (uint32_t)chunk_bytes(TYPE), lane);
   };
+  const uint32_t sh6 = 8u * (uint32_t)(c >> 1);
 
   // One K step on the staged X with the weight fragments cur.
-  auto compute = [&](int64_t sb, const WFrag<TYPE>(&cur)[RT_PER_WAVE], int buf) {
-    const f16 *xh = xh_[buf], *xl = xl_[buf], *gsh = gsh_[buf], *gsl = gsl_[buf];
+  auto compute = [&](const WFrag<TYPE>(&cur)[RT_PER_WAVE], int buf) {
+    const f16 *xh = xh_[buf], *xl = xl_[buf];
     f32x4 cm[RT_PER_WAVE][4];
-#pragma unroll
-    for (int a = 0; a < RT_PER_WAVE; a++)
-#pragma unroll
-      for (int b = 0; b < 4; b++) cm[a][b] = f32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int g = 0; g < 8; g++) {
-      f16x8 af[RT_PER_WAVE], af2[RT_PER_WAVE];
+    uint32_t scb[RT_PER_WAVE][2];
+    if constexpr (TYPE == LGMLH_Q4_K) {
 #pragma unroll
       for (int a = 0; a < RT_PER_WAVE; a++) {
-        if constexpr (TYPE == LGMLH_Q6_K)
-          cur[a].frag(g, c, af[a], af2[a]);
+        scb[a][0] = cur[a].sc03();
+        scb[a][1] = cur[a].sc47();
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+      f16x8 af[RT_PER_WAVE], af2[RT_PER_WAVE], afr[RT_PER_WAVE];
+#pragma unroll
+      for (int a = 0; a < RT_PER_WAVE; a++) {
+        if constexpr (TYPE == LGMLH_Q4_K)
+          af[a] = cur[a].frag(g, scb[a][g >> 2]);
+        else if constexpr (TYPE == LGMLH_Q6_K)
+          cur[a].frag(g, sh6, af[a], af2[a], afr[a]);
         else
           af[a] = cur[a].frag(g);
       }
 #pragma unroll
       for (int ct = 0; ct < 4; ct++) {
         const int off = (ct * 16 + r16) * X_STRIDE + g * 32 + c * 8;
-        f16x8 bh = *(const f16x8 *)(xh + off);
-        f16x8 bl;
-        if constexpr (XF32) bl = *(const f16x8 *)(xl + off);
+        const f16x8 bh = *(const f16x8 *)(xh + off);
+        const f16x8 bl = *(const f16x8 *)(xl + off);
 #pragma unroll
         for (int a = 0; a < RT_PER_WAVE; a++) {
-          cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bh, cm[a][ct], 0, 0, 0);
-          if constexpr (TYPE == LGMLH_Q6_K)
+          // the first product of a K step (of a block for Q8_0) starts from 0
+          const f32x4 c0 = (g == 0 || TYPE == LGMLH_Q8_0) ? f32x4{0, 0, 0, 0} : cm[a][ct];
+          if constexpr (TYPE == LGMLH_Q6_K) {
+            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bh, c0, 0, 0, 0);
             cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af2[a], bh, cm[a][ct], 0, 0, 0);
-          if constexpr (XF32) {
+            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afr[a], bl, cm[a][ct], 0, 0, 0);
+          } else {
+            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bh, c0, 0, 0, 0);
             cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bl, cm[a][ct], 0, 0, 0);
-            if constexpr (TYPE == LGMLH_Q6_K)
-              cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af2[a], bl, cm[a][ct], 0, 0, 0);
           }
         }
       }
       if constexpr (TYPE == LGMLH_Q8_0) {
-        // Q8_0: one scale per 32-value block: flush every group.
+        // one scale per 32-value block: flush every group
 #pragma unroll
         for (int a = 0; a < RT_PER_WAVE; a++) {
-          const uint8_t *hd = chunk_of(a, sb);
+          const u32x2 dv = *(const u32x2 *)(cur[a].hd + 8 * g);
 #pragma unroll
           for (int i = 0; i < 4; i++) {
-            float d = h2f(*(const uint16_t *)(hd + (4 * c + i) * 16 + 2 * g));
+            const float d = h2f((uint16_t)(dv[i >> 1] >> (16 * (i & 1))));
 #pragma unroll
             for (int ct = 0; ct < 4; ct++) {
               acc[a][ct][i] += d * cm[a][ct][i];
-              cm[a][ct][i] = 0.0f;
             }
           }
         }
       }
     }
     if constexpr (TYPE == LGMLH_Q4_K) {
-      // min term: sum_g m_g * S_g[n] as one 16x16x16 MFMA over the 8 groups.
+      // min term: sum_g m_g * S_g[n] as a 16x16x16 MFMA over the 8 groups
+      const f16 *gh = gh_[buf], *gl = gl_[buf];
+      f16x4 sh4[4], sl4[4];
+#pragma unroll
+      for (int ct = 0; ct < 4; ct++) {
+        sh4[ct] = f16x4{0, 0, 0, 0};
+        sl4[ct] = sh4[ct];
+        if (c < 2) {
+          sh4[ct] = *(const f16x4 *)(gh + (ct * 16 + r16) * 8 + 4 * c);
+          sl4[ct] = *(const f16x4 *)(gl + (ct * 16 + r16) * 8 + 4 * c);
+        }
+      }
 #pragma unroll
       for (int a = 0; a < RT_PER_WAVE; a++) {
-        f16x4 am = cur[a].mins(c);
-        const uint8_t *hd = chunk_of(a, sb);
+        const f16x4 am = cur[a].mins(c);
         float dd[4], dm[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          uint32_t h = *(const uint32_t *)(hd + (4 * c + i) * 16);
-          dd[i] = h2f((uint16_t)h);
-          dm[i] = h2f((uint16_t)(h >> 16));
+          dd[i] = h2f((uint16_t)cur[a].dm[i]);
+          dm[i] = h2f((uint16_t)(cur[a].dm[i] >> 16));
         }
 #pragma unroll
         for (int ct = 0; ct < 4; ct++) {
-          f16x4 sh4 = f16x4{0, 0, 0, 0}, sl4 = sh4;
-          if (c < 2) {
-            sh4 = *(const f16x4 *)(gsh + (ct * 16 + r16) * 8 + 4 * c);
-            sl4 = *(const f16x4 *)(gsl + (ct * 16 + r16) * 8 + 4 * c);
-          }
-          f32x4 mn = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sh4, f32x4{0, 0, 0, 0}, 0, 0, 0);
-          mn = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sl4, mn, 0, 0, 0);
+          f32x4 mn = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sh4[ct], f32x4{0, 0, 0, 0}, 0, 0, 0);
+          mn = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sl4[ct], mn, 0, 0, 0);
 #pragma unroll
           for (int i = 0; i < 4; i++) acc[a][ct][i] += dd[i] * cm[a][ct][i] - dm[i] * mn[i];
         }
@@ -392,41 +431,42 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const void *__
     } else if constexpr (TYPE == LGMLH_Q6_K) {
 #pragma unroll
       for (int a = 0; a < RT_PER_WAVE; a++) {
-        const uint8_t *hd = chunk_of(a, sb);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          float d = h2f(*(const uint16_t *)(hd + (4 * c + i) * 18));
+          // the fragments carry sc * q / 4
+          const float d4 = 4.0f * h2f((uint16_t)(cur[a].d4[i >> 1] >> (16 * (i & 1))));
 #pragma unroll
-          for (int ct = 0; ct < 4; ct++) acc[a][ct][i] += d * cm[a][ct][i];
+          for (int ct = 0; ct < 4; ct++) acc[a][ct][i] += d4 * cm[a][ct][i];
         }
       }
     }
   };
 
   // Step sb: the loads of sb + 1 (weights into the other register set, X
-  // pieces into xreg) go out first, compute runs on sb, then the X of sb + 1
-  // is staged into the free LDS buffer and one barrier publishes it.
+  // pieces into registers) go out first, compute runs on sb, then the X of
+  // sb + 1 is staged into the free LDS buffer and one barrier publishes it.
   WFrag<TYPE> w0[RT_PER_WAVE], w1[RT_PER_WAVE];
-  auto step = [&](int64_t sb, const WFrag<TYPE>(&cur)[RT_PER_WAVE],
-                  WFrag<TYPE>(&nxt)[RT_PER_WAVE]) {
-    const bool more = sb + 1 < sb_hi;
+  const uint32_t nsteps = (uint32_t)(sb_hi - sb_lo);
+  auto step = [&](uint32_t k, const WFrag<TYPE>(&cur)[RT_PER_WAVE],
+                  WFrag<TYPE>(&nxt)[RT_PER_WAVE], int buf) {
+    const bool more = k + 1 < nsteps;
     if (more) {
-      load_w(nxt, sb + 1);
-      load_x(sb + 1);
+      load_w(nxt, k + 1);
+      load_x(k + 1);
     }
-    compute(sb, cur, (int)((sb - sb_lo) & 1));
-    if (more) stage_x((int)((sb + 1 - sb_lo) & 1));
+    compute(cur, buf);
+    if (more) stage_x(buf ^ 1);
     __syncthreads();
   };
-  if (sb_lo < sb_hi) {
-    load_w(w0, sb_lo);
-    load_x(sb_lo);
+  if (nsteps > 0) {
+    load_w(w0, 0);
+    load_x(0);
     stage_x(0);
     __syncthreads();
   }
-  for (int64_t sb = sb_lo; sb < sb_hi; sb += 2) {
-    step(sb, w0, w1);
-    if (sb + 1 < sb_hi) step(sb + 1, w1, w0);
+  for (uint32_t k = 0; k < nsteps; k += 2) {
+    step(k, w0, w1, 0);
+    if (k + 1 < nsteps) step(k + 1, w1, w0, 1);
   }
 
   // acc[a][ct][i] = Y[n0 + ct*16 + lane%16][(rt0+a)*16 + 4*(lane/16) + i]
@@ -464,6 +504,30 @@ __global__ void splitk_reduce_kernel(const float *__restrict__ part, int splits,
   }
 }
 
+// X (f32 or f16 rows of K) -> split planes; one thread per 8 values.
+__global__ void xsplit_kernel(const void *__restrict__ x, int xtype, int64_t N, int64_t K,
+                              f16 *__restrict__ planes, int64_t Npad) {
+  const int64_t per_row = K / 8;  // a multiple of 32: groups never straddle rows
+  const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (t >= N * per_row) return;   // whole groups of 4 lanes leave together
+  const int64_t n = t / per_row, k0 = (t % per_row) * 8;
+  float v[8];
+  if (xtype == LGMLH_F32) {
+    const f32x4 *p = (const f32x4 *)((const float *)x + n * K + k0);
+    f32x4 a = p[0], b = p[1];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      v[e] = a[e];
+      v[4 + e] = b[e];
+    }
+  } else {
+    f16x8 h = *(const f16x8 *)((const f16 *)x + n * K + k0);
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = (float)h[e];
+  }
+  split_store8(planes, Npad, K, n, k0, v);
+}
+
 // ---- f32 weights: LDS-tiled VALU GEMM, sequential k order ----------------------
 __global__ void __launch_bounds__(256)
 f32gemm_kernel(const float *__restrict__ w, int64_t M, int64_t K, const float *__restrict__ x,
@@ -489,18 +553,22 @@ f32gemm_kernel(const float *__restrict__ w, int64_t M, int64_t K, const float *_
 }
 
 // K splits depend on M and K only, never on N: each output element is then
-// the same sum in the same order for any batch size.
-int splits_for(int64_t M, int64_t K, int64_t N) {
+// the same sum in the same order for any batch size. Returns the number of
+// splits actually launched (each of sb_per_split K steps, the last may be
+// shorter).
+int splits_for(int64_t M, int64_t K, int64_t N, int *sb_per_split = nullptr) {
   (void)N;
-  int64_t NSB = K / QK_K;
-  int64_t tiles = (M + WG_ROWS - 1) / WG_ROWS;
+  const int64_t NSB = K / QK_K;
+  const int64_t tiles = (M + WG_ROWS - 1) / WG_ROWS;
   // About one workgroup per CU (256) at 64 columns, at least 2 K steps per
   // split so the pipeline has a step to overlap.
   int64_t want = (256 + tiles / 2) / tiles;
-  int64_t maxs = NSB / 2 > 1 ? NSB / 2 : 1;
+  const int64_t maxs = NSB / 2 > 1 ? NSB / 2 : 1;
   if (want > maxs) want = maxs;
   if (want < 1) want = 1;
-  return (int)want;
+  const int64_t spb = (NSB + want - 1) / want;
+  if (sb_per_split) *sb_per_split = (int)spb;
+  return (int)((NSB + spb - 1) / spb);
 }
 
 // Split-K partial sums of a call (0 when K is not split).
@@ -510,26 +578,24 @@ size_t partial_bytes(int type, int64_t M, int64_t K, int64_t N) {
   return s == 1 ? 0 : (size_t)s * N * M * 4;
 }
 
+static size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
+
 size_t workspace_for(int type, int64_t M, int64_t K, int64_t N) {
-  return partial_bytes(type, M, K, N);
+  if (type == LGMLH_F32) return 0;
+  return align256(split_bytes(N, K)) + partial_bytes(type, M, K, N);
 }
 
 template <int TYPE>
-static void launch_q(const void *w, int64_t M, int64_t K, const void *x, int xtype, int64_t N,
-                     float *y, int64_t ldy, const float *res, int splits, float *part,
+static void launch_q(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t N, float *y,
+                     int64_t ldy, const float *res, int splits, float *part, bool defer,
                      hipStream_t st) {
-  int64_t NSB = K / QK_K;
-  int spb = (int)((NSB + splits - 1) / splits);
-  splits = (int)((NSB + spb - 1) / spb);
-  dim3 grid((unsigned)((N + WG_COLS - 1) / WG_COLS), (unsigned)((M + WG_ROWS - 1) / WG_ROWS),
-            (unsigned)splits);
-  if (xtype == LGMLH_F32)
-    hipLaunchKernelGGL((qgemm_kernel<TYPE, true>), grid, dim3(GEMM_THREADS), 0, st,
-                       (const uint8_t *)w, M, K, x, N, y, ldy, res, splits, spb, part);
-  else
-    hipLaunchKernelGGL((qgemm_kernel<TYPE, false>), grid, dim3(GEMM_THREADS), 0, st,
-                       (const uint8_t *)w, M, K, x, N, y, ldy, res, splits, spb, part);
-  if (splits > 1) {
+  int spb = 0;
+  splits = splits_for(M, K, N, &spb);
+  const int64_t Npad = split_npad(N);
+  dim3 grid((unsigned)(Npad / WG_COLS), (unsigned)((M + WG_ROWS - 1) / WG_ROWS), (unsigned)splits);
+  hipLaunchKernelGGL((qgemm_kernel<TYPE>), grid, dim3(GEMM_THREADS), 0, st, (const uint8_t *)w,
+                     M, K, xs, Npad, N, y, ldy, res, splits, spb, part);
+  if (splits > 1 && !defer) {
     int64_t total = N * M;
     unsigned blocks = (unsigned)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, st, part, splits, N, M,
@@ -537,45 +603,61 @@ static void launch_q(const void *w, int64_t M, int64_t K, const void *x, int xty
   }
 }
 
-// Internal entry with an output row stride (the executor writes [q|k|v]
-// and [gate|up] rows from separate weights into one buffer) and a partial-
-// sum region for split K.
-int mul_mat_ldy(int type, const void *w, int64_t M, int64_t K, const void *x, int xtype,
-                int64_t N, float *y, int64_t ldy, const float *residual, float *part,
-                size_t part_bytes, hipStream_t st) {
-  if (!w || !x || !y || M <= 0 || K <= 0 || N < 0 || ldy < M ||
-      (xtype != LGMLH_F32 && xtype != LGMLH_F16)) {
-    set_error("mul_mat: bad arguments");
+// Quantized product on split X (split.h layout for N rows of K). part holds
+// the split-K partial sums (partial_bytes). With `deferred` given, a split
+// product leaves its partials in part ([splits][N][M], added in order by
+// the consumer, which also adds the residual) and *deferred = splits;
+// otherwise the splits are reduced here (*deferred = 0).
+int mul_mat_split(int type, const void *w, int64_t M, int64_t K, const f16 *xs, int64_t N,
+                  float *y, int64_t ldy, const float *residual, float *part, size_t part_bytes,
+                  hipStream_t st, int *deferred) {
+  if (deferred) *deferred = 0;
+  if (!w || !xs || !y || M <= 0 || K <= 0 || N < 0 || ldy < M || K % QK_K) {
+    set_error("mul_mat: bad arguments (M %lld, K %lld)", (long long)M, (long long)K);
     return LGMLH_EINVAL;
   }
   if (N == 0) return LGMLH_OK;
-  if (type == LGMLH_F32) {
-    if (xtype != LGMLH_F32) {
-      set_error("mul_mat: f32 weights take f32 x");
-      return LGMLH_EINVAL;
-    }
-    dim3 grid((unsigned)((M + 15) / 16), (unsigned)((N + 15) / 16));
-    hipLaunchKernelGGL(f32gemm_kernel, grid, dim3(256), 0, st, (const float *)w, M, K,
-                       (const float *)x, N, y, ldy, residual);
-    return hip_check(hipGetLastError(), "mul_mat");
-  }
-  if (K % QK_K) {
-    set_error("mul_mat: K = %lld is not a multiple of 256", (long long)K);
-    return LGMLH_EINVAL;
-  }
   int splits = splits_for(M, K, N);
   if (splits > 1 && (!part || part_bytes < partial_bytes(type, M, K, N))) {
     set_error("mul_mat: workspace too small for %d K splits", splits);
     return LGMLH_ENOMEM;
   }
+  const bool defer = deferred && splits > 1;
   switch (type) {
-    case LGMLH_Q4_K: launch_q<LGMLH_Q4_K>(w, M, K, x, xtype, N, y, ldy, residual, splits, part, st); break;
-    case LGMLH_Q6_K: launch_q<LGMLH_Q6_K>(w, M, K, x, xtype, N, y, ldy, residual, splits, part, st); break;
-    case LGMLH_Q8_0: launch_q<LGMLH_Q8_0>(w, M, K, x, xtype, N, y, ldy, residual, splits, part, st); break;
+    case LGMLH_Q4_K: launch_q<LGMLH_Q4_K>(w, M, K, xs, N, y, ldy, residual, splits, part, defer, st); break;
+    case LGMLH_Q6_K: launch_q<LGMLH_Q6_K>(w, M, K, xs, N, y, ldy, residual, splits, part, defer, st); break;
+    case LGMLH_Q8_0: launch_q<LGMLH_Q8_0>(w, M, K, xs, N, y, ldy, residual, splits, part, defer, st); break;
     default:
       set_error("mul_mat: type %d not supported", type);
       return LGMLH_EINVAL;
   }
+  if (defer) *deferred = splits;
+  return hip_check(hipGetLastError(), "mul_mat");
+}
+
+// X -> split planes (xs holds split_bytes(N, K)).
+int split_x(const void *x, int xtype, int64_t N, int64_t K, f16 *xs, hipStream_t st) {
+  if (K % QK_K || (xtype != LGMLH_F32 && xtype != LGMLH_F16)) {
+    set_error("split: bad arguments");
+    return LGMLH_EINVAL;
+  }
+  int64_t total = N * (K / 8);
+  if (total == 0) return LGMLH_OK;
+  hipLaunchKernelGGL(xsplit_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, x,
+                     xtype, N, K, xs, split_npad(N));
+  return hip_check(hipGetLastError(), "split");
+}
+
+// f32 weights on f32 X.
+int mul_mat_f32(const float *w, int64_t M, int64_t K, const float *x, int64_t N, float *y,
+                int64_t ldy, const float *residual, hipStream_t st) {
+  if (!w || !x || !y || M <= 0 || K <= 0 || N < 0 || ldy < M) {
+    set_error("mul_mat: bad arguments");
+    return LGMLH_EINVAL;
+  }
+  if (N == 0) return LGMLH_OK;
+  dim3 grid((unsigned)((M + 15) / 16), (unsigned)((N + 15) / 16));
+  hipLaunchKernelGGL(f32gemm_kernel, grid, dim3(256), 0, st, w, M, K, x, N, y, ldy, residual);
   return hip_check(hipGetLastError(), "mul_mat");
 }
 
@@ -625,11 +707,33 @@ extern "C" int lgmlh_mul_mat(int type, const void *w, int64_t M, int64_t K, cons
     set_error("mul_mat: the add epilogue needs a residual");
     return LGMLH_EINVAL;
   }
+  if (!x || (xtype != LGMLH_F32 && xtype != LGMLH_F16)) {
+    set_error("mul_mat: x must be f32 or f16");
+    return LGMLH_EINVAL;
+  }
+  const float *res = epi == LGMLH_EPI_ADD ? residual : nullptr;
+  hipStream_t st = as_stream(stream);
+  if (type == LGMLH_F32) {
+    if (xtype != LGMLH_F32) {
+      set_error("mul_mat: f32 weights take f32 x");
+      return LGMLH_EINVAL;
+    }
+    return mul_mat_f32((const float *)w, M, K, (const float *)x, N, y, M, res, st);
+  }
+  if (K <= 0 || K % QK_K || M <= 0 || N < 0) {
+    set_error("mul_mat: bad shape (M %lld, K %lld, N %lld)", (long long)M, (long long)K,
+              (long long)N);
+    return LGMLH_EINVAL;
+  }
   size_t need = workspace_for(type, M, K, N);
-  if (need > 0 && (!workspace || ws_bytes < need)) {
+  if (!workspace || ws_bytes < need) {
     set_error("mul_mat: workspace of %zu bytes, need %zu", ws_bytes, need);
     return LGMLH_ENOMEM;
   }
-  return mul_mat_ldy(type, w, M, K, x, xtype, N, y, M, epi == LGMLH_EPI_ADD ? residual : nullptr,
-                     (float *)workspace, ws_bytes, as_stream(stream));
+  if (N == 0) return LGMLH_OK;
+  f16 *xs = (f16 *)workspace;
+  size_t xb = align256(split_bytes(N, K));
+  LGMLH_TRY(split_x(x, xtype, N, K, xs, st));
+  return mul_mat_split(type, w, M, K, xs, N, y, M, res, (float *)((char *)workspace + xb),
+                       ws_bytes - xb, st, nullptr);
 }

@@ -7,39 +7,29 @@
 
 #include "common.h"
 #include "quant.h"
+#include "split.h"
 
 namespace lgmlh {
 
-int mul_mat_ldy(int type, const void *w, int64_t M, int64_t K, const void *x, int xtype,
-                int64_t N, float *y, int64_t ldy, const float *residual, float *part,
-                size_t part_bytes, hipStream_t st);
+int mul_mat_split(int type, const void *w, int64_t M, int64_t K, const f16 *xs, int64_t N,
+                  float *y, int64_t ldy, const float *residual, float *part, size_t part_bytes,
+                  hipStream_t st, int *deferred);
+int mul_mat_f32(const float *w, int64_t M, int64_t K, const float *x, int64_t N, float *y,
+                int64_t ldy, const float *residual, hipStream_t st);
+int split_x(const void *x, int xtype, int64_t N, int64_t K, f16 *xs, hipStream_t st);
+int rms_norm_dev(float *x, const int32_t *rows, int64_t n_rows, int64_t n, float eps,
+                 const float *w, float *out, f16 *planes, hipStream_t st, Pending pend,
+                 bool writeback);
+int swiglu_dev(const float *gu, int64_t n, int64_t F, float *out, f16 *planes, hipStream_t st,
+               Pending pend);
+int qkv_rope_store_dev(float *qkv, int64_t n, int n_head, int n_head_kv, int head_dim, int n_rot,
+                       int neox, float freq_base, const float *freq_factors, const float *q_norm,
+                       const float *k_norm, float eps, const int32_t *pos, void *kpool,
+                       void *vpool, int64_t n_cells, const int64_t *cells, float *q_out,
+                       void *stream, Pending pa, Pending pb);
 size_t partial_bytes(int type, int64_t M, int64_t K, int64_t N);
 int get_rows_dev(int type, const void *table, int64_t n_cols, const int32_t *ids, int64_t n,
                  float *out, hipStream_t st);
-
-// rms_norm(x[rows[j]]) * w for the logit rows (get_rows + head norm).
-template <typename OutT>
-__global__ void rms_norm_rows_kernel(const float *__restrict__ x, const int32_t *__restrict__ rows,
-                                     int64_t n, float eps, const float *__restrict__ w,
-                                     OutT *__restrict__ out) {
-  __shared__ double part[256];
-  const float *xr = x + (int64_t)rows[blockIdx.x] * n;
-  double s = 0;
-  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) s += (double)xr[i] * (double)xr[i];
-  part[threadIdx.x] = s;
-  __syncthreads();
-  for (int o = blockDim.x / 2; o > 0; o >>= 1) {
-    if ((int)threadIdx.x < o) part[threadIdx.x] += part[threadIdx.x + o];
-    __syncthreads();
-  }
-  float mean = (float)(part[0] / (double)n);
-  float scale = 1.0f / sqrtf(mean + eps);
-  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
-    float v = xr[i] * scale;
-    if (w) v = v * w[i];
-    out[(int64_t)blockIdx.x * n + i] = (OutT)v;
-  }
-}
 
 struct Carve {
   char *p;
@@ -60,7 +50,7 @@ struct Carve {
 
 struct Sizes {
   int64_t N, E, H, Hkv, D, F, V, W, n_out;
-  size_t gemm_ws, attn_ws;
+  size_t gemm_ws, gemm_ws_v, attn_ws, split_ws;
 };
 
 static Sizes sizes_of(const lgmlh_model *m, int64_t n_tokens, int64_t n_items, int n_out) {
@@ -74,7 +64,7 @@ static Sizes sizes_of(const lgmlh_model *m, int64_t n_tokens, int64_t n_items, i
   z.V = m->n_vocab;
   z.W = (z.H + 2 * z.Hkv) * z.D;
   z.n_out = n_out;
-  size_t g = 0;
+  size_t g = 0, gv = 0;
   auto upd = [&](int t, int64_t M, int64_t K, int64_t N) {
     size_t w = partial_bytes(t, M, K, N);
     if (w > g) g = w;
@@ -82,13 +72,21 @@ static Sizes sizes_of(const lgmlh_model *m, int64_t n_tokens, int64_t n_items, i
   for (int il = 0; il < m->n_layer; il++) {
     const lgmlh_layer &L = m->layers[il];
     upd(L.wqkv_type, L.wqkv_rows, z.E, z.N);
-    if (L.wv) upd(L.wv_type, z.W - L.wqkv_rows, z.E, z.N);
+    if (L.wv) {
+      // pending beside the [q|k] partials: a region of its own
+      size_t w = partial_bytes(L.wv_type, z.W - L.wqkv_rows, z.E, z.N);
+      if (w > gv) gv = w;
+    }
     upd(L.wo_type, z.E, z.H * z.D, z.N);
     upd(L.wgu_type, 2 * z.F, z.E, z.N);
     upd(L.wdown_type, z.E, z.F, z.N);
   }
   upd(m->output_type, z.V, z.E, n_out);
   z.gemm_ws = g;
+  z.gemm_ws_v = gv;
+  int64_t kmax = z.E > z.F ? z.E : z.F;
+  if (z.H * z.D > kmax) kmax = z.H * z.D;
+  z.split_ws = split_bytes(z.N > n_out ? z.N : n_out, kmax);
   z.attn_ws = (size_t)n_items * z.Hkv * (16 * z.D + 32) * sizeof(float);
   return z;
 }
@@ -104,8 +102,10 @@ static size_t ws_bytes_of(const Sizes &z) {
   add(z.N * 2 * z.F * 4);    // [gate | up]
   add(z.N * z.F * 4);        // silu(gate) * up
   add(z.n_out * z.E * 4);    // normed logit rows
+  add(z.split_ws);           // split planes of the current product's X
   add(z.attn_ws);
   add(z.gemm_ws);
+  add(z.gemm_ws_v);
   return b + 256;
 }
 
@@ -160,73 +160,93 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
   uintptr_t base = ((uintptr_t)workspace + 255) & ~uintptr_t(255);
   Carve cv{(char *)base, ws_bytes - (size_t)(base - (uintptr_t)workspace), true};
   float *x = (float *)cv.take(z.N * z.E * 4);
-  void *xn = cv.take(z.N * z.E * 4);
+  float *xn = (float *)cv.take(z.N * z.E * 4);
   float *qkv = (float *)cv.take(z.N * z.W * 4);
   float *q = (float *)cv.take(z.N * z.H * z.D * 4);
   float *att = (float *)cv.take(z.N * z.H * z.D * 4);
   float *gu = (float *)cv.take(z.N * 2 * z.F * 4);
-  void *act = cv.take(z.N * z.F * 4);
-  void *xo = cv.take(z.n_out * z.E * 4);
+  float *act = (float *)cv.take(z.N * z.F * 4);
+  float *xo = (float *)cv.take(z.n_out * z.E * 4);
+  f16 *xs = (f16 *)cv.take(z.split_ws);
   void *aws = cv.take(z.attn_ws);
   float *gws = (float *)cv.take(z.gemm_ws);
+  float *gws_v = (float *)cv.take(z.gemm_ws_v);
   if (!cv.ok) {
     set_error("forward: workspace carve failed");
     return LGMLH_ENOMEM;
   }
   const float scale = m->attn_scale > 0 ? m->attn_scale : 1.0f / sqrtf((float)z.D);
 
-#define GEMM(...)                                  \
-  do {                                             \
-    Span sp_(trace, LGMLH_TRACE_GEMM, st);         \
-    LGMLH_TRY(mul_mat_ldy(__VA_ARGS__));           \
-  } while (0)
+  // A product on X given as f32 rows (f32 weights) or as split planes xs
+  // (quantized weights); the producer wrote the form(s) the weights take.
+  // A quantized product split over K leaves its partial sums pending (pd):
+  // the next kernel that reads y adds them in order, then the residual.
+  auto gemm = [&](int type, const void *w, int64_t M, int64_t K, const float *xf, int64_t N,
+                  float *y, int64_t ldy, const float *res, float *part, size_t part_bytes,
+                  Pending &pd) -> int {
+    Span sp(trace, LGMLH_TRACE_GEMM, st);
+    pd = Pending{};
+    if (type == LGMLH_F32) return mul_mat_f32((const float *)w, M, K, xf, N, y, ldy, res, st);
+    int splits = 0;
+    int rc = mul_mat_split(type, w, M, K, xs, N, y, ldy, res, part, part_bytes, st, &splits);
+    if (rc == LGMLH_OK && splits > 1) pd = Pending{part, splits, N, M};
+    return rc;
+  };
+  auto isq = [](int type) { return type != LGMLH_F32; };
+  Pending p_qk, p_v, p_o, p_gu, p_down;
   // token embeddings (get_rows, transformer.lua:2309); the ids were range
   // checked when the plan was made.
   LGMLH_TRY(get_rows_dev(m->tok_embd_type, m->tok_embd, z.E, ub->ids, z.N, x, st));
   for (int il = 0; il < m->n_layer; il++) {
     const lgmlh_layer &L = m->layers[il];
-    // Activations stay f32: the GEMM splits them into f16 hi + lo itself.
-    const int at = LGMLH_F32;
-    LGMLH_TRY(lgmlh_rms_norm(x, z.N, z.E, m->eps, L.attn_norm, xn, at, st));
-    GEMM(L.wqkv_type, L.wqkv, L.wqkv_rows, z.E, xn, at, z.N, qkv, z.W, nullptr,
-                          gws, z.gemm_ws, st);
-    if (L.wv) {
-      GEMM(L.wv_type, L.wv, z.W - L.wqkv_rows, z.E, xn, at, z.N,
-                            qkv + L.wqkv_rows, z.W, nullptr, gws, z.gemm_ws, st);
-    }
-    LGMLH_TRY(lgmlh_qkv_rope_store(qkv, z.N, (int)z.H, (int)z.Hkv, (int)z.D, m->n_rot,
-                                   m->rope_neox, m->rope_base, m->rope_freqs, L.q_norm, L.k_norm,
-                                   m->eps, ub->pos, L.kpool, L.vpool, m->n_cells, ub->cells, q,
-                                   st));
+    const bool v_sep = L.wv != nullptr;
+    const bool qin_q = isq(L.wqkv_type) || (v_sep && isq(L.wv_type));
+    const bool qin_f = !isq(L.wqkv_type) || (v_sep && !isq(L.wv_type));
+    // x += the previous layer's down product, then attn_norm
+    LGMLH_TRY(rms_norm_dev(x, nullptr, z.N, z.E, m->eps, L.attn_norm, qin_f ? xn : nullptr,
+                           qin_q ? xs : nullptr, st, p_down, true));
+    LGMLH_TRY(gemm(L.wqkv_type, L.wqkv, L.wqkv_rows, z.E, xn, z.N, qkv, z.W, nullptr, gws,
+                   z.gemm_ws, p_qk));
+    p_v = Pending{};
+    if (v_sep)
+      LGMLH_TRY(gemm(L.wv_type, L.wv, z.W - L.wqkv_rows, z.E, xn, z.N, qkv + L.wqkv_rows, z.W,
+                     nullptr, gws_v, z.gemm_ws_v, p_v));
+    LGMLH_TRY(qkv_rope_store_dev(qkv, z.N, (int)z.H, (int)z.Hkv, (int)z.D, m->n_rot,
+                                 m->rope_neox, m->rope_base, m->rope_freqs, L.q_norm, L.k_norm,
+                                 m->eps, ub->pos, L.kpool, L.vpool, m->n_cells, ub->cells, q, st,
+                                 p_qk, p_v));
     {
       Span sp(trace, LGMLH_TRACE_ATTN, st);
       LGMLH_TRY(lgmlh_paged_attention(q, (int)z.H, (int)z.Hkv, (int)z.D, scale, L.kpool,
                                       L.vpool, ub, att, aws, z.attn_ws, st));
     }
-    GEMM(L.wo_type, L.wo, z.E, z.H * z.D, att, LGMLH_F32, z.N, x, z.E, x, gws,
-                          z.gemm_ws, st);
-    const int ft = LGMLH_F32;
-    LGMLH_TRY(lgmlh_rms_norm(x, z.N, z.E, m->eps, L.ffn_norm, xn, ft, st));
-    GEMM(L.wgu_type, L.wgu, 2 * z.F, z.E, xn, ft, z.N, gu, 2 * z.F, nullptr,
-                          gws, z.gemm_ws, st);
-    const int dt = LGMLH_F32;
-    LGMLH_TRY(lgmlh_swiglu(gu, z.N, z.F, act, dt, st));
-    GEMM(L.wdown_type, L.wdown, z.E, z.F, act, dt, z.N, x, z.E, x, gws,
-                          z.gemm_ws, st);
+    if (isq(L.wo_type)) LGMLH_TRY(split_x(att, LGMLH_F32, z.N, z.H * z.D, xs, st));
+    LGMLH_TRY(gemm(L.wo_type, L.wo, z.E, z.H * z.D, att, z.N, x, z.E, x, gws, z.gemm_ws, p_o));
+    // x += attention out, then ffn_norm
+    LGMLH_TRY(rms_norm_dev(x, nullptr, z.N, z.E, m->eps, L.ffn_norm,
+                           isq(L.wgu_type) ? nullptr : xn, isq(L.wgu_type) ? xs : nullptr, st,
+                           p_o, true));
+    LGMLH_TRY(gemm(L.wgu_type, L.wgu, 2 * z.F, z.E, xn, z.N, gu, 2 * z.F, nullptr, gws,
+                   z.gemm_ws, p_gu));
+    LGMLH_TRY(swiglu_dev(gu, z.N, z.F, isq(L.wdown_type) ? nullptr : act,
+                         isq(L.wdown_type) ? xs : nullptr, st, p_gu));
+    LGMLH_TRY(gemm(L.wdown_type, L.wdown, z.E, z.F, act, z.N, x, z.E, x, gws, z.gemm_ws,
+                   p_down));
   }
-  // head (transformer.lua:2094-2104) on the logit rows (:2349-2350)
-  const int ot = LGMLH_F32;
+  // head (transformer.lua:2094-2104) on the logit rows (:2349-2350); the last
+  // down product is added to those rows only (x is not needed afterwards)
   if (n_out > 0) {
-    if (ot == LGMLH_F16)
-      hipLaunchKernelGGL(rms_norm_rows_kernel<f16>, dim3(n_out), dim3(256), 0, st, x, out_rows,
-                         z.E, m->eps, m->output_norm, (f16 *)xo);
+    const bool oq = isq(m->output_type);
+    LGMLH_TRY(rms_norm_dev(x, out_rows, n_out, z.E, m->eps, m->output_norm, oq ? nullptr : xo,
+                           oq ? xs : nullptr, st, p_down, false));
+    // the logits are the output: a split head product is reduced here
+    Span sp(trace, LGMLH_TRACE_GEMM, st);
+    if (oq)
+      LGMLH_TRY(mul_mat_split(m->output_type, m->output, z.V, z.E, xs, n_out, logits, z.V,
+                              nullptr, gws, z.gemm_ws, st, nullptr));
     else
-      hipLaunchKernelGGL(rms_norm_rows_kernel<float>, dim3(n_out), dim3(256), 0, st, x, out_rows,
-                         z.E, m->eps, m->output_norm, (float *)xo);
-    LGMLH_TRY(hip_check(hipGetLastError(), "forward: head norm"));
-    GEMM(m->output_type, m->output, z.V, z.E, xo, ot, n_out, logits, z.V,
-                          nullptr, gws, z.gemm_ws, st);
+      LGMLH_TRY(mul_mat_f32((const float *)m->output, z.V, z.E, xo, n_out, logits, z.V, nullptr,
+                            st));
   }
-#undef GEMM
   return LGMLH_OK;
 }

@@ -5,6 +5,7 @@
 
 #include "common.h"
 #include "quant.h"
+#include "split.h"
 
 namespace lgmlh {
 
@@ -40,29 +41,75 @@ __global__ void dequant_kernel(int type, const uint8_t *__restrict__ w, int64_t 
     out[m * K + k] = row_value(type, w + m * rb, k);
 }
 
+constexpr int RMS_THREADS = 256, RMS_PIECES = 4;  // rows of up to 8192 values
+
 // ---- rms_norm * w ----------------------------------------------------------
 // Sum of squares in f64 (as the CPU reference's ggml_float), mean rounded
-// to f32, scale = 1 / sqrtf(mean + eps), y = (x * scale) * w.
+// to f32, scale = 1 / sqrtf(mean + eps), y = (x * scale) * w. Row
+// blockIdx.x of the output is input row rows[blockIdx.x] (all rows when
+// rows is null); the result goes to out (f32 / f16) and / or to split
+// planes for a quantized product (n % 256 == 0).
 template <typename OutT>
-__global__ void rms_norm_kernel(const float *__restrict__ x, int64_t n, float eps,
-                                const float *__restrict__ w, OutT *__restrict__ out) {
-  __shared__ double part[256];
-  int64_t r = blockIdx.x;
-  const float *xr = x + r * n;
+__global__ void rms_norm_kernel(float *__restrict__ x, const int32_t *__restrict__ rows,
+                                int64_t n, float eps, const float *__restrict__ w,
+                                OutT *__restrict__ out, f16 *__restrict__ planes, int64_t npad,
+                                Pending pend, bool writeback) {
+  __shared__ double part[RMS_THREADS / 64];
+  const int tid = threadIdx.x;
+  const int64_t r = blockIdx.x;
+  const int64_t rr = rows ? (int64_t)rows[r] : r;
+  float *xr = x + rr * n;
+  // The row stays in registers: thread tid holds pieces tid + RMS_THREADS j
+  // of 8 values (n % 8 == 0 and n <= 8 * RMS_THREADS * RMS_PIECES).
+  f32x4 v[RMS_PIECES][2];
   double s = 0;
-  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) s += (double)xr[i] * (double)xr[i];
-  part[threadIdx.x] = s;
-  __syncthreads();
-  for (int o = blockDim.x / 2; o > 0; o >>= 1) {
-    if ((int)threadIdx.x < o) part[threadIdx.x] += part[threadIdx.x + o];
-    __syncthreads();
+#pragma unroll
+  for (int j = 0; j < RMS_PIECES; j++) {
+    const int64_t pc = tid + (int64_t)RMS_THREADS * j;
+    if (pc < n / 8) {
+      const f32x4 *src = (const f32x4 *)(xr + 8 * pc);
+      v[j][0] = src[0];
+      v[j][1] = src[1];
+      if (pend.splits) {
+        // x += the pending product (its split sums in order, then the residual)
+        float ps[8];
+        pend.sum8(rr, 8 * pc, ps);
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[j][e >> 2][e & 3] = ps[e] + v[j][e >> 2][e & 3];
+        if (writeback) {
+          f32x4 *dst = (f32x4 *)(xr + 8 * pc);
+          dst[0] = v[j][0];
+          dst[1] = v[j][1];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        s += (double)v[j][0][e] * (double)v[j][0][e] + (double)v[j][1][e] * (double)v[j][1][e];
+    }
   }
-  float mean = (float)(part[0] / (double)n);
-  float scale = 1.0f / sqrtf(mean + eps);
-  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
-    float v = xr[i] * scale;
-    if (w) v = v * w[i];
-    out[r * n + i] = (OutT)v;
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  if ((tid & 63) == 0) part[tid >> 6] = s;
+  __syncthreads();
+  double tot = 0;
+#pragma unroll
+  for (int i = 0; i < RMS_THREADS / 64; i++) tot += part[i];
+  const float mean = (float)(tot / (double)n);
+  const float scale = 1.0f / sqrtf(mean + eps);
+#pragma unroll
+  for (int j = 0; j < RMS_PIECES; j++) {
+    const int64_t pc = tid + (int64_t)RMS_THREADS * j;
+    if (pc < n / 8) {  // n / 8 is a multiple of 4 when planes are written
+      float y[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        y[e] = v[j][e >> 2][e & 3] * scale;
+        if (w) y[e] = y[e] * w[8 * pc + e];
+      }
+      if (out)
+#pragma unroll
+        for (int e = 0; e < 8; e++) out[r * n + 8 * pc + e] = (OutT)y[e];
+      if (planes) split_store8(planes, npad, n, r, 8 * pc, y);
+    }
   }
 }
 
@@ -84,12 +131,26 @@ __global__ void qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int 
                                       const int32_t *__restrict__ pos,
                                       uint16_t *__restrict__ kp, uint16_t *__restrict__ vp,
                                       const int64_t *__restrict__ cells,
-                                      float *__restrict__ q_out) {
+                                      float *__restrict__ q_out, Pending pa, Pending pb) {
   extern __shared__ float row[];
   int64_t t = blockIdx.x;
   int W = (H + 2 * Hkv) * D;
   const float *src = qkv + t * W;
-  for (int e = threadIdx.x; e < W; e += blockDim.x) row[e] = src[e];
+  // Columns [0, pa.cols) may come from pending partials pa, the rest from
+  // pb; pieces of 8 columns (W, pa.cols and pb.cols are multiples of 8).
+  for (int pc = threadIdx.x; pc < W / 8; pc += blockDim.x) {
+    const int e = 8 * pc;
+    float v[8];
+    if (pa.splits && e < pa.cols)
+      pa.sum8(t, e, v);
+    else if (pb.splits && e >= W - pb.cols)
+      pb.sum8(t, e - (W - pb.cols), v);
+    else
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = src[e + i];
+#pragma unroll
+    for (int i = 0; i < 8; i++) row[e + i] = v[i];
+  }
   __syncthreads();
   if (q_norm || k_norm) {
     for (int h = threadIdx.x; h < H + Hkv; h += blockDim.x) {
@@ -98,18 +159,26 @@ __global__ void qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int 
     }
     __syncthreads();
   }
-  int p = pos[t];
-  int half = n_rot / 2;
-  for (int e = threadIdx.x; e < (H + Hkv) * half; e += blockDim.x) {
-    int h = e / half, i = e % half;
-    // theta_0 = pos, theta_{i+1} = theta_i * base^(-2/n_rot), in f32.
+  // One angle per rotated pair i, shared by every head: theta_0 = pos,
+  // theta_{i+1} = theta_i * base^(-2/n_rot) (a running f32 product, as the
+  // CPU reference's rope cache), divided by the frequency factor.
+  const int p = pos[t];
+  const int half = n_rot / 2;
+  float *cs_ = row + W, *sn_ = cs_ + half;
+  for (int i = threadIdx.x; i < half; i += blockDim.x) {
     float theta = (float)p;
     for (int j = 0; j < i; j++) theta *= theta_scale;
-    float tt = theta / (ff ? ff[i] : 1.0f);
-    double cs = (double)cosf(tt), sn = (double)sinf(tt);
+    const float tt = theta / (ff ? ff[i] : 1.0f);
+    cs_[i] = cosf(tt);
+    sn_[i] = sinf(tt);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < (H + Hkv) * half; e += blockDim.x) {
+    const int h = e / half, i = e % half;
+    const double cs = (double)cs_[i], sn = (double)sn_[i];
     float *v = row + h * D;
-    int a = neox ? i : 2 * i, b = neox ? i + half : 2 * i + 1;
-    double x0 = v[a], x1 = v[b];
+    const int a = neox ? i : 2 * i, b = neox ? i + half : 2 * i + 1;
+    const double x0 = v[a], x1 = v[b];
     v[a] = (float)(x0 * cs - x1 * sn);
     v[b] = (float)(x0 * sn + x1 * cs);
   }
@@ -127,47 +196,99 @@ __global__ void qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int 
 // ---- swiglu: silu(g) * u, in f64 --------------------------------------------
 template <typename OutT>
 __global__ void swiglu_kernel(const float *__restrict__ gu, int64_t n, int64_t F,
-                              OutT *__restrict__ out) {
+                              OutT *__restrict__ out, Pending pend) {
   int64_t total = n * F;
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * blockDim.x) {
     int64_t r = e / F, c = e % F;
-    double g = gu[r * 2 * F + c], u = gu[r * 2 * F + F + c];
+    double g = pend.splits ? pend.sum(r, c) : gu[r * 2 * F + c];
+    double u = pend.splits ? pend.sum(r, F + c) : gu[r * 2 * F + F + c];
     out[e] = (OutT)(float)(g / (1.0 + exp(-g)) * u);
   }
 }
 
-// ---- argmax: first index of the maximum --------------------------------------
-__global__ void argmax_kernel(const float *__restrict__ x, int64_t n, int32_t *__restrict__ out) {
-  __shared__ float bv[256];
-  __shared__ int64_t bi[256];
-  int64_t r = blockIdx.x;
-  const float *xr = x + r * n;
-  float best = -INFINITY;
-  int64_t idx = -1;
-  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
-    float v = xr[i];
-    if (idx < 0 || v > best) {
-      best = v;
-      idx = i;
+// The same values into split planes (F % 256 == 0); one thread per 8.
+__global__ void swiglu_split_kernel(const float *__restrict__ gu, int64_t n, int64_t F,
+                                    f16 *__restrict__ planes, int64_t npad, Pending pend) {
+  const int64_t per_row = F / 8;
+  const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (t >= n * per_row) return;  // whole 4-lane groups leave together
+  const int64_t r = t / per_row, c0 = (t % per_row) * 8;
+  float g8[8], u8[8], v[8];
+  if (pend.splits) {
+    pend.sum8(r, c0, g8);
+    pend.sum8(r, F + c0, u8);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      g8[e] = gu[r * 2 * F + c0 + e];
+      u8[e] = gu[r * 2 * F + F + c0 + e];
     }
   }
-  bv[threadIdx.x] = best;
-  bi[threadIdx.x] = idx;
-  __syncthreads();
-  for (int o = blockDim.x / 2; o > 0; o >>= 1) {
-    if ((int)threadIdx.x < o) {
-      float v2 = bv[threadIdx.x + o];
-      int64_t i2 = bi[threadIdx.x + o];
-      if (i2 >= 0 && (bi[threadIdx.x] < 0 || v2 > bv[threadIdx.x] ||
-                      (v2 == bv[threadIdx.x] && i2 < bi[threadIdx.x]))) {
-        bv[threadIdx.x] = v2;
-        bi[threadIdx.x] = i2;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    double g = g8[e], u = u8[e];
+    v[e] = (float)(g / (1.0 + exp(-g)) * u);
+  }
+  split_store8(planes, npad, F, r, c0, v);
+}
+
+// ---- argmax: first index of the maximum --------------------------------------
+// First index of the row maximum (strict >, src/sample.c:914-925). Each
+// thread scans its strided slice (float4 loads when rows are 16-byte
+// aligned), then the candidates meet in a fixed-order tree that keeps the
+// smaller index on ties.
+constexpr int ARGMAX_THREADS = 1024;
+__device__ __forceinline__ void amax_take(float &bv, int64_t &bi, float v, int64_t i) {
+  if (i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi))) {
+    bv = v;
+    bi = i;
+  }
+}
+__global__ void __launch_bounds__(ARGMAX_THREADS)
+argmax_kernel(const float *__restrict__ x, int64_t n, int32_t *__restrict__ out) {
+  __shared__ float sv[ARGMAX_THREADS / 64];
+  __shared__ int64_t si[ARGMAX_THREADS / 64];
+  const int tid = threadIdx.x;
+  const int64_t r = blockIdx.x;
+  const float *xr = x + r * n;
+  float best = 0.0f;
+  int64_t idx = -1;
+  if ((n & 3) == 0 && (((uintptr_t)x) & 15) == 0) {
+    for (int64_t q = tid; q < n / 4; q += ARGMAX_THREADS) {
+      const f32x4 v = ((const f32x4 *)xr)[q];
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        if (idx < 0 || v[e] > best) {
+          best = v[e];
+          idx = 4 * q + e;
+        }
+    }
+  } else {
+    for (int64_t i = tid; i < n; i += ARGMAX_THREADS) {
+      const float v = xr[i];
+      if (idx < 0 || v > best) {
+        best = v;
+        idx = i;
       }
     }
-    __syncthreads();
   }
-  if (threadIdx.x == 0) out[r] = (int32_t)bi[0];
+  for (int o = 1; o < 64; o <<= 1) {
+    const float v2 = __shfl_xor(best, o);
+    const int64_t i2 = __shfl_xor(idx, o);
+    amax_take(best, idx, v2, i2);
+  }
+  if ((tid & 63) == 0) {
+    sv[tid >> 6] = best;
+    si[tid >> 6] = idx;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float b = sv[0];
+    int64_t bi = si[0];
+    for (int k = 1; k < ARGMAX_THREADS / 64; k++) amax_take(b, bi, sv[k], si[k]);
+    out[r] = (int32_t)bi;
+  }
 }
 
 int get_rows_dev(int type, const void *table, int64_t n_cols, const int32_t *ids, int64_t n,
@@ -181,6 +302,45 @@ int get_rows_dev(int type, const void *table, int64_t n_cols, const int32_t *ids
   hipLaunchKernelGGL(get_rows_kernel, dim3((unsigned)n), dim3(256), 0, st, type,
                      (const uint8_t *)table, rb, n_cols, ids, out);
   return hip_check(hipGetLastError(), "get_rows");
+}
+
+
+// rms_norm of n_rows rows (input rows[j] when rows is given) into f32 out
+// and / or split planes (planes sized for n_rows rows).
+// pend: a pending product added to x first (written back to x when
+// writeback; never with rows, which may repeat).
+int rms_norm_dev(float *x, const int32_t *rows, int64_t n_rows, int64_t n, float eps,
+                 const float *w, float *out, f16 *planes, hipStream_t st, Pending pend,
+                 bool writeback) {
+  if (n_rows == 0) return LGMLH_OK;
+  if ((planes && n % 256) || n % 8 || n > 8 * RMS_THREADS * RMS_PIECES) {
+    set_error("rms_norm: bad row length %lld", (long long)n);
+    return LGMLH_EINVAL;
+  }
+  hipLaunchKernelGGL(rms_norm_kernel<float>, dim3((unsigned)n_rows), dim3(RMS_THREADS), 0, st, x, rows,
+                     n, eps, w, out, planes, split_npad(n_rows), pend, writeback && !rows);
+  return hip_check(hipGetLastError(), "rms_norm");
+}
+
+// silu(g) * u into f32 out and / or split planes.
+int swiglu_dev(const float *gu, int64_t n, int64_t F, float *out, f16 *planes, hipStream_t st,
+               Pending pend) {
+  if (n == 0) return LGMLH_OK;
+  if (out) {
+    int64_t total = n * F;
+    unsigned blocks = (unsigned)((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
+    hipLaunchKernelGGL(swiglu_kernel<float>, dim3(blocks), dim3(256), 0, st, gu, n, F, out, pend);
+  }
+  if (planes) {
+    if (F % 256) {
+      set_error("swiglu: split output needs F %% 256 == 0 (F = %lld)", (long long)F);
+      return LGMLH_EINVAL;
+    }
+    int64_t total = n * (F / 8);
+    hipLaunchKernelGGL(swiglu_split_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       st, gu, n, F, planes, split_npad(n), pend);
+  }
+  return hip_check(hipGetLastError(), "swiglu");
 }
 
 }  // namespace lgmlh
@@ -229,19 +389,53 @@ extern "C" int lgmlh_dequantize(int type, const void *src, int64_t M, int64_t K,
 
 extern "C" int lgmlh_rms_norm(const float *x, int64_t n_rows, int64_t n, float eps,
                               const float *w, void *out, int out_type, void *stream) {
-  if (!x || !out || n <= 0 || n_rows < 0 || (out_type != LGMLH_F32 && out_type != LGMLH_F16)) {
-    set_error("rms_norm: bad arguments");
+  if (!x || !out || n <= 0 || n_rows < 0 || n % 8 || n > 8 * RMS_THREADS * RMS_PIECES ||
+      (out_type != LGMLH_F32 && out_type != LGMLH_F16)) {
+    set_error("rms_norm: bad arguments (n must be a multiple of 8, at most %d)",
+              8 * RMS_THREADS * RMS_PIECES);
     return LGMLH_EINVAL;
   }
   if (n_rows == 0) return LGMLH_OK;
   if (out_type == LGMLH_F32)
-    hipLaunchKernelGGL(rms_norm_kernel<float>, dim3((unsigned)n_rows), dim3(256), 0,
-                       as_stream(stream), x, n, eps, w, (float *)out);
+    hipLaunchKernelGGL(rms_norm_kernel<float>, dim3((unsigned)n_rows), dim3(RMS_THREADS), 0,
+                       as_stream(stream), (float *)x, nullptr, n, eps, w, (float *)out, nullptr, 0,
+                       Pending{}, false);
   else
-    hipLaunchKernelGGL(rms_norm_kernel<f16>, dim3((unsigned)n_rows), dim3(256), 0,
-                       as_stream(stream), x, n, eps, w, (f16 *)out);
+    hipLaunchKernelGGL(rms_norm_kernel<f16>, dim3((unsigned)n_rows), dim3(RMS_THREADS), 0,
+                       as_stream(stream), (float *)x, nullptr, n, eps, w, (f16 *)out, nullptr, 0,
+                       Pending{}, false);
   return hip_check(hipGetLastError(), "rms_norm");
 }
+
+namespace lgmlh {
+int qkv_rope_store_dev(float *qkv, int64_t n, int n_head, int n_head_kv,
+                                    int head_dim, int n_rot, int neox, float freq_base,
+                                    const float *freq_factors, const float *q_norm,
+                                    const float *k_norm, float eps, const int32_t *pos,
+                                    void *kpool, void *vpool, int64_t n_cells,
+                                    const int64_t *cells, float *q_out, void *stream, Pending pa,
+                       Pending pb) {
+  if (!qkv || !pos || !kpool || !vpool || !cells || !q_out || n < 0 || n_head <= 0 ||
+      n_head_kv <= 0 || head_dim <= 0 || head_dim % 8 || n_rot <= 0 || n_rot > head_dim ||
+      n_rot % 2 || n_cells % KV_BLOCK || pa.cols % 8 || pb.cols % 8) {
+    set_error("qkv_rope_store: bad arguments");
+    return LGMLH_EINVAL;
+  }
+  if (n == 0) return LGMLH_OK;
+  // base^(-2/n_rot) rounded to f32 on the host, as the CPU reference does.
+  float theta_scale = powf(freq_base, -2.0f / (float)n_rot);
+  size_t lds = ((size_t)(n_head + 2 * n_head_kv) * head_dim + n_rot) * sizeof(float);
+  if (lds > 160 * 1024) {
+    set_error("qkv_rope_store: row too wide");
+    return LGMLH_EINVAL;
+  }
+  hipLaunchKernelGGL(qkv_rope_store_kernel, dim3((unsigned)n), dim3(512), lds,
+                     as_stream(stream), qkv, n_head, n_head_kv, head_dim, n_rot, neox,
+                     theta_scale, freq_factors, q_norm, k_norm, eps, pos, (uint16_t *)kpool,
+                     (uint16_t *)vpool, cells, q_out, pa, pb);
+  return hip_check(hipGetLastError(), "qkv_rope_store");
+}
+}  // namespace lgmlh
 
 extern "C" int lgmlh_qkv_rope_store(float *qkv, int64_t n, int n_head, int n_head_kv,
                                     int head_dim, int n_rot, int neox, float freq_base,
@@ -249,25 +443,9 @@ extern "C" int lgmlh_qkv_rope_store(float *qkv, int64_t n, int n_head, int n_hea
                                     const float *k_norm, float eps, const int32_t *pos,
                                     void *kpool, void *vpool, int64_t n_cells,
                                     const int64_t *cells, float *q_out, void *stream) {
-  if (!qkv || !pos || !kpool || !vpool || !cells || !q_out || n < 0 || n_head <= 0 ||
-      n_head_kv <= 0 || head_dim <= 0 || n_rot <= 0 || n_rot > head_dim || n_rot % 2 ||
-      n_cells % KV_BLOCK) {
-    set_error("qkv_rope_store: bad arguments");
-    return LGMLH_EINVAL;
-  }
-  if (n == 0) return LGMLH_OK;
-  // base^(-2/n_rot) rounded to f32 on the host, as the CPU reference does.
-  float theta_scale = powf(freq_base, -2.0f / (float)n_rot);
-  size_t lds = (size_t)(n_head + 2 * n_head_kv) * head_dim * sizeof(float);
-  if (lds > 160 * 1024) {
-    set_error("qkv_rope_store: row too wide");
-    return LGMLH_EINVAL;
-  }
-  hipLaunchKernelGGL(qkv_rope_store_kernel, dim3((unsigned)n), dim3(256), lds,
-                     as_stream(stream), qkv, n_head, n_head_kv, head_dim, n_rot, neox,
-                     theta_scale, freq_factors, q_norm, k_norm, eps, pos, (uint16_t *)kpool,
-                     (uint16_t *)vpool, cells, q_out);
-  return hip_check(hipGetLastError(), "qkv_rope_store");
+  return qkv_rope_store_dev(qkv, n, n_head, n_head_kv, head_dim, n_rot, neox, freq_base,
+                            freq_factors, q_norm, k_norm, eps, pos, kpool, vpool, n_cells, cells,
+                            q_out, stream, Pending{}, Pending{});
 }
 
 extern "C" int lgmlh_swiglu(const float *gu, int64_t n, int64_t F, void *out, int out_type,
@@ -281,10 +459,10 @@ extern "C" int lgmlh_swiglu(const float *gu, int64_t n, int64_t F, void *out, in
   unsigned blocks = (unsigned)((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
   if (out_type == LGMLH_F32)
     hipLaunchKernelGGL(swiglu_kernel<float>, dim3(blocks), dim3(256), 0, as_stream(stream), gu,
-                       n, F, (float *)out);
+                       n, F, (float *)out, Pending{});
   else
     hipLaunchKernelGGL(swiglu_kernel<f16>, dim3(blocks), dim3(256), 0, as_stream(stream), gu, n,
-                       F, (f16 *)out);
+                       F, (f16 *)out, Pending{});
   return hip_check(hipGetLastError(), "swiglu");
 }
 
@@ -295,7 +473,7 @@ extern "C" int lgmlh_argmax(const float *x, int64_t n_rows, int64_t n_cols, int3
     return LGMLH_EINVAL;
   }
   if (n_rows == 0) return LGMLH_OK;
-  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)n_rows), dim3(256), 0, as_stream(stream), x,
+  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)n_rows), dim3(ARGMAX_THREADS), 0, as_stream(stream), x,
                      n_cols, out);
   return hip_check(hipGetLastError(), "argmax");
 }
