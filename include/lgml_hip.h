@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define LGMLH_ABI_VERSION 1
+#define LGMLH_ABI_VERSION 2
 
 enum {
 	LGMLH_OK = 0,
@@ -153,11 +153,13 @@ typedef struct {
 	const int32_t *block_tab;  /* [n_seq * max_blocks] */
 	const int32_t *logit_rows; /* [n_seq] off + n - 1 (batch_inputs :2540-2545) */
 	const int32_t *items;      /* [n_items * 4] attention work items */
-	const int32_t *merge;      /* [n_merge * 4] split-merge items */
+	const int32_t *merge;      /* [n_merge * 4] split-merge groups */
 } lgmlh_ubatch;
 
 /* Plan a pass. G = n_head / n_head_kv; blocks_per_split bounds the KV
- * blocks one work item reads (0 = choose). With buf NULL only info is
+ * blocks one work item reads (0 = the default, 16). The work list depends
+ * only on each sequence's own length, so a sequence is computed the same
+ * way alone or in any batch. With buf NULL only info is
  * filled (sizes); otherwise buf must hold info->bytes. Errors:
  * LGMLH_ERANGE when a block id that a position needs is outside
  * [0, pool_blocks) (the fill_blocks "position ... is in no column" error,

@@ -11,9 +11,16 @@
 // f32 (each lane owns one row; reductions over 4 lanes with shuffles), and
 // O^T += V^T P^T (V columns straight from the transposed [D][cell] tile, P
 // through 4.6 KB of LDS). K and V are exact f16; Q and P enter the MFMAs as
-// f16 hi + lo pairs, so every product is f32-accurate. Splits of one token group are merged in a fixed
-// order by lgmlh_merge_kernel, so results are deterministic and the same
-// for a sequence alone or in any batch.
+// f16 hi + lo pairs, so every product is f32-accurate. The loads of block
+// b + 1 are issued as soon as block b's registers are consumed (K after
+// S, V after O), so they overlap block b's softmax and products.
+//
+// The splits of a token group are merged by merge_kernel in a fixed order,
+// so results are deterministic and, since the split points depend only on
+// the sequence's own length, the same for a sequence alone or in any batch.
+// (Merging inside the attention kernel by the last split to arrive needs a
+// device-scope release per split, an L2 write-back on this multi-XCD part,
+// which costs more than the second launch.)
 #include <math.h>
 
 #include "common.h"
@@ -49,6 +56,7 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
   constexpr int DT = D / 16;   // d tiles of the output
   __shared__ __align__(16) uint16_t plh[ROWS * P_STRIDE];  // P as f16 hi
   __shared__ __align__(16) uint16_t pll[ROWS * P_STRIDE];  // and lo
+  __shared__ __align__(16) f16x8 qsh[KS * 64], qsl[KS * 64];  // Q fragments, hi and lo
 
   const int lane = threadIdx.x;
   const int item = blockIdx.x;
@@ -56,8 +64,8 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
   const int G = H / Hkv;
   const int s = items[4 * item + 0];
   const int tok0 = items[4 * item + 1];
-  const int ntok = items[4 * item + 2] & 0xffff;
-  const bool direct = (items[4 * item + 2] >> 16) & 1;
+  const int ntok = items[4 * item + 2] & 31;
+  const int mg = (items[4 * item + 2] >> 5) - 1;  // merge group, -1: one split
   const int blo = items[4 * item + 3] & 0xffff;
   const int bhi = (items[4 * item + 3] >> 16) & 0xffff;
 
@@ -70,8 +78,8 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
   const int p_row = p_first + rtok;  // last visible position of the row
 
   // Q fragments (B operand): Q[row][ks*32 + quad*8 .. +7] as f16 hi + lo
-  // (q = hi + lo to 22 bits; K is exact f16, so S^T is f32-accurate).
-  f16x8 qh[KS], ql[KS];
+  // (q = hi + lo to 22 bits; K is exact f16, so S^T is f32-accurate). Kept
+  // in LDS to leave registers for the next block's tiles.
   {
     const float *qr = q + ((int64_t)(tok0 + rtok) * H + rhead) * D;
 #pragma unroll
@@ -88,8 +96,8 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
           lo[4 + e] = (f16)(b[e] - (float)h[4 + e]);
         }
       }
-      qh[ks] = h;
-      ql[ks] = lo;
+      qsh[ks * 64 + lane] = h;
+      qsl[ks * 64 + lane] = lo;
     }
   }
 
@@ -99,19 +107,32 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
   float m = -INFINITY, l = 0.0f;
 
   const int32_t *bt = block_tab + (int64_t)s * max_blocks;
-  for (int blk = blo; blk < bhi; blk++) {
-    const int64_t bid = bt[blk];
-    const uint16_t *kt = kpool + (bid * Hkv + kvh) * (int64_t)(64 * D);
-    const uint16_t *vt = vpool + (bid * Hkv + kvh) * (int64_t)(64 * D);
-
-    // V^T fragments (A operand of O^T += V^T P^T), issued early.
-    f16x8 vf[DT][2];
+  auto ktile = [&](int blk) { return kpool + ((int64_t)bt[blk] * Hkv + kvh) * (int64_t)(64 * D); };
+  auto vtile = [&](int blk) { return vpool + ((int64_t)bt[blk] * Hkv + kvh) * (int64_t)(64 * D); };
+  // K rows (A operand of S^T = K Q^T) and V^T columns (A operand of
+  // O^T += V^T P^T) of one block, straight from the pool tiles.
+  f16x8 kf[4][KS], vf[DT][2];
+  auto load_k = [&](const uint16_t *kt) {
+#pragma unroll
+    for (int ct = 0; ct < 4; ct++)
+#pragma unroll
+      for (int ks = 0; ks < KS; ks++) kf[ct][ks] = load_f16x8(kt + (ct * 16 + row) * D + ks * 32 + quad * 8);
+  };
+  auto load_v = [&](const uint16_t *vt) {
 #pragma unroll
     for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-      for (int kc = 0; kc < 2; kc++)
-        vf[dt][kc] = load_f16x8(vt + (dt * 16 + row) * 64 + kc * 32 + quad * 8);
-
+      for (int kc = 0; kc < 2; kc++) vf[dt][kc] = load_f16x8(vt + (dt * 16 + row) * 64 + kc * 32 + quad * 8);
+  };
+  if (blo < bhi) {
+    load_k(ktile(blo));
+    load_v(vtile(blo));
+  }
+  for (int blk = blo; blk < bhi; blk++) {
+    // The next block's tiles are loaded unconditionally (the last block
+    // reloads its own, still in L2): straight-line code keeps the load
+    // counter waits exact, so the O products do not wait for the next K.
+    const int nxt = blk + 1 < bhi ? blk + 1 : blk;
     // S^T[cell][row] for 4 tiles of 16 cells.
     f32x4 st[4];
 #pragma unroll
@@ -119,22 +140,25 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
       f32x4 acc = f32x4{0, 0, 0, 0};
 #pragma unroll
       for (int ks = 0; ks < KS; ks++) {
-        f16x8 kf = load_f16x8(kt + (ct * 16 + row) * D + ks * 32 + quad * 8);
-        acc = mfma16(kf, qh[ks], acc);
-        acc = mfma16(kf, ql[ks], acc);
+        acc = mfma16(kf[ct][ks], qsh[ks * 64 + lane], acc);
+        acc = mfma16(kf[ct][ks], qsl[ks * 64 + lane], acc);
       }
       st[ct] = acc;
     }
+    load_k(ktile(nxt));
 
-    // Mask and row max: lane holds cells ct*16 + quad*4 + i of its row.
+    // Mask and row max: lane holds cells ct*16 + quad*4 + i of its row. A
+    // block that ends at or before the group's first position is visible to
+    // every valid row.
     const int cbase = blk * 64;
+    const bool full = cbase + 63 <= p_first;
     float mx = -INFINITY;
 #pragma unroll
     for (int ct = 0; ct < 4; ct++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        int p = cbase + ct * 16 + quad * 4 + i;
-        float v = (rvalid && p <= p_row) ? st[ct][i] * scale_log2 : -INFINITY;
+        const int p = cbase + ct * 16 + quad * 4 + i;
+        const float v = (rvalid && (full || p <= p_row)) ? st[ct][i] * scale_log2 : -INFINITY;
         st[ct][i] = v;
         mx = fmaxf(mx, v);
       }
@@ -142,33 +166,40 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_new = fmaxf(m, mx);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = exp2f(m - m_use);  // 0 when m is -inf
     float rs = 0.0f;
 #pragma unroll
     for (int ct = 0; ct < 4; ct++) {
       uint16_t ph[4], pq[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        float pv = exp2f(st[ct][i] - m_use);
+        const float pv = __builtin_amdgcn_exp2f(st[ct][i] - m_use);  // exp2(-inf) = 0
         rs += pv;
-        f16 hv = (f16)pv;
+        const f16 hv = (f16)pv;
         ph[i] = __builtin_bit_cast(uint16_t, hv);
         pq[i] = f2h(pv - (float)hv);
       }
-      u32x2 wh = u32x2{(uint32_t)ph[0] | ((uint32_t)ph[1] << 16),
-                       (uint32_t)ph[2] | ((uint32_t)ph[3] << 16)};
-      u32x2 wl = u32x2{(uint32_t)pq[0] | ((uint32_t)pq[1] << 16),
-                       (uint32_t)pq[2] | ((uint32_t)pq[3] << 16)};
+      const u32x2 wh = u32x2{(uint32_t)ph[0] | ((uint32_t)ph[1] << 16),
+                             (uint32_t)ph[2] | ((uint32_t)ph[3] << 16)};
+      const u32x2 wl = u32x2{(uint32_t)pq[0] | ((uint32_t)pq[1] << 16),
+                             (uint32_t)pq[2] | ((uint32_t)pq[3] << 16)};
       *(u32x2 *)(plh + row * P_STRIDE + ct * 16 + quad * 4) = wh;
       *(u32x2 *)(pll + row * P_STRIDE + ct * 16 + quad * 4) = wl;
     }
     rs += __shfl_xor(rs, 16);
     rs += __shfl_xor(rs, 32);
-    l = l * alpha + rs;
-    m = m_new;
+    // rescale only when some row's maximum moved
+    if (__builtin_amdgcn_ballot_w64(m_new != m)) {
+      const float alpha = __builtin_amdgcn_exp2f(m - m_use);  // 0 when m is -inf
+      l *= alpha;
 #pragma unroll
-    for (int dt = 0; dt < DT; dt++) o[dt] *= alpha;
-    __syncthreads();  // one wave per workgroup: orders the P writes before the reads
+      for (int dt = 0; dt < DT; dt++) o[dt] *= alpha;
+    }
+    l += rs;
+    m = m_new;
+    // The workgroup is one wave and a wave's LDS operations complete in
+    // order: a compiler barrier orders the P writes before the reads (an
+    // s_barrier would also wait for the next block's loads).
+    __asm__ volatile("" ::: "memory");
     f16x8 pfh[2], pfl[2];
 #pragma unroll
     for (int kc = 0; kc < 2; kc++) {
@@ -182,19 +213,24 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
         o[dt] = mfma16(vf[dt][kc], pfh[kc], o[dt]);
         o[dt] = mfma16(vf[dt][kc], pfl[kc], o[dt]);
       }
-    __syncthreads();  // P reads done before the next block's writes
+    load_v(vtile(nxt));
+    __asm__ volatile("" ::: "memory");  // the P reads before the next block's writes
   }
 
   // Lane holds O^T[d = dt*16 + quad*4 + i][row].
-  if (direct) {
+  if (mg < 0) {
     if (rvalid) {
       const float inv = 1.0f / l;
       float *orow = out + ((int64_t)(tok0 + rtok) * H + rhead) * D;
 #pragma unroll
       for (int dt = 0; dt < DT; dt++) *(f32x4 *)(orow + dt * 16 + quad * 4) = o[dt] * inv;
     }
-  } else {
-    float *pp = part + ((int64_t)item * Hkv + kvh) * Partial<D>::floats;
+    return;
+  }
+  // A split: its partial state, rows in use only.
+  const int nrows = ntok * G;
+  float *pp = part + ((int64_t)item * Hkv + kvh) * Partial<D>::floats;
+  if (row < nrows) {
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) *(f32x4 *)(pp + row * D + dt * 16 + quad * 4) = o[dt];
     if (quad == 0) {
@@ -204,33 +240,56 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
   }
 }
 
-// Fixed-order merge of the splits of one token group (merge item:
-// first item, split count, first token, token count).
+// Fixed-order merge of the splits of one token group (merge group: first
+// item, splits, first token, tokens), one wave per (group, KV head). Lane
+// r < rows finds its row's max M, the split weights w = exp2(m - M) and
+// L = sum l w; then every lane adds the split outputs of 4 columns at a
+// time, weighted, in split order.
 template <int D>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(64)
 merge_kernel(const int32_t *__restrict__ merge, int H, int Hkv, const float *__restrict__ part,
              float *__restrict__ out) {
-  const int mi = blockIdx.x, kvh = blockIdx.y;
-  const int first = merge[4 * mi + 0], ns = merge[4 * mi + 1];
-  const int tok0 = merge[4 * mi + 2], ntok = merge[4 * mi + 3];
-  const int G = H / Hkv;
-  for (int e = threadIdx.x; e < ROWS * D; e += blockDim.x) {
-    int row = e / D, d = e % D;
-    int rtok = row / G;
-    if (rtok >= ntok) continue;
+  constexpr int WMAX = 64;  // splits whose weights are kept in LDS
+  __shared__ float wsh[WMAX * ROWS], lsh[2 * ROWS];
+  const int lane = threadIdx.x, mg = blockIdx.x, kvh = blockIdx.y;
+  const int first = merge[4 * mg + 0], ns = merge[4 * mg + 1];
+  const int tok0 = merge[4 * mg + 2], ntok = merge[4 * mg + 3];
+  const int G = H / Hkv, nrows = ntok * G;
+  const float *p0 = part + ((int64_t)first * Hkv + kvh) * Partial<D>::floats;
+  const int64_t pstride = (int64_t)Hkv * Partial<D>::floats;  // from one split to the next
+  if (lane < nrows) {
     float M = -INFINITY;
+    for (int sp = 0; sp < ns; sp++) M = fmaxf(M, p0[sp * pstride + ROWS * D + lane]);
+    float L = 0.0f;
     for (int sp = 0; sp < ns; sp++) {
-      const float *pp = part + ((int64_t)(first + sp) * Hkv + kvh) * Partial<D>::floats;
-      M = fmaxf(M, pp[ROWS * D + row]);
+      const float w = exp2f(p0[sp * pstride + ROWS * D + lane] - M);  // 0 for a split that saw no cell
+      L += p0[sp * pstride + ROWS * D + ROWS + lane] * w;
+      if (sp < WMAX) wsh[sp * ROWS + lane] = w;
     }
-    float L = 0.0f, acc = 0.0f;
-    for (int sp = 0; sp < ns; sp++) {
-      const float *pp = part + ((int64_t)(first + sp) * Hkv + kvh) * Partial<D>::floats;
-      float w = exp2f(pp[ROWS * D + row] - M);  // 0 for a split that saw no cell
-      L += pp[ROWS * D + ROWS + row] * w;
-      acc += pp[row * D + d] * w;
+    lsh[lane] = L;
+    lsh[ROWS + lane] = M;
+  }
+  __syncthreads();
+  for (int e4 = lane; e4 < nrows * (D / 4); e4 += 64) {
+    const int r = e4 / (D / 4), d0 = 4 * (e4 % (D / 4));
+    f32x4 acc = f32x4{0, 0, 0, 0};
+    int sp = 0;
+    for (; sp + 4 <= ns && sp + 4 <= WMAX; sp += 4) {
+      const f32x4 a0 = *(const f32x4 *)(p0 + sp * pstride + r * D + d0);
+      const f32x4 a1 = *(const f32x4 *)(p0 + (sp + 1) * pstride + r * D + d0);
+      const f32x4 a2 = *(const f32x4 *)(p0 + (sp + 2) * pstride + r * D + d0);
+      const f32x4 a3 = *(const f32x4 *)(p0 + (sp + 3) * pstride + r * D + d0);
+      acc += a0 * wsh[sp * ROWS + r];
+      acc += a1 * wsh[(sp + 1) * ROWS + r];
+      acc += a2 * wsh[(sp + 2) * ROWS + r];
+      acc += a3 * wsh[(sp + 3) * ROWS + r];
     }
-    out[((int64_t)(tok0 + rtok) * H + kvh * G + row % G) * D + d] = acc / L;
+    for (; sp < ns; sp++) {
+      const float w = sp < WMAX ? wsh[sp * ROWS + r]
+                                : exp2f(p0[sp * pstride + ROWS * D + r] - lsh[ROWS + r]);
+      acc += *(const f32x4 *)(p0 + sp * pstride + r * D + d0) * w;
+    }
+    *(f32x4 *)(out + ((int64_t)(tok0 + r / G) * H + kvh * G + r % G) * D + d0) = acc / lsh[r];
   }
 }
 
@@ -251,7 +310,7 @@ static void launch_attn(const float *q, int H, int Hkv, float scale_log2, const 
                      scale_log2, (const uint16_t *)kp, (const uint16_t *)vp, ub->items,
                      ub->seq_off, ub->seq_npast, ub->block_tab, ub->max_blocks, out, part);
   if (ub->n_merge > 0)
-    hipLaunchKernelGGL(merge_kernel<D>, dim3(ub->n_merge, Hkv), dim3(256), 0, st, ub->merge, H,
+    hipLaunchKernelGGL(merge_kernel<D>, dim3(ub->n_merge, Hkv), dim3(64), 0, st, ub->merge, H,
                        Hkv, part, out);
 }
 

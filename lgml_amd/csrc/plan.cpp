@@ -61,12 +61,10 @@ extern "C" int lgmlh_plan(int n_seq, const int32_t *seq_n, const int32_t *seq_np
     set_error("plan: too many tokens");
     return LGMLH_EINVAL;
   }
-  int bps = blocks_per_split;
-  if (bps == 0) {
-    // About 4096 waves in flight over the KV heads, at least 2 blocks each.
-    int64_t want = (total_blocks * n_head_kv + 4095) / 4096;
-    bps = (int)(want < 2 ? 2 : want > 64 ? 64 : want);
-  }
+  (void)total_blocks;
+  // A fixed default: the split points of a sequence must not depend on the
+  // rest of the batch (a sequence gives the same bits alone or batched).
+  const int bps = blocks_per_split ? blocks_per_split : 16;
   std::vector<int32_t> items, merge;
   for (int s = 0, off = 0; s < n_seq; off += seq_n[s], s++) {
     for (int g0 = 0; g0 < seq_n[s]; g0 += T) {
@@ -74,11 +72,12 @@ extern "C" int lgmlh_plan(int n_seq, const int32_t *seq_n, const int32_t *seq_np
       int nbg = (int)(((int64_t)seq_npast[s] + ge - 1) / B + 1);
       int ns = (nbg + bps - 1) / bps;
       int first = (int)(items.size() / 4);
+      int mg = ns > 1 ? (int)(merge.size() / 4) + 1 : 0;
       for (int j = 0; j < ns; j++) {
         int lo = j * bps, hi = (j + 1) * bps < nbg ? (j + 1) * bps : nbg;
         items.push_back(s);
         items.push_back(off + g0);
-        items.push_back((ge - g0) | (ns == 1 ? 1 << 16 : 0));
+        items.push_back((ge - g0) | (mg << 5));
         items.push_back(lo | (hi << 16));
       }
       if (ns > 1) {

@@ -35,7 +35,7 @@ def test_exports_every_declared_symbol(hip):
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing
     assert sorted(hip.SYMBOLS) == names
-    assert L.lgmlh_abi_version() == 1
+    assert L.lgmlh_abi_version() == 2
 
 
 def test_sizes(hip):
@@ -102,8 +102,11 @@ def test_plan_packs_like_fill_batch(hip):
     items = arr(buf, info.off_items, 4 * info.n_items, np.int32).reshape(-1, 4)
     # every (token group, block) pair up to the group's last position is covered once
     seen = {}
+    groups = {}
     for s, tok0, nt, blk in items:
         lo, hi = blk & 0xffff, blk >> 16
+        groups.setdefault((int(s), int(tok0)), set()).add(int(nt) >> 5)
+        assert 1 <= (nt & 31) <= 16 // 4
         key = (int(s), int(tok0))
         seen.setdefault(key, []).append((lo, hi))
         assert hi - lo <= 2
@@ -111,6 +114,15 @@ def test_plan_packs_like_fill_batch(hip):
         runs.sort()
         assert runs[0][0] == 0 and all(runs[i][1] == runs[i + 1][0] for i in range(len(runs) - 1))
     assert info.n_merge == sum(1 for r in seen.values() if len(r) > 1)
+    # one merge group per split token group (numbered from 1), 0 for one split
+    mg = arr(buf, info.off_merge, 4 * info.n_merge, np.int32).reshape(-1, 4)
+    for key, runs in seen.items():
+        (g,) = groups[key]
+        if len(runs) == 1:
+            assert g == 0
+        else:
+            first, ns, tok0, nt = mg[g - 1]
+            assert ns == len(runs) and tok0 == key[1]
 
 
 def test_plan_errors(hip):
