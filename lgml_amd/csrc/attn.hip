@@ -220,10 +220,11 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
   // Lane holds O^T[d = dt*16 + quad*4 + i][row].
   if (mg < 0) {
     if (rvalid) {
-      const float inv = 1.0f / l;
+      // o / l, as the merge divides: a token's output does not depend on
+      // whether its group was split (the grouping follows chunk boundaries)
       float *orow = out + ((int64_t)(tok0 + rtok) * H + rhead) * D;
 #pragma unroll
-      for (int dt = 0; dt < DT; dt++) *(f32x4 *)(orow + dt * 16 + quad * 4) = o[dt] * inv;
+      for (int dt = 0; dt < DT; dt++) *(f32x4 *)(orow + dt * 16 + quad * 4) = o[dt] / l;
     }
     return;
   }

@@ -32,7 +32,10 @@ constexpr int GEMM_THREADS = GEMM_WAVES * 64;
 constexpr int RT_PER_WAVE = 2;     // 16-row tiles per wave
 constexpr int WG_ROWS = GEMM_WAVES * RT_PER_WAVE * 16;  // 256
 constexpr int WG_COLS = 64;        // N columns per workgroup (4 tiles)
-constexpr int X_STRIDE = 264;      // f16 per LDS row of X (256 + pad)
+// X in LDS: per plane 64 rows x 32 pieces of 8 f16 (16 B), piece kp of row n
+// at slot n * 32 + (kp ^ (n & 15)) (no padding: global-to-LDS loads write
+// 64 consecutive slots; the swizzle keeps a 16-row B read conflict-free).
+constexpr int X_SLOTS = WG_COLS * 32;
 
 // Bytes of one repacked chunk (16 rows x 256 values).
 __host__ __device__ constexpr int chunk_bytes(int type) {
@@ -270,10 +273,10 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
              int64_t Npad, int64_t N, float *__restrict__ y, int64_t ldy,
              const float *__restrict__ residual, int splits, int sb_per_split,
              float *__restrict__ part) {
-  __shared__ __align__(16) f16 xh_[2][WG_COLS * X_STRIDE];
-  __shared__ __align__(16) f16 xl_[2][WG_COLS * X_STRIDE];
-  __shared__ __align__(16) f16 gh_[2][WG_COLS * 8];  // group sums, hi
-  __shared__ __align__(16) f16 gl_[2][WG_COLS * 8];  // group sums, lo
+  __shared__ __align__(16) u32x4 xh_[2][X_SLOTS];
+  __shared__ __align__(16) u32x4 xl_[2][X_SLOTS];
+  __shared__ __align__(16) u32x4 gh_[2][WG_COLS];  // group sums, hi: 8 f16 per row
+  __shared__ __align__(16) u32x4 gl_[2][WG_COLS];  // group sums, lo
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int64_t NSB = K / QK_K;
@@ -291,38 +294,34 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
 #pragma unroll
     for (int b = 0; b < 4; b++) acc[a][b] = f32x4{0, 0, 0, 0};
 
-  // Staging: the 64 x 256 slice of each plane is 2048 pieces of 8 f16;
-  // thread tid moves pieces tid + 512 j (row i / 32, piece i % 32), so a
-  // wave reads two contiguous 512-byte row segments per load. Offsets are
-  // 32-bit element offsets from the wave-uniform plane bases.
-  constexpr int XP = WG_COLS * 32 / GEMM_THREADS;  // 4
+  // Staging: global-to-LDS loads (no registers). Per plane and step, wave
+  // w fills slots [256 w, 256 w + 256) with 4 loads of 64 slots; lane l of
+  // load j writes slot s = 256 w + 64 j + l, which holds piece
+  // kp = (s % 32) ^ (row & 15) of row s / 32.
+  typedef __attribute__((address_space(3))) void lds_t;
+  constexpr int XJ = X_SLOTS / (GEMM_WAVES * 64);  // 4
   const f16 *xhi = xs + n0 * K + sb_lo * QK_K, *xlo = xhi + Npad * K;
   const f16 *ghi = xs + 2 * Npad * K + n0 * (K / 32) + sb_lo * 8, *glo = ghi + Npad * (K / 32);
-  const uint32_t xoff = (uint32_t)((tid >> 5) * K + (tid & 31) * 8);
-  const uint32_t xrow16 = (uint32_t)(16 * K);
-  const uint32_t goff = (uint32_t)((tid & 63) * (K / 32));
-  u32x4 xrh[XP], xrl[XP], xrg;
-  auto load_x = [&](uint32_t kstep) {  // kstep = sb - sb_lo
-    const uint32_t o = xoff + kstep * QK_K;
+  uint32_t xoff[XJ];
 #pragma unroll
-    for (int j = 0; j < XP; j++) {
-      xrh[j] = *(const u32x4 *)(xhi + (o + j * xrow16));
-      xrl[j] = *(const u32x4 *)(xlo + (o + j * xrow16));
+  for (int j = 0; j < XJ; j++) {
+    const int sl = (wave * XJ + j) * 64 + lane, n = sl >> 5, kp = (sl & 31) ^ (n & 15);
+    xoff[j] = (uint32_t)(n * K + kp * 8);
+  }
+  auto load_x = [&](uint32_t kstep, int buf) {  // kstep = sb - sb_lo
+#pragma unroll
+    for (int j = 0; j < XJ; j++) {
+      const int slot0 = (wave * XJ + j) * 64;
+      __builtin_amdgcn_global_load_lds((const void *)(xhi + xoff[j] + kstep * QK_K),
+                                       (lds_t *)&xh_[buf][slot0], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void *)(xlo + xoff[j] + kstep * QK_K),
+                                       (lds_t *)&xl_[buf][slot0], 16, 0, 0);
     }
     if constexpr (TYPE == LGMLH_Q4_K) {
-      if (tid < 2 * WG_COLS) xrg = *(const u32x4 *)((tid < WG_COLS ? ghi : glo) + (goff + kstep * 8));
-    }
-  };
-  auto stage_x = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < XP; j++) {
-      const int i = tid + GEMM_THREADS * j;
-      const int o = (i >> 5) * X_STRIDE + (i & 31) * 8;
-      *(u32x4 *)(xh_[buf] + o) = xrh[j];
-      *(u32x4 *)(xl_[buf] + o) = xrl[j];
-    }
-    if constexpr (TYPE == LGMLH_Q4_K) {
-      if (tid < 2 * WG_COLS) *(u32x4 *)((tid < WG_COLS ? gh_[buf] : gl_[buf]) + (tid & 63) * 8) = xrg;
+      if (wave < 2)  // wave 0: hi sums, wave 1: lo sums; lane = row
+        __builtin_amdgcn_global_load_lds(
+            (const void *)((wave == 0 ? ghi : glo) + (uint32_t)lane * (uint32_t)(K / 32) + kstep * 8),
+            (lds_t *)(wave == 0 ? &gh_[buf][0] : &gl_[buf][0]), 16, 0, 0);
     }
   };
   // Chunk of tile a at K step sb_lo + kstep: a wave-uniform address (rows
@@ -339,9 +338,12 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   };
   const uint32_t sh6 = 8u * (uint32_t)(c >> 1);
 
-  // One K step on the staged X with the weight fragments cur.
+  // One K step on the staged X with the weight fragments cur. The B
+  // fragments of group g + 1 are read while group g multiplies; within a
+  // group the products with hi go before those with lo, so no MFMA waits
+  // for the one just issued.
   auto compute = [&](const WFrag<TYPE>(&cur)[RT_PER_WAVE], int buf) {
-    const f16 *xh = xh_[buf], *xl = xl_[buf];
+    const u32x4 *xh = xh_[buf], *xl = xl_[buf];
     f32x4 cm[RT_PER_WAVE][4];
     uint32_t scb[RT_PER_WAVE][2];
     if constexpr (TYPE == LGMLH_Q4_K) {
@@ -351,8 +353,20 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
         scb[a][1] = cur[a].sc47();
       }
     }
+    f16x8 bh[2][4], bl[2][4];
+    auto read_b = [&](int g, int d) {
+      const int slot = r16 * 32 + ((4 * g + c) ^ r16);
+#pragma unroll
+      for (int ct = 0; ct < 4; ct++) {
+        bh[d][ct] = __builtin_bit_cast(f16x8, xh[ct * 16 * 32 + slot]);
+        bl[d][ct] = __builtin_bit_cast(f16x8, xl[ct * 16 * 32 + slot]);
+      }
+    };
+    read_b(0, 0);
 #pragma unroll
     for (int g = 0; g < 8; g++) {
+      const int d = g & 1;
+      if (g < 7) read_b(g + 1, d ^ 1);
       f16x8 af[RT_PER_WAVE], af2[RT_PER_WAVE], afr[RT_PER_WAVE];
 #pragma unroll
       for (int a = 0; a < RT_PER_WAVE; a++) {
@@ -363,25 +377,27 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
         else
           af[a] = cur[a].frag(g);
       }
+      // the first product of a K step (of a block for Q8_0) starts from 0
 #pragma unroll
-      for (int ct = 0; ct < 4; ct++) {
-        const int off = (ct * 16 + r16) * X_STRIDE + g * 32 + c * 8;
-        const f16x8 bh = *(const f16x8 *)(xh + off);
-        const f16x8 bl = *(const f16x8 *)(xl + off);
+      for (int a = 0; a < RT_PER_WAVE; a++)
 #pragma unroll
-        for (int a = 0; a < RT_PER_WAVE; a++) {
-          // the first product of a K step (of a block for Q8_0) starts from 0
+        for (int ct = 0; ct < 4; ct++) {
           const f32x4 c0 = (g == 0 || TYPE == LGMLH_Q8_0) ? f32x4{0, 0, 0, 0} : cm[a][ct];
-          if constexpr (TYPE == LGMLH_Q6_K) {
-            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bh, c0, 0, 0, 0);
-            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af2[a], bh, cm[a][ct], 0, 0, 0);
-            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afr[a], bl, cm[a][ct], 0, 0, 0);
-          } else {
-            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bh, c0, 0, 0, 0);
-            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bl, cm[a][ct], 0, 0, 0);
-          }
+          cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bh[d][ct], c0, 0, 0, 0);
         }
+      if constexpr (TYPE == LGMLH_Q6_K) {
+#pragma unroll
+        for (int a = 0; a < RT_PER_WAVE; a++)
+#pragma unroll
+          for (int ct = 0; ct < 4; ct++)
+            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af2[a], bh[d][ct], cm[a][ct], 0, 0, 0);
       }
+#pragma unroll
+      for (int a = 0; a < RT_PER_WAVE; a++)
+#pragma unroll
+        for (int ct = 0; ct < 4; ct++)
+          cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(TYPE == LGMLH_Q6_K ? afr[a] : af[a],
+                                                              bl[d][ct], cm[a][ct], 0, 0, 0);
       if constexpr (TYPE == LGMLH_Q8_0) {
         // one scale per 32-value block: flush every group
 #pragma unroll
@@ -400,7 +416,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
     }
     if constexpr (TYPE == LGMLH_Q4_K) {
       // min term: sum_g m_g * S_g[n] as a 16x16x16 MFMA over the 8 groups
-      const f16 *gh = gh_[buf], *gl = gl_[buf];
+      const f16 *gh = (const f16 *)gh_[buf], *gl = (const f16 *)gl_[buf];
       f16x4 sh4[4], sl4[4];
 #pragma unroll
       for (int ct = 0; ct < 4; ct++) {
@@ -443,25 +459,26 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   };
 
   // Step sb: the loads of sb + 1 (weights into the other register set, X
-  // pieces into registers) go out first, compute runs on sb, then the X of
-  // sb + 1 is staged into the free LDS buffer and one barrier publishes it.
+  // straight into the other LDS buffer) go out first, compute runs on sb,
+  // then one barrier publishes the new X.
   WFrag<TYPE> w0[RT_PER_WAVE], w1[RT_PER_WAVE];
   const uint32_t nsteps = (uint32_t)(sb_hi - sb_lo);
+  // The next step's loads go out unconditionally (the last step reloads
+  // its own chunk and X, still in L2): straight-line code keeps the load
+  // counter waits exact, so compute never waits for the next step's data.
   auto step = [&](uint32_t k, const WFrag<TYPE>(&cur)[RT_PER_WAVE],
                   WFrag<TYPE>(&nxt)[RT_PER_WAVE], int buf) {
-    const bool more = k + 1 < nsteps;
-    if (more) {
-      load_w(nxt, k + 1);
-      load_x(k + 1);
-    }
+    const uint32_t kn = k + 1 < nsteps ? k + 1 : k;
+    load_w(nxt, kn);
+    load_x(kn, buf ^ 1);
     compute(cur, buf);
-    if (more) stage_x(buf ^ 1);
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's X loads have landed in LDS
+    __syncthreads();                // ... and everyone's; buffer buf is free again
   };
   if (nsteps > 0) {
     load_w(w0, 0);
-    load_x(0);
-    stage_x(0);
+    load_x(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
   for (uint32_t k = 0; k < nsteps; k += 2) {

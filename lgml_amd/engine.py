@@ -11,6 +11,13 @@ arrival order first, and an entry that gets no block fails alone with
 "kv pool full". Prompts go in chunks of at most ubatch tokens
 (E:prefill_batched, :2213-2255, ubatch 512, :57). Greedy sampling is the
 first maximum (src/sample.c:914-925) on the device.
+
+With prefix_cache, a request attaches the cached blocks of its prompt
+before its first pass (E:attach / E:cached_blocks / E:attach_blocks,
+engine.lua:2010-2077): the full blocks whose chained keys it finds are
+shared, the best partial match is copied into a block of its own, and only
+the rest of the prompt runs. Full prompt blocks get keys as their prefill
+completes (E:publish, :1829-1841), so later requests can share them.
 """
 import ctypes as C
 
@@ -135,12 +142,18 @@ class Request:
         return [self.out[-1]]
 
 
+ROOT_KEY = "lgml:"  # E:root_key (engine.lua:1823-1825) without adapters
+
+
 class Engine:
     """Slots over one pool; step() runs one batched pass (E:flush)."""
 
-    def __init__(self, model, n_slots, ubatch=UBATCH, blocks_per_split=0, trace=None):
+    def __init__(self, model, n_slots, ubatch=UBATCH, blocks_per_split=0, trace=None,
+                 prefix_cache=False):
         self.model = model
         self.seqs = PoolSeqs(model)
+        self.prefix_cache = prefix_cache
+        self.hits = self.hit_blocks = 0
         self.n_slots = n_slots
         self.ubatch = ubatch
         self.bps = blocks_per_split
@@ -148,6 +161,7 @@ class Engine:
         self.trace = trace
         self.passes = self.rows = self.tokens = 0
         self.last_plan = None
+        self.last_logits = None
         self._ids = torch.empty(0, dtype=torch.int32, device="cuda")
 
     def submit(self, req):
@@ -155,7 +169,68 @@ class Engine:
             raise RuntimeError("no free slot")
         req.seq = Seq(self.seqs, req.prio)
         self.active.append(req)
+        if self.prefix_cache:
+            req.fed = self.attach(req)
+            req.seq.n_past = req.fed
         return req
+
+    # -- prefix sharing ------------------------------------------------------
+    def cached_blocks(self, prompt, max_, prio):
+        """E:cached_blocks (engine.lua:1873-1892): the cached blocks holding the
+        first full blocks of prompt (at most max_ tokens), each referenced."""
+        alloc, blocks, keys, parent = self.seqs.alloc, [], [], ROOT_KEY
+        while (len(blocks) + 1) * BLOCK <= max_:
+            k = kvpool.key(parent, prompt, len(blocks) * BLOCK + 1, BLOCK)
+            b = alloc.lookup(k)
+            if b is None:
+                break
+            alloc.ref(b, prio)
+            blocks.append(b)
+            keys.append(k)
+            parent = k
+        return blocks, keys
+
+    def attach(self, req):
+        """E:attach_blocks (engine.lua:2038-2077) for a new request: returns
+        the number of prompt tokens already in the cache."""
+        prompt, c, alloc = req.prompt, req.seq, self.seqs.alloc
+        max_ = len(prompt) - 1  # at least one prompt token must run
+        blocks, keys = self.cached_blocks(prompt, max_, c.prio)
+        try:
+            m = len(blocks) * BLOCK
+            kid, part = alloc.longest_kid(keys[-1] if keys else ROOT_KEY, prompt, m + 1,
+                                          min(BLOCK - 1, max_ - m))
+            if m + part <= 0:
+                return 0
+            self.seqs.share(c, blocks, keys)
+            if part > 0:
+                alloc.ref(kid)  # hold it while the copy takes a new block
+                try:
+                    self.seqs.reserve(c, m + part)
+                    self.seqs.copy_block(kid, c.blocks[len(blocks)], part)
+                    c.n_past = m + part
+                except PoolFull:
+                    part = 0
+                    c.n_past = m
+                alloc.unref(kid)
+            self.hits += 1
+            self.hit_blocks += len(blocks)
+            return m + part
+        finally:
+            for b in blocks:  # E:drop_held
+                alloc.unref(b)
+
+    def publish(self, req):
+        """E:publish (engine.lua:1829-1841): keys for the full prompt blocks
+        of the request that have none yet."""
+        c, alloc = req.seq, self.seqs.alloc
+        upto = min(c.n_past, len(req.prompt)) // BLOCK
+        for i in range(len(c.keys) + 1, upto + 1):
+            parent = c.keys[i - 2] if i >= 2 else ROOT_KEY
+            k = kvpool.key(parent, req.prompt, (i - 1) * BLOCK + 1, BLOCK)
+            c.keys.append(k)
+            alloc.publish(c.blocks[i - 1], k, parent, i,
+                          req.prompt[(i - 1) * BLOCK:i * BLOCK], c.prio)
 
     def finish(self, req):
         self.seqs.free(req.seq)
@@ -186,7 +261,9 @@ class Engine:
         ids = np.concatenate([np.asarray(x, np.int32) for _, x in entries])
         plan = self.model.plan(seq_n, npast, bt, ids, self.bps)
         self.last_plan = plan
+        self.last_entries = [r for r, _ in entries]
         logits = self.model.forward(plan, trace=self.trace)
+        self.last_logits = logits
         if self._ids.numel() < len(entries):
             self._ids = torch.empty(len(entries), dtype=torch.int32, device="cuda")
         check(hip.lib().lgmlh_argmax(logits.data_ptr(), len(entries), self.model.hp["n_vocab"],
@@ -200,6 +277,8 @@ class Engine:
             r.seq.n_past += len(x)
             if r.fed < len(r.prompt):
                 r.fed += len(x)
+                if self.prefix_cache:
+                    self.publish(r)
                 if r.fed < len(r.prompt):
                     continue  # mid-prompt chunk: its logits are not sampled
             r.out.append(int(tok))
