@@ -342,9 +342,25 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   // fragments of group g + 1 are read while group g multiplies; within a
   // group the products with hi go before those with lo, so no MFMA waits
   // for the one just issued.
-  auto compute = [&](const WFrag<TYPE>(&cur)[RT_PER_WAVE], int buf) {
+  auto compute = [&](const WFrag<TYPE>(&cur)[RT_PER_WAVE], int buf, auto &&after_lds) {
     const u32x4 *xh = xh_[buf], *xl = xl_[buf];
     f32x4 cm[RT_PER_WAVE][4];
+    // The group sums are read first: every LDS read of the step must be
+    // issued before the next step's global-to-LDS loads (after_lds), or the
+    // compiler, unable to tell the buffers apart, waits for those loads.
+    f16x4 sh4[4], sl4[4];
+    if constexpr (TYPE == LGMLH_Q4_K) {
+      const f16 *gh = (const f16 *)gh_[buf], *gl = (const f16 *)gl_[buf];
+#pragma unroll
+      for (int ct = 0; ct < 4; ct++) {
+        sh4[ct] = f16x4{0, 0, 0, 0};
+        sl4[ct] = sh4[ct];
+        if (c < 2) {
+          sh4[ct] = *(const f16x4 *)(gh + (ct * 16 + r16) * 8 + 4 * c);
+          sl4[ct] = *(const f16x4 *)(gl + (ct * 16 + r16) * 8 + 4 * c);
+        }
+      }
+    }
     uint32_t scb[RT_PER_WAVE][2];
     if constexpr (TYPE == LGMLH_Q4_K) {
 #pragma unroll
@@ -353,20 +369,23 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
         scb[a][1] = cur[a].sc47();
       }
     }
-    f16x8 bh[2][4], bl[2][4];
-    auto read_b = [&](int g, int d) {
+    // B fragments: a group's hi (lo) fragments are read right after the
+    // previous group's products with hi (lo) are issued.
+    f16x8 bh[4], bl[4];
+    auto read_bh = [&](int g) {
       const int slot = r16 * 32 + ((4 * g + c) ^ r16);
 #pragma unroll
-      for (int ct = 0; ct < 4; ct++) {
-        bh[d][ct] = __builtin_bit_cast(f16x8, xh[ct * 16 * 32 + slot]);
-        bl[d][ct] = __builtin_bit_cast(f16x8, xl[ct * 16 * 32 + slot]);
-      }
+      for (int ct = 0; ct < 4; ct++) bh[ct] = __builtin_bit_cast(f16x8, xh[ct * 16 * 32 + slot]);
     };
-    read_b(0, 0);
+    auto read_bl = [&](int g) {
+      const int slot = r16 * 32 + ((4 * g + c) ^ r16);
+#pragma unroll
+      for (int ct = 0; ct < 4; ct++) bl[ct] = __builtin_bit_cast(f16x8, xl[ct * 16 * 32 + slot]);
+    };
+    read_bh(0);
+    read_bl(0);
 #pragma unroll
     for (int g = 0; g < 8; g++) {
-      const int d = g & 1;
-      if (g < 7) read_b(g + 1, d ^ 1);
       f16x8 af[RT_PER_WAVE], af2[RT_PER_WAVE], afr[RT_PER_WAVE];
 #pragma unroll
       for (int a = 0; a < RT_PER_WAVE; a++) {
@@ -383,21 +402,24 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
 #pragma unroll
         for (int ct = 0; ct < 4; ct++) {
           const f32x4 c0 = (g == 0 || TYPE == LGMLH_Q8_0) ? f32x4{0, 0, 0, 0} : cm[a][ct];
-          cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bh[d][ct], c0, 0, 0, 0);
+          cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bh[ct], c0, 0, 0, 0);
         }
       if constexpr (TYPE == LGMLH_Q6_K) {
 #pragma unroll
         for (int a = 0; a < RT_PER_WAVE; a++)
 #pragma unroll
           for (int ct = 0; ct < 4; ct++)
-            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af2[a], bh[d][ct], cm[a][ct], 0, 0, 0);
+            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af2[a], bh[ct], cm[a][ct], 0, 0, 0);
       }
+      if (g < 7) read_bh(g + 1);
 #pragma unroll
       for (int a = 0; a < RT_PER_WAVE; a++)
 #pragma unroll
         for (int ct = 0; ct < 4; ct++)
           cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(TYPE == LGMLH_Q6_K ? afr[a] : af[a],
-                                                              bl[d][ct], cm[a][ct], 0, 0, 0);
+                                                              bl[ct], cm[a][ct], 0, 0, 0);
+      if (g < 7) read_bl(g + 1);
+      if (g == 6) after_lds();  // the last LDS reads of the step are out
       if constexpr (TYPE == LGMLH_Q8_0) {
         // one scale per 32-value block: flush every group
 #pragma unroll
@@ -416,17 +438,6 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
     }
     if constexpr (TYPE == LGMLH_Q4_K) {
       // min term: sum_g m_g * S_g[n] as a 16x16x16 MFMA over the 8 groups
-      const f16 *gh = (const f16 *)gh_[buf], *gl = (const f16 *)gl_[buf];
-      f16x4 sh4[4], sl4[4];
-#pragma unroll
-      for (int ct = 0; ct < 4; ct++) {
-        sh4[ct] = f16x4{0, 0, 0, 0};
-        sl4[ct] = sh4[ct];
-        if (c < 2) {
-          sh4[ct] = *(const f16x4 *)(gh + (ct * 16 + r16) * 8 + 4 * c);
-          sl4[ct] = *(const f16x4 *)(gl + (ct * 16 + r16) * 8 + 4 * c);
-        }
-      }
 #pragma unroll
       for (int a = 0; a < RT_PER_WAVE; a++) {
         const f16x4 am = cur[a].mins(c);
@@ -470,8 +481,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
                   WFrag<TYPE>(&nxt)[RT_PER_WAVE], int buf) {
     const uint32_t kn = k + 1 < nsteps ? k + 1 : k;
     load_w(nxt, kn);
-    load_x(kn, buf ^ 1);
-    compute(cur, buf);
+    compute(cur, buf, [&] { load_x(kn, buf ^ 1); });
     __builtin_amdgcn_s_waitcnt(0);  // this wave's X loads have landed in LDS
     __syncthreads();                // ... and everyone's; buffer buf is free again
   };
