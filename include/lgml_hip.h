@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define LGMLH_ABI_VERSION 2
+#define LGMLH_ABI_VERSION 3
 
 enum {
 	LGMLH_OK = 0,
@@ -218,6 +218,50 @@ int lgmlh_mul_mat(int type, const void *w, int64_t M, int64_t K, const void *x, 
     void *stream);
 
 /* ===================================================================== *
+ * Routed experts (qwen3moe): the router of M.moe (transformer.lua:
+ * 1989-2027) and graph:mul_mat_id (src/ops_nn.c:322-362) with the weighted
+ * sum of the picks (experts / sum_picks, transformer.lua:1875-1910).
+ * ===================================================================== */
+/* Expert gating functions, as gguf expert_gating_func numbers
+ * (transformer.lua:32-35). */
+enum { LGMLH_GATING_SOFTMAX = 1, LGMLH_GATING_SIGMOID = 2 };
+
+/* The router tail of M.moe (transformer.lua:1998-2008): for each row of
+ * logits (n, n_expert) f32, probs = soft_max (or sigmoid); ids (n, n_used)
+ * = the n_used largest, largest first (g:argsort_top_k,
+ * src/ops_nn.c:266-286), ties to the smaller index, chosen on the logits
+ * (the gating is monotone); weights (n, n_used) = probs[ids]
+ * (get_rows), divided by max(sum, 6.103515625e-5) when norm_topk, then
+ * times scale (expert_scale). n_expert <= 512, n_used <= 16,
+ * n * n_used <= 8192. */
+int lgmlh_moe_route(const float *logits, int64_t n, int n_expert, int n_used, int gating,
+    int norm_topk, float scale, int32_t *ids, float *weights, void *stream);
+
+/* Workspace of lgmlh_mul_mat_id (the grouping of the picks by expert and,
+ * for quantized weights, the split X). Its contents need no
+ * initialisation. */
+size_t lgmlh_mul_mat_id_workspace(int type, int64_t n_expert, int64_t M, int64_t K, int64_t T,
+    int64_t U, int n_used);
+/* graph:mul_mat_id (src/ops_nn.c:322-362): w holds n_expert matrices
+ * (M, K) of `type`, each repacked (lgmlh_repack) and stored one after the
+ * other, lgmlh_repacked_bytes(type, M, K) apart (f32: M * K floats
+ * apart); x (T, U, K) f32 (or f16 for quantized w); ids (T, n_used) i32
+ * on the device; row (t, j) of y (T, n_used, M) f32 = w[ids[t, j]] times
+ * x[t, j % U]. U is 1 or n_used. Each expert's rows are read once per
+ * 16 (or 64) of its picks; an expert nobody picked costs nothing. ids
+ * outside [0, n_expert) give rows of zeros (the reference asserts).
+ * n_expert <= 512, T * n_used <= 8192. */
+int lgmlh_mul_mat_id(int type, const void *w, int64_t n_expert, int64_t M, int64_t K,
+    const void *x, int xtype, int64_t U, const int32_t *ids, int64_t T, int n_used, float *y,
+    void *workspace, size_t ws_bytes, void *stream);
+/* The tail of experts / sum_picks (transformer.lua:1888,1894-1910) and the
+ * residual add of ffn (:2079): out[t] = y[t, 0] w[t, 0] + y[t, 1] w[t, 1]
+ * + ... (+ residual[t]), products and sums in pick order. y (T, n_used, M),
+ * weights (T, n_used); residual may be NULL or alias out. */
+int lgmlh_moe_sum(const float *y, const float *weights, int64_t T, int n_used, int64_t M,
+    const float *residual, float *out, void *stream);
+
+/* ===================================================================== *
  * Dense-layer ops around the hot ops (transformer.lua:1754-1789,
  * 1859-1872, 2042-2104).
  * ===================================================================== */
@@ -249,7 +293,7 @@ int lgmlh_gen_normal(uint64_t seed, int type, int64_t rows, int64_t cols, double
     void *out, void *stream);
 
 /* ===================================================================== *
- * One forward pass of a dense llama / qwen3 model over a planned ubatch:
+ * One forward pass of a llama / qwen3 / qwen3moe model over a planned ubatch:
  * transformer.lua forward (:2285-2365) with the batched attention of
  * attention_batch (:2389-2416), for every sequence of the pass at once.
  * Weights are device pointers: quantized matrices repacked, f32 in place.
@@ -262,6 +306,14 @@ typedef struct {
 	int64_t wqkv_rows;       /* rows of wqkv: (H + 2 Hkv) D, or (H + Hkv) D */
 	const void *wqkv, *wv, *wo, *wgu, *wdown; /* wv NULL when inside wqkv */
 	void *kpool, *vpool;     /* this layer's pool tensors */
+	/* Routed experts (transformer.lua:2054-2068), used when gate_inp is set
+	 * (wgu / wdown are then unused): the router (n_expert, n_embd) f32;
+	 * exp_gu n_expert matrices [gate | up] (2 n_ff_exp, n_embd) and
+	 * exp_down n_expert matrices (n_embd, n_ff_exp), as lgmlh_mul_mat_id
+	 * takes them. */
+	const float *gate_inp;
+	int exp_gu_type, exp_down_type;
+	const void *exp_gu, *exp_down;
 } lgmlh_layer;
 
 typedef struct {
@@ -274,6 +326,10 @@ typedef struct {
 	const float *output_norm;
 	int64_t n_cells;                  /* pool cells per layer */
 	const lgmlh_layer *layers;        /* host array of n_layer */
+	/* MoE (transformer.lua:160-170): experts, picks per token, expert FFN
+	 * width, LGMLH_GATING_*, norm_topk, expert_scale. */
+	int n_expert, n_used, n_ff_exp, gating, norm_topk;
+	float expert_scale;
 } lgmlh_model;
 
 /* Workspace bytes of lgmlh_forward for a plan and n_out logit rows. Its

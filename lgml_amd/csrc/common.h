@@ -29,12 +29,20 @@ inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s);
 // Split-K partial sums of a product not yet reduced: part[z][n][m] for
 // z < splits, n < rows, m < cols (cols = the product's M). The consumer
 // adds them in order z = 0, 1, ... (then the residual, if any).
+// With wts set, the terms are the expert outputs of a token's picks
+// instead: part[n][z][m] times wts[n][z] for the splits = n_used picks.
 struct Pending {
   const float *part = nullptr;
   int splits = 0;
   int64_t rows = 0, cols = 0;
+  const float *wts = nullptr;
   __device__ __forceinline__ float sum(int64_t n, int64_t m) const {
     float v = 0.0f;
+    if (wts) {
+      for (int z = 0; z < splits; z++)
+        v += part[((int64_t)n * splits + z) * cols + m] * wts[(int64_t)n * splits + z];
+      return v;
+    }
     for (int z = 0; z < splits; z++) v += part[((int64_t)z * rows + n) * cols + m];
     return v;
   }
@@ -43,6 +51,21 @@ struct Pending {
   __device__ __forceinline__ void sum8(int64_t n, int64_t m0, float (&v)[8]) const {
     typedef float f4 __attribute__((ext_vector_type(4)));
     f4 a = {0.0f, 0.0f, 0.0f, 0.0f}, b = a;
+    if (wts) {
+      const float *p = part + (int64_t)n * splits * cols + m0;
+      const float *wp = wts + (int64_t)n * splits;
+      for (int z = 0; z < splits; z++, p += cols) {
+        const float wz = wp[z];
+        const f4 a0 = *(const f4 *)p, b0 = *(const f4 *)(p + 4);
+        a += a0 * wz;
+        b += b0 * wz;
+      }
+      for (int e = 0; e < 4; e++) {
+        v[e] = a[e];
+        v[4 + e] = b[e];
+      }
+      return;
+    }
     const float *p = part + n * cols + m0;
     const int64_t zs = rows * cols;
     int z = 0;

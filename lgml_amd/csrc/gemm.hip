@@ -31,11 +31,26 @@ constexpr int GEMM_WAVES = 8;      // waves per workgroup
 constexpr int GEMM_THREADS = GEMM_WAVES * 64;
 constexpr int RT_PER_WAVE = 2;     // 16-row tiles per wave
 constexpr int WG_ROWS = GEMM_WAVES * RT_PER_WAVE * 16;  // 256
-constexpr int WG_COLS = 64;        // N columns per workgroup (4 tiles)
-// X in LDS: per plane 64 rows x 32 pieces of 8 f16 (16 B), piece kp of row n
-// at slot n * 32 + (kp ^ (n & 15)) (no padding: global-to-LDS loads write
-// 64 consecutive slots; the swizzle keeps a 16-row B read conflict-free).
-constexpr int X_SLOTS = WG_COLS * 32;
+constexpr int WG_COLS = 64;        // N columns per workgroup of a plain product (4 tiles)
+// X in LDS: per plane NCT * 16 rows x 32 pieces of 8 f16 (16 B), piece kp
+// of row n at slot n * 32 + (kp ^ (n & 15)) (no padding: global-to-LDS
+// loads write 64 consecutive slots; the swizzle keeps a 16-row B read
+// conflict-free).
+
+// Grouped products (mul_mat_id): the columns of a workgroup are picks of
+// one expert, gathered from the X planes. tiles[i] = {expert, first,
+// count, 0}: columns 0..count-1 are picks sorted[first ..]; pick p reads
+// X row (p / n_used) * U + (p % n_used) % U and writes Y row p.
+struct Gather {
+  const int32_t *sorted = nullptr;
+  const int4 *tiles = nullptr;
+  const int32_t *n_tiles = nullptr;  // tiles in use (device)
+  int64_t expert_bytes = 0;          // one expert's repacked matrix
+  int n_used = 1, U = 1;
+  __device__ __forceinline__ int64_t xrow(int p) const {
+    return (int64_t)(p / n_used) * U + (p % n_used) % U;
+  }
+};
 
 // Bytes of one repacked chunk (16 rows x 256 values).
 __host__ __device__ constexpr int chunk_bytes(int type) {
@@ -267,47 +282,68 @@ struct WFrag<LGMLH_Q8_0> {
 // registers while sb computes (two register sets, two LDS X buffers, one
 // barrier per step). A split writes its partial sums; a second kernel adds
 // the splits in order (no inter-workgroup sync).
-template <int TYPE>
+template <int TYPE, int NCT, bool GATHER>
 __global__ void __launch_bounds__(GEMM_THREADS)
 qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__restrict__ xs,
              int64_t Npad, int64_t N, float *__restrict__ y, int64_t ldy,
              const float *__restrict__ residual, int splits, int sb_per_split,
-             float *__restrict__ part) {
+             float *__restrict__ part, Gather gt) {
+  constexpr int COLS = NCT * 16;            // N columns per workgroup
+  constexpr int X_SLOTS = COLS * 32;
   __shared__ __align__(16) u32x4 xh_[2][X_SLOTS];
   __shared__ __align__(16) u32x4 xl_[2][X_SLOTS];
-  __shared__ __align__(16) u32x4 gh_[2][WG_COLS];  // group sums, hi: 8 f16 per row
-  __shared__ __align__(16) u32x4 gl_[2][WG_COLS];  // group sums, lo
+  __shared__ __align__(16) u32x4 gh_[2][64];  // group sums, hi: 8 f16 per row
+  __shared__ __align__(16) u32x4 gl_[2][64];  // group sums, lo
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int64_t NSB = K / QK_K;
   const int64_t MT = (M + 15) / 16;
-  const int64_t n0 = (int64_t)blockIdx.x * WG_COLS;
+  int64_t n0 = (int64_t)blockIdx.x * COLS;
+  int first = 0, count = 0;
+  if constexpr (GATHER) {
+    // tiles past the ones in use leave at once (the whole workgroup)
+    if ((int)blockIdx.x >= *gt.n_tiles) return;
+    const int4 tl = gt.tiles[blockIdx.x];
+    w += tl.x * gt.expert_bytes;
+    first = tl.y;
+    count = tl.z;
+    n0 = 0;
+  }
   const int64_t rt0 = (int64_t)blockIdx.y * (WG_ROWS / 16) + wave * RT_PER_WAVE;
   const int z = blockIdx.z;
   const int64_t sb_lo = (int64_t)z * sb_per_split;
   const int64_t sb_hi = sb_lo + sb_per_split < NSB ? sb_lo + sb_per_split : NSB;
   const int c = lane >> 4, r16 = lane & 15;
+  // X row of column n (GATHER: of its pick; columns past count repeat the
+  // first pick and are never stored)
+  auto xrow = [&](int n) -> int64_t {
+    if constexpr (GATHER) return gt.xrow(gt.sorted[first + (n < count ? n : 0)]);
+    else return n;
+  };
 
-  f32x4 acc[RT_PER_WAVE][4];
+  f32x4 acc[RT_PER_WAVE][NCT];
 #pragma unroll
   for (int a = 0; a < RT_PER_WAVE; a++)
 #pragma unroll
-    for (int b = 0; b < 4; b++) acc[a][b] = f32x4{0, 0, 0, 0};
+    for (int b = 0; b < NCT; b++) acc[a][b] = f32x4{0, 0, 0, 0};
 
   // Staging: global-to-LDS loads (no registers). Per plane and step, wave
-  // w fills slots [256 w, 256 w + 256) with 4 loads of 64 slots; lane l of
-  // load j writes slot s = 256 w + 64 j + l, which holds piece
+  // w fills slots [64 XJ w, 64 XJ (w + 1)) with XJ loads of 64 slots; lane
+  // l of load j writes slot s = 64 (XJ w + j) + l, which holds piece
   // kp = (s % 32) ^ (row & 15) of row s / 32.
   typedef __attribute__((address_space(3))) void lds_t;
-  constexpr int XJ = X_SLOTS / (GEMM_WAVES * 64);  // 4
+  constexpr int XJ = X_SLOTS / (GEMM_WAVES * 64);  // NCT
   const f16 *xhi = xs + n0 * K + sb_lo * QK_K, *xlo = xhi + Npad * K;
   const f16 *ghi = xs + 2 * Npad * K + n0 * (K / 32) + sb_lo * 8, *glo = ghi + Npad * (K / 32);
   uint32_t xoff[XJ];
 #pragma unroll
   for (int j = 0; j < XJ; j++) {
     const int sl = (wave * XJ + j) * 64 + lane, n = sl >> 5, kp = (sl & 31) ^ (n & 15);
-    xoff[j] = (uint32_t)(n * K + kp * 8);
+    xoff[j] = (uint32_t)(xrow(n) * K + kp * 8);
   }
+  // group sums: lane = column (lanes past the workgroup's columns load a
+  // valid row into slots that are never read)
+  const uint32_t goff = (uint32_t)(xrow(lane < COLS ? lane : 0) * (K / 32));
   auto load_x = [&](uint32_t kstep, int buf) {  // kstep = sb - sb_lo
 #pragma unroll
     for (int j = 0; j < XJ; j++) {
@@ -318,9 +354,9 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
                                        (lds_t *)&xl_[buf][slot0], 16, 0, 0);
     }
     if constexpr (TYPE == LGMLH_Q4_K) {
-      if (wave < 2)  // wave 0: hi sums, wave 1: lo sums; lane = row
+      if (wave < 2)  // wave 0: hi sums, wave 1: lo sums
         __builtin_amdgcn_global_load_lds(
-            (const void *)((wave == 0 ? ghi : glo) + (uint32_t)lane * (uint32_t)(K / 32) + kstep * 8),
+            (const void *)((wave == 0 ? ghi : glo) + goff + kstep * 8),
             (lds_t *)(wave == 0 ? &gh_[buf][0] : &gl_[buf][0]), 16, 0, 0);
     }
   };
@@ -344,15 +380,15 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   // for the one just issued.
   auto compute = [&](const WFrag<TYPE>(&cur)[RT_PER_WAVE], int buf, auto &&after_lds) {
     const u32x4 *xh = xh_[buf], *xl = xl_[buf];
-    f32x4 cm[RT_PER_WAVE][4];
+    f32x4 cm[RT_PER_WAVE][NCT];
     // The group sums are read first: every LDS read of the step must be
     // issued before the next step's global-to-LDS loads (after_lds), or the
     // compiler, unable to tell the buffers apart, waits for those loads.
-    f16x4 sh4[4], sl4[4];
+    f16x4 sh4[NCT], sl4[NCT];
     if constexpr (TYPE == LGMLH_Q4_K) {
       const f16 *gh = (const f16 *)gh_[buf], *gl = (const f16 *)gl_[buf];
 #pragma unroll
-      for (int ct = 0; ct < 4; ct++) {
+      for (int ct = 0; ct < NCT; ct++) {
         sh4[ct] = f16x4{0, 0, 0, 0};
         sl4[ct] = sh4[ct];
         if (c < 2) {
@@ -371,16 +407,16 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
     }
     // B fragments: a group's hi (lo) fragments are read right after the
     // previous group's products with hi (lo) are issued.
-    f16x8 bh[4], bl[4];
+    f16x8 bh[NCT], bl[NCT];
     auto read_bh = [&](int g) {
       const int slot = r16 * 32 + ((4 * g + c) ^ r16);
 #pragma unroll
-      for (int ct = 0; ct < 4; ct++) bh[ct] = __builtin_bit_cast(f16x8, xh[ct * 16 * 32 + slot]);
+      for (int ct = 0; ct < NCT; ct++) bh[ct] = __builtin_bit_cast(f16x8, xh[ct * 16 * 32 + slot]);
     };
     auto read_bl = [&](int g) {
       const int slot = r16 * 32 + ((4 * g + c) ^ r16);
 #pragma unroll
-      for (int ct = 0; ct < 4; ct++) bl[ct] = __builtin_bit_cast(f16x8, xl[ct * 16 * 32 + slot]);
+      for (int ct = 0; ct < NCT; ct++) bl[ct] = __builtin_bit_cast(f16x8, xl[ct * 16 * 32 + slot]);
     };
     read_bh(0);
     read_bl(0);
@@ -400,7 +436,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
 #pragma unroll
       for (int a = 0; a < RT_PER_WAVE; a++)
 #pragma unroll
-        for (int ct = 0; ct < 4; ct++) {
+        for (int ct = 0; ct < NCT; ct++) {
           const f32x4 c0 = (g == 0 || TYPE == LGMLH_Q8_0) ? f32x4{0, 0, 0, 0} : cm[a][ct];
           cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bh[ct], c0, 0, 0, 0);
         }
@@ -408,14 +444,14 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
 #pragma unroll
         for (int a = 0; a < RT_PER_WAVE; a++)
 #pragma unroll
-          for (int ct = 0; ct < 4; ct++)
+          for (int ct = 0; ct < NCT; ct++)
             cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af2[a], bh[ct], cm[a][ct], 0, 0, 0);
       }
       if (g < 7) read_bh(g + 1);
 #pragma unroll
       for (int a = 0; a < RT_PER_WAVE; a++)
 #pragma unroll
-        for (int ct = 0; ct < 4; ct++)
+        for (int ct = 0; ct < NCT; ct++)
           cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(TYPE == LGMLH_Q6_K ? afr[a] : af[a],
                                                               bl[ct], cm[a][ct], 0, 0, 0);
       if (g < 7) read_bl(g + 1);
@@ -429,7 +465,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
           for (int i = 0; i < 4; i++) {
             const float d = h2f((uint16_t)(dv[i >> 1] >> (16 * (i & 1))));
 #pragma unroll
-            for (int ct = 0; ct < 4; ct++) {
+            for (int ct = 0; ct < NCT; ct++) {
               acc[a][ct][i] += d * cm[a][ct][i];
             }
           }
@@ -448,7 +484,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
           dm[i] = h2f((uint16_t)(cur[a].dm[i] >> 16));
         }
 #pragma unroll
-        for (int ct = 0; ct < 4; ct++) {
+        for (int ct = 0; ct < NCT; ct++) {
           f32x4 mn = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sh4[ct], f32x4{0, 0, 0, 0}, 0, 0, 0);
           mn = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sl4[ct], mn, 0, 0, 0);
 #pragma unroll
@@ -463,7 +499,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
           // the fragments carry sc * q / 4
           const float d4 = 4.0f * h2f((uint16_t)(cur[a].d4[i >> 1] >> (16 * (i & 1))));
 #pragma unroll
-          for (int ct = 0; ct < 4; ct++) acc[a][ct][i] += d4 * cm[a][ct][i];
+          for (int ct = 0; ct < NCT; ct++) acc[a][ct][i] += d4 * cm[a][ct][i];
         }
       }
     }
@@ -497,15 +533,21 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   }
 
   // acc[a][ct][i] = Y[n0 + ct*16 + lane%16][(rt0+a)*16 + 4*(lane/16) + i]
+  // (GATHER: Y row = the pick of column ct*16 + lane%16)
   float *dst = splits == 1 ? y : part + (int64_t)z * N * M;
   const int64_t ld = splits == 1 ? ldy : M;
 #pragma unroll
   for (int a = 0; a < RT_PER_WAVE; a++)
 #pragma unroll
-    for (int ct = 0; ct < 4; ct++) {
+    for (int ct = 0; ct < NCT; ct++) {
       int64_t n = n0 + ct * 16 + r16;
       int64_t m = (rt0 + a) * 16 + 4 * c;
-      if (n >= N) continue;
+      if constexpr (GATHER) {
+        if (ct * 16 + r16 >= count) continue;
+        n = gt.sorted[first + ct * 16 + r16];
+      } else if (n >= N) {
+        continue;
+      }
 #pragma unroll
       for (int i = 0; i < 4; i++)
         if (m + i < M) {
@@ -620,8 +662,9 @@ static void launch_q(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t
   splits = splits_for(M, K, N, &spb);
   const int64_t Npad = split_npad(N);
   dim3 grid((unsigned)(Npad / WG_COLS), (unsigned)((M + WG_ROWS - 1) / WG_ROWS), (unsigned)splits);
-  hipLaunchKernelGGL((qgemm_kernel<TYPE>), grid, dim3(GEMM_THREADS), 0, st, (const uint8_t *)w,
-                     M, K, xs, Npad, N, y, ldy, res, splits, spb, part);
+  hipLaunchKernelGGL((qgemm_kernel<TYPE, WG_COLS / 16, false>), grid, dim3(GEMM_THREADS), 0, st,
+                     (const uint8_t *)w, M, K, xs, Npad, N, y, ldy, res, splits, spb, part,
+                     Gather{});
   if (splits > 1 && !defer) {
     int64_t total = N * M;
     unsigned blocks = (unsigned)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
@@ -660,6 +703,52 @@ int mul_mat_split(int type, const void *w, int64_t M, int64_t K, const f16 *xs, 
   }
   if (defer) *deferred = splits;
   return hip_check(hipGetLastError(), "mul_mat");
+}
+
+template <int TYPE, int NCT>
+static void launch_grouped(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t Npad,
+                           const Gather &gt, int max_tiles, float *y, hipStream_t st) {
+  const int NSB = (int)(K / QK_K);
+  dim3 grid((unsigned)max_tiles, (unsigned)((M + WG_ROWS - 1) / WG_ROWS), 1);
+  hipLaunchKernelGGL((qgemm_kernel<TYPE, NCT, true>), grid, dim3(GEMM_THREADS), 0, st,
+                     (const uint8_t *)w, M, K, xs, Npad, (int64_t)0, y, M, (const float *)nullptr,
+                     1, NSB, (float *)nullptr, gt);
+}
+
+// Grouped product (mul_mat_id): for each column tile of the grouping (see
+// Gather), Y rows of its picks = expert matrix x X rows, K unsplit. w holds
+// n_expert repacked matrices of M rows, expert_bytes apart; xs the split
+// planes of the X rows (Npad rows). tile_cols is 16 or 64, the tile width
+// the grouping was made for; max_tiles bounds the tiles in use.
+int mul_mat_grouped(int type, const void *w, int64_t expert_bytes, int64_t M, int64_t K,
+                    const f16 *xs, int64_t Npad, int n_used, int U, const int32_t *sorted,
+                    const int4 *tiles, const int32_t *n_tiles, int max_tiles, int tile_cols,
+                    float *y, hipStream_t st) {
+  if (!w || !xs || !y || M <= 0 || K <= 0 || K % QK_K || (tile_cols != 16 && tile_cols != 64)) {
+    set_error("mul_mat_id: bad arguments (M %lld, K %lld)", (long long)M, (long long)K);
+    return LGMLH_EINVAL;
+  }
+  if (max_tiles <= 0) return LGMLH_OK;
+  Gather gt;
+  gt.sorted = sorted;
+  gt.tiles = tiles;
+  gt.n_tiles = n_tiles;
+  gt.expert_bytes = expert_bytes;
+  gt.n_used = n_used;
+  gt.U = U;
+#define LGMLH_GROUPED(T_)                                                              \
+  (tile_cols == 16 ? launch_grouped<T_, 1>(w, M, K, xs, Npad, gt, max_tiles, y, st)    \
+                   : launch_grouped<T_, 4>(w, M, K, xs, Npad, gt, max_tiles, y, st))
+  switch (type) {
+    case LGMLH_Q4_K: LGMLH_GROUPED(LGMLH_Q4_K); break;
+    case LGMLH_Q6_K: LGMLH_GROUPED(LGMLH_Q6_K); break;
+    case LGMLH_Q8_0: LGMLH_GROUPED(LGMLH_Q8_0); break;
+    default:
+      set_error("mul_mat_id: type %d not supported", type);
+      return LGMLH_EINVAL;
+  }
+#undef LGMLH_GROUPED
+  return hip_check(hipGetLastError(), "mul_mat_id");
 }
 
 // X -> split planes (xs holds split_bytes(N, K)).

@@ -1,4 +1,4 @@
-// One forward pass of a dense llama / qwen3 decoder over a planned ubatch:
+// One forward pass of a llama / qwen3 / qwen3moe decoder over a planned ubatch:
 // the launches that ggml's graph compute runs for the graph that
 // transformer.lua forward (:2285-2365) builds, with the per-sequence
 // attention loop of attention_batch (:2389-2416) replaced by one paged
@@ -6,6 +6,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "moe.h"
 #include "quant.h"
 #include "split.h"
 
@@ -51,6 +52,10 @@ struct Carve {
 struct Sizes {
   int64_t N, E, H, Hkv, D, F, V, W, n_out;
   size_t gemm_ws, gemm_ws_v, attn_ws, split_ws;
+  // routed experts: experts, picks per token, expert width, picks, tile width
+  bool moe;
+  int NE, NU, tc;
+  int64_t FX, P;
 };
 
 static Sizes sizes_of(const lgmlh_model *m, int64_t n_tokens, int64_t n_items, int n_out) {
@@ -69,6 +74,13 @@ static Sizes sizes_of(const lgmlh_model *m, int64_t n_tokens, int64_t n_items, i
     size_t w = partial_bytes(t, M, K, N);
     if (w > g) g = w;
   };
+  z.moe = false;
+  for (int il = 0; il < m->n_layer; il++) z.moe = z.moe || m->layers[il].gate_inp != nullptr;
+  z.NE = z.moe ? m->n_expert : 0;
+  z.NU = z.moe ? m->n_used : 0;
+  z.FX = z.moe ? m->n_ff_exp : 0;
+  z.P = z.N * z.NU;
+  z.tc = z.moe ? moe_tile_cols(z.P, z.NE) : 16;
   for (int il = 0; il < m->n_layer; il++) {
     const lgmlh_layer &L = m->layers[il];
     upd(L.wqkv_type, L.wqkv_rows, z.E, z.N);
@@ -78,15 +90,20 @@ static Sizes sizes_of(const lgmlh_model *m, int64_t n_tokens, int64_t n_items, i
       if (w > gv) gv = w;
     }
     upd(L.wo_type, z.E, z.H * z.D, z.N);
-    upd(L.wgu_type, 2 * z.F, z.E, z.N);
-    upd(L.wdown_type, z.E, z.F, z.N);
+    if (!L.gate_inp) {
+      upd(L.wgu_type, 2 * z.F, z.E, z.N);
+      upd(L.wdown_type, z.E, z.F, z.N);
+    }
   }
   upd(m->output_type, z.V, z.E, n_out);
   z.gemm_ws = g;
   z.gemm_ws_v = gv;
   int64_t kmax = z.E > z.F ? z.E : z.F;
   if (z.H * z.D > kmax) kmax = z.H * z.D;
-  z.split_ws = split_bytes(z.N > n_out ? z.N : n_out, kmax);
+  if (z.FX > kmax) kmax = z.FX;
+  int64_t rmax = z.N > n_out ? z.N : n_out;
+  if (z.P > rmax) rmax = z.P;  // the expert activations of the picks
+  z.split_ws = split_bytes(rmax, kmax);
   z.attn_ws = (size_t)n_items * z.Hkv * (16 * z.D + 32) * sizeof(float);
   return z;
 }
@@ -106,6 +123,15 @@ static size_t ws_bytes_of(const Sizes &z) {
   add(z.attn_ws);
   add(z.gemm_ws);
   add(z.gemm_ws_v);
+  if (z.moe) {
+    add((size_t)router_splits(z.E) * z.N * z.NE * 4);  // router partials
+    add(z.P * 4);                                        // ids
+    add(z.P * 4);                                        // weights
+    add(group_bytes(z.P, z.NE, z.tc));                   // grouping
+    add(z.P * 2 * z.FX * 4);                             // [gate | up] of the picks
+    add(z.P * z.FX * 4);                                 // f32 activations (f32 experts)
+    add(z.P * z.E * 4);                                  // expert outputs (pending)
+  }
   return b + 256;
 }
 
@@ -171,6 +197,19 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
   void *aws = cv.take(z.attn_ws);
   float *gws = (float *)cv.take(z.gemm_ws);
   float *gws_v = (float *)cv.take(z.gemm_ws_v);
+  float *rpart = nullptr, *mwts = nullptr, *gu_e = nullptr, *act_e = nullptr, *y_e = nullptr;
+  int32_t *mids = nullptr;
+  GroupOut go{};
+  if (z.moe) {
+    rpart = (float *)cv.take((size_t)router_splits(z.E) * z.N * z.NE * 4);
+    mids = (int32_t *)cv.take(z.P * 4);
+    mwts = (float *)cv.take(z.P * 4);
+    void *gb = cv.take(group_bytes(z.P, z.NE, z.tc));
+    gu_e = (float *)cv.take(z.P * 2 * z.FX * 4);
+    act_e = (float *)cv.take(z.P * z.FX * 4);
+    y_e = (float *)cv.take(z.P * z.E * 4);
+    if (gb) go = group_carve(gb, z.P, z.NE, z.tc);
+  }
   if (!cv.ok) {
     set_error("forward: workspace carve failed");
     return LGMLH_ENOMEM;
@@ -222,6 +261,36 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
     }
     if (isq(L.wo_type)) LGMLH_TRY(split_x(att, LGMLH_F32, z.N, z.H * z.D, xs, st));
     LGMLH_TRY(gemm(L.wo_type, L.wo, z.E, z.H * z.D, att, z.N, x, z.E, x, gws, z.gemm_ws, p_o));
+    if (L.gate_inp) {
+      // routed experts (transformer.lua:2054-2068, M.moe :1989-2027): x +=
+      // attention out, then ffn_norm for the router (f32) and the experts
+      const bool gq = isq(L.exp_gu_type), dq = isq(L.exp_down_type);
+      LGMLH_TRY(rms_norm_dev(x, nullptr, z.N, z.E, m->eps, L.ffn_norm, xn, gq ? xs : nullptr,
+                             st, p_o, true));
+      {
+        Span sp(trace, LGMLH_TRACE_GEMM, st);
+        LGMLH_TRY(router_logits(L.gate_inp, z.NE, z.E, xn, z.N, rpart, st));
+      }
+      LGMLH_TRY(moe_route_dev(rpart, router_splits(z.E), z.N, z.NE, z.NU, m->gating,
+                              m->norm_topk, m->expert_scale, mids, mwts, &go, st));
+      {
+        Span sp(trace, LGMLH_TRACE_GEMM, st);
+        LGMLH_TRY(experts_dev(L.exp_gu_type, L.exp_gu, z.NE, 2 * z.FX, z.E, xn, xs,
+                              split_npad(z.N), 1, mids, z.N, z.NU, go, gu_e, st));
+      }
+      // swiglu_split on the picks' rows; their split planes replace x's
+      LGMLH_TRY(swiglu_dev(gu_e, z.P, z.FX, dq ? nullptr : act_e, dq ? xs : nullptr, st,
+                           Pending{}));
+      {
+        Span sp(trace, LGMLH_TRACE_GEMM, st);
+        LGMLH_TRY(experts_dev(L.exp_down_type, L.exp_down, z.NE, z.E, z.FX, act_e, xs,
+                              split_npad(z.P), z.NU, mids, z.N, z.NU, go, y_e, st));
+      }
+      // the weighted sum of the picks (g:mul, sum_picks) is added to x by
+      // the next norm
+      p_down = Pending{y_e, z.NU, z.N, z.E, mwts};
+      continue;
+    }
     // x += attention out, then ffn_norm
     LGMLH_TRY(rms_norm_dev(x, nullptr, z.N, z.E, m->eps, L.ffn_norm,
                            isq(L.wgu_type) ? nullptr : xn, isq(L.wgu_type) ? xs : nullptr, st,

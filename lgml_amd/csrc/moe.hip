@@ -1,0 +1,507 @@
+// Routed experts (mixture of experts) of qwen3moe-style layers: the router
+// of M.moe (transformer.lua:1989-2027) and graph:mul_mat_id
+// (src/ops_nn.c:322-362) with the weighted sum of the picks (experts and
+// sum_picks, transformer.lua:1875-1910).
+//
+// A pass of T tokens with n_used picks each has P = T n_used picks. The
+// router logits come from a split-K f32 product; one workgroup then turns
+// them into the picks and weights and groups the picks by expert: sorted
+// holds the picks of expert 0, then of expert 1, ... (each in pick order),
+// and a tile list cuts every expert's picks into column tiles of 16 (or
+// 64) for the grouped quantized product (gemm.hip, Gather). Experts nobody
+// picked cost nothing; an expert's weights are read once per tile.
+#include <math.h>
+
+#include "common.h"
+#include "moe.h"
+#include "quant.h"
+#include "split.h"
+
+namespace lgmlh {
+
+int mul_mat_grouped(int type, const void *w, int64_t expert_bytes, int64_t M, int64_t K,
+                    const f16 *xs, int64_t Npad, int n_used, int U, const int32_t *sorted,
+                    const int4 *tiles, const int32_t *n_tiles, int max_tiles, int tile_cols,
+                    float *y, hipStream_t st);
+int split_x(const void *x, int xtype, int64_t N, int64_t K, f16 *xs, hipStream_t st);
+
+constexpr int ROUTE_THREADS = 1024;
+constexpr int ROUTE_WAVES = ROUTE_THREADS / 64;
+constexpr int MOE_MAX_EXPERTS = 512;  // 8 logits per lane
+constexpr int MOE_MAX_USED = 16;
+constexpr int MOE_MAX_PICKS = 8192;   // picks of one pass (LDS)
+
+// ---- router logits: split-K f32 product -------------------------------------
+// part[z][n][e] = sum over k in [256 z, 256 z + 256) of W[e][k] x[n][k], in
+// k order (fmaf). A 16 x 16 tile of (expert, token) per workgroup.
+constexpr int ROUTER_KC = 256;
+__global__ void __launch_bounds__(256)
+router_part_kernel(const float *__restrict__ w, int NE, int64_t K, const float *__restrict__ x,
+                   int64_t N, float *__restrict__ part) {
+  __shared__ float ws_[16][ROUTER_KC + 1], xs_[16][ROUTER_KC + 1];
+  const int t = threadIdx.x, tx = t & 15, ty = t >> 4;
+  const int64_t e0 = (int64_t)blockIdx.x * 16, n0 = (int64_t)blockIdx.y * 16;
+  const int64_t k0 = (int64_t)blockIdx.z * ROUTER_KC;
+  for (int i = t; i < 16 * ROUTER_KC; i += 256) {
+    const int r = i / ROUTER_KC, cc = i % ROUTER_KC;
+    const bool kin = k0 + cc < K;
+    ws_[r][cc] = (e0 + r < NE && kin) ? w[(e0 + r) * K + k0 + cc] : 0.0f;
+    xs_[r][cc] = (n0 + r < N && kin) ? x[(n0 + r) * K + k0 + cc] : 0.0f;
+  }
+  __syncthreads();
+  float acc = 0.0f;
+#pragma unroll 8
+  for (int cc = 0; cc < ROUTER_KC; cc++) acc = fmaf(ws_[tx][cc], xs_[ty][cc], acc);
+  if (e0 + tx < NE && n0 + ty < N) part[((int64_t)blockIdx.z * N + n0 + ty) * NE + e0 + tx] = acc;
+}
+
+// ---- picks and weights ---------------------------------------------------------
+// (value, index) order of the top-k: larger value first, then smaller index.
+__device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
+  return a > b || (a == b && ia < ib);
+}
+
+// One wave per token: logits l = sum of the nz partial rows (in order);
+// probs = soft_max (f32: max, exp, sum over the wave in a fixed tree) or
+// sigmoid; the n_used largest logits (the gating is monotone) as ids,
+// largest first, ties to the smaller index (argsort_top_k); weights =
+// probs of the ids, / max(sum, 6.103515625e-5) when norm_topk
+// (transformer.lua:2003-2005), times scale (:2006-2008).
+__device__ void route_token(const float *__restrict__ part, int nz, int64_t T, int64_t t, int NE,
+                            int n_used, int gating, int norm_topk, float scale, int lane,
+                            int32_t *__restrict__ ids, float *__restrict__ wts,
+                            int32_t *ids_lds) {
+  constexpr int PER = MOE_MAX_EXPERTS / 64;
+  float l[PER], p[PER];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int e = lane + 64 * i;
+    l[i] = -INFINITY;
+    if (e < NE) {
+      float v = 0.0f;
+      for (int z = 0; z < nz; z++) v += part[((int64_t)z * T + t) * NE + e];
+      l[i] = v;
+    }
+    mx = fmaxf(mx, l[i]);
+  }
+  for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if (gating == LGMLH_GATING_SOFTMAX) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      p[i] = lane + 64 * i < NE ? expf(l[i] - mx) : 0.0f;
+      s += p[i];
+    }
+    for (int o = 1; o < 64; o <<= 1) s += __shfl_xor(s, o);
+#pragma unroll
+    for (int i = 0; i < PER; i++) p[i] = p[i] / s;
+  } else {
+#pragma unroll
+    for (int i = 0; i < PER; i++) p[i] = 1.0f / (1.0f + expf(-l[i]));
+  }
+  uint32_t taken = 0;
+  int sel[MOE_MAX_USED];
+  float w[MOE_MAX_USED];
+#pragma unroll
+  for (int j = 0; j < MOE_MAX_USED; j++) {
+    sel[j] = 0;
+    w[j] = 0.0f;
+    if (j >= n_used) continue;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      const int e = lane + 64 * i;
+      if (e < NE && !(taken >> i & 1u) && better(l[i], e, bv, bi)) {
+        bv = l[i];
+        bi = e;
+      }
+    }
+    for (int o = 1; o < 64; o <<= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oi = __shfl_xor(bi, o);
+      if (better(ov, oi, bv, bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    // every lane holds the winner now (none when the logits are NaN: expert
+    // 0 then, so ids stay in range); its owner marks it and sends its prob
+    if (bi >= NE) bi = 0;
+    float pw = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; i++)
+      if (bi == lane + 64 * i) {
+        taken |= 1u << i;
+        pw = p[i];
+      }
+    sel[j] = bi;
+    w[j] = __shfl(pw, bi & 63);
+  }
+  if (norm_topk) {
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MOE_MAX_USED; j++)
+      if (j < n_used) s += w[j];
+    s = fmaxf(s, 6.103515625e-5f);
+#pragma unroll
+    for (int j = 0; j < MOE_MAX_USED; j++) w[j] = w[j] / s;
+  }
+  if (scale != 1.0f)
+#pragma unroll
+    for (int j = 0; j < MOE_MAX_USED; j++) w[j] = w[j] * scale;
+#pragma unroll
+  for (int j = 0; j < MOE_MAX_USED; j++)
+    if (j < n_used && lane == j) {
+      ids[t * n_used + j] = sel[j];
+      wts[t * n_used + j] = w[j];
+      if (ids_lds) ids_lds[t * n_used + j] = sel[j];
+    }
+}
+
+// ---- grouping of the picks by expert ------------------------------------------
+
+struct GroupLds {
+  int32_t ids[MOE_MAX_PICKS];
+  int32_t base[ROUTE_WAVES][MOE_MAX_EXPERTS];  // per wave chunk: counts, then bases
+  int32_t off[MOE_MAX_EXPERTS + 1];
+  int32_t toff[MOE_MAX_EXPERTS + 1];
+};
+
+// Counting sort of the picks (ids in lds.ids; negative = no expert) by
+// expert, stable: wave w ranks the picks of its chunk. Called by all
+// ROUTE_THREADS threads.
+__device__ void group_picks(GroupLds &lds, int P, int NE, const GroupOut &go) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i < ROUTE_WAVES * MOE_MAX_EXPERTS; i += ROUTE_THREADS)
+    (&lds.base[0][0])[i] = 0;
+  __syncthreads();
+  const int chunk = ((P + ROUTE_WAVES - 1) / ROUTE_WAVES + 63) & ~63;
+  const int lo = wave * chunk, hi = lo + chunk < P ? lo + chunk : P;
+  for (int p = lo + lane; p < hi; p += 64) {
+    int e = lds.ids[p];
+    if ((unsigned)e >= (unsigned)NE) lds.ids[p] = e = -1;  // no expert
+    if (e >= 0) atomicAdd(&lds.base[wave][e], 1);  // counts: order-free
+  }
+  __syncthreads();
+  // totals, tiles per expert, and the exclusive scans (one wave, 8 experts
+  // per lane)
+  if (wave == 0) {
+    constexpr int PER = MOE_MAX_EXPERTS / 64;
+    int cnt[PER], nt[PER], cs = 0, ts = 0;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      const int e = lane * PER + i;
+      cnt[i] = 0;
+      if (e < NE)
+        for (int ww = 0; ww < ROUTE_WAVES; ww++) cnt[i] += lds.base[ww][e];
+      nt[i] = (cnt[i] + go.tile_cols - 1) / go.tile_cols;
+      cs += cnt[i];
+      ts += nt[i];
+    }
+    int ci = cs, ti = ts;  // inclusive scans over lanes
+    for (int o = 1; o < 64; o <<= 1) {
+      const int a = __shfl_up(ci, o), b = __shfl_up(ti, o);
+      if (lane >= o) {
+        ci += a;
+        ti += b;
+      }
+    }
+    int c0 = ci - cs, t0 = ti - ts;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      const int e = lane * PER + i;
+      if (e < NE) {
+        lds.off[e] = c0;
+        lds.toff[e] = t0;
+        // per-wave bases of expert e
+        int b = c0;
+        for (int ww = 0; ww < ROUTE_WAVES; ww++) {
+          const int cw = lds.base[ww][e];
+          lds.base[ww][e] = b;
+          b += cw;
+        }
+      }
+      c0 += cnt[i];
+      t0 += nt[i];
+    }
+    if (lane == 63) {
+      lds.off[NE] = c0;
+      lds.toff[NE] = t0;
+      *go.n_tiles = t0;
+    }
+  }
+  __syncthreads();
+  // stable placement: rounds of 64 picks; a pick's rank among the round's
+  // picks of the same expert comes from the lanes before it
+  for (int r0 = lo; r0 < hi; r0 += 64) {
+    const int p = r0 + lane;
+    const int e = p < hi ? lds.ids[p] : -1;
+    int rank = 0, tot = 0;
+    for (int l2 = 0; l2 < 64; l2++) {
+      const int e2 = __shfl(e, l2);
+      const int same = e2 == e ? 1 : 0;
+      tot += same;
+      rank += l2 < lane ? same : 0;
+    }
+    const int b = e >= 0 ? lds.base[wave][e] : 0;
+    if (e >= 0) go.sorted[b + rank] = p;
+    __builtin_amdgcn_wave_barrier();  // all lanes read base before it moves
+    if (e >= 0 && rank == 0) lds.base[wave][e] = b + tot;
+    __builtin_amdgcn_wave_barrier();
+  }
+  __syncthreads();
+  // the tile list, expert by expert
+  for (int e = tid; e < NE; e += ROUTE_THREADS) {
+    const int c = lds.off[e + 1] - lds.off[e];
+    for (int i = 0, t = lds.toff[e]; i * go.tile_cols < c; i++, t++) {
+      const int first = lds.off[e] + i * go.tile_cols;
+      const int n = c - i * go.tile_cols < go.tile_cols ? c - i * go.tile_cols : go.tile_cols;
+      go.tiles[t] = int4{e, first, n, 0};
+    }
+  }
+}
+
+// Routing of T tokens (one workgroup); with group set, also the grouping.
+__global__ void __launch_bounds__(ROUTE_THREADS)
+route_kernel(const float *__restrict__ part, int nz, int64_t T, int NE, int n_used, int gating,
+             int norm_topk, float scale, int32_t *__restrict__ ids, float *__restrict__ wts,
+             int group, GroupOut go) {
+  __shared__ GroupLds lds;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int64_t t = wave; t < T; t += ROUTE_WAVES)
+    route_token(part, nz, T, t, NE, n_used, gating, norm_topk, scale, lane, ids, wts,
+                group ? lds.ids : nullptr);
+  if (!group) return;
+  __syncthreads();
+  group_picks(lds, (int)(T * n_used), NE, go);
+}
+
+// Grouping of given ids (graph:mul_mat_id's ids). Picks whose id is outside
+// [0, NE) join no expert; their Y rows (M values) are written as zeros.
+__global__ void __launch_bounds__(ROUTE_THREADS)
+group_kernel(const int32_t *__restrict__ ids, int P, int NE, GroupOut go, float *__restrict__ y,
+             int64_t M) {
+  __shared__ GroupLds lds;
+  for (int p = threadIdx.x; p < P; p += ROUTE_THREADS) {
+    const int e = ids[p];
+    const bool ok = e >= 0 && e < NE;
+    lds.ids[p] = ok ? e : -1;
+    if (!ok)
+      for (int64_t m = 0; m < M; m++) y[(int64_t)p * M + m] = 0.0f;
+  }
+  __syncthreads();
+  group_picks(lds, P, NE, go);
+}
+
+// ---- f32 experts: one workgroup per (pick, 256 rows), k in order ---------------
+__global__ void __launch_bounds__(256)
+f32_id_kernel(const float *__restrict__ w, int NE, int64_t M, int64_t K,
+              const float *__restrict__ x, int U, const int32_t *__restrict__ ids, int n_used,
+              float *__restrict__ y) {
+  const int64_t p = blockIdx.x;
+  const int64_t m = (int64_t)blockIdx.y * 256 + threadIdx.x;
+  const int e = ids[p];
+  if (m >= M) return;
+  if (e < 0 || e >= NE) {
+    y[p * M + m] = 0.0f;
+    return;
+  }
+  const float *xr = x + ((p / n_used) * U + (p % n_used) % U) * K;
+  const float *wr = w + ((int64_t)e * M + m) * K;
+  float acc = 0.0f;
+  for (int64_t k = 0; k < K; k++) acc = fmaf(wr[k], xr[k], acc);
+  y[p * M + m] = acc;
+}
+
+// ---- weighted sum of the picks ------------------------------------------------------
+// out[t][m] = (y[t][0][m] w[t][0] + y[t][1][m] w[t][1] + ...) (+ residual),
+// products and sums in pick order (g:mul then sum_picks).
+__global__ void moe_sum_kernel(const float *__restrict__ y, const float *__restrict__ wts,
+                               int64_t T, int n_used, int64_t M,
+                               const float *__restrict__ residual, float *__restrict__ out) {
+  const int64_t total = T * M;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / M, m = i % M;
+    float s = 0.0f;
+    for (int j = 0; j < n_used; j++) s += y[(t * n_used + j) * M + m] * wts[t * n_used + j];
+    if (residual) s += residual[i];
+    out[i] = s;
+  }
+}
+
+// ---- host side --------------------------------------------------------------------
+static size_t a256(size_t b) { return (b + 255) & ~size_t(255); }
+
+// Column tile width for P picks over NE experts: 64 once an expert averages
+// 32 picks (prefill), else 16.
+int moe_tile_cols(int64_t P, int NE) { return P >= 32 * (int64_t)NE ? 64 : 16; }
+
+// An upper bound of the tiles of a grouping: sum over experts of
+// ceil(c_e / tc) <= (P + (tc - 1) * min(NE, P)) / tc, and <= P.
+int moe_max_tiles(int64_t P, int NE, int tc) {
+  const int64_t nz = P < NE ? P : NE;
+  int64_t b = (P + (int64_t)(tc - 1) * nz) / tc;
+  return (int)(b < P ? b : P);
+}
+
+int router_splits(int64_t K) { return (int)((K + ROUTER_KC - 1) / ROUTER_KC); }
+
+// Router partials (router_splits(K) x T x NE floats) of rows x (T, K).
+int router_logits(const float *w, int NE, int64_t K, const float *x, int64_t T, float *part,
+                  hipStream_t st) {
+  if (T == 0) return LGMLH_OK;
+  dim3 grid((unsigned)((NE + 15) / 16), (unsigned)((T + 15) / 16), (unsigned)router_splits(K));
+  hipLaunchKernelGGL(router_part_kernel, grid, dim3(256), 0, st, w, NE, K, x, T, part);
+  return hip_check(hipGetLastError(), "moe router");
+}
+
+static int check_route(int64_t T, int NE, int n_used, int gating) {
+  if (NE < 1 || NE > MOE_MAX_EXPERTS || n_used < 1 || n_used > MOE_MAX_USED || n_used > NE ||
+      T < 0 || (gating != LGMLH_GATING_SOFTMAX && gating != LGMLH_GATING_SIGMOID)) {
+    set_error("moe: bad routing arguments (experts %d, used %d, gating %d)", NE, n_used, gating);
+    return LGMLH_EINVAL;
+  }
+  if (T * n_used > MOE_MAX_PICKS) {
+    set_error("moe: %lld picks in one pass (at most %d)", (long long)(T * n_used), MOE_MAX_PICKS);
+    return LGMLH_EINVAL;
+  }
+  return LGMLH_OK;
+}
+
+// Picks, weights and (with go) the grouping, from nz router partials.
+int moe_route_dev(const float *part, int nz, int64_t T, int NE, int n_used, int gating,
+                  int norm_topk, float scale, int32_t *ids, float *wts, const GroupOut *go,
+                  hipStream_t st) {
+  LGMLH_TRY(check_route(T, NE, n_used, gating));
+  if (T == 0) return LGMLH_OK;
+  GroupOut g = go ? *go : GroupOut{nullptr, nullptr, nullptr, 16};
+  hipLaunchKernelGGL(route_kernel, dim3(1), dim3(ROUTE_THREADS), 0, st,
+                     part, nz, T, NE, n_used, gating, norm_topk, scale, ids, wts, go ? 1 : 0, g);
+  return hip_check(hipGetLastError(), "moe route");
+}
+
+// Workspace of a grouping of P picks: sorted, tiles, count.
+size_t group_bytes(int64_t P, int NE, int tc) {
+  return a256((size_t)P * 4) + a256((size_t)moe_max_tiles(P, NE, tc) * 16) + 256;
+}
+
+GroupOut group_carve(void *ws, int64_t P, int NE, int tc) {
+  char *b = (char *)ws;
+  GroupOut g;
+  g.sorted = (int32_t *)b;
+  b += a256((size_t)P * 4);
+  g.tiles = (int4 *)b;
+  b += a256((size_t)moe_max_tiles(P, NE, tc) * 16);
+  g.n_tiles = (int32_t *)b;
+  g.tile_cols = tc;
+  return g;
+}
+
+// Y (P, M) of the experts of the picks; x is f32 (T * U rows, f32
+// experts) or split planes (quantized experts, xnpad rows).
+int experts_dev(int type, const void *w, int NE, int64_t M, int64_t K, const float *xf,
+                const f16 *xs, int64_t xnpad, int U, const int32_t *ids, int64_t T, int n_used,
+                const GroupOut &go, float *y, hipStream_t st) {
+  const int64_t P = T * n_used;
+  if (P == 0) return LGMLH_OK;
+  if (type == LGMLH_F32) {
+    dim3 grid((unsigned)P, (unsigned)((M + 255) / 256));
+    hipLaunchKernelGGL(f32_id_kernel, grid, dim3(256), 0, st, (const float *)w, NE, M, K, xf, U,
+                       ids, n_used, y);
+    return hip_check(hipGetLastError(), "mul_mat_id");
+  }
+  const int64_t eb = lgmlh_repacked_bytes(type, M, K);
+  if (eb < 0) {
+    set_error("mul_mat_id: type %d with K %lld", type, (long long)K);
+    return LGMLH_EINVAL;
+  }
+  return mul_mat_grouped(type, w, eb, M, K, xs, xnpad, n_used, U, go.sorted, go.tiles, go.n_tiles,
+                         moe_max_tiles(P, NE, go.tile_cols), go.tile_cols, y, st);
+}
+
+}  // namespace lgmlh
+
+using namespace lgmlh;
+
+extern "C" int lgmlh_moe_route(const float *logits, int64_t n, int n_expert, int n_used,
+                               int gating, int norm_topk, float scale, int32_t *ids,
+                               float *weights, void *stream) {
+  if (!logits || !ids || !weights) {
+    set_error("moe_route: null argument");
+    return LGMLH_EINVAL;
+  }
+  return moe_route_dev(logits, 1, n, n_expert, n_used, gating, norm_topk, scale, ids, weights,
+                       nullptr, as_stream(stream));
+}
+
+extern "C" size_t lgmlh_mul_mat_id_workspace(int type, int64_t n_expert, int64_t M, int64_t K,
+                                             int64_t T, int64_t U, int n_used) {
+  (void)M;
+  const int64_t P = T * n_used;
+  const int tc = moe_tile_cols(P, (int)n_expert);
+  size_t b = group_bytes(P, (int)n_expert, tc);
+  if (type != LGMLH_F32) b += a256(split_bytes(T * U, K));
+  return b;
+}
+
+extern "C" int lgmlh_mul_mat_id(int type, const void *w, int64_t n_expert, int64_t M, int64_t K,
+                                const void *x, int xtype, int64_t U, const int32_t *ids,
+                                int64_t T, int n_used, float *y, void *workspace,
+                                size_t ws_bytes, void *stream) {
+  if (!w || !x || !ids || !y || M <= 0 || K <= 0 || T < 0 || U < 1 || n_used < 1 ||
+      n_used % U || n_expert < 1 || n_expert > MOE_MAX_EXPERTS) {
+    set_error("mul_mat_id: bad arguments (experts %lld, M %lld, K %lld, U %lld, used %d)",
+              (long long)n_expert, (long long)M, (long long)K, (long long)U, n_used);
+    return LGMLH_EINVAL;
+  }
+  if (T * n_used > MOE_MAX_PICKS) {
+    set_error("mul_mat_id: %lld picks (at most %d)", (long long)(T * n_used), MOE_MAX_PICKS);
+    return LGMLH_EINVAL;
+  }
+  if (type == LGMLH_F32 ? xtype != LGMLH_F32 : (xtype != LGMLH_F32 && xtype != LGMLH_F16)) {
+    set_error("mul_mat_id: bad x type %d for weights of type %d", xtype, type);
+    return LGMLH_EINVAL;
+  }
+  if (type != LGMLH_F32 && K % QK_K) {
+    set_error("mul_mat_id: K %lld is not a multiple of 256", (long long)K);
+    return LGMLH_EINVAL;
+  }
+  const size_t need = lgmlh_mul_mat_id_workspace(type, n_expert, M, K, T, U, n_used);
+  if (!workspace || ws_bytes < need) {
+    set_error("mul_mat_id: workspace of %zu bytes, need %zu", ws_bytes, need);
+    return LGMLH_ENOMEM;
+  }
+  const int64_t P = T * n_used;
+  if (P == 0) return LGMLH_OK;
+  hipStream_t st = as_stream(stream);
+  const int NE = (int)n_expert;
+  const int tc = moe_tile_cols(P, NE);
+  GroupOut go = group_carve(workspace, P, NE, tc);
+  hipLaunchKernelGGL(group_kernel, dim3(1), dim3(ROUTE_THREADS), 0, st, ids,
+                     (int)P, NE, go, y, M);
+  LGMLH_TRY(hip_check(hipGetLastError(), "mul_mat_id group"));
+  f16 *xs = nullptr;
+  if (type != LGMLH_F32) {
+    xs = (f16 *)((char *)workspace + group_bytes(P, NE, tc));
+    LGMLH_TRY(split_x(x, xtype, T * U, K, xs, st));
+  }
+  return experts_dev(type, w, NE, M, K, (const float *)x, xs, split_npad(T * U), (int)U, ids, T,
+                     n_used, go, y, st);
+}
+
+extern "C" int lgmlh_moe_sum(const float *y, const float *weights, int64_t T, int n_used,
+                             int64_t M, const float *residual, float *out, void *stream) {
+  if (!y || !weights || !out || T < 0 || n_used < 1 || M <= 0) {
+    set_error("moe_sum: bad arguments");
+    return LGMLH_EINVAL;
+  }
+  const int64_t total = T * M;
+  if (total == 0) return LGMLH_OK;
+  unsigned blocks = (unsigned)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
+  hipLaunchKernelGGL(moe_sum_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), y, weights,
+                     T, n_used, M, residual, out);
+  return hip_check(hipGetLastError(), "moe_sum");
+}

@@ -27,8 +27,10 @@ SYMBOLS = (
     "lgmlh_kvpool_ref", "lgmlh_kvpool_unref", "lgmlh_kvpool_refs_of", "lgmlh_kvpool_publish",
     "lgmlh_kvpool_publish_part", "lgmlh_kvpool_key_of", "lgmlh_kvpool_lookup",
     "lgmlh_kvpool_longest_kid", "lgmlh_kvpool_set_cap", "lgmlh_kvpool_stats", "lgmlh_block_key",
-    "lgmlh_gen_normal",
+    "lgmlh_gen_normal", "lgmlh_moe_route", "lgmlh_mul_mat_id_workspace", "lgmlh_mul_mat_id",
+    "lgmlh_moe_sum",
 )
+GATING_SOFTMAX, GATING_SIGMOID = 1, 2
 TRACE_ATTN, TRACE_GEMM = 1, 2
 
 
@@ -59,7 +61,9 @@ class Layer(C.Structure):
                 ("wo_type", C.c_int), ("wgu_type", C.c_int), ("wdown_type", C.c_int),
                 ("wqkv_rows", C.c_int64), ("wqkv", C.c_void_p), ("wv", C.c_void_p),
                 ("wo", C.c_void_p), ("wgu", C.c_void_p), ("wdown", C.c_void_p),
-                ("kpool", C.c_void_p), ("vpool", C.c_void_p)]
+                ("kpool", C.c_void_p), ("vpool", C.c_void_p), ("gate_inp", C.c_void_p),
+                ("exp_gu_type", C.c_int), ("exp_down_type", C.c_int), ("exp_gu", C.c_void_p),
+                ("exp_down", C.c_void_p)]
 
 
 class Trace(C.Structure):
@@ -73,7 +77,9 @@ class Model(C.Structure):
                [("eps", C.c_float), ("rope_base", C.c_float), ("attn_scale", C.c_float),
                 ("rope_freqs", C.c_void_p), ("tok_embd_type", C.c_int), ("output_type", C.c_int),
                 ("tok_embd", C.c_void_p), ("output", C.c_void_p), ("output_norm", C.c_void_p),
-                ("n_cells", C.c_int64), ("layers", C.POINTER(Layer))]
+                ("n_cells", C.c_int64), ("layers", C.POINTER(Layer))] + \
+               [(n, C.c_int) for n in ("n_expert", "n_used", "n_ff_exp", "gating", "norm_topk")] + \
+               [("expert_scale", C.c_float)]
 
 
 _lib = None
@@ -144,6 +150,11 @@ def _declare(L):
         "lgmlh_kvpool_stats": ([vp, vp], i32),
         "lgmlh_block_key": ([C.c_char_p, vp, C.c_int32, vp], i32),
         "lgmlh_gen_normal": ([C.c_uint64, i32, i64, i64, C.c_double, C.c_double, vp, vp], i32),
+        "lgmlh_moe_route": ([vp, i64, i32, i32, i32, i32, C.c_float, vp, vp, vp], i32),
+        "lgmlh_mul_mat_id_workspace": ([i32, i64, i64, i64, i64, i64, i32], sz),
+        "lgmlh_mul_mat_id": ([i32, vp, i64, i64, i64, vp, i32, i64, vp, i64, i32, vp, vp, sz, vp],
+                             i32),
+        "lgmlh_moe_sum": ([vp, vp, i64, i32, i64, vp, vp, vp], i32),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)

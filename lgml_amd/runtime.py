@@ -67,10 +67,32 @@ def repack_concat(parts, K):
     return out, ty, M
 
 
+def repack_experts(gate, up, n_expert, K):
+    """n_expert matrices of R rows each (gate: (arr, type) or (dev, type,
+    rows) with n_expert * R rows, expert-major) repacked one after the other,
+    as lgmlh_mul_mat_id takes them; with up given, each expert's matrix is
+    [gate_e | up_e] (2R rows). R must be a multiple of 16."""
+    g, ty, rows = repack_concat([gate], K)
+    R = rows // n_expert
+    assert R * n_expert == rows and R % 16 == 0
+    if up is None:
+        return g, ty
+    u, tyu, _ = repack_concat([up], K)
+    assert tyu == ty, "gate and up experts must share a type"
+    return torch.stack([g.view(n_expert, -1), u.view(n_expert, -1)], 1).reshape(-1), ty
+
+
+def router_sd(hp):
+    """Router weights N(0, 1 / sqrt(n_embd)): logits of a unit-rms h are then
+    N(0, 1) (BASELINE.json's MoE config)."""
+    return 1.0 / float(np.sqrt(hp["n_embd"]))
+
+
 def generated_weights(hp, seed, policy):
     """A weights source for DeviceModel that makes each matrix on the device
-    with lgmlh_gen_normal: N(0, 0.02), one seed per tensor in draw order;
-    norms are 1. policy(name, layer) gives the weight type."""
+    with lgmlh_gen_normal: N(0, 0.02) (the router N(0, 1/sqrt(n_embd))), one
+    seed per tensor in draw order; norms are 1. policy(name, layer) gives
+    the weight type."""
     counter = [0]
 
     def get(name, layer, rows, cols):
@@ -78,7 +100,8 @@ def generated_weights(hp, seed, policy):
         counter[0] += 1
         nb = hip.lib().lgmlh_row_size(ty, cols) * rows
         t = _empty(nb)
-        check(hip.lib().lgmlh_gen_normal(seed * 1000003 + counter[0], ty, rows, cols, 0.0, 0.02,
+        sd = router_sd(hp) if name == "gate_inp" else 0.02
+        check(hip.lib().lgmlh_gen_normal(seed * 1000003 + counter[0], ty, rows, cols, 0.0, sd,
                                          t.data_ptr(), stream()))
         return (t, ty, rows)
 
@@ -148,7 +171,7 @@ class EventTrace:
 
 
 class DeviceModel:
-    """A dense llama / qwen3 model on the device with its paged KV pool."""
+    """A llama / qwen3 / qwen3moe model on the device with its paged KV pool."""
 
     def __init__(self, hp, w, n_cells):
         """w: a weights dict of numpy arrays, or a callable source
@@ -181,14 +204,15 @@ class DeviceModel:
         kvb = L.lgmlh_kv_layer_bytes(self.n_cells, Hkv, D)
         self.kpools, self.vpools = [], []
         self.layers = (hip.Layer * hp["n_layer"])()
+        qk_norm = hp["arch"] in ("qwen3", "qwen3moe")
+        NE = hp.get("n_expert", 0)
         for il in range(hp["n_layer"]):
             Ly = self.layers[il]
             Ly.attn_norm = vec("attn_norm", il, E)
             Ly.ffn_norm = vec("ffn_norm", il, E)
-            if not gen:
-                for nm in ("q_norm", "k_norm"):
-                    if w["layers"][il].get(nm) is not None:
-                        setattr(Ly, nm, vec(nm, il, D))
+            for nm in ("q_norm", "k_norm"):
+                if (gen and qk_norm) or (not gen and w["layers"][il].get(nm) is not None):
+                    setattr(Ly, nm, vec(nm, il, D))
             wq, wk, wv = mat("wq", il, H * D, E), mat("wk", il, Hkv * D, E), mat("wv", il, Hkv * D, E)
             if wv[1] == wq[1] == wk[1]:
                 t, ty, M = repack_concat([wq, wk, wv], E)
@@ -201,10 +225,22 @@ class DeviceModel:
             del wq, wk, wv
             t, ty, _ = repack_concat([mat("wo", il, E, H * D)], H * D)
             Ly.wo, Ly.wo_type = keep(t).data_ptr(), ty
-            t, ty, _ = repack_concat([mat("gate", il, F, E), mat("up", il, F, E)], E)
-            Ly.wgu, Ly.wgu_type = keep(t).data_ptr(), ty
-            t, ty, _ = repack_concat([mat("down", il, E, F)], F)
-            Ly.wdown, Ly.wdown_type = keep(t).data_ptr(), ty
+            if NE:
+                # routed experts: the router stays f32 (convert.lua:135-137)
+                FX = hp["n_ff_exp"]
+                gi = mat("gate_inp", il, NE, E)
+                assert gi[1] == hip.F32, "the router is f32"
+                Ly.gate_inp = keep(gi[0] if gen else _dev(np.asarray(gi[0], np.float32))).data_ptr()
+                t, ty = repack_experts(mat("gate_exps", il, NE * FX, E),
+                                       mat("up_exps", il, NE * FX, E), NE, E)
+                Ly.exp_gu, Ly.exp_gu_type = keep(t).data_ptr(), ty
+                t, ty = repack_experts(mat("down_exps", il, NE * E, FX), None, NE, FX)
+                Ly.exp_down, Ly.exp_down_type = keep(t).data_ptr(), ty
+            else:
+                t, ty, _ = repack_concat([mat("gate", il, F, E), mat("up", il, F, E)], E)
+                Ly.wgu, Ly.wgu_type = keep(t).data_ptr(), ty
+                t, ty, _ = repack_concat([mat("down", il, E, F)], F)
+                Ly.wdown, Ly.wdown_type = keep(t).data_ptr(), ty
             kp, vp = keep(_zeros(kvb)), keep(_zeros(kvb))
             self.kpools.append(kp)
             self.vpools.append(vp)
@@ -227,6 +263,11 @@ class DeviceModel:
         m.output_norm = vec("output_norm", None, E)
         m.n_cells = self.n_cells
         m.layers = self.layers
+        if NE:
+            m.n_expert, m.n_used, m.n_ff_exp = NE, hp["n_used"], hp["n_ff_exp"]
+            m.gating = hp.get("gating", hip.GATING_SOFTMAX)
+            m.norm_topk = int(bool(hp.get("norm_topk", True)))
+            m.expert_scale = hp.get("expert_scale", 1.0)
         self.m = m
         self.ws = None
         self.ws_bytes = 0

@@ -38,7 +38,8 @@ class Tensor(C.Structure):
 
 class Layer(C.Structure):
     _fields_ = [(n, Tensor) for n in ("attn_norm", "wq", "wk", "wv", "wo", "q_norm", "k_norm",
-                                      "ffn_norm", "gate", "up", "down")]
+                                      "ffn_norm", "gate", "up", "down", "gate_inp", "gate_exps",
+                                      "up_exps", "down_exps")]
 
 
 class Model(C.Structure):
@@ -47,7 +48,9 @@ class Model(C.Structure):
                 ("n_vocab", C.c_int), ("n_rot", C.c_int), ("eps", C.c_float),
                 ("rope_base", C.c_float), ("attn_scale", C.c_float), ("rope_neox", C.c_int),
                 ("rope_freqs", C.c_void_p), ("tok_embd", Tensor), ("output", Tensor),
-                ("output_norm", Tensor), ("layers", C.POINTER(Layer))]
+                ("output_norm", Tensor), ("layers", C.POINTER(Layer)),
+                ("n_expert", C.c_int), ("n_used", C.c_int), ("n_ff_exp", C.c_int),
+                ("gating", C.c_int), ("norm_topk", C.c_int), ("expert_scale", C.c_float)]
 
 
 class Batch(C.Structure):
@@ -78,6 +81,8 @@ def _declare(L):
                                       vp, i32]
     L.orc_set_rows_f16.argtypes = [vp, i64, i64, vp, vp, i64]
     L.orc_mul_mat.argtypes = [i32, vp, i64, i64, vp, i64, vp, i32]
+    L.orc_moe_route.argtypes = [vp, i64, i32, i32, i32, i32, C.c_float, vp, vp]
+    L.orc_mul_mat_id.argtypes = [i32, vp, i64, i64, i64, vp, i64, vp, i64, i32, vp, i32]
     L.orc_argmax.argtypes = [vp, i64]
     L.orc_argmax.restype = C.c_int32
 
@@ -186,6 +191,35 @@ def mul_mat(t, w, M, K, x, nthreads=None):
     return y
 
 
+GATING_SOFTMAX, GATING_SIGMOID = 1, 2
+
+
+def moe_route(logits, n_used, gating=GATING_SOFTMAX, norm_topk=True, scale=1.0):
+    """Router picks (ids i32 (n, n_used)) and weights (f32) of logits (n, n_expert)."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    n, ne = lg.shape
+    ids = np.empty((n, n_used), np.int32)
+    w = np.empty((n, n_used), np.float32)
+    if lib().orc_moe_route(_p(lg), n, ne, n_used, gating, int(bool(norm_topk)), scale, _p(ids),
+                           _p(w)) != 0:
+        raise ValueError("moe_route failed")
+    return ids, w
+
+
+def mul_mat_id(t, w, n_expert, M, K, x, ids, nthreads=None):
+    """y (T, n_used, M): row (t, j) = w[ids[t, j]] x[t, j % U], x (T, U, K)."""
+    x = np.ascontiguousarray(x, np.float32)
+    ids = np.ascontiguousarray(ids, np.int32)
+    T, n_used = ids.shape
+    U = x.shape[1] if x.ndim == 3 else 1
+    y = np.empty((T, n_used, M), np.float32)
+    w = np.ascontiguousarray(w)
+    if lib().orc_mul_mat_id(t, _p(w), n_expert, M, K, _p(x), U, _p(ids), T, n_used, _p(y),
+                            nthreads or threads()) != 0:
+        raise ValueError("mul_mat_id failed")
+    return y
+
+
 def argmax(v):
     v = np.ascontiguousarray(v, np.float32)
     return int(lib().orc_argmax(_p(v), v.size))
@@ -259,6 +293,11 @@ class OracleModel:
             self._keep.append(arr)
             setattr(self.c, f, Tensor(ty, _p(arr).value))
         self.c.layers = self.layers
+        for k in ("n_expert", "n_used", "n_ff_exp"):
+            setattr(self.c, k, int(hp.get(k, 0)))
+        self.c.gating = int(hp.get("gating", GATING_SOFTMAX))
+        self.c.norm_topk = int(bool(hp.get("norm_topk", True)))
+        self.c.expert_scale = float(hp.get("expert_scale", 1.0))
 
     def forward(self, kpools, vpools, batch, nthreads=None):
         """kpools/vpools: lists of (cap, Hkv*D) uint16 arrays (f16 bits), updated in place."""

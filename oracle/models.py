@@ -20,16 +20,21 @@ LAYER_KEYS = ("attn_norm", "wq", "wk", "wv", "wo", "q_norm", "k_norm", "ffn_norm
 
 
 def ref_tiny(arch):
-    """The tiny llama / qwen3 of test/test_qwen_moe.lua:66-200 (build()).
+    """The tiny llama / qwen3 / qwen3moe of test/test_qwen_moe.lua:66-200 (build()).
 
     Seed #arch * 7919 (:70); tensors drawn in the order build() lists them
     (:140-195); w(): U(-s, s), s = gain * sqrt(3 / fan_in) (:88-91); norms
     U(0.9, 1.1) (:92-94); llama rope_freqs U(1, 8) x D/2 (:143-147). All
     stored as f32 (gguf.lua:41-50). Shapes: E=64, H=4, HKV=2, D=16,
     FF=2E, 2 layers, vocab 259 (:41-64,66,96-104), eps 1e-6, base 1e6.
+    qwen3moe layers replace the dense FFN by X=8 experts of width F=32,
+    USED=2 picks (:66,116-118,183-191): ffn_gate_inp (X, E) gain 3, then
+    ffn_gate_exps / ffn_up_exps (X, F, E) and ffn_down_exps (X, E, F);
+    softmax gating with norm_topk (transformer.lua:162-165 defaults).
     """
-    assert arch in ("llama", "qwen3")
+    assert arch in ("llama", "qwen3", "qwen3moe")
     E, H, HKV, D = 64, 4, 2, 16
+    X, USED, FX = 8, 2, 32
     nv = 256 + 3
     r = core.Lcg(len(arch) * 7919)
 
@@ -59,14 +64,24 @@ def ref_tiny(arch):
             L["q_norm"] = norm(D)
             L["k_norm"] = norm(D)
         L["ffn_norm"] = norm(E)
-        L["gate"] = w(2 * E, E)
-        L["up"] = w(2 * E, E)
-        L["down"] = w(E, 2 * E)
+        if arch == "qwen3moe":
+            L["gate_inp"] = w(X, E, 3.0)
+            L["gate_exps"] = w(X * FX, E)
+            L["up_exps"] = w(X * FX, E)
+            s = math.sqrt(3.0 / FX)
+            L["down_exps"] = (r.fill(X * E * FX, -s, s).reshape(X * E, FX), core.F32)
+        else:
+            L["gate"] = w(2 * E, E)
+            L["up"] = w(2 * E, E)
+            L["down"] = w(E, 2 * E)
         layers.append(L)
     out["layers"] = layers
     hp = dict(arch=arch, n_layer=2, n_embd=E, n_head=H, n_head_kv=HKV, head_dim=D, n_ff=2 * E,
               n_vocab=nv, n_rot=D, eps=1e-6, rope_base=1e6, rope_neox=0 if arch == "llama" else 1,
               attn_scale=0.0)
+    if arch == "qwen3moe":
+        hp.update(n_expert=X, n_used=USED, n_ff_exp=FX, gating=core.GATING_SOFTMAX,
+                  norm_topk=True, expert_scale=1.0)
     return hp, out
 
 
@@ -78,6 +93,12 @@ SHAPES = {
     # C2: Llama-3-8B shape, Q4_K_M mix, f16 KV.
     "c2": dict(arch="llama", n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128,
                n_ff=14336, n_vocab=128256, rope_base=5e5, eps=1e-5, wtype="q4_K_M"),
+    # C5: a 30B-A3B-shaped qwen3moe (Qwen3-30B-A3B sizes: vocab 151936, rope
+    # base 1e6, eps 1e-6, q/k norms), 128 experts of width 768, top-8
+    # softmax routing with norm_topk; Q4_K weights, f32 router.
+    "c5": dict(arch="qwen3moe", n_layer=48, n_embd=2048, n_head=32, n_head_kv=4, head_dim=128,
+               n_ff=768, n_vocab=151936, rope_base=1e6, eps=1e-6, wtype="q4_K", n_expert=128,
+               n_used=8, n_ff_exp=768, gating=1, norm_topk=True, expert_scale=1.0),
 }
 
 
@@ -87,9 +108,10 @@ def more_bits(i, n):
 
 
 def weight_type(wtype, name, layer, n_layer):
-    """lua/lgml/convert.lua:128-165 policies: 1-D tensors stay f32; q4_K_M
-    gives output Q6_K and attn_v / ffn_down Q6_K on more_bits layers."""
-    if wtype == "f32":
+    """lua/lgml/convert.lua:128-165 policies: 1-D tensors and the router
+    stay f32; q4_K_M gives output Q6_K and attn_v / ffn_down (also the
+    expert ffn_down_exps) Q6_K on more_bits layers."""
+    if wtype == "f32" or name == "gate_inp":
         return core.F32
     if wtype == "q8_0":
         return core.Q8_0
@@ -98,7 +120,7 @@ def weight_type(wtype, name, layer, n_layer):
     if wtype == "q4_K_M":
         if name == "output":
             return core.Q6_K
-        if layer is not None and name in ("wv", "down") and more_bits(layer, n_layer):
+        if layer is not None and name in ("wv", "down", "down_exps") and more_bits(layer, n_layer):
             return core.Q6_K
         return core.Q4_K
     raise ValueError(wtype)
@@ -111,7 +133,8 @@ def build(shape, seed=1234, n_layer=None, init="uniform"):
     norms U(0.9, 1.1), drawn from the reference LCG.
     init "normal": N(0, 0.02) weights from the reference splitmix64 +
     Box-Muller fill (src/lgml.c:3130-3136), one seed per tensor (seed + i),
-    norms 1.0; quantized per the shape's weight policy.
+    norms 1.0; quantized per the shape's weight policy. A MoE router is
+    N(0, 1/sqrt(n_embd)), so that the logits of a unit-rms row are N(0, 1).
     n_layer overrides the depth (reduced-depth parity runs keep the width).
     """
     hp = dict(SHAPES[shape]) if isinstance(shape, str) else dict(shape)
@@ -136,9 +159,10 @@ def build(shape, seed=1234, n_layer=None, init="uniform"):
         else:
             counter[0] += 1
             tseed = seed * 1000003 + counter[0]
+            sd = 1.0 / math.sqrt(E) if name == "gate_inp" else 0.02
             if ty == core.F32:
-                return (core.gen_normal(rows * cols, 0.0, 0.02, tseed).reshape(rows, cols), ty)
-            return (core.gen_normal_quant(ty, rows, cols, 0.0, 0.02, tseed), ty)
+                return (core.gen_normal(rows * cols, 0.0, sd, tseed).reshape(rows, cols), ty)
+            return (core.gen_normal_quant(ty, rows, cols, 0.0, sd, tseed), ty)
         if ty == core.F32:
             return (x, ty)
         return (core.quantize(ty, x), ty)
@@ -161,10 +185,20 @@ def build(shape, seed=1234, n_layer=None, init="uniform"):
         L["wk"] = mat("wk", Hkv * D, E, il)
         L["wv"] = mat("wv", Hkv * D, E, il)
         L["wo"] = mat("wo", E, H * D, il)
+        if hp["arch"] in ("qwen3", "qwen3moe"):
+            L["q_norm"] = norm(D)
+            L["k_norm"] = norm(D)
         L["ffn_norm"] = norm(E)
-        L["gate"] = mat("gate", F, E, il)
-        L["up"] = mat("up", F, E, il)
-        L["down"] = mat("down", E, F, il)
+        if hp.get("n_expert"):
+            NE, FX = hp["n_expert"], hp["n_ff_exp"]
+            L["gate_inp"] = mat("gate_inp", NE, E, il)
+            L["gate_exps"] = mat("gate_exps", NE * FX, E, il)
+            L["up_exps"] = mat("up_exps", NE * FX, E, il)
+            L["down_exps"] = mat("down_exps", NE * E, FX, il)
+        else:
+            L["gate"] = mat("gate", F, E, il)
+            L["up"] = mat("up", F, E, il)
+            L["down"] = mat("down", E, F, il)
         layers.append(L)
     w["layers"] = layers
     return hp, w

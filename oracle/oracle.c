@@ -699,6 +699,114 @@ orc_paged_attention(const float *q, const uint16_t *kpool, const uint16_t *vpool
 	return bad ? -1 : 0;
 }
 
+int
+orc_moe_route(const float *logits, int64_t n, int n_expert, int n_used, int gating,
+    int norm_topk, float scale, int32_t *ids, float *w)
+{
+	if (n_expert <= 0 || n_used < 1 || n_used > n_expert ||
+	    (gating != ORC_GATING_SOFTMAX && gating != ORC_GATING_SIGMOID))
+		return -1;
+	float *p = malloc(sizeof(float) * (size_t)n_expert);
+	char *taken = malloc((size_t)n_expert);
+	if (!p || !taken) {
+		free(p);
+		free(taken);
+		return -1;
+	}
+	for (int64_t t = 0; t < n; t++) {
+		const float *l = logits + t * n_expert;
+		/* probs: ggml soft_max / sigmoid of the row */
+		if (gating == ORC_GATING_SOFTMAX) {
+			double mx = -INFINITY, sum = 0;
+			for (int e = 0; e < n_expert; e++)
+				if (l[e] > mx)
+					mx = l[e];
+			for (int e = 0; e < n_expert; e++)
+				sum += exp((double)l[e] - mx);
+			for (int e = 0; e < n_expert; e++)
+				p[e] = (float)(exp((double)l[e] - mx) / sum);
+		} else {
+			for (int e = 0; e < n_expert; e++)
+				p[e] = (float)(1.0 / (1.0 + exp(-(double)l[e])));
+		}
+		/* argsort_top_k: the n_used largest, largest first */
+		memset(taken, 0, (size_t)n_expert);
+		for (int j = 0; j < n_used; j++) {
+			int best = -1;
+			for (int e = 0; e < n_expert; e++)
+				if (!taken[e] && (best < 0 || l[e] > l[best]))
+					best = e;
+			taken[best] = 1;
+			ids[t * n_used + j] = best;
+			w[t * n_used + j] = p[best];
+		}
+		/* w / clamp(sum_rows(w), 6.103515625e-5, inf) (:2003-2005) */
+		if (norm_topk) {
+			double s = 0;
+			for (int j = 0; j < n_used; j++)
+				s += w[t * n_used + j];
+			float sf = (float)s;
+			if (sf < 6.103515625e-5f)
+				sf = 6.103515625e-5f;
+			for (int j = 0; j < n_used; j++)
+				w[t * n_used + j] = w[t * n_used + j] / sf;
+		}
+		if (scale != 1.0f)
+			for (int j = 0; j < n_used; j++)
+				w[t * n_used + j] = w[t * n_used + j] * scale;
+	}
+	free(p);
+	free(taken);
+	return 0;
+}
+
+/* The picks of each expert gathered into one orc_mul_mat call, so each
+ * expert row is dequantized once per call. */
+int
+orc_mul_mat_id(int type, const void *w, int64_t n_expert, int64_t M, int64_t K,
+    const float *x, int64_t U, const int32_t *ids, int64_t T, int n_used, float *y,
+    int n_threads)
+{
+	int64_t rs = orc_row_size(type, K), P = T * n_used;
+	int rc = 0;
+
+	if (rs <= 0 || U < 1 || n_used % U)
+		return -1;
+	for (int64_t p = 0; p < P; p++)
+		if (ids[p] < 0 || ids[p] >= n_expert)
+			return -1;
+	float *xg = malloc(sizeof(float) * (size_t)(P * K + 1));
+	float *yg = malloc(sizeof(float) * (size_t)(P * M + 1));
+	int64_t *which = malloc(sizeof(int64_t) * (size_t)(P + 1));
+	if (!xg || !yg || !which) {
+		rc = -1;
+		goto done;
+	}
+	for (int64_t e = 0; e < n_expert; e++) {
+		int64_t c = 0;
+		for (int64_t p = 0; p < P; p++) {
+			if (ids[p] != e)
+				continue;
+			int64_t t = p / n_used, j = p % n_used;
+			memcpy(xg + c * K, x + (t * U + j % U) * K, sizeof(float) * (size_t)K);
+			which[c++] = p;
+		}
+		if (!c)
+			continue;
+		if (orc_mul_mat(type, (const uint8_t *)w + e * M * rs, M, K, xg, c, yg, n_threads)) {
+			rc = -1;
+			goto done;
+		}
+		for (int64_t i = 0; i < c; i++)
+			memcpy(y + which[i] * M, yg + i * M, sizeof(float) * (size_t)M);
+	}
+done:
+	free(xg);
+	free(yg);
+	free(which);
+	return rc;
+}
+
 int32_t
 orc_argmax(const float *v, int64_t n)
 {
@@ -728,11 +836,63 @@ mm(const orc_tensor *w, int64_t M, int64_t K, const float *x, int64_t N, float *
 	return orc_mul_mat(w->type, w->data, M, K, x, N, y, nt);
 }
 
+/* The routed-expert FFN (transformer.lua:2054-2068 with M.moe :1989-2027,
+ * experts :1875-1889, sum_picks :1894-1910) on the normed rows h; adds
+ * the weighted sum of the picks to x (the residual add of :2079). */
+static int
+moe_ffn(const orc_model *m, const orc_layer *L, const float *h, int64_t N, float *x, int nt)
+{
+	const int64_t E = m->n_embd, NE = m->n_expert, K = m->n_used, F = m->n_ff_exp;
+	const int64_t P = N * K;
+	int rc = -1;
+	float *lg = malloc(sizeof(float) * (size_t)(N * NE));
+	int32_t *ids = malloc(sizeof(int32_t) * (size_t)P);
+	float *w = malloc(sizeof(float) * (size_t)P);
+	float *g = malloc(sizeof(float) * (size_t)(P * F));
+	float *u = malloc(sizeof(float) * (size_t)(P * F));
+	float *dn = malloc(sizeof(float) * (size_t)(P * E));
+
+	if (!lg || !ids || !w || !g || !u || !dn)
+		goto done;
+	if (mm(&L->gate_inp, NE, E, h, N, lg, nt) ||
+	    orc_moe_route(lg, N, (int)NE, (int)K, m->gating, m->norm_topk, m->expert_scale, ids, w) ||
+	    orc_mul_mat_id(L->gate_exps.type, L->gate_exps.data, NE, F, E, h, 1, ids, N, (int)K, g,
+	    nt) ||
+	    orc_mul_mat_id(L->up_exps.type, L->up_exps.data, NE, F, E, h, 1, ids, N, (int)K, u, nt))
+		goto done;
+	/* swiglu_split: silu(gate) * up */
+	for (int64_t i = 0; i < P * F; i++) {
+		double gv = g[i];
+		g[i] = (float)(gv / (1.0 + exp(-gv)) * (double)u[i]);
+	}
+	if (orc_mul_mat_id(L->down_exps.type, L->down_exps.data, NE, E, F, g, K, ids, N, (int)K, dn,
+	    nt))
+		goto done;
+	/* mul by the weights, then the picks added in order, then x */
+	for (int64_t t = 0; t < N; t++)
+		for (int64_t e = 0; e < E; e++) {
+			double s = 0;
+			for (int64_t j = 0; j < K; j++)
+				s += (double)(dn[(t * K + j) * E + e] * w[t * K + j]);
+			x[t * E + e] = (float)s + x[t * E + e];
+		}
+	rc = 0;
+done:
+	free(lg);
+	free(ids);
+	free(w);
+	free(g);
+	free(u);
+	free(dn);
+	return rc;
+}
+
 /* transformer.lua:2285-2365 (forward) with qkv (:1754-1789), the batched
  * attention (:2389-2416: set_rows into the pool, then attend per
  * sequence), attn_out (:1859-1872), ffn (:2042-2080, SwiGLU), and head
- * (:2094-2104) on the rows of logit_rows (:2349-2350). Dense llama / qwen3
- * layers; every matrix is an f32 or quantized weight. */
+ * (:2094-2104) on the rows of logit_rows (:2349-2350). llama / qwen3
+ * layers with a dense FFN, or qwen3moe layers with routed experts
+ * (moe_ffn); every matrix is an f32 or quantized weight. */
 int
 orc_forward(const orc_model *m, uint16_t *const *kpool, uint16_t *const *vpool,
     int64_t cap, const orc_batch *b, float *logits, int nt)
@@ -811,6 +971,13 @@ orc_forward(const orc_model *m, uint16_t *const *kpool, uint16_t *const *vpool,
 			x[i] = tmp[i] + x[i];
 		for (int64_t t = 0; t < N; t++)
 			rms_norm_row(x + t * E, cur + t * E, E, m->eps, (const float *)L->ffn_norm.data);
+		if (L->gate_inp.data) {
+			if (moe_ffn(m, L, cur, N, x, nt)) {
+				rc = -6;
+				goto done;
+			}
+			continue;
+		}
 		if (mm(&L->gate, F, E, cur, N, g, nt) || mm(&L->up, F, E, cur, N, u, nt)) {
 			rc = -3;
 			goto done;

@@ -63,7 +63,15 @@ typedef struct {
 
 typedef struct {
 	orc_tensor attn_norm, wq, wk, wv, wo, q_norm, k_norm, ffn_norm, gate, up, down;
+	/* Routed experts (qwen3moe): gate_inp (n_expert, n_embd) router;
+	 * gate_exps / up_exps n_expert matrices (n_ff_exp, n_embd), down_exps
+	 * n_expert matrices (n_embd, n_ff_exp), each expert's rows contiguous.
+	 * A layer with gate_inp.data set has no dense FFN. */
+	orc_tensor gate_inp, gate_exps, up_exps, down_exps;
 } orc_layer;
+
+/* Expert gating functions (transformer.lua:32-35). */
+enum { ORC_GATING_SOFTMAX = 1, ORC_GATING_SIGMOID = 2 };
 
 typedef struct {
 	int n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab, n_rot;
@@ -72,6 +80,10 @@ typedef struct {
 	const float *rope_freqs;          /* n_rot/2 factors or NULL */
 	orc_tensor tok_embd, output, output_norm;
 	const orc_layer *layers;
+	/* MoE hyperparameters (transformer.lua:160-170): experts, picks per
+	 * token, expert FFN width, gating, norm_topk, expert_scale. */
+	int n_expert, n_used, n_ff_exp, gating, norm_topk;
+	float expert_scale;
 } orc_model;
 
 /* One ubatch over a paged pool. Sequence s owns tokens
@@ -106,6 +118,23 @@ int orc_set_rows_f16(uint16_t *dst, int64_t dst_rows, int64_t row, const float *
  * src/lgml.c:1811-1839). f64 accumulation. */
 int orc_mul_mat(int type, const void *w, int64_t M, int64_t K, const float *x, int64_t N,
     float *y, int n_threads);
+
+/* The router of M.moe (transformer.lua:1998-2008): probs = soft_max (or
+ * sigmoid) of each logits row (n_expert values, f64 sums); ids = the
+ * n_used largest, largest first (argsort_top_k, src/ops_nn.c:266-286),
+ * chosen on the logits (the gating is monotone), ties to the smaller
+ * index; w = probs[ids], divided by max(sum, 6.103515625e-5) when
+ * norm_topk, then times scale. ids, w: (n, n_used). */
+int orc_moe_route(const float *logits, int64_t n, int n_expert, int n_used, int gating,
+    int norm_topk, float scale, int32_t *ids, float *w);
+
+/* ggml_mul_mat_id via graph:mul_mat_id (src/ops_nn.c:322-362): w holds
+ * n_expert matrices (M, K) of `type`; row (t, j) of y (T, n_used, M) is
+ * w[ids[t][j]] times x[t][j % U] (x is (T, U, K)). f64 accumulation.
+ * Returns -1 on an id outside [0, n_expert). */
+int orc_mul_mat_id(int type, const void *w, int64_t n_expert, int64_t M, int64_t K,
+    const float *x, int64_t U, const int32_t *ids, int64_t T, int n_used, float *y,
+    int n_threads);
 
 /* Greedy first-max argmax (src/sample.c:914-925). */
 int32_t orc_argmax(const float *v, int64_t n);

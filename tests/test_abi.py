@@ -35,7 +35,63 @@ def test_exports_every_declared_symbol(hip):
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing
     assert sorted(hip.SYMBOLS) == names
-    assert L.lgmlh_abi_version() == 2
+    assert L.lgmlh_abi_version() == 3
+
+
+def test_struct_layouts_match_the_header(hip, tmp_path):
+    """The ctypes mirrors of lgmlh_layer / lgmlh_model / lgmlh_ubatch /
+    lgmlh_plan_info have the C layout (gcc on the header: size and every
+    field offset)."""
+    import shutil
+    import subprocess
+    if not shutil.which("gcc"):
+        pytest.skip("no gcc")
+    structs = {"lgmlh_layer": hip.Layer, "lgmlh_model": hip.Model, "lgmlh_ubatch": hip.Ubatch,
+               "lgmlh_plan_info": hip.PlanInfo, "lgmlh_trace": hip.Trace}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "lgml_hip.h"',
+             'int main(void) {']
+    for cn, py in structs.items():
+        lines.append('printf("%s %%zu\\n", sizeof(%s));' % (cn, cn))
+        for f, _ in py._fields_:
+            lines.append('printf("%s.%s %%zu\\n", offsetof(%s, %s));' % (cn, f, cn, f))
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)],
+                   check=True)
+    out = dict(l.split() for l in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                 check=True).stdout.splitlines())
+    for cn, py in structs.items():
+        assert int(out[cn]) == C.sizeof(py), cn
+        for f, _ in py._fields_:
+            assert int(out["%s.%s" % (cn, f)]) == getattr(py, f).offset, (cn, f)
+
+
+def test_moe_entry_points_check_arguments(hip):
+    """Host-side argument checks of the MoE entry points (no GPU work)."""
+    L = hip.lib()
+    # the grouping and the split X grow with the picks; f32 needs no split X
+    a = L.lgmlh_mul_mat_id_workspace(hip.Q4_K, 128, 1536, 2048, 64, 1, 8)
+    b = L.lgmlh_mul_mat_id_workspace(hip.Q4_K, 128, 1536, 2048, 128, 1, 8)
+    f = L.lgmlh_mul_mat_id_workspace(hip.F32, 128, 1536, 2048, 64, 1, 8)
+    assert 0 < f < a < b
+    dummy = C.c_void_p(16)
+    # bad shapes / types are refused before any device work
+    assert L.lgmlh_mul_mat_id(hip.Q4_K, dummy, 128, 768, 100, dummy, hip.F32, 1, dummy, 4, 8,
+                              dummy, dummy, 1 << 30, None) == hip.EINVAL
+    assert b"256" in L.lgmlh_last_error()
+    assert L.lgmlh_mul_mat_id(hip.Q4_K, dummy, 1000, 768, 256, dummy, hip.F32, 1, dummy, 4, 8,
+                              dummy, dummy, 1 << 30, None) == hip.EINVAL
+    assert L.lgmlh_mul_mat_id(hip.Q4_K, dummy, 128, 768, 256, dummy, hip.F32, 3, dummy, 4, 8,
+                              dummy, dummy, 1 << 30, None) == hip.EINVAL
+    assert L.lgmlh_mul_mat_id(hip.Q4_K, dummy, 128, 768, 256, dummy, hip.F32, 1, dummy, 4, 8,
+                              dummy, dummy, 16, None) == hip.ENOMEM
+    assert L.lgmlh_mul_mat_id(hip.Q4_K, dummy, 128, 768, 256, dummy, hip.F32, 1, dummy, 2000, 8,
+                              dummy, dummy, 1 << 30, None) == hip.EINVAL
+    assert L.lgmlh_moe_route(dummy, 4, 128, 17, 1, 1, 1.0, dummy, dummy, None) == hip.EINVAL
+    assert L.lgmlh_moe_route(dummy, 4, 128, 8, 3, 1, 1.0, dummy, dummy, None) == hip.EINVAL
+    assert L.lgmlh_moe_route(dummy, 4, 4, 8, 1, 1, 1.0, dummy, dummy, None) == hip.EINVAL
 
 
 def test_sizes(hip):

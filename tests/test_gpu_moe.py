@@ -1,0 +1,169 @@
+"""GPU parity of the routed-expert path (C5) against
+the CPU oracle, through the C ABI.
+
+Routing (lgmlh_moe_route): ids bit-exact on the same logits (ties to the
+smaller index), weights within 1e-6. Grouped expert products
+(lgmlh_mul_mat_id): within 2e-3 max relative error of the oracle's f64
+result (they meet 1e-5: exact weights, f16 hi + lo activations), every
+weight type, U = 1 and U = n_used, the decode (16-column) and prefill
+(64-column) groupings, an expert picked twice by one token, ids out of range
+(rows of zeros). A pick's row is the same bits alone or in any batch. Whole
+C5-shaped passes at reduced depth (2 of 48 layers, full width) on ragged
+batches: logits within 2e-3, identical greedy ids, batched == lone.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import core, models
+from tests.gpu_util import Schedule, lcg_ints, rel_err
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def L():
+    from lgml_amd import hip
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    return hip.lib()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+def st():
+    return torch.cuda.current_stream().cuda_stream
+
+
+@pytest.mark.parametrize("ne,k,gating,norm,scale,n", [
+    (128, 8, 1, 1, 1.0, 64), (128, 8, 1, 1, 1.0, 512), (8, 2, 1, 1, 1.0, 5), (60, 4, 1, 0, 1.0, 33),
+    (128, 8, 2, 1, 2.5, 64), (512, 16, 1, 1, 1.0, 64), (3, 1, 1, 1, 1.0, 7)])
+def test_route_matches_oracle(L, ne, k, gating, norm, scale, n):
+    from lgml_amd import hip
+    rng = np.random.default_rng(ne + 7 * k + n)
+    lg = rng.standard_normal((n, ne)).astype(np.float32)
+    lg[0, :] = 0.25                                  # all tied
+    if ne >= 4:
+        lg[1, 1] = lg[1, 3] = lg[1].max() + 1.0      # a tie at the top
+    ids = torch.empty((n, k), dtype=torch.int32, device="cuda")
+    w = torch.empty((n, k), dtype=torch.float32, device="cuda")
+    hip.check(L.lgmlh_moe_route(dev(lg).data_ptr(), n, ne, k, gating, norm, scale,
+                                ids.data_ptr(), w.data_ptr(), st()))
+    oi, ow = core.moe_route(lg, k, gating, bool(norm), scale)
+    gi, gw = ids.cpu().numpy(), w.cpu().numpy()
+    assert np.array_equal(gi, oi)
+    np.testing.assert_allclose(gw, ow, rtol=1e-6, atol=1e-7)
+
+
+def repacked_experts(L, ty, wq, NE, M, K):
+    """n_expert matrices repacked back to back, as lgmlh_mul_mat_id takes them."""
+    from lgml_amd import hip
+    if ty == hip.F32:
+        return dev(wq)
+    eb = L.lgmlh_repacked_bytes(ty, M, K)
+    out = torch.empty(NE * eb, dtype=torch.uint8, device="cuda")
+    src = dev(wq)
+    hip.check(L.lgmlh_repack(ty, NE * M, K, src.data_ptr(), out.data_ptr(), st()))
+    torch.cuda.synchronize()
+    return out
+
+
+def run_id(L, ty, w_dev, NE, M, K, x, ids):
+    from lgml_amd import hip
+    T, k = ids.shape
+    U = x.shape[1]
+    y = torch.full((T, k, M), float("nan"), dtype=torch.float32, device="cuda")
+    nb = L.lgmlh_mul_mat_id_workspace(ty, NE, M, K, T, U, k)
+    ws = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda")
+    hip.check(L.lgmlh_mul_mat_id(ty, w_dev.data_ptr(), NE, M, K, dev(x).data_ptr(), hip.F32, U,
+                                 dev(ids).data_ptr(), T, k, y.data_ptr(), ws.data_ptr(), nb, st()))
+    return y.cpu().numpy()
+
+
+@pytest.mark.parametrize("ty", [core.Q4_K, core.Q6_K, core.Q8_0, core.F32])
+@pytest.mark.parametrize("T,U", [(64, 1), (64, 8), (600, 1)])
+def test_mul_mat_id_matches_oracle(L, ty, T, U):
+    NE, k = 128, 8
+    M, K = (256, 512) if ty != core.F32 else (64, 96)
+    rng = np.random.default_rng(ty * 1000 + T + U)
+    wf = (rng.standard_normal((NE * M, K)) * 0.02).astype(np.float32)
+    wq = wf if ty == core.F32 else core.quantize(ty, wf)
+    x = rng.standard_normal((T, U, K)).astype(np.float32)
+    ids = np.stack([rng.choice(NE, k, replace=False) for _ in range(T)]).astype(np.int32)
+    ids[0, :3] = [5, 5, 5]   # one expert picked three times by a token
+    ids[1, :] = np.arange(k)
+    w_dev = repacked_experts(L, ty, wq, NE, M, K)
+    got = run_id(L, ty, w_dev, NE, M, K, x, ids)
+    want = core.mul_mat_id(ty, wq, NE, M, K, x, ids)
+    assert rel_err(got.reshape(T * k, M), want.reshape(T * k, M)) < 1e-5
+    # a token alone gives the same bits as in the batch
+    one = run_id(L, ty, w_dev, NE, M, K, x[3:4], ids[3:4])
+    assert np.array_equal(one[0].view(np.uint32), got[3].view(np.uint32))
+
+
+def test_mul_mat_id_bad_ids_give_zero_rows(L):
+    NE, M, K, T, k = 16, 64, 256, 8, 2
+    rng = np.random.default_rng(5)
+    wq = core.quantize(core.Q4_K, (rng.standard_normal((NE * M, K)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((T, 1, K)).astype(np.float32)
+    ids = rng.integers(0, NE, size=(T, k)).astype(np.int32)
+    ids[2, 1], ids[5, 0] = -1, NE
+    got = run_id(L, core.Q4_K, repacked_experts(L, core.Q4_K, wq, NE, M, K), NE, M, K, x, ids)
+    assert not got[2, 1].any() and not got[5, 0].any()
+    ok = ids.copy()
+    ok[2, 1], ok[5, 0] = 0, 0
+    want = core.mul_mat_id(core.Q4_K, wq, NE, M, K, x, ok)
+    mask = np.ones((T, k), bool)
+    mask[2, 1] = mask[5, 0] = False
+    assert rel_err(got[mask], want[mask]) < 1e-5
+
+
+def test_moe_sum(L):
+    from lgml_amd import hip
+    rng = np.random.default_rng(9)
+    T, k, M = 13, 8, 2048
+    y = rng.standard_normal((T, k, M)).astype(np.float32)
+    w = rng.random((T, k)).astype(np.float32)
+    r = rng.standard_normal((T, M)).astype(np.float32)
+    out = torch.empty((T, M), dtype=torch.float32, device="cuda")
+    hip.check(L.lgmlh_moe_sum(dev(y).data_ptr(), dev(w).data_ptr(), T, k, M, dev(r).data_ptr(),
+                              out.data_ptr(), st()))
+    want = (y.astype(np.float64) * w[:, :, None]).sum(axis=1) + r
+    np.testing.assert_allclose(out.cpu().numpy(), want, rtol=1e-5, atol=1e-5)
+
+
+def c5_run(hp, w, prompts, steps, n_cells=2048):
+    from lgml_amd import runtime
+    from tests.test_gpu_model import run_both
+    return run_both(hp, w, n_cells, prompts, steps)
+
+
+def test_c5_shape_reduced_depth_ragged_passes():
+    """C5 width (2048, 32/4 heads, 128 experts x 768, top-8) at 2 of 48 layers:
+    a ragged prefill of 6 sequences, then 3 batched decode steps."""
+    hp, w = models.build("c5", seed=5, n_layer=2, init="normal")
+    lens = [5, 70, 1, 130, 33, 64]
+    prompts = [lcg_ints(5000 + i, n, 0, hp["n_vocab"]) for i, n in enumerate(lens)]
+    errs, same, tg, to, *_ = c5_run(hp, w, prompts, 3)
+    assert max(errs) < 2e-3, errs
+    assert same, (tg, to)
+
+
+def test_c5_batched_pass_equals_lone_pass():
+    from lgml_amd import runtime
+    hp, w = models.build("c5", seed=6, n_layer=1, init="normal")
+    gm = runtime.DeviceModel(hp, w, 1024)
+    prompts = [lcg_ints(6000 + i, n, 0, hp["n_vocab"]) for i, n in enumerate([9, 40, 3])]
+    sch = Schedule(16, 3)
+    for s, p in enumerate(prompts):
+        sch.grow(s, len(p) + 1)
+    bt = sch.table([0, 1, 2])
+    ids = np.concatenate([np.array(p, np.int32) for p in prompts])
+    lb = gm.forward(gm.plan([9, 40, 3], [0, 0, 0], bt, ids)).cpu().numpy()
+    for s, p in enumerate(prompts):
+        la = gm.forward(gm.plan([len(p)], [0], bt[s:s + 1], np.array(p, np.int32)))
+        assert np.array_equal(la.cpu().numpy()[0].view(np.uint32), lb[s].view(np.uint32))

@@ -1,6 +1,6 @@
 """Pins the CPU oracle against the reference's llama.cpp golden rows.
 
-REF.llama / REF.qwen3 (test/test_qwen_moe.lua:202-241, fixture
+REF.llama / REF.qwen3 / REF.qwen3moe (test/test_qwen_moe.lua:202-273, fixture
 tests/golden/ref_logits.json): logits at 8 vocab indices plus the argmax of
 14 rows (two prompt batches, then 6 greedy decode ids), TOL 2e-3 absolute
 max error and argmax on every row (test_qwen_moe.lua:378-400,1019-1023).
@@ -36,7 +36,7 @@ def run_rows(arch, block_tab=None, cap=64, block=64):
     return d, ref, rows
 
 
-@pytest.mark.parametrize("arch", ["llama", "qwen3"])
+@pytest.mark.parametrize("arch", ["llama", "qwen3", "qwen3moe"])
 def test_oracle_matches_llama_cpp_rows(oracle_lib, arch):
     d, ref, rows = run_rows(arch)
     idx = [i - 1 for i in d["idx_1based"]]
