@@ -78,8 +78,9 @@ def test_kv_store_gather_bit_exact(L):
     for which, pool in ((0, kp), (1, vp)):
         def g(c):
             o = torch.empty((64, Hkv * D), dtype=torch.int16, device="cuda")
+            cd = dev(c)
             hip.check(L.lgmlh_kv_gather(pool.data_ptr(), which, cells_n, Hkv, D,
-                                        dev(c).data_ptr(), 64, o.data_ptr(), st()))
+                                        cd.data_ptr(), 64, o.data_ptr(), st()))
             return o.cpu().numpy()
         a, b = g(sc), g(dcs)
         assert np.array_equal(a[:37], b[:37]) and np.all(b[37:] == 0)
@@ -105,7 +106,8 @@ def test_dequantize_bit_exact(L, ty):
                 raw[:, o + 2:o + 4] = np.frombuffer(np.float16(0.003).tobytes(), np.uint8)
     for data in (q, raw):
         out = torch.empty((M, K), dtype=torch.float32, device="cuda")
-        hip.check(L.lgmlh_dequantize(ty, dev(data).data_ptr(), M, K, out.data_ptr(), st()))
+        dd = dev(data)
+        hip.check(L.lgmlh_dequantize(ty, dd.data_ptr(), M, K, out.data_ptr(), st()))
         want = core.dequantize(ty, data, K)
         assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
@@ -115,7 +117,8 @@ def run_mul_mat(L, ty, w, M, K, x, xtype=None):
     N = x.shape[0]
     nb = L.lgmlh_repacked_bytes(ty, M, K)
     rp = torch.empty(nb, dtype=torch.uint8, device="cuda")
-    hip.check(L.lgmlh_repack(ty, M, K, dev(w).data_ptr(), rp.data_ptr(), st()))
+    wd = dev(w)
+    hip.check(L.lgmlh_repack(ty, M, K, wd.data_ptr(), rp.data_ptr(), st()))
     ws_n = L.lgmlh_mul_mat_workspace(ty, M, K, N)
     ws = torch.zeros(max(ws_n, 1), dtype=torch.uint8, device="cuda")
     y = torch.empty((N, M), dtype=torch.float32, device="cuda")
@@ -159,12 +162,14 @@ def test_mul_mat_f32_input_and_residual(L):
     assert np.array_equal(y16, y32)  # an f16 x is the f32 x with a zero lo part
     nb = L.lgmlh_repacked_bytes(core.Q4_K, M, K)
     rp = torch.empty(nb, dtype=torch.uint8, device="cuda")
-    hip.check(L.lgmlh_repack(core.Q4_K, M, K, dev(w).data_ptr(), rp.data_ptr(), st()))
+    wd = dev(w)
+    hip.check(L.lgmlh_repack(core.Q4_K, M, K, wd.data_ptr(), rp.data_ptr(), st()))
     res = core.fill_normal(N * M, 0, 1, 11).reshape(N, M)
     yd = dev(res.copy())
     ws_n = L.lgmlh_mul_mat_workspace(core.Q4_K, M, K, N)
     ws = torch.zeros(max(ws_n, 1), dtype=torch.uint8, device="cuda")
-    hip.check(L.lgmlh_mul_mat(core.Q4_K, rp.data_ptr(), M, K, dev(x).data_ptr(), hip.F32, N,
+    xd = dev(x)
+    hip.check(L.lgmlh_mul_mat(core.Q4_K, rp.data_ptr(), M, K, xd.data_ptr(), hip.F32, N,
                               yd.data_ptr(), hip.EPI_ADD, yd.data_ptr(), ws.data_ptr(), ws_n,
                               st()))
     assert np.array_equal(yd.cpu().numpy(), (y32 + res).astype(np.float32))
@@ -204,14 +209,15 @@ def gpu_attention(L, q, kpool_rows, vpool_rows, H, Hkv, D, seqs, bt, bps=0, n_ce
     allc = np.arange(n_cells, dtype=np.int64)
     kf = dev(core.f16_bits_to_f32(kpool_rows))
     vf = dev(core.f16_bits_to_f32(vpool_rows))
+    cd = dev(allc)
     hip.check(L.lgmlh_kv_store(kp.data_ptr(), vp.data_ptr(), n_cells, Hkv, D, kf.data_ptr(),
-                               vf.data_ptr(), dev(allc).data_ptr(), allc.ctypes.data, n_cells,
-                               st()))
+                               vf.data_ptr(), cd.data_ptr(), allc.ctypes.data, n_cells, st()))
     out = torch.full(q.shape, float("nan"), dtype=torch.float32, device="cuda")
     wsb = L.lgmlh_attention_workspace(C.byref(plan.info), D)
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
     scale = 1.0 / np.sqrt(D)
-    hip.check(L.lgmlh_paged_attention(dev(q).data_ptr(), H, Hkv, D, scale, kp.data_ptr(),
+    qd = dev(q)
+    hip.check(L.lgmlh_paged_attention(qd.data_ptr(), H, Hkv, D, scale, kp.data_ptr(),
                                       vp.data_ptr(), C.byref(plan.ub), out.data_ptr(),
                                       ws.data_ptr(), wsb, st()))
     return out.cpu().numpy(), plan

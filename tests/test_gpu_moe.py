@@ -51,7 +51,8 @@ def test_route_matches_oracle(L, ne, k, gating, norm, scale, n):
         lg[1, 1] = lg[1, 3] = lg[1].max() + 1.0      # a tie at the top
     ids = torch.empty((n, k), dtype=torch.int32, device="cuda")
     w = torch.empty((n, k), dtype=torch.float32, device="cuda")
-    hip.check(L.lgmlh_moe_route(dev(lg).data_ptr(), n, ne, k, gating, norm, scale,
+    lgd = dev(lg)  # held: a temporary's memory could be reused before the kernel runs
+    hip.check(L.lgmlh_moe_route(lgd.data_ptr(), n, ne, k, gating, norm, scale,
                                 ids.data_ptr(), w.data_ptr(), st()))
     oi, ow = core.moe_route(lg, k, gating, bool(norm), scale)
     gi, gw = ids.cpu().numpy(), w.cpu().numpy()
@@ -79,8 +80,9 @@ def run_id(L, ty, w_dev, NE, M, K, x, ids):
     y = torch.full((T, k, M), float("nan"), dtype=torch.float32, device="cuda")
     nb = L.lgmlh_mul_mat_id_workspace(ty, NE, M, K, T, U, k)
     ws = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda")
-    hip.check(L.lgmlh_mul_mat_id(ty, w_dev.data_ptr(), NE, M, K, dev(x).data_ptr(), hip.F32, U,
-                                 dev(ids).data_ptr(), T, k, y.data_ptr(), ws.data_ptr(), nb, st()))
+    xd, idd = dev(x), dev(ids)  # held until the kernels have run
+    hip.check(L.lgmlh_mul_mat_id(ty, w_dev.data_ptr(), NE, M, K, xd.data_ptr(), hip.F32, U,
+                                 idd.data_ptr(), T, k, y.data_ptr(), ws.data_ptr(), nb, st()))
     return y.cpu().numpy()
 
 
@@ -130,7 +132,8 @@ def test_moe_sum(L):
     w = rng.random((T, k)).astype(np.float32)
     r = rng.standard_normal((T, M)).astype(np.float32)
     out = torch.empty((T, M), dtype=torch.float32, device="cuda")
-    hip.check(L.lgmlh_moe_sum(dev(y).data_ptr(), dev(w).data_ptr(), T, k, M, dev(r).data_ptr(),
+    yd, wd, rd = dev(y), dev(w), dev(r)
+    hip.check(L.lgmlh_moe_sum(yd.data_ptr(), wd.data_ptr(), T, k, M, rd.data_ptr(),
                               out.data_ptr(), st()))
     want = (y.astype(np.float64) * w[:, :, None]).sum(axis=1) + r
     np.testing.assert_allclose(out.cpu().numpy(), want, rtol=1e-5, atol=1e-5)
