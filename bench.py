@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Decode throughput of lgml's ragged continuous-batching path on one MI355X.
 
-Workload ("C2"): a Llama-3-8B-shaped model
+Default workload ("C2"): a Llama-3-8B-shaped model
 (32 layers, d 4096, 32 / 8 heads, head 128, FFN 14336, vocab 128256) with
 N(0, 0.02) weights quantized Q4_K_M (output and attn_v / ffn_down of the
 more_bits layers Q6_K), f16 KV in 64-cell blocks; 64 slots with prompt
@@ -12,6 +12,12 @@ The initial 64 contexts are filled with synthetic KV (the attention reads
 cost the same whatever the values); joining prompts run the real prefill.
 One step = one pass of the engine (E:flush): the next token of every
 decoding slot plus the prompt chunks of joining slots.
+
+--workload c5: the same loop on a 30B-A3B-shaped
+qwen3moe (48 layers, d 2048, 32 / 4 heads, head 128, 128 experts of width
+768, top-8 softmax routing, router logits N(0, 1), Q4_K), prompts
+U[256, 8192]: tokens are grouped by expert for the grouped Q4_K expert
+products.
 
 value = decoded tokens / wall seconds of the K timed steps (inputs resident
 in HBM; the per-step host plan upload and the 64 sampled ids read back are
@@ -35,6 +41,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--slots", type=int, default=64)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2")
     ap.add_argument("--bps", type=int, default=0, help="KV blocks per attention work item (0 = auto)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quiet", action="store_true")
@@ -45,6 +52,17 @@ def parse():
 
 
 HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s
+WORKLOADS = {
+    "c2": dict(prompt=(128, 4096),
+               metric="decode tok/s, 64 ragged seqs, Llama-3-8B-shape Q4_K; paged-attn HBM GB/s %",
+               text="C2: Llama-3-8B shape, Q4_K_M, f16 KV, 64 ragged slots, prompts U[128,4096], "
+                    "continuous batching (budgets U[64,2048], joins prefilled in 512-token chunks)"),
+    "c5": dict(prompt=(256, 8192),
+               metric="decode tok/s, 64 ragged seqs, 30B-A3B-shape MoE Q4_K; paged-attn HBM GB/s %",
+               text="C5: 30B-A3B-shaped qwen3moe, 128 experts x 768, top-8 softmax routing, Q4_K, "
+                    "f16 KV, 64 ragged slots, prompts U[256,8192], continuous batching (budgets "
+                    "U[64,2048], joins prefilled in 512-token chunks), tokens grouped by expert"),
+}
 HERE = os.path.dirname(os.path.abspath(__file__))
 # HBM bytes per paged-attention launch of this workload, from rocprofv3
 # FETCH_SIZE / WRITE_SIZE passes scaled by a copy kernel (see the file).
@@ -57,16 +75,16 @@ def log(args, *a):
 
 
 def cpu_baseline(hp, contexts, seed, args):
-    """The C oracle on one decode step of the workload's shape: 1 of the 32
-    layers plus the output head, 64 sequences at the workload's contexts
-    (synthetic KV), timed on the host cores; scaled to a 32-layer step."""
+    """The C oracle on one decode step of the workload's shape: 1 of the
+    n_layer layers plus the output head, 64 sequences at the workload's
+    contexts (synthetic KV), timed on the host cores; scaled to a full step."""
     import numpy as np
 
     from oracle import core, models
 
     E, V = hp["n_embd"], hp["n_vocab"]
     threads = core.threads()
-    ohp, w = models.build("c2", seed=seed, n_layer=1, init="normal")
+    ohp, w = models.build(args.workload, seed=seed, n_layer=1, init="normal")
     om = core.OracleModel(ohp, w)
     S = len(contexts)
     B = 64
@@ -97,10 +115,10 @@ def cpu_baseline(hp, contexts, seed, args):
     t_layer = max(t_all / reps - t_head, 1e-9)
     t_step = t_head + hp["n_layer"] * t_layer
     return {"value": S / t_step, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": "oracle/ (C, OpenMP) decode pass of the C2 shape at %d sequences (contexts "
-                      "as the GPU run, synthetic KV) with 1 layer, %d times (%.1f s), output head "
-                      "%.1f s; step = head + 32 x layer (%.2f s)" % (S, reps, t_all, t_head,
-                                                                      t_layer)}
+            "sample": "oracle/ (C, OpenMP) decode pass of the %s shape at %d sequences "
+                      "(contexts as the GPU run, synthetic KV) with 1 layer, %d times (%.1f s), "
+                      "output head %.1f s; step = head + %d x layer (%.2f s)" % (
+                          args.workload.upper(), S, reps, t_all, t_head, hp["n_layer"], t_layer)}
 
 
 def traffic_of(path, args):
@@ -111,7 +129,8 @@ def traffic_of(path, args):
             t = json.load(f)
     except (OSError, ValueError):
         return None
-    if t.get("seed") != args.seed or t.get("slots") != args.slots:
+    if (t.get("seed") != args.seed or t.get("slots") != args.slots or
+            t.get("bench_workload") != args.workload):
         return None
     return t.get("bytes_per_launch")
 
@@ -138,11 +157,13 @@ def main():
 
     from lgml_amd import engine, hip, runtime, workload
 
-    hp = dict(workload.SHAPES["c2"])
+    wl = WORKLOADS[args.workload]
+    hp = dict(workload.SHAPES[args.workload])
     ty = workload.policy(hp["wtype"], hp["n_layer"])
     rng = workload.Lcg(args.seed)
     S = args.slots
-    max_ctx = 4096 + 2048 + 64
+    plo, phi = wl["prompt"]
+    max_ctx = phi + 2048 + 64
     n_cells = ((S * max_ctx + 63) // 64) * 64
     log(args, "building the model on the device ...")
     t0 = time.time()
@@ -158,11 +179,11 @@ def main():
         t.view(torch.float16).uniform_(-1.0, 1.0, generator=g)
 
     trace = runtime.EventTrace(args.steps * hp["n_layer"] * 8 + 64,
-                               hip.TRACE_ATTN | hip.TRACE_GEMM)
+                               hip.TRACE_ATTN | hip.TRACE_GEMM | hip.TRACE_EXPERTS)
     eng = engine.Engine(model, S, blocks_per_split=args.bps)
 
     def new_request(prefilled):
-        n = rng.int(128, 4096)
+        n = rng.int(plo, phi)
         prompt = [rng.int(0, hp["n_vocab"] - 1) for _ in range(n)]
         r = engine.Request(prompt, rng.int(64, 2048))
         eng.submit(r)
@@ -194,7 +215,8 @@ def main():
     decoded = prefill_tok = 0
     attn_bytes = []
     step_bytes = []
-    wbytes = workload.weight_bytes(hp)
+    wbytes = workload.weight_bytes(hp, S)
+    xbytes = workload.expert_bytes(hp, S)
     kvb = 2 * hp["n_layer"] * hp["n_head_kv"] * hp["head_dim"] * 2  # K+V bytes per cell, all layers
     joins[0] = 0
     torch.cuda.synchronize()
@@ -216,17 +238,19 @@ def main():
     wall = time.perf_counter() - t0
     at = trace.times_ms(hip.TRACE_ATTN)
     gt = trace.times_ms(hip.TRACE_GEMM)
+    xt = trace.times_ms(hip.TRACE_EXPERTS)
     L = hp["n_layer"]
     # attention launches are recorded in step order, L per step
     n_att = len(at)
     tot_bytes = sum(attn_bytes[i // L] for i in range(n_att))
     attn_gbs = tot_bytes / (sum(at) / 1e3) if at else 0.0
     avg_attn_ms = sum(at) / max(n_att, 1)
-    gemm_ms = sum(gt) / args.steps
+    gemm_ms = (sum(gt) + sum(xt)) / args.steps
+    exp_ms = sum(xt) / args.steps
     ms_step = wall * 1e3 / args.steps
     step_gbs = sum(step_bytes) / wall
     result = {
-        "metric": "decode tok/s, 64 ragged seqs, Llama-3-8B-shape Q4_K; paged-attn HBM GB/s %",
+        "metric": wl["metric"],
         "value": decoded / wall,
         "unit": "tok/s",
         "n_gpus": 1,
@@ -236,12 +260,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_K_M weights, f16 KV, f32 accumulate",
+        "dtype": "%s weights, f16 KV, f32 accumulate" % hp["wtype"],
         "data": "synthetic (seeded random-init weights, LCG prompts, synthetic initial KV)",
         "config": {
-            "workload": "C2: Llama-3-8B shape, Q4_K_M, f16 KV, 64 ragged slots, prompts "
-                        "U[128,4096], continuous batching (budgets U[64,2048], joins prefilled "
-                        "in 512-token chunks)",
+            "workload": wl["text"],
             "slots": S, "seed": args.seed, "decoded_tokens": decoded,
             "prefill_tokens": prefill_tok, "joins": joins[0],
             "mean_context": float(np.mean(contexts0)),
@@ -259,6 +281,11 @@ def main():
             "gemm_GBps": wbytes / (gemm_ms / 1e3) / 1e9 if gemm_ms else None,
         },
     }
+    if xbytes:
+        # grouped expert products: expected distinct experts' bytes per step
+        result["step_roofline"].update({
+            "expert_bytes_per_step": xbytes, "expert_ms_per_step": exp_ms,
+            "expert_GBps": xbytes / (exp_ms / 1e3) / 1e9 if exp_ms else None})
     if not args.no_cpu_baseline:
         log(args, "timing the CPU oracle sample ...")
         try:

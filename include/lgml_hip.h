@@ -339,9 +339,10 @@ size_t lgmlh_forward_workspace(const lgmlh_model *m, const lgmlh_plan_info *info
 /* Optional timing: hipEvent_t handles (created by the caller), two per
  * slot, recorded on the pass's stream right before and after each traced
  * launch group. kinds: LGMLH_TRACE_ATTN (paged attention + merge, one slot
- * per layer), LGMLH_TRACE_GEMM (each weight product). used counts slots;
- * a pass stops recording when capacity runs out. */
-enum { LGMLH_TRACE_ATTN = 1, LGMLH_TRACE_GEMM = 2 };
+ * per layer), LGMLH_TRACE_GEMM (each dense weight product and the MoE
+ * router), LGMLH_TRACE_EXPERTS (each grouped expert product). used counts
+ * slots; a pass stops recording when capacity runs out. */
+enum { LGMLH_TRACE_ATTN = 1, LGMLH_TRACE_GEMM = 2, LGMLH_TRACE_EXPERTS = 4 };
 typedef struct {
 	void *const *events; /* 2 * capacity hipEvent_t */
 	int32_t capacity, used, kinds;

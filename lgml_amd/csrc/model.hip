@@ -274,7 +274,7 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
       LGMLH_TRY(moe_route_dev(rpart, router_splits(z.E), z.N, z.NE, z.NU, m->gating,
                               m->norm_topk, m->expert_scale, mids, mwts, &go, st));
       {
-        Span sp(trace, LGMLH_TRACE_GEMM, st);
+        Span sp(trace, LGMLH_TRACE_EXPERTS, st);
         LGMLH_TRY(experts_dev(L.exp_gu_type, L.exp_gu, z.NE, 2 * z.FX, z.E, xn, xs,
                               split_npad(z.N), 1, mids, z.N, z.NU, go, gu_e, st));
       }
@@ -282,7 +282,7 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
       LGMLH_TRY(swiglu_dev(gu_e, z.P, z.FX, dq ? nullptr : act_e, dq ? xs : nullptr, st,
                            Pending{}));
       {
-        Span sp(trace, LGMLH_TRACE_GEMM, st);
+        Span sp(trace, LGMLH_TRACE_EXPERTS, st);
         LGMLH_TRY(experts_dev(L.exp_down_type, L.exp_down, z.NE, z.E, z.FX, act_e, xs,
                               split_npad(z.P), z.NU, mids, z.N, z.NU, go, y_e, st));
       }

@@ -31,7 +31,7 @@ SYMBOLS = (
     "lgmlh_moe_sum",
 )
 GATING_SOFTMAX, GATING_SIGMOID = 1, 2
-TRACE_ATTN, TRACE_GEMM = 1, 2
+TRACE_ATTN, TRACE_GEMM, TRACE_EXPERTS = 1, 2, 4
 
 
 class LgmlhError(RuntimeError):

@@ -10,6 +10,11 @@ SHAPES = {
     "c2": dict(arch="llama", n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128,
                n_ff=14336, n_vocab=128256, rope_base=5e5, eps=1e-5, n_rot=128, rope_neox=0,
                attn_scale=0.0, wtype="q4_K_M"),
+    # C5: 30B-A3B-shaped qwen3moe, Q4_K, 128 experts of width 768, top-8.
+    "c5": dict(arch="qwen3moe", n_layer=48, n_embd=2048, n_head=32, n_head_kv=4, head_dim=128,
+               n_ff=768, n_vocab=151936, rope_base=1e6, eps=1e-6, n_rot=128, rope_neox=1,
+               attn_scale=0.0, wtype="q4_K", n_expert=128, n_used=8, n_ff_exp=768, gating=1,
+               norm_topk=True, expert_scale=1.0),
 }
 
 F32, Q8_0, Q4_K, Q6_K = 0, 8, 12, 14
@@ -24,7 +29,7 @@ def policy(wtype, n_layer):
     """lua/lgml/convert.lua:128-165: weight type of matrix `name` of `layer`
     (None for the embeddings / output)."""
     def ty(name, layer):
-        if wtype == "f32":
+        if wtype == "f32" or name == "gate_inp":  # the router stays f32
             return F32
         if wtype == "q8_0":
             return Q8_0
@@ -32,7 +37,7 @@ def policy(wtype, n_layer):
             return Q4_K
         if name == "output":
             return Q6_K
-        if layer is not None and name in ("wv", "down") and more_bits(layer, n_layer):
+        if layer is not None and name in ("wv", "down", "down_exps") and more_bits(layer, n_layer):
             return Q6_K
         return Q4_K
     return ty
@@ -54,17 +59,45 @@ class Lcg:
         return lo + int(self.next() * (hi - lo + 1))
 
 
-def weight_bytes(hp):
-    """Bytes of the weights a decode step reads (all layer matrices and the
-    output head; the embedding table is read only at the ubatch's ids)."""
+def expected_experts(hp, n_tokens):
+    """Distinct experts a layer reads for n_tokens tokens under uniform
+    routing: NE (1 - (1 - k / NE) ** n_tokens) (125.9 of 128 at 64 tokens)."""
+    NE, k = hp["n_expert"], hp["n_used"]
+    return NE * (1.0 - (1.0 - k / NE) ** n_tokens)
+
+
+def weight_bytes(hp, n_tokens=64):
+    """Bytes of the weights a decode step of n_tokens reads (all layer
+    matrices and the output head; the embedding table is read only at the
+    ubatch's ids; routed experts: the expected distinct experts per layer)."""
     E, H, Hkv, D, F, V, L = (hp[k] for k in ("n_embd", "n_head", "n_head_kv", "head_dim", "n_ff",
                                              "n_vocab", "n_layer"))
     ty = policy(hp["wtype"], L)
     size = {F32: 4.0, Q8_0: 34 / 32, Q4_K: 144 / 256, Q6_K: 210 / 256}
     b = size[ty("output", None)] * V * E
+    moe = bool(hp.get("n_expert"))
     for il in range(L):
         b += size[ty("wq", il)] * H * D * E + size[ty("wk", il)] * Hkv * D * E
         b += size[ty("wv", il)] * Hkv * D * E + size[ty("wo", il)] * E * H * D
-        b += size[ty("gate", il)] * F * E + size[ty("up", il)] * F * E
-        b += size[ty("down", il)] * E * F
+        if moe:
+            FX = hp["n_ff_exp"]
+            b += 4.0 * hp["n_expert"] * E  # router
+            b += expected_experts(hp, n_tokens) * (
+                (size[ty("gate_exps", il)] + size[ty("up_exps", il)]) * FX * E +
+                size[ty("down_exps", il)] * E * FX)
+        else:
+            b += size[ty("gate", il)] * F * E + size[ty("up", il)] * F * E
+            b += size[ty("down", il)] * E * F
     return int(b)
+
+
+def expert_bytes(hp, n_tokens=64):
+    """The routed-expert part of weight_bytes (0 for a dense model)."""
+    if not hp.get("n_expert"):
+        return 0
+    ty = policy(hp["wtype"], hp["n_layer"])
+    size = {F32: 4.0, Q8_0: 34 / 32, Q4_K: 144 / 256, Q6_K: 210 / 256}
+    E, FX = hp["n_embd"], hp["n_ff_exp"]
+    return int(sum(expected_experts(hp, n_tokens) * (
+        (size[ty("gate_exps", il)] + size[ty("up_exps", il)]) * FX * E +
+        size[ty("down_exps", il)] * E * FX) for il in range(hp["n_layer"])))
