@@ -21,11 +21,12 @@ products.
 
 value = decoded tokens / wall seconds of the K timed steps (inputs resident
 in HBM; the per-step host plan upload and the 64 sampled ids read back are
-inside). roofline = the paged attention kernel (the dominant kernel: ~80% of
-the step's bytes): its algorithmic bytes (K + V of every visible cell, q
-in, out) per launch over its HIP-event-timed duration on its own stream,
-against 8 TB/s. cpu_baseline = the C oracle (oracle/) timed on a bounded
-sample of the same step on the host cores.
+inside; no instrumentation). roofline = the paged attention kernel (the
+dominant kernel: ~80% of the step's bytes): its algorithmic bytes (K + V of
+every visible cell, q in, out) per launch over its duration, timed with HIP
+events on the pass's stream during min(K, 16) further steps, against
+8 TB/s. cpu_baseline = the C oracle (oracle/) timed on a bounded sample of
+the same step on the host cores.
 """
 import argparse
 import json
@@ -178,7 +179,8 @@ def main():
     for t in model.kpools + model.vpools:
         t.view(torch.float16).uniform_(-1.0, 1.0, generator=g)
 
-    trace = runtime.EventTrace(args.steps * hp["n_layer"] * 8 + 64,
+    n_trace = min(args.steps, 16)
+    trace = runtime.EventTrace(n_trace * hp["n_layer"] * 8 + 64,
                                hip.TRACE_ATTN | hip.TRACE_GEMM | hip.TRACE_EXPERTS)
     eng = engine.Engine(model, S, blocks_per_split=args.bps)
 
@@ -213,29 +215,39 @@ def main():
     torch.cuda.synchronize()
     trace.reset()
     decoded = prefill_tok = 0
-    attn_bytes = []
-    step_bytes = []
     wbytes = workload.weight_bytes(hp, S)
     xbytes = workload.expert_bytes(hp, S)
     kvb = 2 * hp["n_layer"] * hp["n_head_kv"] * hp["head_dim"] * 2  # K+V bytes per cell, all layers
+
+    def bytes_of_last_step():
+        """(attention bytes per layer, step bytes) of the step just run."""
+        plan = eng.last_plan
+        seq_n = plan.seq_n
+        n_kv = (plan.seq_npast.astype(np.int64) + seq_n)
+        N = int(seq_n.sum())
+        per_layer_kv = int(n_kv.sum()) * kvb // hp["n_layer"]
+        qo = N * hp["n_head"] * hp["head_dim"] * 4 * 2
+        return per_layer_kv + qo, wbytes + int(n_kv.sum()) * kvb + N * kvb
+
+    # The timed steps run without instrumentation (value, ms_per_step); the
+    # kernel times come from n_trace more steps with HIP events around
+    # each attention launch group and weight product.
+    step_bytes = []
     joins[0] = 0
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        got = step(True)
-        plan = eng.last_plan
-        seq_n = plan.seq_n
-        npast = plan.seq_npast
-        n_kv = (npast.astype(np.int64) + seq_n)
-        N = int(seq_n.sum())
+        got = step(False)
+        seq_n = eng.last_plan.seq_n
         decoded += len(got)
         prefill_tok += int(seq_n[seq_n > 1].sum())
-        per_layer_kv = int(n_kv.sum()) * kvb // hp["n_layer"]
-        qo = N * hp["n_head"] * hp["head_dim"] * 4 * 2
-        attn_bytes.append(per_layer_kv + qo)
-        step_bytes.append(wbytes + int(n_kv.sum()) * kvb + N * kvb)
+        step_bytes.append(bytes_of_last_step()[1])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    attn_bytes = []
+    for _ in range(n_trace):
+        step(True)
+        attn_bytes.append(bytes_of_last_step()[0])
     at = trace.times_ms(hip.TRACE_ATTN)
     gt = trace.times_ms(hip.TRACE_GEMM)
     xt = trace.times_ms(hip.TRACE_EXPERTS)
@@ -245,8 +257,8 @@ def main():
     tot_bytes = sum(attn_bytes[i // L] for i in range(n_att))
     attn_gbs = tot_bytes / (sum(at) / 1e3) if at else 0.0
     avg_attn_ms = sum(at) / max(n_att, 1)
-    gemm_ms = (sum(gt) + sum(xt)) / args.steps
-    exp_ms = sum(xt) / args.steps
+    gemm_ms = (sum(gt) + sum(xt)) / n_trace
+    exp_ms = sum(xt) / n_trace
     ms_step = wall * 1e3 / args.steps
     step_gbs = sum(step_bytes) / wall
     result = {
@@ -277,7 +289,8 @@ def main():
         "step_roofline": {
             "bytes_per_step": sum(step_bytes) / len(step_bytes),
             "achieved_GBps": step_gbs / 1e9, "frac": step_gbs / HBM_PEAK,
-            "gemm_ms_per_step": gemm_ms, "attn_ms_per_step": sum(at) / args.steps,
+            "gemm_ms_per_step": gemm_ms, "attn_ms_per_step": sum(at) / n_trace,
+            "traced_steps": n_trace,
             "gemm_GBps": wbytes / (gemm_ms / 1e3) / 1e9 if gemm_ms else None,
         },
     }

@@ -33,26 +33,66 @@ constexpr int MOE_MAX_PICKS = 8192;   // picks of one pass (LDS)
 
 // ---- router logits: split-K f32 product -------------------------------------
 // part[z][n][e] = sum over k in [256 z, 256 z + 256) of W[e][k] x[n][k], in
-// k order (fmaf). A 16 x 16 tile of (expert, token) per workgroup.
+// k order (fmaf). A workgroup takes 16 experts x 64 tokens of one K chunk;
+// thread t owns expert t % 16 for tokens t / 16 + 16 j (j < 4).
 constexpr int ROUTER_KC = 256;
+constexpr int ROUTER_TOK = 64;
+constexpr int ROUTER_LD = ROUTER_KC + 4;  // row pitch (floats): 16-byte rows, no bank conflicts
 __global__ void __launch_bounds__(256)
 router_part_kernel(const float *__restrict__ w, int NE, int64_t K, const float *__restrict__ x,
                    int64_t N, float *__restrict__ part) {
-  __shared__ float ws_[16][ROUTER_KC + 1], xs_[16][ROUTER_KC + 1];
-  const int t = threadIdx.x, tx = t & 15, ty = t >> 4;
-  const int64_t e0 = (int64_t)blockIdx.x * 16, n0 = (int64_t)blockIdx.y * 16;
-  const int64_t k0 = (int64_t)blockIdx.z * ROUTER_KC;
-  for (int i = t; i < 16 * ROUTER_KC; i += 256) {
-    const int r = i / ROUTER_KC, cc = i % ROUTER_KC;
-    const bool kin = k0 + cc < K;
-    ws_[r][cc] = (e0 + r < NE && kin) ? w[(e0 + r) * K + k0 + cc] : 0.0f;
-    xs_[r][cc] = (n0 + r < N && kin) ? x[(n0 + r) * K + k0 + cc] : 0.0f;
+  __shared__ __align__(16) float ws_[16 * ROUTER_LD];
+  __shared__ __align__(16) float xs_[ROUTER_TOK * ROUTER_LD];
+  const int t = threadIdx.x, e = t & 15, tq = t >> 4;
+  const int64_t e0 = (int64_t)blockIdx.x * 16, n0 = (int64_t)blockIdx.z * ROUTER_TOK;
+  const int64_t k0 = (int64_t)blockIdx.y * ROUTER_KC;
+  // 16-byte loads, all issued before the first LDS store: float4 i of a
+  // row of ROUTER_KC / 4 (K % 4 == 0)
+  constexpr int Q = ROUTER_KC / 4;
+  constexpr int WJ = 16 * Q / 256, XJ = ROUTER_TOK * Q / 256;
+  f32x4 wv_[WJ], xv_[XJ];
+#pragma unroll
+  for (int j = 0; j < WJ; j++) {
+    const int i = t + 256 * j, r = i / Q, c4 = 4 * (i % Q);
+    wv_[j] = f32x4{0, 0, 0, 0};
+    if (e0 + r < NE && k0 + c4 < K) wv_[j] = *(const f32x4 *)(w + (e0 + r) * K + k0 + c4);
+  }
+#pragma unroll
+  for (int j = 0; j < XJ; j++) {
+    const int i = t + 256 * j, r = i / Q, c4 = 4 * (i % Q);
+    xv_[j] = f32x4{0, 0, 0, 0};
+    if (n0 + r < N && k0 + c4 < K) xv_[j] = *(const f32x4 *)(x + (n0 + r) * K + k0 + c4);
+  }
+#pragma unroll
+  for (int j = 0; j < WJ; j++) {
+    const int i = t + 256 * j;
+    *(f32x4 *)&ws_[(i / Q) * ROUTER_LD + 4 * (i % Q)] = wv_[j];
+  }
+#pragma unroll
+  for (int j = 0; j < XJ; j++) {
+    const int i = t + 256 * j;
+    *(f32x4 *)&xs_[(i / Q) * ROUTER_LD + 4 * (i % Q)] = xv_[j];
   }
   __syncthreads();
-  float acc = 0.0f;
-#pragma unroll 8
-  for (int cc = 0; cc < ROUTER_KC; cc++) acc = fmaf(ws_[tx][cc], xs_[ty][cc], acc);
-  if (e0 + tx < NE && n0 + ty < N) part[((int64_t)blockIdx.z * N + n0 + ty) * NE + e0 + tx] = acc;
+  float acc[4] = {0, 0, 0, 0};
+  const float *wr = ws_ + e * ROUTER_LD;
+#pragma unroll 4
+  for (int c = 0; c < ROUTER_KC; c += 4) {
+    const f32x4 wv = *(const f32x4 *)(wr + c);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const f32x4 xv = *(const f32x4 *)(xs_ + (tq + 16 * j) * ROUTER_LD + c);
+      acc[j] = fmaf(wv[0], xv[0], acc[j]);
+      acc[j] = fmaf(wv[1], xv[1], acc[j]);
+      acc[j] = fmaf(wv[2], xv[2], acc[j]);
+      acc[j] = fmaf(wv[3], xv[3], acc[j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int64_t n = n0 + tq + 16 * j;
+    if (e0 + e < NE && n < N) part[((int64_t)blockIdx.y * N + n) * NE + e0 + e] = acc[j];
+  }
 }
 
 // ---- picks and weights ---------------------------------------------------------
@@ -61,39 +101,49 @@ __device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
   return a > b || (a == b && ia < ib);
 }
 
-// One wave per token: logits l = sum of the nz partial rows (in order);
-// probs = soft_max (f32: max, exp, sum over the wave in a fixed tree) or
-// sigmoid; the n_used largest logits (the gating is monotone) as ids,
-// largest first, ties to the smaller index (argsort_top_k); weights =
-// probs of the ids, / max(sum, 6.103515625e-5) when norm_topk
-// (transformer.lua:2003-2005), times scale (:2006-2008).
+// Routing of token t by the 16 lanes sub = 0..15 of a lane group (lane
+// holds experts sub + 16 i, i < PER): logits l = sum of the nz partial
+// rows (in order); probs = soft_max (f32: max, exp, sum over the group in a
+// fixed tree) or sigmoid; the n_used largest logits (the gating is
+// monotone) as ids, largest first, ties to the smaller index
+// (argsort_top_k); weights = probs of the ids, / max(sum, 6.103515625e-5)
+// when norm_topk (transformer.lua:2003-2005), times scale (:2006-2008).
+// Tokens t >= T run along (their lanes take part in the shuffles) and
+// write nothing.
+template <int PER>
 __device__ void route_token(const float *__restrict__ part, int nz, int64_t T, int64_t t, int NE,
-                            int n_used, int gating, int norm_topk, float scale, int lane,
+                            int n_used, int gating, int norm_topk, float scale, int sub,
                             int32_t *__restrict__ ids, float *__restrict__ wts,
                             int32_t *ids_lds) {
-  constexpr int PER = MOE_MAX_EXPERTS / 64;
+  const bool live = t < T;
   float l[PER], p[PER];
+#pragma unroll
+  for (int i = 0; i < PER; i++) l[i] = 0.0f;
+  // split sums in split order; the loads of a split are independent
+#pragma unroll 8
+  for (int z = 0; z < nz; z++) {
+    const float *pz = part + ((int64_t)z * T + (live ? t : 0)) * NE;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      const int e = sub + 16 * i;
+      if (e < NE) l[i] += pz[e];
+    }
+  }
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < PER; i++) {
-    const int e = lane + 64 * i;
-    l[i] = -INFINITY;
-    if (e < NE) {
-      float v = 0.0f;
-      for (int z = 0; z < nz; z++) v += part[((int64_t)z * T + t) * NE + e];
-      l[i] = v;
-    }
+    if (sub + 16 * i >= NE) l[i] = -INFINITY;
     mx = fmaxf(mx, l[i]);
   }
-  for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
   if (gating == LGMLH_GATING_SOFTMAX) {
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
-      p[i] = lane + 64 * i < NE ? expf(l[i] - mx) : 0.0f;
+      p[i] = sub + 16 * i < NE ? expf(l[i] - mx) : 0.0f;
       s += p[i];
     }
-    for (int o = 1; o < 64; o <<= 1) s += __shfl_xor(s, o);
+    for (int o = 1; o < 16; o <<= 1) s += __shfl_xor(s, o);
 #pragma unroll
     for (int i = 0; i < PER; i++) p[i] = p[i] / s;
   } else {
@@ -112,13 +162,13 @@ __device__ void route_token(const float *__restrict__ part, int nz, int64_t T, i
     int bi = 0x7fffffff;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
-      const int e = lane + 64 * i;
+      const int e = sub + 16 * i;
       if (e < NE && !(taken >> i & 1u) && better(l[i], e, bv, bi)) {
         bv = l[i];
         bi = e;
       }
     }
-    for (int o = 1; o < 64; o <<= 1) {
+    for (int o = 1; o < 16; o <<= 1) {
       const float ov = __shfl_xor(bv, o);
       const int oi = __shfl_xor(bi, o);
       if (better(ov, oi, bv, bi)) {
@@ -126,18 +176,20 @@ __device__ void route_token(const float *__restrict__ part, int nz, int64_t T, i
         bi = oi;
       }
     }
-    // every lane holds the winner now (none when the logits are NaN: expert
-    // 0 then, so ids stay in range); its owner marks it and sends its prob
+    // every lane of the group holds the winner now (none when the logits
+    // are NaN: expert 0 then, so ids stay in range); its owner marks it
+    // and sends its prob
     if (bi >= NE) bi = 0;
     float pw = 0.0f;
 #pragma unroll
     for (int i = 0; i < PER; i++)
-      if (bi == lane + 64 * i) {
+      if (bi == sub + 16 * i) {
         taken |= 1u << i;
         pw = p[i];
       }
+    // from lane (bi % 16) of this group
+    w[j] = __shfl(pw, (int)(__lane_id() & ~15u) + (bi & 15));
     sel[j] = bi;
-    w[j] = __shfl(pw, bi & 63);
   }
   if (norm_topk) {
     float s = 0.0f;
@@ -151,9 +203,10 @@ __device__ void route_token(const float *__restrict__ part, int nz, int64_t T, i
   if (scale != 1.0f)
 #pragma unroll
     for (int j = 0; j < MOE_MAX_USED; j++) w[j] = w[j] * scale;
+  if (!live) return;
 #pragma unroll
   for (int j = 0; j < MOE_MAX_USED; j++)
-    if (j < n_used && lane == j) {
+    if (j < n_used && sub == j) {
       ids[t * n_used + j] = sel[j];
       wts[t * n_used + j] = w[j];
       if (ids_lds) ids_lds[t * n_used + j] = sel[j];
@@ -185,51 +238,51 @@ __device__ void group_picks(GroupLds &lds, int P, int NE, const GroupOut &go) {
     if (e >= 0) atomicAdd(&lds.base[wave][e], 1);  // counts: order-free
   }
   __syncthreads();
-  // totals, tiles per expert, and the exclusive scans (one wave, 8 experts
-  // per lane)
-  if (wave == 0) {
-    constexpr int PER = MOE_MAX_EXPERTS / 64;
-    int cnt[PER], nt[PER], cs = 0, ts = 0;
+  // per expert (one thread each): its total, its tiles, and the bases of
+  // the wave chunks relative to the expert's first pick
+  int cnt = 0, nt = 0;
+  if (tid < NE) {
+    int c[ROUTE_WAVES];
 #pragma unroll
-    for (int i = 0; i < PER; i++) {
-      const int e = lane * PER + i;
-      cnt[i] = 0;
-      if (e < NE)
-        for (int ww = 0; ww < ROUTE_WAVES; ww++) cnt[i] += lds.base[ww][e];
-      nt[i] = (cnt[i] + go.tile_cols - 1) / go.tile_cols;
-      cs += cnt[i];
-      ts += nt[i];
-    }
-    int ci = cs, ti = ts;  // inclusive scans over lanes
-    for (int o = 1; o < 64; o <<= 1) {
-      const int a = __shfl_up(ci, o), b = __shfl_up(ti, o);
-      if (lane >= o) {
-        ci += a;
-        ti += b;
-      }
-    }
-    int c0 = ci - cs, t0 = ti - ts;
+    for (int ww = 0; ww < ROUTE_WAVES; ww++) c[ww] = lds.base[ww][tid];
 #pragma unroll
-    for (int i = 0; i < PER; i++) {
-      const int e = lane * PER + i;
-      if (e < NE) {
-        lds.off[e] = c0;
-        lds.toff[e] = t0;
-        // per-wave bases of expert e
-        int b = c0;
-        for (int ww = 0; ww < ROUTE_WAVES; ww++) {
-          const int cw = lds.base[ww][e];
-          lds.base[ww][e] = b;
-          b += cw;
-        }
-      }
-      c0 += cnt[i];
-      t0 += nt[i];
+    for (int ww = 0; ww < ROUTE_WAVES; ww++) {
+      lds.base[ww][tid] = cnt;
+      cnt += c[ww];
     }
-    if (lane == 63) {
-      lds.off[NE] = c0;
-      lds.toff[NE] = t0;
-      *go.n_tiles = t0;
+    nt = (cnt + go.tile_cols - 1) / go.tile_cols;
+  }
+  // exclusive scans of cnt and nt over the experts: within each wave, then
+  // over the waves (NE <= 512: 8 waves)
+  int ci = cnt, ti = nt;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int a = __shfl_up(ci, o), b = __shfl_up(ti, o);
+    if (lane >= o) {
+      ci += a;
+      ti += b;
+    }
+  }
+  if (lane == 63 && wave < MOE_MAX_EXPERTS / 64) {
+    lds.off[wave] = ci;   // wave totals (off / toff are rewritten below)
+    lds.toff[wave] = ti;
+  }
+  __syncthreads();
+  int cw = 0, tw = 0;
+  for (int ww = 0; ww < wave && ww < MOE_MAX_EXPERTS / 64; ww++) {
+    cw += lds.off[ww];
+    tw += lds.toff[ww];
+  }
+  __syncthreads();
+  if (tid < NE) {
+    const int c0 = cw + ci - cnt, t0 = tw + ti - nt;
+    lds.off[tid] = c0;
+    lds.toff[tid] = t0;
+#pragma unroll
+    for (int ww = 0; ww < ROUTE_WAVES; ww++) lds.base[ww][tid] += c0;
+    if (tid == NE - 1) {
+      lds.off[NE] = c0 + cnt;
+      lds.toff[NE] = t0 + nt;
+      *go.n_tiles = t0 + nt;
     }
   }
   __syncthreads();
@@ -263,16 +316,18 @@ __device__ void group_picks(GroupLds &lds, int P, int NE, const GroupOut &go) {
   }
 }
 
-// Routing of T tokens (one workgroup); with group set, also the grouping.
+// Routing of T tokens (one workgroup, 16 lanes per token); with group
+// set, also the grouping. PER = experts per lane (NE <= 16 PER).
+template <int PER>
 __global__ void __launch_bounds__(ROUTE_THREADS)
 route_kernel(const float *__restrict__ part, int nz, int64_t T, int NE, int n_used, int gating,
              int norm_topk, float scale, int32_t *__restrict__ ids, float *__restrict__ wts,
              int group, GroupOut go) {
   __shared__ GroupLds lds;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int64_t t = wave; t < T; t += ROUTE_WAVES)
-    route_token(part, nz, T, t, NE, n_used, gating, norm_topk, scale, lane, ids, wts,
-                group ? lds.ids : nullptr);
+  const int tid = threadIdx.x;
+  for (int64_t t0 = 0; t0 < T; t0 += ROUTE_THREADS / 16)
+    route_token<PER>(part, nz, T, t0 + tid / 16, NE, n_used, gating, norm_topk, scale, tid & 15,
+                     ids, wts, group ? lds.ids : nullptr);
   if (!group) return;
   __syncthreads();
   group_picks(lds, (int)(T * n_used), NE, go);
@@ -353,7 +408,12 @@ int router_splits(int64_t K) { return (int)((K + ROUTER_KC - 1) / ROUTER_KC); }
 int router_logits(const float *w, int NE, int64_t K, const float *x, int64_t T, float *part,
                   hipStream_t st) {
   if (T == 0) return LGMLH_OK;
-  dim3 grid((unsigned)((NE + 15) / 16), (unsigned)((T + 15) / 16), (unsigned)router_splits(K));
+  if (K % 4) {
+    set_error("moe router: K %lld is not a multiple of 4", (long long)K);
+    return LGMLH_EINVAL;
+  }
+  dim3 grid((unsigned)((NE + 15) / 16), (unsigned)router_splits(K),
+            (unsigned)((T + ROUTER_TOK - 1) / ROUTER_TOK));
   hipLaunchKernelGGL(router_part_kernel, grid, dim3(256), 0, st, w, NE, K, x, T, part);
   return hip_check(hipGetLastError(), "moe router");
 }
@@ -378,8 +438,16 @@ int moe_route_dev(const float *part, int nz, int64_t T, int NE, int n_used, int 
   LGMLH_TRY(check_route(T, NE, n_used, gating));
   if (T == 0) return LGMLH_OK;
   GroupOut g = go ? *go : GroupOut{nullptr, nullptr, nullptr, 16};
-  hipLaunchKernelGGL(route_kernel, dim3(1), dim3(ROUTE_THREADS), 0, st,
-                     part, nz, T, NE, n_used, gating, norm_topk, scale, ids, wts, go ? 1 : 0, g);
+  const int grp = go ? 1 : 0;
+  if (NE <= 128)
+    hipLaunchKernelGGL(route_kernel<8>, dim3(1), dim3(ROUTE_THREADS), 0, st, part, nz, T, NE,
+                       n_used, gating, norm_topk, scale, ids, wts, grp, g);
+  else if (NE <= 256)
+    hipLaunchKernelGGL(route_kernel<16>, dim3(1), dim3(ROUTE_THREADS), 0, st, part, nz, T, NE,
+                       n_used, gating, norm_topk, scale, ids, wts, grp, g);
+  else
+    hipLaunchKernelGGL(route_kernel<32>, dim3(1), dim3(ROUTE_THREADS), 0, st, part, nz, T, NE,
+                       n_used, gating, norm_topk, scale, ids, wts, grp, g);
   return hip_check(hipGetLastError(), "moe route");
 }
 
