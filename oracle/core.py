@@ -36,10 +36,16 @@ class Tensor(C.Structure):
     _fields_ = [("type", C.c_int), ("data", C.c_void_p)]
 
 
+TENSOR_FIELDS = ("attn_norm", "wq", "wk", "wv", "wo", "q_norm", "k_norm", "ffn_norm", "gate",
+                 "up", "down", "gate_inp", "gate_exps", "up_exps", "down_exps", "post_attn_norm",
+                 "post_ffn_norm")
+
+
 class Layer(C.Structure):
-    _fields_ = [(n, Tensor) for n in ("attn_norm", "wq", "wk", "wv", "wo", "q_norm", "k_norm",
-                                      "ffn_norm", "gate", "up", "down", "gate_inp", "gate_exps",
-                                      "up_exps", "down_exps")]
+    _fields_ = [(n, Tensor) for n in TENSOR_FIELDS[:15]] + \
+               [("post_attn_norm", Tensor), ("post_ffn_norm", Tensor), ("out_scale", C.c_float),
+                ("swa", C.c_int), ("head_dim", C.c_int), ("n_head_kv", C.c_int),
+                ("n_rot", C.c_int), ("rope_base", C.c_float), ("rope_freqs", C.c_void_p)]
 
 
 class Model(C.Structure):
@@ -50,13 +56,16 @@ class Model(C.Structure):
                 ("rope_freqs", C.c_void_p), ("tok_embd", Tensor), ("output", Tensor),
                 ("output_norm", Tensor), ("layers", C.POINTER(Layer)),
                 ("n_expert", C.c_int), ("n_used", C.c_int), ("n_ff_exp", C.c_int),
-                ("gating", C.c_int), ("norm_topk", C.c_int), ("expert_scale", C.c_float)]
+                ("gating", C.c_int), ("norm_topk", C.c_int), ("expert_scale", C.c_float),
+                ("gemma", C.c_int), ("n_swa", C.c_int), ("embd_scale", C.c_float),
+                ("softcap", C.c_float)]
 
 
 class Batch(C.Structure):
     _fields_ = [("n_seq", C.c_int), ("max_blocks", C.c_int), ("block", C.c_int),
                 ("seq_n", C.c_void_p), ("seq_npast", C.c_void_p), ("block_tab", C.c_void_p),
-                ("ids", C.c_void_p), ("n_out", C.c_int), ("out_rows", C.c_void_p)]
+                ("ids", C.c_void_p), ("n_out", C.c_int), ("out_rows", C.c_void_p),
+                ("ring_blocks", C.c_int), ("ring_tab", C.c_void_p)]
 
 
 def _declare(L):
@@ -79,6 +88,8 @@ def _declare(L):
     L.orc_forward.argtypes = [C.POINTER(Model), vp, vp, i64, C.POINTER(Batch), vp, i32]
     L.orc_paged_attention.argtypes = [vp, vp, vp, i32, i32, i32, C.c_float, C.POINTER(Batch),
                                       vp, i32]
+    L.orc_paged_attention_swa.argtypes = [vp, vp, vp, i32, i32, i32, C.c_float, i32,
+                                          C.POINTER(Batch), vp, i32]
     L.orc_set_rows_f16.argtypes = [vp, i64, i64, vp, vp, i64]
     L.orc_mul_mat.argtypes = [i32, vp, i64, i64, vp, i64, vp, i32]
     L.orc_moe_route.argtypes = [vp, i64, i32, i32, i32, i32, C.c_float, vp, vp]
@@ -228,7 +239,9 @@ def argmax(v):
 class BatchDesc:
     """Keeps the arrays of an orc_batch alive."""
 
-    def __init__(self, seq_n, seq_npast, block_tab, block, ids, out_rows):
+    def __init__(self, seq_n, seq_npast, block_tab, block, ids, out_rows, ring_tab=None):
+        """ring_tab: (n_seq, ring_blocks) block ids of each sequence's ring
+        (the cells of sliding-window layers), or None."""
         self.seq_n = np.ascontiguousarray(seq_n, np.int32)
         self.seq_npast = np.ascontiguousarray(seq_npast, np.int32)
         bt = np.ascontiguousarray(block_tab, np.int32)
@@ -239,6 +252,13 @@ class BatchDesc:
         self.out_rows = np.ascontiguousarray(out_rows, np.int32)
         self.c = Batch(len(self.seq_n), bt.shape[1], block, _p(self.seq_n), _p(self.seq_npast),
                        _p(self.block_tab), _p(self.ids), len(self.out_rows), _p(self.out_rows))
+        if ring_tab is not None:
+            rt = np.ascontiguousarray(ring_tab, np.int32)
+            if rt.ndim == 1:
+                rt = rt.reshape(len(self.seq_n), -1)
+            self.ring_tab = rt
+            self.c.ring_blocks = rt.shape[1]
+            self.c.ring_tab = _p(rt)
 
 
 def paged_attention(q, kpool, vpool, H, Hkv, D, scale, batch, nthreads=None):
@@ -248,6 +268,16 @@ def paged_attention(q, kpool, vpool, H, Hkv, D, scale, batch, nthreads=None):
                                    C.byref(batch.c), _p(out), nthreads or threads())
     if rc:
         raise ValueError("paged_attention failed")
+    return out
+
+
+def paged_attention_swa(q, kpool, vpool, H, Hkv, D, scale, window, batch, nthreads=None):
+    q = np.ascontiguousarray(q, np.float32)
+    out = np.empty_like(q)
+    rc = lib().orc_paged_attention_swa(_p(q), _p(kpool), _p(vpool), H, Hkv, D, scale, window,
+                                       C.byref(batch.c), _p(out), nthreads or threads())
+    if rc:
+        raise ValueError("paged_attention_swa failed")
     return out
 
 
@@ -269,13 +299,22 @@ class OracleModel:
         self.layers = (Layer * L)()
         for il in range(L):
             lw = w["layers"][il]
-            for f, _ in Layer._fields_:
+            Ly = self.layers[il]
+            for f in TENSOR_FIELDS:
                 t = lw.get(f)
                 if t is not None:
                     arr, ty = t
                     arr = np.ascontiguousarray(arr)
                     self._keep.append(arr)
-                    setattr(self.layers[il], f, Tensor(ty, _p(arr).value))
+                    setattr(Ly, f, Tensor(ty, _p(arr).value))
+            # per-layer attention shape / rope / gemma scalars
+            for f in ("out_scale", "swa", "head_dim", "n_head_kv", "n_rot", "rope_base"):
+                if lw.get(f) is not None:
+                    setattr(Ly, f, lw[f])
+            if lw.get("rope_freqs") is not None:
+                rf = np.ascontiguousarray(lw["rope_freqs"], np.float32)
+                self._keep.append(rf)
+                Ly.rope_freqs = _p(rf).value
         self.c = Model()
         for k in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "n_ff", "n_vocab",
                   "n_rot", "rope_neox"):
@@ -296,6 +335,10 @@ class OracleModel:
         for k in ("n_expert", "n_used", "n_ff_exp"):
             setattr(self.c, k, int(hp.get(k, 0)))
         self.c.gating = int(hp.get("gating", GATING_SOFTMAX))
+        self.c.gemma = int(bool(hp.get("gemma", False)))
+        self.c.n_swa = int(hp.get("n_swa", 0))
+        self.c.embd_scale = float(hp.get("embd_scale", 0.0))
+        self.c.softcap = float(hp.get("softcap", 0.0))
         self.c.norm_topk = int(bool(hp.get("norm_topk", True)))
         self.c.expert_scale = float(hp.get("expert_scale", 1.0))
 

@@ -85,6 +85,66 @@ def ref_tiny(arch):
     return hp, out
 
 
+def ref_tiny_gemma4():
+    """The tiny gemma4 "dense" model of test/test_gemma4.lua:38-174 (build("dense")).
+
+    Seed #"dense" * 7919 (:58); tensors drawn in the order build() lists
+    them (:120-171): w() is U(-s, s), s = gain * sqrt(3 / fan_in) (:72-79);
+    norms U(0.8, 1.2) (:80-82). E=64, H=4, FF=96, vocab 289 (bpe_vocab
+    gemma4_kv: 9 specials, 255 byte tokens, 13 chars, 10 merges, 2 more).
+    Layer 0 slides (window 6, head 16, 2 KV heads, rope base 1e4); layer 1
+    is global (head 32, 1 KV head, rope base 1e6, proportional rope: freq
+    factors 1 for the first half of the pairs, 1e30 after (:123-128), no
+    attn_v: V is the raw K). Layer output scales 0.8 + 0.3 i (:168), logit
+    softcap 30, embeddings times sqrt(64), attention scale 1, tied output
+    (transformer.lua:171-183,408).
+    """
+    E, H, D, DS, FF, NSWA = 64, 4, 32, 16, 96, 6
+    nv = 9 + 255 + 13 + 10 + 2
+    r = core.Lcg(len("dense") * 7919)
+
+    def w(rows, cols, gain=1.0):
+        s = gain * math.sqrt(3.0 / cols)
+        return (r.fill(rows * cols, -s, s).reshape(rows, cols), core.F32)
+
+    def norm(d):
+        return (r.fill(d, 0.8, 1.2), core.F32)
+
+    out = {"tok_embd": w(nv, E, 0.3), "output_norm": norm(E), "rope_freqs": None}
+    out["output"] = out["tok_embd"]
+    freqs = np.array([1.0 if i <= D // 4 else 1e30 for i in range(1, D // 2 + 1)], np.float32)
+    swa, hkv = [True, False], [2, 1]
+    layers = []
+    for i in range(2):
+        d = DS if swa[i] else D
+        L = {"swa": int(swa[i]), "head_dim": d, "n_head_kv": hkv[i], "n_rot": d,
+             "rope_base": 1e4 if swa[i] else 1e6}
+        if not swa[i]:
+            L["rope_freqs"] = freqs
+        L["attn_norm"] = norm(E)
+        L["wq"] = w(H * d, E)
+        L["wk"] = w(hkv[i] * d, E)
+        L["k_norm"] = norm(d)
+        if swa[i]:
+            L["wv"] = w(hkv[i] * d, E)
+        L["wo"] = w(E, H * d)
+        L["q_norm"] = norm(d)
+        L["post_attn_norm"] = norm(E)
+        L["ffn_norm"] = norm(E)
+        L["gate"] = w(FF, E)
+        L["up"] = w(FF, E)
+        L["down"] = w(E, FF)
+        L["post_ffn_norm"] = norm(E)
+        L["out_scale"] = float(np.float32(0.8 + 0.3 * i))
+        layers.append(L)
+    out["layers"] = layers
+    hp = dict(arch="gemma4", n_layer=2, n_embd=E, n_head=H, n_head_kv=hkv[1], head_dim=D,
+              n_ff=FF, n_vocab=nv, n_rot=D, eps=1e-6, rope_base=1e6, rope_neox=1,
+              attn_scale=1.0, gemma=True, n_swa=NSWA, embd_scale=float(np.float32(math.sqrt(E))),
+              softcap=30.0)
+    return hp, out
+
+
 # Named model shapes of BASELINE.json's configs.
 SHAPES = {
     # C1: tiny llama-style f32 model runnable on CPU.

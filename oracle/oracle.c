@@ -606,6 +606,15 @@ cell_of(const orc_batch *b, int s, int p)
 	    p % b->block;
 }
 
+/* The ring cell of position p (rows_swa = p % ring, transformer.lua:
+ * 2469-2476, ring = ring_blocks * block). */
+static int64_t
+ring_cell_of(const orc_batch *b, int s, int p)
+{
+	return (int64_t)b->ring_tab[(int64_t)s * b->ring_blocks + (p / b->block) % b->ring_blocks] *
+	    b->block + p % b->block;
+}
+
 int
 orc_set_rows_f16(uint16_t *dst, int64_t dst_rows, int64_t row, const float *src,
     const int64_t *ids, int64_t n)
@@ -624,9 +633,31 @@ orc_set_rows_f16(uint16_t *dst, int64_t dst_rows, int64_t row, const float *src,
  * the cells of positions 0..npast+j; other cells are -inf and drop out.
  * GQA: query head h reads kv head h / (H / Hkv) (src/lgml.c:1805-1809).
  * Scores and sums in f64, K and V read from f16 storage. */
+static int attend(const float *q, const uint16_t *kpool, const uint16_t *vpool, int H, int Hkv,
+    int D, float scale, int window, int ring, const orc_batch *b, float *out, int n_threads);
+
 int
 orc_paged_attention(const float *q, const uint16_t *kpool, const uint16_t *vpool, int H,
     int Hkv, int D, float scale, const orc_batch *b, float *out, int n_threads)
+{
+	return attend(q, kpool, vpool, H, Hkv, D, scale, 0, 0, b, out, n_threads);
+}
+
+int
+orc_paged_attention_swa(const float *q, const uint16_t *kpool, const uint16_t *vpool, int H,
+    int Hkv, int D, float scale, int window, const orc_batch *b, float *out, int n_threads)
+{
+	if (window < 1 || b->ring_blocks < 1 || !b->ring_tab)
+		return -1;
+	return attend(q, kpool, vpool, H, Hkv, D, scale, window, 1, b, out, n_threads);
+}
+
+/* With window > 0, query j (position p) sees positions max(0, p - window
+ * + 1)..p only (tensor_fill_mask's window, src/lgml.c:2920-2923); with
+ * ring, they are read from the sequence's ring cells. */
+static int
+attend(const float *q, const uint16_t *kpool, const uint16_t *vpool, int H, int Hkv, int D,
+    float scale, int window, int ring, const orc_batch *b, float *out, int n_threads)
 {
 	int64_t N = 0;
 	int64_t *off = malloc(sizeof(int64_t) * (size_t)(b->n_seq + 1));
@@ -665,8 +696,10 @@ orc_paged_attention(const float *q, const uint16_t *kpool, const uint16_t *vpool
 				int kh = h / G;
 				const float *qh = q + (t * H + h) * D;
 				double mx = -INFINITY;
-				for (int j = 0; j <= p; j++) {
-					const uint16_t *kr = kpool + cell_of(b, s, j) * row + (int64_t)kh * D;
+				int j0 = window > 0 && p - window + 1 > 0 ? p - window + 1 : 0;
+				for (int j = j0; j <= p; j++) {
+					int64_t cell = ring ? ring_cell_of(b, s, j) : cell_of(b, s, j);
+					const uint16_t *kr = kpool + cell * row + (int64_t)kh * D;
 					double a = 0;
 					for (int d = 0; d < D; d++)
 						a += (double)qh[d] * (double)orc_f16_to_f32(kr[d]);
@@ -675,14 +708,15 @@ orc_paged_attention(const float *q, const uint16_t *kpool, const uint16_t *vpool
 						mx = sc[j];
 				}
 				double sum = 0;
-				for (int j = 0; j <= p; j++) {
+				for (int j = j0; j <= p; j++) {
 					sc[j] = exp(sc[j] - mx);
 					sum += sc[j];
 				}
 				for (int d = 0; d < D; d++)
 					acc[d] = 0;
-				for (int j = 0; j <= p; j++) {
-					const uint16_t *vr = vpool + cell_of(b, s, j) * row + (int64_t)kh * D;
+				for (int j = j0; j <= p; j++) {
+					int64_t cell = ring ? ring_cell_of(b, s, j) : cell_of(b, s, j);
+					const uint16_t *vr = vpool + cell * row + (int64_t)kh * D;
 					double w = sc[j] / sum;
 					for (int d = 0; d < D; d++)
 						acc[d] += w * (double)orc_f16_to_f32(vr[d]);
@@ -887,37 +921,56 @@ done:
 	return rc;
 }
 
+/* ggml_gelu [ggml] (the tanh form): 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))),
+ * as geglu_split applies it to the gate (src/ops_nn.c:165-172). */
+static double
+gelu(double x)
+{
+	return 0.5 * x * (1.0 + tanh(0.7978845608028654 * (x + 0.044715 * x * x * x)));
+}
+
 /* transformer.lua:2285-2365 (forward) with qkv (:1754-1789), the batched
- * attention (:2389-2416: set_rows into the pool, then attend per
- * sequence), attn_out (:1859-1872), ffn (:2042-2080, SwiGLU), and head
- * (:2094-2104) on the rows of logit_rows (:2349-2350). llama / qwen3
- * layers with a dense FFN, or qwen3moe layers with routed experts
- * (moe_ffn); every matrix is an f32 or quantized weight. */
+ * attention (:2389-2416: set_rows into the pool or, for sliding layers, the
+ * ring, then attend per sequence), attn_out (:1859-1872), ffn (:2042-2080),
+ * and head (:2094-2104) on the rows of logit_rows (:2349-2350). llama /
+ * qwen3 layers with a dense FFN, qwen3moe layers with routed experts
+ * (moe_ffn), gemma layers (embedding scale :2304-2306, V rms-normed
+ * :1782-1784, post norms :1866-1868,2070-2072, GeGLU :2048, layer output
+ * scale :2334-2336, logit softcap :2097-2099). Every matrix is an f32 or
+ * quantized weight. */
 int
 orc_forward(const orc_model *m, uint16_t *const *kpool, uint16_t *const *vpool,
     int64_t cap, const orc_batch *b, float *logits, int nt)
 {
-	const int64_t E = m->n_embd, H = m->n_head, Hkv = m->n_head_kv, D = m->head_dim;
-	const int64_t F = m->n_ff, V = m->n_vocab;
-	int64_t N = 0;
+	const int64_t E = m->n_embd, H = m->n_head, F = m->n_ff, V = m->n_vocab;
+	int64_t N = 0, Dmax = m->head_dim, HKmax = m->n_head_kv;
 	int rc = 0;
 
 	for (int s = 0; s < b->n_seq; s++)
 		N += b->seq_n[s];
 	if (N == 0)
 		return 0;
+	for (int il = 0; il < m->n_layer; il++) {
+		const orc_layer *L = &m->layers[il];
+		if (L->head_dim > Dmax)
+			Dmax = L->head_dim;
+		if (L->n_head_kv > HKmax)
+			HKmax = L->n_head_kv;
+	}
+	const int64_t QW = H * Dmax > E ? H * Dmax : E;
 	float *x = malloc(sizeof(float) * (size_t)(N * E));
 	float *cur = malloc(sizeof(float) * (size_t)(N * E));
-	float *q = malloc(sizeof(float) * (size_t)(N * H * D));
-	float *k = malloc(sizeof(float) * (size_t)(N * Hkv * D));
-	float *v = malloc(sizeof(float) * (size_t)(N * Hkv * D));
-	float *o = malloc(sizeof(float) * (size_t)(N * H * D));
-	float *tmp = malloc(sizeof(float) * (size_t)(N * (E > H * D ? E : H * D)));
+	float *q = malloc(sizeof(float) * (size_t)(N * H * Dmax));
+	float *k = malloc(sizeof(float) * (size_t)(N * HKmax * Dmax));
+	float *v = malloc(sizeof(float) * (size_t)(N * HKmax * Dmax));
+	float *o = malloc(sizeof(float) * (size_t)(N * H * Dmax));
+	float *tmp = malloc(sizeof(float) * (size_t)(N * QW));
 	float *g = malloc(sizeof(float) * (size_t)(N * F));
 	float *u = malloc(sizeof(float) * (size_t)(N * F));
 	int32_t *pos = malloc(sizeof(int32_t) * (size_t)N);
 	int64_t *cells = malloc(sizeof(int64_t) * (size_t)N);
-	if (!x || !cur || !q || !k || !v || !o || !tmp || !g || !u || !pos || !cells) {
+	int64_t *rcells = malloc(sizeof(int64_t) * (size_t)N);
+	if (!x || !cur || !q || !k || !v || !o || !tmp || !g || !u || !pos || !cells || !rcells) {
 		rc = -1;
 		goto done;
 	}
@@ -925,22 +978,42 @@ orc_forward(const orc_model *m, uint16_t *const *kpool, uint16_t *const *vpool,
 		for (int j = 0; j < b->seq_n[s]; j++, t++) {
 			pos[t] = b->seq_npast[s] + j;
 			cells[t] = cell_of(b, s, pos[t]);
-			if (cells[t] < 0 || cells[t] >= cap) {
+			rcells[t] = b->ring_blocks > 0 ? ring_cell_of(b, s, pos[t]) : -1;
+			if (cells[t] < 0 || cells[t] >= cap || (b->ring_blocks > 0 && rcells[t] >= cap)) {
 				rc = -2;
 				goto done;
 			}
 		}
 	}
 	embed_rows(&m->tok_embd, E, b->ids, N, x);
-	float scale = m->attn_scale > 0 ? m->attn_scale : 1.0f / sqrtf((float)D);
+	if (m->embd_scale > 0)
+		for (int64_t i = 0; i < N * E; i++)
+			x[i] = x[i] * m->embd_scale;
 	for (int il = 0; il < m->n_layer; il++) {
 		const orc_layer *L = &m->layers[il];
+		const int64_t D = L->head_dim ? L->head_dim : m->head_dim;
+		const int64_t Hkv = L->n_head_kv ? L->n_head_kv : m->n_head_kv;
+		const int n_rot = L->n_rot ? L->n_rot : m->n_rot;
+		const float base = L->rope_base > 0 ? L->rope_base : m->rope_base;
+		const float *ff = L->rope_freqs ? L->rope_freqs : (m->gemma ? NULL : m->rope_freqs);
+		const float scale = m->attn_scale > 0 ? m->attn_scale : 1.0f / sqrtf((float)D);
+		if (L->swa && (b->ring_blocks < 1 || m->n_swa < 1)) {
+			rc = -7;
+			goto done;
+		}
 		for (int64_t t = 0; t < N; t++)
 			rms_norm_row(x + t * E, cur + t * E, E, m->eps, (const float *)L->attn_norm.data);
-		if (mm(&L->wq, H * D, E, cur, N, q, nt) || mm(&L->wk, Hkv * D, E, cur, N, k, nt) ||
-		    mm(&L->wv, Hkv * D, E, cur, N, v, nt)) {
+		if (mm(&L->wq, H * D, E, cur, N, q, nt) || mm(&L->wk, Hkv * D, E, cur, N, k, nt)) {
 			rc = -3;
 			goto done;
+		}
+		if (L->wv.data) {
+			if (mm(&L->wv, Hkv * D, E, cur, N, v, nt)) {
+				rc = -3;
+				goto done;
+			}
+		} else {
+			memcpy(v, k, sizeof(float) * (size_t)(N * Hkv * D));  /* V = raw K */
 		}
 		for (int64_t t = 0; t < N; t++) {
 			if (L->q_norm.data)
@@ -951,15 +1024,18 @@ orc_forward(const orc_model *m, uint16_t *const *kpool, uint16_t *const *vpool,
 				for (int h = 0; h < Hkv; h++)
 					rms_norm_row(k + (t * Hkv + h) * D, k + (t * Hkv + h) * D, D, m->eps,
 					    (const float *)L->k_norm.data);
-			rope_row(q + t * H * D, (int)H, (int)D, m->n_rot, m->rope_neox, m->rope_base,
-			    m->rope_freqs, pos[t]);
-			rope_row(k + t * Hkv * D, (int)Hkv, (int)D, m->n_rot, m->rope_neox, m->rope_base,
-			    m->rope_freqs, pos[t]);
+			if (m->gemma)
+				for (int h = 0; h < Hkv; h++)
+					rms_norm_row(v + (t * Hkv + h) * D, v + (t * Hkv + h) * D, D, m->eps,
+					    NULL);
+			rope_row(q + t * H * D, (int)H, (int)D, n_rot, m->rope_neox, base, ff, pos[t]);
+			rope_row(k + t * Hkv * D, (int)Hkv, (int)D, n_rot, m->rope_neox, base, ff, pos[t]);
 		}
-		orc_set_rows_f16(kpool[il], cap, Hkv * D, k, cells, N);
-		orc_set_rows_f16(vpool[il], cap, Hkv * D, v, cells, N);
-		if (orc_paged_attention(q, kpool[il], vpool[il], (int)H, (int)Hkv, (int)D, scale, b, o,
-		    nt)) {
+		const int64_t *wc = L->swa ? rcells : cells;
+		orc_set_rows_f16(kpool[il], cap, Hkv * D, k, wc, N);
+		orc_set_rows_f16(vpool[il], cap, Hkv * D, v, wc, N);
+		if (attend(q, kpool[il], vpool[il], (int)H, (int)Hkv, (int)D, scale,
+		    L->swa ? m->n_swa : 0, L->swa, b, o, nt)) {
 			rc = -4;
 			goto done;
 		}
@@ -967,6 +1043,10 @@ orc_forward(const orc_model *m, uint16_t *const *kpool, uint16_t *const *vpool,
 			rc = -3;
 			goto done;
 		}
+		if (L->post_attn_norm.data)
+			for (int64_t t = 0; t < N; t++)
+				rms_norm_row(tmp + t * E, tmp + t * E, E, m->eps,
+				    (const float *)L->post_attn_norm.data);
 		for (int64_t i = 0; i < N * E; i++)
 			x[i] = tmp[i] + x[i];
 		for (int64_t t = 0; t < N; t++)
@@ -976,22 +1056,30 @@ orc_forward(const orc_model *m, uint16_t *const *kpool, uint16_t *const *vpool,
 				rc = -6;
 				goto done;
 			}
-			continue;
+		} else {
+			if (mm(&L->gate, F, E, cur, N, g, nt) || mm(&L->up, F, E, cur, N, u, nt)) {
+				rc = -3;
+				goto done;
+			}
+			for (int64_t i = 0; i < N * F; i++) {
+				double gv = g[i];
+				double a = m->gemma ? gelu(gv) : gv / (1.0 + exp(-gv));
+				g[i] = (float)(a * (double)u[i]);
+			}
+			if (mm(&L->down, E, F, g, N, tmp, nt)) {
+				rc = -3;
+				goto done;
+			}
+			if (L->post_ffn_norm.data)
+				for (int64_t t = 0; t < N; t++)
+					rms_norm_row(tmp + t * E, tmp + t * E, E, m->eps,
+					    (const float *)L->post_ffn_norm.data);
+			for (int64_t i = 0; i < N * E; i++)
+				x[i] = tmp[i] + x[i];
 		}
-		if (mm(&L->gate, F, E, cur, N, g, nt) || mm(&L->up, F, E, cur, N, u, nt)) {
-			rc = -3;
-			goto done;
-		}
-		for (int64_t i = 0; i < N * F; i++) {
-			double gv = g[i];
-			g[i] = (float)(gv / (1.0 + exp(-gv)) * (double)u[i]);
-		}
-		if (mm(&L->down, E, F, g, N, tmp, nt)) {
-			rc = -3;
-			goto done;
-		}
-		for (int64_t i = 0; i < N * E; i++)
-			x[i] = tmp[i] + x[i];
+		if (L->out_scale != 0.0f)
+			for (int64_t i = 0; i < N * E; i++)
+				x[i] = x[i] * L->out_scale;
 	}
 	for (int r = 0; r < b->n_out; r++) {
 		if (b->out_rows[r] < 0 || b->out_rows[r] >= N) {
@@ -1001,8 +1089,13 @@ orc_forward(const orc_model *m, uint16_t *const *kpool, uint16_t *const *vpool,
 		rms_norm_row(x + (int64_t)b->out_rows[r] * E, cur + (int64_t)r * E, E, m->eps,
 		    (const float *)m->output_norm.data);
 	}
-	if (mm(&m->output, V, E, cur, b->n_out, logits, nt))
+	if (mm(&m->output, V, E, cur, b->n_out, logits, nt)) {
 		rc = -3;
+		goto done;
+	}
+	if (m->softcap > 0)
+		for (int64_t i = 0; i < (int64_t)b->n_out * V; i++)
+			logits[i] = (float)((double)m->softcap * tanh((double)logits[i] / m->softcap));
 done:
 	free(x);
 	free(cur);
@@ -1015,5 +1108,6 @@ done:
 	free(u);
 	free(pos);
 	free(cells);
+	free(rcells);
 	return rc;
 }

@@ -68,6 +68,18 @@ typedef struct {
 	 * n_expert matrices (n_embd, n_ff_exp), each expert's rows contiguous.
 	 * A layer with gate_inp.data set has no dense FFN. */
 	orc_tensor gate_inp, gate_exps, up_exps, down_exps;
+	/* gemma (transformer.lua:300-333): post-attention and post-FFN norms
+	 * (data NULL = none), the layer output scale (0 = none). swa: a
+	 * sliding-window layer (its K/V in the sequence's ring, the window
+	 * mask). head_dim, n_head_kv, n_rot, rope_base: this layer's attention
+	 * shape and rope (0 = the model's); rope_freqs: its frequency factors
+	 * (NULL = none). A gemma layer with wv.data NULL takes V = the raw K
+	 * (:1779). */
+	orc_tensor post_attn_norm, post_ffn_norm;
+	float out_scale;
+	int swa, head_dim, n_head_kv, n_rot;
+	float rope_base;
+	const float *rope_freqs;
 } orc_layer;
 
 /* Expert gating functions (transformer.lua:32-35). */
@@ -84,6 +96,11 @@ typedef struct {
 	 * token, expert FFN width, gating, norm_topk, expert_scale. */
 	int n_expert, n_used, n_ff_exp, gating, norm_topk;
 	float expert_scale;
+	/* gemma (transformer.lua:171-183): V rms-normed, GeGLU, embeddings
+	 * times embd_scale (0 = none), logits softcap * tanh(l / softcap)
+	 * (0 = none); n_swa: the sliding window of swa layers. */
+	int gemma, n_swa;
+	float embd_scale, softcap;
 } orc_model;
 
 /* One ubatch over a paged pool. Sequence s owns tokens
@@ -99,6 +116,13 @@ typedef struct {
 	const int32_t *ids;
 	int n_out;
 	const int32_t *out_rows;
+	/* Sliding-window layers keep a ring of ring_blocks blocks per
+	 * sequence: position p of sequence s lives in cell
+	 * ring_tab[s * ring_blocks + (p / block) % ring_blocks] * block +
+	 * p % block of those layers' pools (rows_swa = p % ring,
+	 * transformer.lua:2469-2476, with ring = ring_blocks * block). */
+	int ring_blocks;
+	const int32_t *ring_tab;
 } orc_batch;
 
 int orc_forward(const orc_model *m, uint16_t *const *kpool, uint16_t *const *vpool,
@@ -109,6 +133,12 @@ int orc_forward(const orc_model *m, uint16_t *const *kpool, uint16_t *const *vpo
  * sequence's own positions 0..npast+j. */
 int orc_paged_attention(const float *q, const uint16_t *kpool, const uint16_t *vpool,
     int H, int Hkv, int D, float scale, const orc_batch *b, float *out, int n_threads);
+/* The same over the sequences' rings with a sliding window
+ * (tensor_fill_mask window + ring, src/lgml.c:2873-2935): query j sees
+ * positions max(0, p - window + 1)..p, p = npast + j. */
+int orc_paged_attention_swa(const float *q, const uint16_t *kpool, const uint16_t *vpool,
+    int H, int Hkv, int D, float scale, int window, const orc_batch *b, float *out,
+    int n_threads);
 
 /* ggml_set_rows (src/lgml.c:1937-1969): dst[ids[j]] = f16(src[j]). */
 int orc_set_rows_f16(uint16_t *dst, int64_t dst_rows, int64_t row, const float *src,

@@ -63,3 +63,52 @@ def test_greedy_stream_follows_reference(oracle_lib):
     nb = sum(len(b) for b in d["batches"])
     for i in range(nb, len(ref)):
         assert ref[i]["id"] == core.argmax(rows[i - 1])
+
+
+GOLDEN_G4 = os.path.join(os.path.dirname(__file__), "golden", "ref_gemma4.json")
+
+
+def run_gemma4_rows(block=64, ring_blocks=1):
+    """The tiny gemma4 rows: the two prompt batches, then the greedy ids.
+    Global layers use a paged pool; the sliding layer a ring of
+    ring_blocks blocks of `block` cells (it must hold window - 1 + 20)."""
+    hp, w = models.ref_tiny_gemma4()
+    m = core.OracleModel(hp, w)
+    d = json.load(open(GOLDEN_G4))
+    ref = d["rows"]["dense"]
+    cap = 256
+    kp = [np.zeros((cap, L["n_head_kv"] * L["head_dim"]), np.uint16) for L in w["layers"]]
+    vp = [np.zeros((cap, L["n_head_kv"] * L["head_dim"]), np.uint16) for L in w["layers"]]
+    block_tab = list(range(64 // block))            # positions 0..63: cells 0..63
+    ring_tab = [cap // block - 1 - i for i in range(ring_blocks)]  # the ring from the top
+    nb = sum(len(b) for b in d["batches"])
+    passes = d["batches"] + [[r["id"]] for r in ref[nb:]]
+    rows, npast = [], 0
+    for ids in passes:
+        b = core.BatchDesc([len(ids)], [npast], [block_tab], block, ids, list(range(len(ids))),
+                           ring_tab=[ring_tab])
+        rows.extend(m.forward(kp, vp, b))
+        npast += len(ids)
+    return d, ref, rows
+
+
+def test_oracle_matches_gemma4_rows(oracle_lib):
+    """REF.dense of test/test_gemma4.lua:192-224: a sliding layer (window 6,
+    a 20-token prompt longer than it) and a global one; TOL 2e-3 + argmax."""
+    d, ref, rows = run_gemma4_rows()
+    idx = [i - 1 for i in d["idx_1based"]]
+    assert len(rows) == len(ref) == 31
+    err = 0.0
+    for r, got in zip(ref, rows):
+        err = max(err, max(abs(float(got[i]) - v) for i, v in zip(idx, r["v"])))
+        assert core.argmax(got) == r["best"], "argmax differs from llama.cpp"
+    assert err < d["tol"], "max logit error %.3g" % err
+
+
+def test_oracle_ring_wraps_give_the_same_rows(oracle_lib):
+    """A ring of 7 blocks of 4 cells (28 >= window - 1 + 20) wraps at
+    position 28; the rows equal those of an unwrapped ring bit for bit
+    (rows_swa = p % ring, transformer.lua:2469-2476)."""
+    _, _, a = run_gemma4_rows(block=64, ring_blocks=1)
+    _, _, b = run_gemma4_rows(block=4, ring_blocks=7)
+    assert np.array_equal(np.array(a), np.array(b))
