@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define LGMLH_ABI_VERSION 3
+#define LGMLH_ABI_VERSION 4
 
 enum {
 	LGMLH_OK = 0,
@@ -140,6 +140,7 @@ typedef struct {
 	/* byte offsets of the arrays inside the plan buffer */
 	int64_t off_ids, off_pos, off_cells, off_seq_off, off_npast, off_block_tab, off_logit_rows,
 	    off_items, off_merge;
+	int32_t window, ring;  /* a ring plan (lgmlh_plan_ring): window, ring blocks; else 0 */
 } lgmlh_plan_info;
 
 typedef struct {
@@ -154,6 +155,7 @@ typedef struct {
 	const int32_t *logit_rows; /* [n_seq] off + n - 1 (batch_inputs :2540-2545) */
 	const int32_t *items;      /* [n_items * 4] attention work items */
 	const int32_t *merge;      /* [n_merge * 4] split-merge groups */
+	int32_t window, ring;      /* ring plans: the window and the ring's blocks; else 0 */
 } lgmlh_ubatch;
 
 /* Plan a pass. G = n_head / n_head_kv; blocks_per_split bounds the KV
@@ -166,6 +168,19 @@ typedef struct {
  * src/lgml.c:3003-3008), or a position passes 65535 blocks. */
 int lgmlh_plan(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
     const int32_t *block_tab, int max_blocks, int64_t pool_blocks, const int32_t *ids,
+    int n_head, int n_head_kv, int blocks_per_split, void *buf, size_t buf_bytes,
+    lgmlh_plan_info *info);
+/* The plan of a pass over the sliding-window layers (transformer.lua:
+ * 2464-2476, tensor_fill_mask with window and ring, src/lgml.c:2873-2935):
+ * sequence s keeps a ring of ring_blocks blocks, ring_tab[s * ring_blocks
+ * + i]; position p lives in cell ring_tab[s * ring_blocks + (p / 64) %
+ * ring_blocks] * 64 + p % 64 (rows_swa = p % ring, ring = 64 ring_blocks
+ * cells). Query p sees positions max(0, p - window + 1)..p. The ring must
+ * hold window - 1 + seq_n[s] cells (the "tokens in one pass" error of
+ * transformer.lua:1544-1546, LGMLH_ERANGE). block_tab / max_blocks of the
+ * resulting plan are the ring tables; items hold logical block ranges. */
+int lgmlh_plan_ring(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
+    const int32_t *ring_tab, int ring_blocks, int64_t pool_blocks, int window, const int32_t *ids,
     int n_head, int n_head_kv, int blocks_per_split, void *buf, size_t buf_bytes,
     lgmlh_plan_info *info);
 /* Device views of a plan buffer at dev (a device copy of buf). */
@@ -281,6 +296,12 @@ int lgmlh_qkv_rope_store(float *qkv, int64_t n, int n_head, int n_head_kv, int h
     int64_t n_cells, const int64_t *cells, float *q_out, void *stream);
 /* silu(g) * u (transformer.lua:2048) for gu = (n, 2F) rows [g | u]; out f32 or f16. */
 int lgmlh_swiglu(const float *gu, int64_t n, int64_t F, void *out, int out_type, void *stream);
+/* gelu(g) * u, the gemma FFN (graph:geglu_split, src/ops_nn.c:165-172;
+ * transformer.lua:2048): gelu in ggml's tanh form. Same layout as swiglu. */
+int lgmlh_geglu(const float *gu, int64_t n, int64_t F, void *out, int out_type, void *stream);
+/* The final logit softcap (transformer.lua:2097-2099): x = cap * tanh(x *
+ * (1 / cap)) in place, n values. */
+int lgmlh_softcap(float *x, int64_t n, float cap, void *stream);
 /* Greedy id of each row: the first index of the maximum (src/sample.c:914-925). */
 int lgmlh_argmax(const float *x, int64_t n_rows, int64_t n_cols, int32_t *out, void *stream);
 
@@ -314,6 +335,18 @@ typedef struct {
 	const float *gate_inp;
 	int exp_gu_type, exp_down_type;
 	const void *exp_gu, *exp_down;
+	/* Gemma and sliding-window layers (transformer.lua:171-183,215-235,
+	 * 300-333). swa: K / V in the ring pools (kpool / vpool hold ring
+	 * blocks), attention through the ring plan. v_from_k: wqkv holds
+	 * [wq | wk] only and V is the raw K (:1779). post_attn_norm /
+	 * post_ffn_norm: rms-norm weights of the attention / FFN outputs before
+	 * the residual add (NULL = none). out_scale: the layer output scale
+	 * (0 = none). rope_base / rope_freqs: this layer's rope (0 / NULL = the
+	 * model's). */
+	int swa, v_from_k;
+	const float *post_attn_norm, *post_ffn_norm;
+	float out_scale, rope_base;
+	const float *rope_freqs;
 } lgmlh_layer;
 
 typedef struct {
@@ -330,12 +363,19 @@ typedef struct {
 	 * width, LGMLH_GATING_*, norm_topk, expert_scale. */
 	int n_expert, n_used, n_ff_exp, gating, norm_topk;
 	float expert_scale;
+	/* Gemma (transformer.lua:171-183): V rms-normed, GeGLU FFN, embeddings
+	 * times embd_scale (0 = none), logits softcapped (softcap 0 = none).
+	 * ring_cells: cells of each sliding layer's ring pools. */
+	int gemma;
+	float embd_scale, softcap;
+	int64_t ring_cells;
 } lgmlh_model;
 
 /* Workspace bytes of lgmlh_forward for a plan and n_out logit rows. Its
  * contents need no initialisation; one workspace (grown when a larger pass
  * needs more) serves passes of any size on one stream. */
-size_t lgmlh_forward_workspace(const lgmlh_model *m, const lgmlh_plan_info *info, int n_out);
+size_t lgmlh_forward_workspace(const lgmlh_model *m, const lgmlh_plan_info *info,
+    const lgmlh_plan_info *info_ring, int n_out);
 /* Optional timing: hipEvent_t handles (created by the caller), two per
  * slot, recorded on the pass's stream right before and after each traced
  * launch group. kinds: LGMLH_TRACE_ATTN (paged attention + merge, one slot
@@ -352,10 +392,11 @@ typedef struct {
 /* Run the pass: logits (n_out, n_vocab) f32 for the ubatch rows out_rows
  * (device; NULL = ub->logit_rows with n_out = n_seq). ids must be in range
  * (checked by the caller's plan, h_ids) -- the kernel reads them unchecked.
- * trace may be NULL. */
-int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub, const int32_t *out_rows,
-    int n_out, float *logits, void *workspace, size_t ws_bytes, lgmlh_trace *trace,
-    void *stream);
+ * ub_ring: the ring plan of the same pass (lgmlh_plan_ring), needed when
+ * a layer slides (NULL otherwise). trace may be NULL. */
+int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub, const lgmlh_ubatch *ub_ring,
+    const int32_t *out_rows, int n_out, float *logits, void *workspace, size_t ws_bytes,
+    lgmlh_trace *trace, void *stream);
 
 #ifdef __cplusplus
 }

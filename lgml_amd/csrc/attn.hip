@@ -45,13 +45,17 @@ struct Partial {
   static constexpr int floats = ROWS * D + 2 * ROWS;
 };
 
-template <int D>
+// RING: a sliding-window plan. Items hold logical block ranges; logical
+// block b of sequence s is ring entry b % ring, and row position p sees
+// positions p - window + 1 .. p only.
+template <int D, bool RING>
 __global__ void __launch_bounds__(64)
 paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
                   const uint16_t *__restrict__ kpool, const uint16_t *__restrict__ vpool,
                   const int32_t *__restrict__ items, const int32_t *__restrict__ seq_off,
                   const int32_t *__restrict__ seq_npast, const int32_t *__restrict__ block_tab,
-                  int max_blocks, float *__restrict__ out, float *__restrict__ part) {
+                  int max_blocks, int ring, int window, float *__restrict__ out,
+                  float *__restrict__ part) {
   constexpr int KS = D / 32;   // MFMA k-steps over D
   constexpr int DT = D / 16;   // d tiles of the output
   __shared__ __align__(16) uint16_t plh[ROWS * P_STRIDE];  // P as f16 hi
@@ -107,8 +111,9 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
   float m = -INFINITY, l = 0.0f;
 
   const int32_t *bt = block_tab + (int64_t)s * max_blocks;
-  auto ktile = [&](int blk) { return kpool + ((int64_t)bt[blk] * Hkv + kvh) * (int64_t)(64 * D); };
-  auto vtile = [&](int blk) { return vpool + ((int64_t)bt[blk] * Hkv + kvh) * (int64_t)(64 * D); };
+  auto phys = [&](int blk) -> int64_t { return RING ? bt[blk % ring] : bt[blk]; };
+  auto ktile = [&](int blk) { return kpool + (phys(blk) * Hkv + kvh) * (int64_t)(64 * D); };
+  auto vtile = [&](int blk) { return vpool + (phys(blk) * Hkv + kvh) * (int64_t)(64 * D); };
   // K rows (A operand of S^T = K Q^T) and V^T columns (A operand of
   // O^T += V^T P^T) of one block, straight from the pool tiles.
   f16x8 kf[4][KS], vf[DT][2];
@@ -148,17 +153,20 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
     load_k(ktile(nxt));
 
     // Mask and row max: lane holds cells ct*16 + quad*4 + i of its row. A
-    // block that ends at or before the group's first position is visible to
-    // every valid row.
+    // block that ends at or before the group's first position (and, with a
+    // window, starts inside the window of its last) is visible to every
+    // valid row.
     const int cbase = blk * 64;
-    const bool full = cbase + 63 <= p_first;
+    const bool full = cbase + 63 <= p_first &&
+                      (!RING || cbase > p_first + ntok - 1 - window);
     float mx = -INFINITY;
 #pragma unroll
     for (int ct = 0; ct < 4; ct++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int p = cbase + ct * 16 + quad * 4 + i;
-        const float v = (rvalid && (full || p <= p_row)) ? st[ct][i] * scale_log2 : -INFINITY;
+        const bool vis = full || (p <= p_row && (!RING || p > p_row - window));
+        const float v = (rvalid && vis) ? st[ct][i] * scale_log2 : -INFINITY;
         st[ct][i] = v;
         mx = fmaxf(mx, v);
       }
@@ -307,9 +315,16 @@ template <int D>
 static void launch_attn(const float *q, int H, int Hkv, float scale_log2, const void *kp,
                         const void *vp, const lgmlh_ubatch *ub, float *out, float *part,
                         hipStream_t st) {
-  hipLaunchKernelGGL(paged_attn_kernel<D>, dim3(ub->n_items, Hkv), dim3(64), 0, st, q, H, Hkv,
-                     scale_log2, (const uint16_t *)kp, (const uint16_t *)vp, ub->items,
-                     ub->seq_off, ub->seq_npast, ub->block_tab, ub->max_blocks, out, part);
+  if (ub->ring > 0)
+    hipLaunchKernelGGL((paged_attn_kernel<D, true>), dim3(ub->n_items, Hkv), dim3(64), 0, st, q,
+                       H, Hkv, scale_log2, (const uint16_t *)kp, (const uint16_t *)vp, ub->items,
+                       ub->seq_off, ub->seq_npast, ub->block_tab, ub->max_blocks, ub->ring,
+                       ub->window, out, part);
+  else
+    hipLaunchKernelGGL((paged_attn_kernel<D, false>), dim3(ub->n_items, Hkv), dim3(64), 0, st, q,
+                       H, Hkv, scale_log2, (const uint16_t *)kp, (const uint16_t *)vp, ub->items,
+                       ub->seq_off, ub->seq_npast, ub->block_tab, ub->max_blocks, 0, 0, out,
+                       part);
   if (ub->n_merge > 0)
     hipLaunchKernelGGL(merge_kernel<D>, dim3(ub->n_merge, Hkv), dim3(64), 0, st, ub->merge, H,
                        Hkv, part, out);

@@ -31,11 +31,16 @@ inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s);
 // adds them in order z = 0, 1, ... (then the residual, if any).
 // With wts set, the terms are the expert outputs of a token's picks
 // instead: part[n][z][m] times wts[n][z] for the splits = n_used picks.
+// With post set (gemma post norms), the consumer adds rms_norm(sum) * post
+// rather than the sum; then, with scale != 0, multiplies the new residual
+// by scale (the layer output scale).
 struct Pending {
   const float *part = nullptr;
   int splits = 0;
   int64_t rows = 0, cols = 0;
   const float *wts = nullptr;
+  const float *post = nullptr;
+  float scale = 0.0f;
   __device__ __forceinline__ float sum(int64_t n, int64_t m) const {
     float v = 0.0f;
     if (wts) {

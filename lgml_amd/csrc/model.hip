@@ -22,15 +22,17 @@ int rms_norm_dev(float *x, const int32_t *rows, int64_t n_rows, int64_t n, float
                  const float *w, float *out, f16 *planes, hipStream_t st, Pending pend,
                  bool writeback);
 int swiglu_dev(const float *gu, int64_t n, int64_t F, float *out, f16 *planes, hipStream_t st,
-               Pending pend);
+               Pending pend, int gelu);
+int softcap_dev(float *x, int64_t n, float cap, hipStream_t st);
 int qkv_rope_store_dev(float *qkv, int64_t n, int n_head, int n_head_kv, int head_dim, int n_rot,
                        int neox, float freq_base, const float *freq_factors, const float *q_norm,
                        const float *k_norm, float eps, const int32_t *pos, void *kpool,
                        void *vpool, int64_t n_cells, const int64_t *cells, float *q_out,
-                       void *stream, Pending pa, Pending pb);
+                       void *stream, Pending pa, Pending pb, int vmode);
 size_t partial_bytes(int type, int64_t M, int64_t K, int64_t N);
 int get_rows_dev(int type, const void *table, int64_t n_cols, const int32_t *ids, int64_t n,
-                 float *out, hipStream_t st);
+                 float *out, hipStream_t st, float scale);
+constexpr int QKV_V_FROM_K = 1, QKV_V_NORM = 2;
 
 struct Carve {
   char *p;
@@ -119,6 +121,7 @@ static size_t ws_bytes_of(const Sizes &z) {
   add(z.N * 2 * z.F * 4);    // [gate | up]
   add(z.N * z.F * 4);        // silu(gate) * up
   add(z.n_out * z.E * 4);    // normed logit rows
+  add(z.N * z.E * 4);        // a post-normed product (gemma), pending
   add(z.split_ws);           // split planes of the current product's X
   add(z.attn_ws);
   add(z.gemm_ws);
@@ -140,9 +143,11 @@ static size_t ws_bytes_of(const Sizes &z) {
 using namespace lgmlh;
 
 extern "C" size_t lgmlh_forward_workspace(const lgmlh_model *m, const lgmlh_plan_info *info,
-                                          int n_out) {
+                                          const lgmlh_plan_info *info_ring, int n_out) {
   if (!m || !info || !m->layers) return 0;
-  return ws_bytes_of(sizes_of(m, info->n_tokens, info->n_items, n_out));
+  int items = info->n_items;
+  if (info_ring && info_ring->n_items > items) items = info_ring->n_items;
+  return ws_bytes_of(sizes_of(m, info->n_tokens, items, n_out));
 }
 
 namespace {
@@ -164,19 +169,27 @@ struct Span {
 }  // namespace
 
 extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
-                             const int32_t *out_rows, int n_out, float *logits, void *workspace,
-                             size_t ws_bytes, lgmlh_trace *trace, void *stream) {
+                             const lgmlh_ubatch *ub_ring, const int32_t *out_rows, int n_out,
+                             float *logits, void *workspace, size_t ws_bytes, lgmlh_trace *trace,
+                             void *stream) {
   if (!m || !ub || !logits || !workspace || !m->layers || m->n_layer <= 0 ||
       m->n_head_kv != ub->n_head_kv) {
     set_error("forward: bad arguments");
     return LGMLH_EINVAL;
   }
+  for (int il = 0; il < m->n_layer; il++)
+    if (m->layers[il].swa && (!ub_ring || ub_ring->ring <= 0 || ub_ring->n_tokens != ub->n_tokens ||
+                              ub_ring->n_head_kv != ub->n_head_kv)) {
+      set_error("forward: layer %d slides and needs the pass's ring plan", il);
+      return LGMLH_EINVAL;
+    }
   if (!out_rows) {
     out_rows = ub->logit_rows;
     n_out = ub->n_seq;
   }
   hipStream_t st = as_stream(stream);
-  Sizes z = sizes_of(m, ub->n_tokens, ub->n_items, n_out);
+  const int items = ub_ring && ub_ring->n_items > ub->n_items ? ub_ring->n_items : ub->n_items;
+  Sizes z = sizes_of(m, ub->n_tokens, items, n_out);
   size_t need = ws_bytes_of(z);
   if (ws_bytes < need) {
     set_error("forward: workspace of %zu bytes, need %zu", ws_bytes, need);
@@ -193,6 +206,7 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
   float *gu = (float *)cv.take(z.N * 2 * z.F * 4);
   float *act = (float *)cv.take(z.N * z.F * 4);
   float *xo = (float *)cv.take(z.n_out * z.E * 4);
+  float *ao = (float *)cv.take(z.N * z.E * 4);
   f16 *xs = (f16 *)cv.take(z.split_ws);
   void *aws = cv.take(z.attn_ws);
   float *gws = (float *)cv.take(z.gemm_ws);
@@ -232,10 +246,26 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
     return rc;
   };
   auto isq = [](int type) { return type != LGMLH_F32; };
+  // A product whose output goes to the residual stream x: added into x by
+  // the GEMM (or left pending, the consumer adds it), or, with a post norm
+  // or an output scale (gemma), left pending in ao: the next norm adds
+  // rms_norm(product) * post to x, then scales.
+  auto out_product = [&](int type, const void *w, int64_t K, const float *xf, const float *post,
+                         float oscale, Pending &pd) -> int {
+    if (!post && oscale == 0.0f)
+      return gemm(type, w, z.E, K, xf, z.N, x, z.E, x, gws, z.gemm_ws, pd);
+    LGMLH_TRY(gemm(type, w, z.E, K, xf, z.N, ao, z.E, nullptr, gws, z.gemm_ws, pd));
+    if (!pd.splits) pd = Pending{ao, 1, z.N, z.E};
+    pd.post = post;
+    pd.scale = oscale;
+    return LGMLH_OK;
+  };
   Pending p_qk, p_v, p_o, p_gu, p_down;
-  // token embeddings (get_rows, transformer.lua:2309); the ids were range
-  // checked when the plan was made.
-  LGMLH_TRY(get_rows_dev(m->tok_embd_type, m->tok_embd, z.E, ub->ids, z.N, x, st));
+  // token embeddings (get_rows, transformer.lua:2309; times the gemma
+  // embedding scale, :2304-2306); the ids were range checked when the plan
+  // was made.
+  LGMLH_TRY(get_rows_dev(m->tok_embd_type, m->tok_embd, z.E, ub->ids, z.N, x, st,
+                         m->embd_scale));
   for (int il = 0; il < m->n_layer; il++) {
     const lgmlh_layer &L = m->layers[il];
     const bool v_sep = L.wv != nullptr;
@@ -250,17 +280,23 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
     if (v_sep)
       LGMLH_TRY(gemm(L.wv_type, L.wv, z.W - L.wqkv_rows, z.E, xn, z.N, qkv + L.wqkv_rows, z.W,
                      nullptr, gws_v, z.gemm_ws_v, p_v));
+    // a sliding layer keeps its K / V in the sequences' rings (rows_swa,
+    // transformer.lua:2469-2476) and attends through the ring plan
+    const lgmlh_ubatch *lub = L.swa ? ub_ring : ub;
+    const int vmode = (L.v_from_k ? QKV_V_FROM_K : 0) | (m->gemma ? QKV_V_NORM : 0);
     LGMLH_TRY(qkv_rope_store_dev(qkv, z.N, (int)z.H, (int)z.Hkv, (int)z.D, m->n_rot,
-                                 m->rope_neox, m->rope_base, m->rope_freqs, L.q_norm, L.k_norm,
-                                 m->eps, ub->pos, L.kpool, L.vpool, m->n_cells, ub->cells, q, st,
-                                 p_qk, p_v));
+                                 m->rope_neox, L.rope_base > 0 ? L.rope_base : m->rope_base,
+                                 L.rope_freqs ? L.rope_freqs : m->rope_freqs, L.q_norm, L.k_norm,
+                                 m->eps, ub->pos, L.kpool, L.vpool,
+                                 L.swa ? m->ring_cells : m->n_cells, lub->cells, q, st, p_qk, p_v,
+                                 vmode));
     {
       Span sp(trace, LGMLH_TRACE_ATTN, st);
       LGMLH_TRY(lgmlh_paged_attention(q, (int)z.H, (int)z.Hkv, (int)z.D, scale, L.kpool,
-                                      L.vpool, ub, att, aws, z.attn_ws, st));
+                                      L.vpool, lub, att, aws, z.attn_ws, st));
     }
     if (isq(L.wo_type)) LGMLH_TRY(split_x(att, LGMLH_F32, z.N, z.H * z.D, xs, st));
-    LGMLH_TRY(gemm(L.wo_type, L.wo, z.E, z.H * z.D, att, z.N, x, z.E, x, gws, z.gemm_ws, p_o));
+    LGMLH_TRY(out_product(L.wo_type, L.wo, z.H * z.D, att, L.post_attn_norm, 0.0f, p_o));
     if (L.gate_inp) {
       // routed experts (transformer.lua:2054-2068, M.moe :1989-2027): x +=
       // attention out, then ffn_norm for the router (f32) and the experts
@@ -280,7 +316,7 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
       }
       // swiglu_split on the picks' rows; their split planes replace x's
       LGMLH_TRY(swiglu_dev(gu_e, z.P, z.FX, dq ? nullptr : act_e, dq ? xs : nullptr, st,
-                           Pending{}));
+                           Pending{}, 0));
       {
         Span sp(trace, LGMLH_TRACE_EXPERTS, st);
         LGMLH_TRY(experts_dev(L.exp_down_type, L.exp_down, z.NE, z.E, z.FX, act_e, xs,
@@ -297,10 +333,10 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
                            p_o, true));
     LGMLH_TRY(gemm(L.wgu_type, L.wgu, 2 * z.F, z.E, xn, z.N, gu, 2 * z.F, nullptr, gws,
                    z.gemm_ws, p_gu));
+    // SwiGLU, or GeGLU on gemma (transformer.lua:2048)
     LGMLH_TRY(swiglu_dev(gu, z.N, z.F, isq(L.wdown_type) ? nullptr : act,
-                         isq(L.wdown_type) ? xs : nullptr, st, p_gu));
-    LGMLH_TRY(gemm(L.wdown_type, L.wdown, z.E, z.F, act, z.N, x, z.E, x, gws, z.gemm_ws,
-                   p_down));
+                         isq(L.wdown_type) ? xs : nullptr, st, p_gu, m->gemma));
+    LGMLH_TRY(out_product(L.wdown_type, L.wdown, z.F, act, L.post_ffn_norm, L.out_scale, p_down));
   }
   // head (transformer.lua:2094-2104) on the logit rows (:2349-2350); the last
   // down product is added to those rows only (x is not needed afterwards)
@@ -316,6 +352,8 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
     else
       LGMLH_TRY(mul_mat_f32((const float *)m->output, z.V, z.E, xo, n_out, logits, z.V, nullptr,
                             st));
+    // the final logit softcap (transformer.lua:2097-2099)
+    if (m->softcap > 0) LGMLH_TRY(softcap_dev(logits, (int64_t)n_out * z.V, m->softcap, st));
   }
   return LGMLH_OK;
 }

@@ -25,13 +25,17 @@ int hip_check(hipError_t e, const char *what) {
 }
 
 // ---- get_rows (graph:get_rows, src/lgml.c:1913-1935) ----------------------
+// With scale != 0 the rows are multiplied by it (the gemma embedding scale,
+// transformer.lua:2304-2306).
 __global__ void get_rows_kernel(int type, const uint8_t *__restrict__ table, int64_t rb,
                                 int64_t n_cols, const int32_t *__restrict__ ids,
-                                float *__restrict__ out) {
+                                float *__restrict__ out, float scale) {
   int64_t j = blockIdx.x;
   const uint8_t *row = table + (int64_t)ids[j] * rb;
-  for (int64_t k = threadIdx.x; k < n_cols; k += blockDim.x)
-    out[j * n_cols + k] = row_value(type, row, k);
+  for (int64_t k = threadIdx.x; k < n_cols; k += blockDim.x) {
+    const float v = row_value(type, row, k);
+    out[j * n_cols + k] = scale != 0.0f ? v * scale : v;
+  }
 }
 
 __global__ void dequant_kernel(int type, const uint8_t *__restrict__ w, int64_t rb, int64_t K,
@@ -54,15 +58,25 @@ __global__ void rms_norm_kernel(float *__restrict__ x, const int32_t *__restrict
                                 int64_t n, float eps, const float *__restrict__ w,
                                 OutT *__restrict__ out, f16 *__restrict__ planes, int64_t npad,
                                 Pending pend, bool writeback) {
-  __shared__ double part[RMS_THREADS / 64];
+  __shared__ double part[2][RMS_THREADS / 64];
   const int tid = threadIdx.x;
   const int64_t r = blockIdx.x;
   const int64_t rr = rows ? (int64_t)rows[r] : r;
   float *xr = x + rr * n;
+  // sum of squares over the row (f64, fixed order) into slot k
+  auto row_sumsq = [&](double s, int k) -> double {
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    if ((tid & 63) == 0) part[k][tid >> 6] = s;
+    __syncthreads();
+    double tot = 0;
+#pragma unroll
+    for (int i = 0; i < RMS_THREADS / 64; i++) tot += part[k][i];
+    return tot;
+  };
   // The row stays in registers: thread tid holds pieces tid + RMS_THREADS j
   // of 8 values (n % 8 == 0 and n <= 8 * RMS_THREADS * RMS_PIECES).
-  f32x4 v[RMS_PIECES][2];
-  double s = 0;
+  f32x4 v[RMS_PIECES][2], t[RMS_PIECES][2];
+  double st = 0;
 #pragma unroll
   for (int j = 0; j < RMS_PIECES; j++) {
     const int64_t pc = tid + (int64_t)RMS_THREADS * j;
@@ -71,28 +85,54 @@ __global__ void rms_norm_kernel(float *__restrict__ x, const int32_t *__restrict
       v[j][0] = src[0];
       v[j][1] = src[1];
       if (pend.splits) {
-        // x += the pending product (its split sums in order, then the residual)
+        // the pending product: its split sums in order
         float ps[8];
         pend.sum8(rr, 8 * pc, ps);
 #pragma unroll
-        for (int e = 0; e < 8; e++) v[j][e >> 2][e & 3] = ps[e] + v[j][e >> 2][e & 3];
-        if (writeback) {
-          f32x4 *dst = (f32x4 *)(xr + 8 * pc);
-          dst[0] = v[j][0];
-          dst[1] = v[j][1];
+        for (int e = 0; e < 8; e++) {
+          if (pend.post) {
+            t[j][e >> 2][e & 3] = ps[e];
+            st += (double)ps[e] * (double)ps[e];
+          } else {
+            v[j][e >> 2][e & 3] = ps[e] + v[j][e >> 2][e & 3];  // then the residual
+          }
         }
+      }
+    }
+  }
+  if (pend.splits && pend.post) {
+    // x += rms_norm(product) * post (the gemma post norm, then the residual)
+    const float mean_t = (float)(row_sumsq(st, 1) / (double)n);
+    const float sc_t = 1.0f / sqrtf(mean_t + eps);
+#pragma unroll
+    for (int j = 0; j < RMS_PIECES; j++) {
+      const int64_t pc = tid + (int64_t)RMS_THREADS * j;
+      if (pc < n / 8)
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+          v[j][e >> 2][e & 3] = t[j][e >> 2][e & 3] * sc_t * pend.post[8 * pc + e] + v[j][e >> 2][e & 3];
+    }
+  }
+  double s = 0;
+#pragma unroll
+  for (int j = 0; j < RMS_PIECES; j++) {
+    const int64_t pc = tid + (int64_t)RMS_THREADS * j;
+    if (pc < n / 8) {
+      if (pend.splits && pend.scale != 0.0f) {
+        v[j][0] *= pend.scale;  // the layer output scale
+        v[j][1] *= pend.scale;
+      }
+      if (pend.splits && writeback) {
+        f32x4 *dst = (f32x4 *)(xr + 8 * pc);
+        dst[0] = v[j][0];
+        dst[1] = v[j][1];
       }
 #pragma unroll
       for (int e = 0; e < 4; e++)
         s += (double)v[j][0][e] * (double)v[j][0][e] + (double)v[j][1][e] * (double)v[j][1][e];
     }
   }
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
-  if ((tid & 63) == 0) part[tid >> 6] = s;
-  __syncthreads();
-  double tot = 0;
-#pragma unroll
-  for (int i = 0; i < RMS_THREADS / 64; i++) tot += part[i];
+  const double tot = row_sumsq(s, 0);
   const float mean = (float)(tot / (double)n);
   const float scale = 1.0f / sqrtf(mean + eps);
 #pragma unroll
@@ -114,13 +154,14 @@ __global__ void rms_norm_kernel(float *__restrict__ x, const int32_t *__restrict
 }
 
 // ---- q/k norm, rope and KV store -------------------------------------------
+constexpr int QKV_V_FROM_K = 1, QKV_V_NORM = 2;
 // One workgroup per token. The row [q | k | v] is staged in LDS.
 __device__ void head_rms_norm(float *v, int D, float eps, const float *w) {
   double s = 0;
   for (int i = 0; i < D; i++) s += (double)v[i] * (double)v[i];
   float mean = (float)(s / (double)D);
   float scale = 1.0f / sqrtf(mean + eps);
-  for (int i = 0; i < D; i++) v[i] = (v[i] * scale) * w[i];
+  for (int i = 0; i < D; i++) v[i] = w ? (v[i] * scale) * w[i] : v[i] * scale;
 }
 
 __global__ void qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int Hkv, int D,
@@ -131,7 +172,8 @@ __global__ void qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int 
                                       const int32_t *__restrict__ pos,
                                       uint16_t *__restrict__ kp, uint16_t *__restrict__ vp,
                                       const int64_t *__restrict__ cells,
-                                      float *__restrict__ q_out, Pending pa, Pending pb) {
+                                      float *__restrict__ q_out, Pending pa, Pending pb,
+                                      int vmode) {
   extern __shared__ float row[];
   int64_t t = blockIdx.x;
   int W = (H + 2 * Hkv) * D;
@@ -152,10 +194,17 @@ __global__ void qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int 
     for (int i = 0; i < 8; i++) row[e + i] = v[i];
   }
   __syncthreads();
-  if (q_norm || k_norm) {
-    for (int h = threadIdx.x; h < H + Hkv; h += blockDim.x) {
+  if (vmode & QKV_V_FROM_K) {
+    // no V rows: V is the raw K (transformer.lua:1779)
+    for (int e = threadIdx.x; e < Hkv * D; e += blockDim.x) row[(H + Hkv) * D + e] = row[H * D + e];
+    __syncthreads();
+  }
+  if (q_norm || k_norm || (vmode & QKV_V_NORM)) {
+    for (int h = threadIdx.x; h < H + 2 * Hkv; h += blockDim.x) {
       if (h < H && q_norm) head_rms_norm(row + h * D, D, eps, q_norm);
-      if (h >= H && k_norm) head_rms_norm(row + h * D, D, eps, k_norm);
+      if (h >= H && h < H + Hkv && k_norm) head_rms_norm(row + h * D, D, eps, k_norm);
+      // gemma: V rms-normed, no weight (:1782-1784)
+      if (h >= H + Hkv && (vmode & QKV_V_NORM)) head_rms_norm(row + h * D, D, eps, nullptr);
     }
     __syncthreads();
   }
@@ -193,23 +242,31 @@ __global__ void qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int 
   }
 }
 
-// ---- swiglu: silu(g) * u, in f64 --------------------------------------------
+// ---- gated units: silu(g) * u (swiglu) or gelu(g) * u (geglu), in f64 ------
+// gelu is ggml's tanh form, 0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3)))
+// (geglu_split, src/ops_nn.c:165-172).
+__device__ __forceinline__ double glu_act(double g, int gelu) {
+  return gelu ? 0.5 * g * (1.0 + tanh(0.7978845608028654 * (g + 0.044715 * g * g * g)))
+              : g / (1.0 + exp(-g));
+}
+
 template <typename OutT>
 __global__ void swiglu_kernel(const float *__restrict__ gu, int64_t n, int64_t F,
-                              OutT *__restrict__ out, Pending pend) {
+                              OutT *__restrict__ out, Pending pend, int gelu) {
   int64_t total = n * F;
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * blockDim.x) {
     int64_t r = e / F, c = e % F;
     double g = pend.splits ? pend.sum(r, c) : gu[r * 2 * F + c];
     double u = pend.splits ? pend.sum(r, F + c) : gu[r * 2 * F + F + c];
-    out[e] = (OutT)(float)(g / (1.0 + exp(-g)) * u);
+    out[e] = (OutT)(float)(glu_act(g, gelu) * u);
   }
 }
 
 // The same values into split planes (F % 256 == 0); one thread per 8.
 __global__ void swiglu_split_kernel(const float *__restrict__ gu, int64_t n, int64_t F,
-                                    f16 *__restrict__ planes, int64_t npad, Pending pend) {
+                                    f16 *__restrict__ planes, int64_t npad, Pending pend,
+                                    int gelu) {
   const int64_t per_row = F / 8;
   const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (t >= n * per_row) return;  // whole 4-lane groups leave together
@@ -226,11 +283,16 @@ __global__ void swiglu_split_kernel(const float *__restrict__ gu, int64_t n, int
     }
   }
 #pragma unroll
-  for (int e = 0; e < 8; e++) {
-    double g = g8[e], u = u8[e];
-    v[e] = (float)(g / (1.0 + exp(-g)) * u);
-  }
+  for (int e = 0; e < 8; e++) v[e] = (float)(glu_act(g8[e], gelu) * (double)u8[e]);
   split_store8(planes, npad, F, r, c0, v);
+}
+
+// ---- logit softcap: cap * tanh(x * (1 / cap)) (transformer.lua:2097-2099) ----
+__global__ void softcap_kernel(float *__restrict__ x, int64_t n, float cap) {
+  const float inv = 1.0f / cap;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    x[i] = tanhf(x[i] * inv) * cap;
 }
 
 // ---- argmax: first index of the maximum --------------------------------------
@@ -292,7 +354,7 @@ argmax_kernel(const float *__restrict__ x, int64_t n, int32_t *__restrict__ out)
 }
 
 int get_rows_dev(int type, const void *table, int64_t n_cols, const int32_t *ids, int64_t n,
-                 float *out, hipStream_t st) {
+                 float *out, hipStream_t st, float scale) {
   int64_t rb = row_bytes(type, n_cols);
   if (rb <= 0) {
     set_error("get_rows: bad type %d for %lld columns", type, (long long)n_cols);
@@ -300,7 +362,7 @@ int get_rows_dev(int type, const void *table, int64_t n_cols, const int32_t *ids
   }
   if (n == 0) return LGMLH_OK;
   hipLaunchKernelGGL(get_rows_kernel, dim3((unsigned)n), dim3(256), 0, st, type,
-                     (const uint8_t *)table, rb, n_cols, ids, out);
+                     (const uint8_t *)table, rb, n_cols, ids, out, scale);
   return hip_check(hipGetLastError(), "get_rows");
 }
 
@@ -322,14 +384,15 @@ int rms_norm_dev(float *x, const int32_t *rows, int64_t n_rows, int64_t n, float
   return hip_check(hipGetLastError(), "rms_norm");
 }
 
-// silu(g) * u into f32 out and / or split planes.
+// silu(g) * u (gelu(g) * u with gelu set) into f32 out and / or split planes.
 int swiglu_dev(const float *gu, int64_t n, int64_t F, float *out, f16 *planes, hipStream_t st,
-               Pending pend) {
+               Pending pend, int gelu) {
   if (n == 0) return LGMLH_OK;
   if (out) {
     int64_t total = n * F;
     unsigned blocks = (unsigned)((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
-    hipLaunchKernelGGL(swiglu_kernel<float>, dim3(blocks), dim3(256), 0, st, gu, n, F, out, pend);
+    hipLaunchKernelGGL(swiglu_kernel<float>, dim3(blocks), dim3(256), 0, st, gu, n, F, out, pend,
+                       gelu);
   }
   if (planes) {
     if (F % 256) {
@@ -338,9 +401,16 @@ int swiglu_dev(const float *gu, int64_t n, int64_t F, float *out, f16 *planes, h
     }
     int64_t total = n * (F / 8);
     hipLaunchKernelGGL(swiglu_split_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                       st, gu, n, F, planes, split_npad(n), pend);
+                       st, gu, n, F, planes, split_npad(n), pend, gelu);
   }
   return hip_check(hipGetLastError(), "swiglu");
+}
+
+int softcap_dev(float *x, int64_t n, float cap, hipStream_t st) {
+  if (n == 0 || cap <= 0.0f) return LGMLH_OK;
+  unsigned blocks = (unsigned)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+  hipLaunchKernelGGL(softcap_kernel, dim3(blocks), dim3(256), 0, st, x, n, cap);
+  return hip_check(hipGetLastError(), "softcap");
 }
 
 }  // namespace lgmlh
@@ -370,7 +440,7 @@ extern "C" int lgmlh_get_rows(int type, const void *table, int64_t n_rows, int64
     }
   if (n == 0) return LGMLH_OK;
   hipLaunchKernelGGL(get_rows_kernel, dim3((unsigned)n), dim3(256), 0, as_stream(stream), type,
-                     (const uint8_t *)table, rb, n_cols, ids, out);
+                     (const uint8_t *)table, rb, n_cols, ids, out, 0.0f);
   return hip_check(hipGetLastError(), "get_rows");
 }
 
@@ -414,7 +484,7 @@ int qkv_rope_store_dev(float *qkv, int64_t n, int n_head, int n_head_kv,
                                     const float *k_norm, float eps, const int32_t *pos,
                                     void *kpool, void *vpool, int64_t n_cells,
                                     const int64_t *cells, float *q_out, void *stream, Pending pa,
-                       Pending pb) {
+                       Pending pb, int vmode) {
   if (!qkv || !pos || !kpool || !vpool || !cells || !q_out || n < 0 || n_head <= 0 ||
       n_head_kv <= 0 || head_dim <= 0 || head_dim % 8 || n_rot <= 0 || n_rot > head_dim ||
       n_rot % 2 || n_cells % KV_BLOCK || pa.cols % 8 || pb.cols % 8) {
@@ -432,7 +502,7 @@ int qkv_rope_store_dev(float *qkv, int64_t n, int n_head, int n_head_kv,
   hipLaunchKernelGGL(qkv_rope_store_kernel, dim3((unsigned)n), dim3(512), lds,
                      as_stream(stream), qkv, n_head, n_head_kv, head_dim, n_rot, neox,
                      theta_scale, freq_factors, q_norm, k_norm, eps, pos, (uint16_t *)kpool,
-                     (uint16_t *)vpool, cells, q_out, pa, pb);
+                     (uint16_t *)vpool, cells, q_out, pa, pb, vmode);
   return hip_check(hipGetLastError(), "qkv_rope_store");
 }
 }  // namespace lgmlh
@@ -445,7 +515,7 @@ extern "C" int lgmlh_qkv_rope_store(float *qkv, int64_t n, int n_head, int n_hea
                                     const int64_t *cells, float *q_out, void *stream) {
   return qkv_rope_store_dev(qkv, n, n_head, n_head_kv, head_dim, n_rot, neox, freq_base,
                             freq_factors, q_norm, k_norm, eps, pos, kpool, vpool, n_cells, cells,
-                            q_out, stream, Pending{}, Pending{});
+                            q_out, stream, Pending{}, Pending{}, 0);
 }
 
 extern "C" int lgmlh_swiglu(const float *gu, int64_t n, int64_t F, void *out, int out_type,
@@ -459,11 +529,37 @@ extern "C" int lgmlh_swiglu(const float *gu, int64_t n, int64_t F, void *out, in
   unsigned blocks = (unsigned)((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
   if (out_type == LGMLH_F32)
     hipLaunchKernelGGL(swiglu_kernel<float>, dim3(blocks), dim3(256), 0, as_stream(stream), gu,
-                       n, F, (float *)out, Pending{});
+                       n, F, (float *)out, Pending{}, 0);
   else
     hipLaunchKernelGGL(swiglu_kernel<f16>, dim3(blocks), dim3(256), 0, as_stream(stream), gu, n,
-                       F, (f16 *)out, Pending{});
+                       F, (f16 *)out, Pending{}, 0);
   return hip_check(hipGetLastError(), "swiglu");
+}
+
+extern "C" int lgmlh_geglu(const float *gu, int64_t n, int64_t F, void *out, int out_type,
+                           void *stream) {
+  if (!gu || !out || n < 0 || F <= 0 || (out_type != LGMLH_F32 && out_type != LGMLH_F16)) {
+    set_error("geglu: bad arguments");
+    return LGMLH_EINVAL;
+  }
+  if (n == 0) return LGMLH_OK;
+  int64_t total = n * F;
+  unsigned blocks = (unsigned)((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
+  if (out_type == LGMLH_F32)
+    hipLaunchKernelGGL(swiglu_kernel<float>, dim3(blocks), dim3(256), 0, as_stream(stream), gu,
+                       n, F, (float *)out, Pending{}, 1);
+  else
+    hipLaunchKernelGGL(swiglu_kernel<f16>, dim3(blocks), dim3(256), 0, as_stream(stream), gu, n,
+                       F, (f16 *)out, Pending{}, 1);
+  return hip_check(hipGetLastError(), "geglu");
+}
+
+extern "C" int lgmlh_softcap(float *x, int64_t n, float cap, void *stream) {
+  if (!x || n < 0 || !(cap > 0.0f)) {
+    set_error("softcap: bad arguments");
+    return LGMLH_EINVAL;
+  }
+  return softcap_dev(x, n, cap, as_stream(stream));
 }
 
 extern "C" int lgmlh_argmax(const float *x, int64_t n_rows, int64_t n_cols, int32_t *out,

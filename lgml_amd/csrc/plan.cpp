@@ -6,7 +6,9 @@
 // off + n - 1 -- into one buffer for a single host-to-device copy, and adds
 // the work list of the paged attention kernel: for every sequence, groups
 // of 16 / G query tokens, each split into runs of at most blocks_per_split
-// KV blocks, plus one merge item per group with more than one split.
+// KV blocks, plus one merge item per group with more than one split. A
+// ring plan (sliding-window layers) maps positions into each sequence's
+// ring of blocks and starts each group's runs at its window.
 #include <string.h>
 
 #include <vector>
@@ -19,18 +21,20 @@ static int64_t align16(int64_t x) { return (x + 15) & ~int64_t(15); }
 
 using namespace lgmlh;
 
-extern "C" int lgmlh_plan(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
-                          const int32_t *block_tab, int max_blocks, int64_t pool_blocks,
-                          const int32_t *ids, int n_head, int n_head_kv, int blocks_per_split,
-                          void *buf, size_t buf_bytes, lgmlh_plan_info *info) {
+// The plan of a pass; ring > 0 makes the sliding-window plan of
+// lgmlh_plan_ring (block_tab = the ring tables, max_blocks = ring).
+static int plan_impl(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
+                     const int32_t *block_tab, int max_blocks, int64_t pool_blocks,
+                     const int32_t *ids, int n_head, int n_head_kv, int blocks_per_split,
+                     int window, int ring, void *buf, size_t buf_bytes, lgmlh_plan_info *info) {
   if (n_seq < 0 || !seq_n || !seq_npast || !block_tab || max_blocks <= 0 || !info ||
       n_head_kv <= 0 || n_head % n_head_kv || n_head / n_head_kv > 16 ||
-      16 % (n_head / n_head_kv) || blocks_per_split < 0) {
+      16 % (n_head / n_head_kv) || blocks_per_split < 0 || (ring > 0 && window < 1)) {
     set_error("plan: bad arguments");
     return LGMLH_EINVAL;
   }
   const int G = n_head / n_head_kv, T = 16 / G, B = KV_BLOCK;
-  int64_t N = 0, total_blocks = 0;
+  int64_t N = 0;
   for (int s = 0; s < n_seq; s++) {
     if (seq_n[s] < 0 || seq_npast[s] < 0) {
       set_error("plan: negative count");
@@ -38,10 +42,19 @@ extern "C" int lgmlh_plan(int n_seq, const int32_t *seq_n, const int32_t *seq_np
     }
     int64_t n_kv = (int64_t)seq_npast[s] + seq_n[s];
     int64_t nb = (n_kv + B - 1) / B;
-    if (nb > max_blocks || nb > 0xffff) {
+    if (nb > 0xffff || (!ring && nb > max_blocks)) {
       set_error("plan: sequence %d needs %lld blocks (table has %d)", s, (long long)nb,
                 max_blocks);
       return LGMLH_ERANGE;
+    }
+    if (ring) {
+      // every query's window must still be in the ring after the pass writes
+      if ((int64_t)ring * B < (int64_t)window - 1 + seq_n[s]) {
+        set_error("plan: %d tokens in one pass; the ring of %d cells takes %lld", seq_n[s],
+                  ring * B, (long long)ring * B - window + 1);
+        return LGMLH_ERANGE;
+      }
+      nb = nb < ring ? nb : ring;  // the ring entries in use
     }
     for (int64_t i = 0; i < nb; i++) {
       int32_t b = block_tab[(int64_t)s * max_blocks + i];
@@ -52,16 +65,11 @@ extern "C" int lgmlh_plan(int n_seq, const int32_t *seq_n, const int32_t *seq_np
       }
     }
     N += seq_n[s];
-    for (int g0 = 0; g0 < seq_n[s]; g0 += T) {
-      int ge = g0 + T < seq_n[s] ? g0 + T : seq_n[s];
-      total_blocks += ((int64_t)seq_npast[s] + ge - 1) / B + 1;
-    }
   }
   if (N > INT32_MAX / 2) {
     set_error("plan: too many tokens");
     return LGMLH_EINVAL;
   }
-  (void)total_blocks;
   // A fixed default: the split points of a sequence must not depend on the
   // rest of the batch (a sequence gives the same bits alone or batched).
   const int bps = blocks_per_split ? blocks_per_split : 16;
@@ -69,12 +77,18 @@ extern "C" int lgmlh_plan(int n_seq, const int32_t *seq_n, const int32_t *seq_np
   for (int s = 0, off = 0; s < n_seq; off += seq_n[s], s++) {
     for (int g0 = 0; g0 < seq_n[s]; g0 += T) {
       int ge = g0 + T < seq_n[s] ? g0 + T : seq_n[s];
-      int nbg = (int)(((int64_t)seq_npast[s] + ge - 1) / B + 1);
-      int ns = (nbg + bps - 1) / bps;
+      // logical blocks [b0, nbg): from the window of the group's first
+      // token (ring plans) or from 0, to the group's last position
+      const int64_t pf = (int64_t)seq_npast[s] + g0, pl = (int64_t)seq_npast[s] + ge - 1;
+      int b0 = ring ? (int)((pf - window + 1 > 0 ? pf - window + 1 : 0) / B) : 0;
+      int nbg = (int)(pl / B + 1);
+      int ns = (nbg - b0 + bps - 1) / bps;
+      // ring plans: runs of equal length (a window is a fixed span)
+      int run = ring ? (nbg - b0 + ns - 1) / ns : bps;
       int first = (int)(items.size() / 4);
       int mg = ns > 1 ? (int)(merge.size() / 4) + 1 : 0;
       for (int j = 0; j < ns; j++) {
-        int lo = j * bps, hi = (j + 1) * bps < nbg ? (j + 1) * bps : nbg;
+        int lo = b0 + j * run, hi = b0 + (j + 1) * run < nbg ? b0 + (j + 1) * run : nbg;
         items.push_back(s);
         items.push_back(off + g0);
         items.push_back((ge - g0) | (mg << 5));
@@ -98,6 +112,8 @@ extern "C" int lgmlh_plan(int n_seq, const int32_t *seq_n, const int32_t *seq_np
   in.n_merge = (int32_t)(merge.size() / 4);
   in.rows = 16;
   in.n_head_kv = n_head_kv;
+  in.window = ring ? window : 0;
+  in.ring = ring;
   int64_t o = 0;
   in.off_ids = o;          o = align16(o + 4 * N);
   in.off_pos = o;          o = align16(o + 4 * N);
@@ -129,7 +145,8 @@ extern "C" int lgmlh_plan(int n_seq, const int32_t *seq_n, const int32_t *seq_np
       int p = seq_npast[s] + j;
       if (ids) pid[t] = ids[t];
       ppos[t] = p;
-      pcell[t] = (int64_t)block_tab[(int64_t)s * max_blocks + p / B] * B + p % B;
+      const int bi = ring ? (p / B) % ring : p / B;
+      pcell[t] = (int64_t)block_tab[(int64_t)s * max_blocks + bi] * B + p % B;
     }
     plr[s] = (int32_t)t - 1;
   }
@@ -138,6 +155,27 @@ extern "C" int lgmlh_plan(int n_seq, const int32_t *seq_n, const int32_t *seq_np
   if (!items.empty()) memcpy(b + in.off_items, items.data(), 4 * items.size());
   if (!merge.empty()) memcpy(b + in.off_merge, merge.data(), 4 * merge.size());
   return LGMLH_OK;
+}
+
+extern "C" int lgmlh_plan(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
+                          const int32_t *block_tab, int max_blocks, int64_t pool_blocks,
+                          const int32_t *ids, int n_head, int n_head_kv, int blocks_per_split,
+                          void *buf, size_t buf_bytes, lgmlh_plan_info *info) {
+  return plan_impl(n_seq, seq_n, seq_npast, block_tab, max_blocks, pool_blocks, ids, n_head,
+                   n_head_kv, blocks_per_split, 0, 0, buf, buf_bytes, info);
+}
+
+extern "C" int lgmlh_plan_ring(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
+                               const int32_t *ring_tab, int ring_blocks, int64_t pool_blocks,
+                               int window, const int32_t *ids, int n_head, int n_head_kv,
+                               int blocks_per_split, void *buf, size_t buf_bytes,
+                               lgmlh_plan_info *info) {
+  if (ring_blocks < 1 || window < 1) {
+    set_error("plan_ring: ring of %d blocks, window %d", ring_blocks, window);
+    return LGMLH_EINVAL;
+  }
+  return plan_impl(n_seq, seq_n, seq_npast, ring_tab, ring_blocks, pool_blocks, ids, n_head,
+                   n_head_kv, blocks_per_split, window, ring_blocks, buf, buf_bytes, info);
 }
 
 extern "C" int lgmlh_plan_bind(const lgmlh_plan_info *info, const void *dev, lgmlh_ubatch *ub) {
@@ -163,5 +201,7 @@ extern "C" int lgmlh_plan_bind(const lgmlh_plan_info *info, const void *dev, lgm
   ub->logit_rows = (const int32_t *)(b + info->off_logit_rows);
   ub->items = (const int32_t *)(b + info->off_items);
   ub->merge = (const int32_t *)(b + info->off_merge);
+  ub->window = info->window;
+  ub->ring = info->ring;
   return LGMLH_OK;
 }

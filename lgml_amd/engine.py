@@ -18,6 +18,11 @@ engine.lua:2010-2077): the full blocks whose chained keys it finds are
 shared, the best partial match is copied into a block of its own, and only
 the rest of the prompt runs. Full prompt blocks get keys as their prefill
 completes (E:publish, :1829-1841), so later requests can share them.
+
+A model with sliding-window layers gives each slot a ring of its own in
+the ring pools (M:cache's per-slot rings, transformer.lua:575-600): slot
+i owns ring blocks i R .. i R + R - 1, R = ring_cells / 64 / n_slots, and
+a request holds a slot from submit to finish.
 """
 import ctypes as C
 
@@ -163,10 +168,22 @@ class Engine:
         self.last_plan = None
         self.last_logits = None
         self._ids = torch.empty(0, dtype=torch.int32, device="cuda")
+        self.ring_blocks = 0
+        if any(getattr(model, "swa", [])):
+            if prefix_cache:
+                raise ValueError("prefix sharing covers the paged pool only, not the rings")
+            self.ring_blocks = model.ring_cells // BLOCK // n_slots
+            need = model.hp["n_swa"] - 1 + ubatch
+            if self.ring_blocks * BLOCK < need:
+                # "tokens in one pass; the ring takes" (transformer.lua:1544-1546)
+                raise ValueError("rings of %d cells per slot; a pass of %d tokens needs %d" % (
+                    self.ring_blocks * BLOCK, ubatch, need))
+        self.free_slots = list(range(n_slots))
 
     def submit(self, req):
         if len(self.active) >= self.n_slots:
             raise RuntimeError("no free slot")
+        req.slot = self.free_slots.pop(0)
         req.seq = Seq(self.seqs, req.prio)
         self.active.append(req)
         if self.prefix_cache:
@@ -234,6 +251,7 @@ class Engine:
 
     def finish(self, req):
         self.seqs.free(req.seq)
+        self.free_slots.append(req.slot)
         req.done = True
         self.active.remove(req)
 
@@ -259,7 +277,12 @@ class Engine:
         for i, (r, _) in enumerate(entries):
             bt[i, :len(r.seq.blocks)] = r.seq.blocks
         ids = np.concatenate([np.asarray(x, np.int32) for _, x in entries])
-        plan = self.model.plan(seq_n, npast, bt, ids, self.bps)
+        ring_tab = None
+        if self.ring_blocks:
+            R = self.ring_blocks
+            ring_tab = np.array([np.arange(r.slot * R, (r.slot + 1) * R) for r, _ in entries],
+                                np.int32)
+        plan = self.model.plan(seq_n, npast, bt, ids, self.bps, ring_tab=ring_tab)
         self.last_plan = plan
         self.last_entries = [r for r, _ in entries]
         logits = self.model.forward(plan, trace=self.trace)

@@ -28,7 +28,7 @@ SYMBOLS = (
     "lgmlh_kvpool_publish_part", "lgmlh_kvpool_key_of", "lgmlh_kvpool_lookup",
     "lgmlh_kvpool_longest_kid", "lgmlh_kvpool_set_cap", "lgmlh_kvpool_stats", "lgmlh_block_key",
     "lgmlh_gen_normal", "lgmlh_moe_route", "lgmlh_mul_mat_id_workspace", "lgmlh_mul_mat_id",
-    "lgmlh_moe_sum",
+    "lgmlh_moe_sum", "lgmlh_plan_ring", "lgmlh_geglu", "lgmlh_softcap",
 )
 GATING_SOFTMAX, GATING_SIGMOID = 1, 2
 TRACE_ATTN, TRACE_GEMM, TRACE_EXPERTS = 1, 2, 4
@@ -45,14 +45,16 @@ class PlanInfo(C.Structure):
                                          "n_merge", "rows", "n_head_kv")] + \
                [(n, C.c_int64) for n in ("bytes", "off_ids", "off_pos", "off_cells", "off_seq_off",
                                          "off_npast", "off_block_tab", "off_logit_rows",
-                                         "off_items", "off_merge")]
+                                         "off_items", "off_merge")] + \
+               [("window", C.c_int32), ("ring", C.c_int32)]
 
 
 class Ubatch(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("n_seq", "n_tokens", "max_blocks", "block", "n_items",
                                          "n_merge", "rows", "n_head_kv")] + \
                [(n, C.c_void_p) for n in ("ids", "pos", "cells", "seq_off", "seq_npast",
-                                          "block_tab", "logit_rows", "items", "merge")]
+                                          "block_tab", "logit_rows", "items", "merge")] + \
+               [("window", C.c_int32), ("ring", C.c_int32)]
 
 
 class Layer(C.Structure):
@@ -63,7 +65,9 @@ class Layer(C.Structure):
                 ("wo", C.c_void_p), ("wgu", C.c_void_p), ("wdown", C.c_void_p),
                 ("kpool", C.c_void_p), ("vpool", C.c_void_p), ("gate_inp", C.c_void_p),
                 ("exp_gu_type", C.c_int), ("exp_down_type", C.c_int), ("exp_gu", C.c_void_p),
-                ("exp_down", C.c_void_p)]
+                ("exp_down", C.c_void_p), ("swa", C.c_int), ("v_from_k", C.c_int),
+                ("post_attn_norm", C.c_void_p), ("post_ffn_norm", C.c_void_p),
+                ("out_scale", C.c_float), ("rope_base", C.c_float), ("rope_freqs", C.c_void_p)]
 
 
 class Trace(C.Structure):
@@ -79,7 +83,8 @@ class Model(C.Structure):
                 ("tok_embd", C.c_void_p), ("output", C.c_void_p), ("output_norm", C.c_void_p),
                 ("n_cells", C.c_int64), ("layers", C.POINTER(Layer))] + \
                [(n, C.c_int) for n in ("n_expert", "n_used", "n_ff_exp", "gating", "norm_topk")] + \
-               [("expert_scale", C.c_float)]
+               [("expert_scale", C.c_float), ("gemma", C.c_int), ("embd_scale", C.c_float),
+                ("softcap", C.c_float), ("ring_cells", C.c_int64)]
 
 
 _lib = None
@@ -114,6 +119,8 @@ def _declare(L):
         "lgmlh_plan": ([i32, vp, vp, vp, i32, i64, vp, i32, i32, i32, vp, sz,
                         C.POINTER(PlanInfo)], i32),
         "lgmlh_plan_bind": ([C.POINTER(PlanInfo), vp, C.POINTER(Ubatch)], i32),
+        "lgmlh_plan_ring": ([i32, vp, vp, vp, i32, i64, i32, vp, i32, i32, i32, vp, sz,
+                             C.POINTER(PlanInfo)], i32),
         "lgmlh_attention_workspace": ([C.POINTER(PlanInfo), i32], sz),
         "lgmlh_paged_attention": ([vp, i32, i32, i32, C.c_float, vp, vp, C.POINTER(Ubatch), vp,
                                    vp, sz, vp], i32),
@@ -127,10 +134,13 @@ def _declare(L):
         "lgmlh_qkv_rope_store": ([vp, i64, i32, i32, i32, i32, i32, C.c_float, vp, vp, vp,
                                   C.c_float, vp, vp, vp, i64, vp, vp, vp], i32),
         "lgmlh_swiglu": ([vp, i64, i64, vp, i32, vp], i32),
+        "lgmlh_geglu": ([vp, i64, i64, vp, i32, vp], i32),
+        "lgmlh_softcap": ([vp, i64, C.c_float, vp], i32),
         "lgmlh_argmax": ([vp, i64, i64, vp, vp], i32),
-        "lgmlh_forward_workspace": ([C.POINTER(Model), C.POINTER(PlanInfo), i32], sz),
-        "lgmlh_forward": ([C.POINTER(Model), C.POINTER(Ubatch), vp, i32, vp, vp, sz,
-                           C.POINTER(Trace), vp], i32),
+        "lgmlh_forward_workspace": ([C.POINTER(Model), C.POINTER(PlanInfo), C.POINTER(PlanInfo),
+                                     i32], sz),
+        "lgmlh_forward": ([C.POINTER(Model), C.POINTER(Ubatch), C.POINTER(Ubatch), vp, i32, vp,
+                           vp, sz, C.POINTER(Trace), vp], i32),
         "lgmlh_kvpool_bytes": ([C.c_int32, C.c_int32], sz),
         "lgmlh_kvpool_init": ([vp, sz, C.c_int32, C.c_int32, C.c_int32], i32),
         "lgmlh_kvpool_take": ([vp, C.c_int32], C.c_int32),

@@ -7,7 +7,10 @@ Weights arrive as a dict of numpy arrays in ggml layouts:
 {"tok_embd": (arr, type), "output": ..., "output_norm": (f32, F32),
  "rope_freqs": f32 or None, "layers": [{"attn_norm", "wq", "wk", "wv",
  "wo", "ffn_norm", "gate", "up", "down", optional "q_norm", "k_norm"}]},
-quantized arrays as uint8 (rows, row_bytes), f32 as (rows, cols).
+quantized arrays as uint8 (rows, row_bytes), f32 as (rows, cols). Gemma
+layers add "post_attn_norm", "post_ffn_norm" and the scalars "swa",
+"rope_base", "out_scale", optional "rope_freqs"; a layer without "wv"
+takes V from the raw K; "output" may be the "tok_embd" entry (tied).
 """
 import ctypes as C
 
@@ -109,11 +112,15 @@ def generated_weights(hp, seed, policy):
 
 
 class Plan:
-    """A planned ubatch (lgmlh_plan), copied to the device."""
+    """A planned ubatch (lgmlh_plan), copied to the device. With ring_tab
+    (n_seq, ring_blocks) and window, the plan of the sliding-window layers
+    over the sequences' rings (lgmlh_plan_ring); pool_blocks is then the
+    ring pools' block count. .ring: the pass's ring plan, if any."""
 
     def __init__(self, seq_n, seq_npast, block_tab, ids, n_head, n_head_kv, pool_blocks,
-                 blocks_per_split=0):
+                 blocks_per_split=0, ring_tab=None, window=0):
         L = hip.lib()
+        self.ring = None
         self.seq_n = np.ascontiguousarray(seq_n, np.int32)
         self.seq_npast = np.ascontiguousarray(seq_npast, np.int32)
         bt = np.ascontiguousarray(block_tab, np.int32)
@@ -123,11 +130,18 @@ class Plan:
         self.ids = np.ascontiguousarray(ids, np.int32)
         assert len(self.ids) == int(self.seq_n.sum())
         self.info = hip.PlanInfo()
-        args = (len(self.seq_n), ptr(self.seq_n), ptr(self.seq_npast), ptr(bt), bt.shape[1],
-                int(pool_blocks), ptr(self.ids), n_head, n_head_kv, blocks_per_split)
-        check(L.lgmlh_plan(*args, None, 0, C.byref(self.info)))
+        if ring_tab is None:
+            fn = L.lgmlh_plan
+            args = (len(self.seq_n), ptr(self.seq_n), ptr(self.seq_npast), ptr(bt), bt.shape[1],
+                    int(pool_blocks), ptr(self.ids), n_head, n_head_kv, blocks_per_split)
+        else:
+            fn = L.lgmlh_plan_ring
+            args = (len(self.seq_n), ptr(self.seq_n), ptr(self.seq_npast), ptr(bt), bt.shape[1],
+                    int(pool_blocks), int(window), ptr(self.ids), n_head, n_head_kv,
+                    blocks_per_split)
+        check(fn(*args, None, 0, C.byref(self.info)))
         self.host = np.zeros(self.info.bytes, np.uint8)
-        check(L.lgmlh_plan(*args, ptr(self.host), self.host.nbytes, C.byref(self.info)))
+        check(fn(*args, ptr(self.host), self.host.nbytes, C.byref(self.info)))
         self.dev = torch.from_numpy(self.host).to(DEV)
         self.ub = hip.Ubatch()
         check(L.lgmlh_plan_bind(C.byref(self.info), self.dev.data_ptr(), C.byref(self.ub)))
@@ -171,20 +185,34 @@ class EventTrace:
 
 
 class DeviceModel:
-    """A llama / qwen3 / qwen3moe model on the device with its paged KV pool."""
+    """A llama / qwen3 / qwen3moe / gemma model on the device with its paged
+    KV pool (and, for sliding-window layers, ring pools)."""
 
-    def __init__(self, hp, w, n_cells):
+    def __init__(self, hp, w, n_cells, ring_cells=0):
         """w: a weights dict of numpy arrays, or a callable source
         w(name, layer, rows, cols) -> (device tensor, type, rows) such as
-        generated_weights()."""
+        generated_weights() (gemma layers then follow workload.gemma_layer).
+        ring_cells: cells of each sliding layer's ring pools (a multiple of
+        64; the sequences' ring tables index its blocks)."""
+        from . import workload
         L = hip.lib()
         self.hp = hp
         E, H, Hkv, D = hp["n_embd"], hp["n_head"], hp["n_head_kv"], hp["head_dim"]
         F, V = hp["n_ff"], hp["n_vocab"]
         self.n_cells = int(n_cells)
-        assert self.n_cells % 64 == 0
+        self.ring_cells = int(ring_cells)
+        assert self.n_cells % 64 == 0 and self.ring_cells % 64 == 0
         self._keep = []
         gen = callable(w)
+        gemma = bool(hp.get("gemma"))
+
+        def layer_info(il):
+            if not gemma:
+                return {}
+            if gen:
+                return workload.gemma_layer(hp, il)
+            lw = w["layers"][il]
+            return {k: lw[k] for k in ("swa", "rope_base", "out_scale", "rope_freqs") if k in lw}
 
         def keep(t):
             self._keep.append(t)
@@ -197,24 +225,48 @@ class DeviceModel:
 
         def vec(name, layer, n):
             if gen:
-                return keep(torch.ones(n, dtype=torch.float32, device=DEV)).data_ptr()
+                # norms 1; gemma's q / k norms D^(-1/4): scores of unit scale
+                # at attention scale 1
+                v = D ** -0.25 if gemma and name in ("q_norm", "k_norm") else 1.0
+                return keep(torch.full((n,), v, dtype=torch.float32, device=DEV)).data_ptr()
             arr = w["layers"][layer][name][0] if layer is not None else w[name][0]
             return keep(_dev(np.asarray(arr, np.float32))).data_ptr()
 
         kvb = L.lgmlh_kv_layer_bytes(self.n_cells, Hkv, D)
+        kvb_ring = L.lgmlh_kv_layer_bytes(self.ring_cells, Hkv, D)
         self.kpools, self.vpools = [], []
         self.layers = (hip.Layer * hp["n_layer"])()
-        qk_norm = hp["arch"] in ("qwen3", "qwen3moe")
+        qk_norm = hp["arch"] in ("qwen3", "qwen3moe", "gemma4")
         NE = hp.get("n_expert", 0)
+        self.swa = []
         for il in range(hp["n_layer"]):
             Ly = self.layers[il]
+            g = layer_info(il)
             Ly.attn_norm = vec("attn_norm", il, E)
             Ly.ffn_norm = vec("ffn_norm", il, E)
             for nm in ("q_norm", "k_norm"):
                 if (gen and qk_norm) or (not gen and w["layers"][il].get(nm) is not None):
                     setattr(Ly, nm, vec(nm, il, D))
-            wq, wk, wv = mat("wq", il, H * D, E), mat("wk", il, Hkv * D, E), mat("wv", il, Hkv * D, E)
-            if wv[1] == wq[1] == wk[1]:
+            if gemma:
+                for nm in ("post_attn_norm", "post_ffn_norm"):
+                    if gen or w["layers"][il].get(nm) is not None:
+                        setattr(Ly, nm, vec(nm, il, E))
+                Ly.out_scale = g.get("out_scale", 0.0)
+                Ly.rope_base = g.get("rope_base", 0.0)
+                if g.get("rope_freqs") is not None:
+                    Ly.rope_freqs = keep(_dev(np.asarray(g["rope_freqs"], np.float32))).data_ptr()
+            Ly.swa = int(g.get("swa", 0))
+            self.swa.append(bool(Ly.swa))
+            if Ly.swa and self.ring_cells <= 0:
+                raise ValueError("layer %d slides: the model needs ring_cells" % il)
+            has_wv = g.get("has_wv", True) if gen else "wv" in w["layers"][il]
+            wq, wk = mat("wq", il, H * D, E), mat("wk", il, Hkv * D, E)
+            wv = mat("wv", il, Hkv * D, E) if has_wv else None
+            if wv is None:
+                # V is the raw K (transformer.lua:1779): wqkv holds [wq | wk]
+                t, ty, M = repack_concat([wq, wk], E)
+                Ly.wv, Ly.v_from_k = None, 1
+            elif wv[1] == wq[1] == wk[1]:
                 t, ty, M = repack_concat([wq, wk, wv], E)
                 Ly.wv = None
             else:
@@ -241,7 +293,8 @@ class DeviceModel:
                 Ly.wgu, Ly.wgu_type = keep(t).data_ptr(), ty
                 t, ty, _ = repack_concat([mat("down", il, E, F)], F)
                 Ly.wdown, Ly.wdown_type = keep(t).data_ptr(), ty
-            kp, vp = keep(_zeros(kvb)), keep(_zeros(kvb))
+            kp = keep(_zeros(kvb_ring if Ly.swa else kvb))
+            vp = keep(_zeros(kvb_ring if Ly.swa else kvb))
             self.kpools.append(kp)
             self.vpools.append(vp)
             Ly.kpool, Ly.vpool = kp.data_ptr(), vp.data_ptr()
@@ -255,14 +308,25 @@ class DeviceModel:
             m.rope_freqs = keep(_dev(np.asarray(w["rope_freqs"], np.float32))).data_ptr()
         te = mat("tok_embd", None, V, E)
         if gen:
-            m.tok_embd, m.tok_embd_type = keep(te[0]).data_ptr(), te[1]
+            ted = keep(te[0])
         else:
-            m.tok_embd, m.tok_embd_type = keep(_dev(te[0])).data_ptr(), te[1]
-        t, ty, _ = repack_concat([mat("output", None, V, E)], E)
+            ted = keep(_dev(te[0]))
+        m.tok_embd, m.tok_embd_type = ted.data_ptr(), te[1]
+        if gemma or (not gen and w["output"] is w["tok_embd"]):
+            # tied output (transformer.lua:408): the head reads a repacked
+            # copy of the embedding table
+            t, ty, _ = repack_concat([(ted, te[1], V)], E)
+        else:
+            t, ty, _ = repack_concat([mat("output", None, V, E)], E)
         m.output, m.output_type = keep(t).data_ptr(), ty
         m.output_norm = vec("output_norm", None, E)
         m.n_cells = self.n_cells
+        m.ring_cells = self.ring_cells
         m.layers = self.layers
+        if gemma:
+            m.gemma = 1
+            m.embd_scale = hp.get("embd_scale", 0.0)
+            m.softcap = hp.get("softcap", 0.0)
         if NE:
             m.n_expert, m.n_used, m.n_ff_exp = NE, hp["n_used"], hp["n_ff_exp"]
             m.gating = hp.get("gating", hip.GATING_SOFTMAX)
@@ -276,15 +340,26 @@ class DeviceModel:
     def pool_blocks(self):
         return self.n_cells // 64
 
-    def plan(self, seq_n, seq_npast, block_tab, ids, blocks_per_split=0):
+    def plan(self, seq_n, seq_npast, block_tab, ids, blocks_per_split=0, ring_tab=None):
+        """The pass's plan; with sliding layers also its ring plan (.ring)
+        over ring_tab (n_seq, ring blocks), the sequences' rings."""
         ids = np.ascontiguousarray(ids, np.int32)
         if len(ids) and (ids.min() < 0 or ids.max() >= self.hp["n_vocab"]):
             raise ValueError("token id out of range [0, %d)" % self.hp["n_vocab"])
-        return Plan(seq_n, seq_npast, block_tab, ids, self.hp["n_head"], self.hp["n_head_kv"],
-                    self.pool_blocks, blocks_per_split)
+        p = Plan(seq_n, seq_npast, block_tab, ids, self.hp["n_head"], self.hp["n_head_kv"],
+                 self.pool_blocks, blocks_per_split)
+        if any(self.swa):
+            if ring_tab is None:
+                raise ValueError("the model has sliding-window layers: pass ring_tab")
+            p.ring = Plan(seq_n, seq_npast, ring_tab, ids, self.hp["n_head"],
+                          self.hp["n_head_kv"], self.ring_cells // 64, blocks_per_split,
+                          ring_tab=ring_tab, window=self.hp["n_swa"])
+        return p
 
     def workspace(self, plan, n_out):
-        need = hip.lib().lgmlh_forward_workspace(C.byref(self.m), C.byref(plan.info), n_out)
+        need = hip.lib().lgmlh_forward_workspace(
+            C.byref(self.m), C.byref(plan.info),
+            C.byref(plan.ring.info) if plan.ring is not None else None, n_out)
         if need > self.ws_bytes:
             self.ws = _empty(need)
             self.ws_bytes = need
@@ -302,19 +377,23 @@ class DeviceModel:
         ws = self.workspace(plan, n_out)
         if logits is None:
             logits = torch.empty((n_out, self.hp["n_vocab"]), dtype=torch.float32, device=DEV)
-        check(hip.lib().lgmlh_forward(C.byref(self.m), C.byref(plan.ub), ptr(rows), n_out,
-                                      logits.data_ptr(), ws.data_ptr(), self.ws_bytes,
+        check(hip.lib().lgmlh_forward(C.byref(self.m), C.byref(plan.ub),
+                                      C.byref(plan.ring.ub) if plan.ring is not None else None,
+                                      ptr(rows), n_out, logits.data_ptr(), ws.data_ptr(),
+                                      self.ws_bytes,
                                       C.byref(trace.c) if trace is not None else None, stream()))
         return logits
 
     def gather_kv(self, layer, cells, which=0):
-        """Cells of a layer's K (0) or V (1) as (n, Hkv*D) f16 bits (uint16)."""
+        """Cells of a layer's K (0) or V (1) as (n, Hkv*D) f16 bits (uint16)
+        (ring cells for a sliding layer)."""
         cells = np.ascontiguousarray(cells, np.int64)
         dc = torch.from_numpy(cells).to(DEV)
         out = torch.empty((len(cells), self.hp["n_head_kv"] * self.hp["head_dim"]),
                           dtype=torch.int16, device=DEV)
         pool = (self.kpools if which == 0 else self.vpools)[layer]
-        check(hip.lib().lgmlh_kv_gather(pool.data_ptr(), which, self.n_cells,
+        n = self.ring_cells if self.swa[layer] else self.n_cells
+        check(hip.lib().lgmlh_kv_gather(pool.data_ptr(), which, n,
                                         self.hp["n_head_kv"], self.hp["head_dim"],
                                         dc.data_ptr(), len(cells), out.data_ptr(), stream()))
         return out.cpu().numpy().view(np.uint16)

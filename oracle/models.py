@@ -159,7 +159,31 @@ SHAPES = {
     "c5": dict(arch="qwen3moe", n_layer=48, n_embd=2048, n_head=32, n_head_kv=4, head_dim=128,
                n_ff=768, n_vocab=151936, rope_base=1e6, eps=1e-6, wtype="q4_K", n_expert=128,
                n_used=8, n_ff_exp=768, gating=1, norm_topk=True, expert_scale=1.0),
+    # C4: a Gemma-4-style model: 5 sliding-window layers (1024-token window,
+    # rope base 1e4) to 1 global layer (rope base 1e6, proportional rope, V
+    # from the raw K), q/k norms, V norm, post norms, GeGLU, layer output
+    # scales, tied output, logit softcap 30; Q8_0 weights.
+    "c4": dict(arch="gemma4", n_layer=26, n_embd=2560, n_head=8, n_head_kv=4, head_dim=256,
+               n_ff=10240, n_vocab=262144, rope_base=1e6, eps=1e-6, wtype="q8_0", gemma=True,
+               n_swa=1024, swa_period=6, rope_base_swa=1e4, softcap=30.0),
 }
+
+
+def gemma_layer(hp, il):
+    """Per-layer structure of a gemma shape (transformer.lua:215-235,
+    test/test_gemma4.lua:116-128): layer il slides unless il % swa_period
+    == swa_period - 1; sliding layers use rope_base_swa and have attn_v;
+    global layers use rope_base with proportional rope (factors 1 for the
+    first head_dim / 4 pairs, 1e30 after) and take V from the raw K. Layer
+    output scales 0.8 + 0.05 (il % 7)."""
+    D, per = hp["head_dim"], hp["swa_period"]
+    swa = il % per != per - 1
+    L = {"swa": int(swa), "rope_base": hp["rope_base_swa"] if swa else hp["rope_base"],
+         "out_scale": float(np.float32(0.8 + 0.05 * (il % 7))), "has_wv": swa}
+    if not swa:
+        L["rope_freqs"] = np.array([1.0 if i <= D // 4 else 1e30 for i in range(1, D // 2 + 1)],
+                                   np.float32)
+    return L
 
 
 def more_bits(i, n):
@@ -202,7 +226,12 @@ def build(shape, seed=1234, n_layer=None, init="uniform"):
         hp["n_layer"] = n_layer
     hp.setdefault("n_rot", hp["head_dim"])
     hp["rope_neox"] = 0 if hp["arch"] == "llama" else 1
-    hp["attn_scale"] = 0.0
+    gemma = hp["arch"] == "gemma4"
+    # gemma: attention scale 1, embeddings times sqrt(n_embd) rounded to f32
+    # (transformer.lua:171-183)
+    hp["attn_scale"] = 1.0 if gemma else 0.0
+    if gemma:
+        hp["embd_scale"] = float(np.float32(math.sqrt(hp["n_embd"])))
     E, H, Hkv, D, F, V = (hp[k] for k in ("n_embd", "n_head", "n_head_kv", "head_dim", "n_ff",
                                           "n_vocab"))
     nl = hp["n_layer"]
@@ -227,27 +256,46 @@ def build(shape, seed=1234, n_layer=None, init="uniform"):
             return (x, ty)
         return (core.quantize(ty, x), ty)
 
-    def norm(d):
+    def norm(d, mean=1.0):
         if init == "uniform":
-            return (lcg.fill(d, 0.9, 1.1), core.F32)
+            return (lcg.fill(d, 0.9 * mean, 1.1 * mean), core.F32)
+        if gemma:  # norm weights N(mean, mean / 10): the post norms are then visible
+            counter[0] += 1
+            return (core.gen_normal(d, mean, 0.1 * mean, seed * 1000003 + counter[0]), core.F32)
         return (np.ones(d, np.float32), core.F32)
+
+    # gemma attends at scale 1 to rms-normed q and k: q / k norm weights of
+    # mean D^(-1/4) give scores of unit scale, as trained weights keep them
+    # (with weights near 1 the scores of random heads have sd sqrt(D) = 16,
+    # every softmax is nearly one-hot and a 1-ulp change of any weight moves
+    # 6-layer logits by ~5e-3)
+    qk_mean = D ** -0.25 if gemma else 1.0
 
     w = {}
     w["tok_embd"] = mat("tok_embd", V, E)
     w["output_norm"] = norm(E)
-    w["output"] = mat("output", V, E)
+    # gemma ties the output to the embeddings (transformer.lua:408)
+    w["output"] = w["tok_embd"] if gemma else mat("output", V, E)
     w["rope_freqs"] = None
     layers = []
     for il in range(nl):
         L = {}
+        g = gemma_layer(hp, il) if gemma else {}
         L["attn_norm"] = norm(E)
         L["wq"] = mat("wq", H * D, E, il)
         L["wk"] = mat("wk", Hkv * D, E, il)
-        L["wv"] = mat("wv", Hkv * D, E, il)
+        if g.get("has_wv", True):
+            L["wv"] = mat("wv", Hkv * D, E, il)
         L["wo"] = mat("wo", E, H * D, il)
-        if hp["arch"] in ("qwen3", "qwen3moe"):
-            L["q_norm"] = norm(D)
-            L["k_norm"] = norm(D)
+        if hp["arch"] in ("qwen3", "qwen3moe", "gemma4"):
+            L["q_norm"] = norm(D, qk_mean)
+            L["k_norm"] = norm(D, qk_mean)
+        if gemma:
+            L["post_attn_norm"] = norm(E)
+            L["post_ffn_norm"] = norm(E)
+            for k in ("swa", "rope_base", "out_scale", "rope_freqs"):
+                if k in g:
+                    L[k] = g[k]
         L["ffn_norm"] = norm(E)
         if hp.get("n_expert"):
             NE, FX = hp["n_expert"], hp["n_ff_exp"]

@@ -35,7 +35,7 @@ def test_exports_every_declared_symbol(hip):
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing
     assert sorted(hip.SYMBOLS) == names
-    assert L.lgmlh_abi_version() == 3
+    assert L.lgmlh_abi_version() == 4
 
 
 def test_struct_layouts_match_the_header(hip, tmp_path):
@@ -190,3 +190,66 @@ def test_plan_errors(hip):
     rc, _, _ = plan(hip, [1], [0], np.array([[1]], np.int32), [0], 6, 4, 16)  # H % Hkv
     assert rc == hip.EINVAL
     assert "plan" in hip.last_error()
+
+
+def plan_ring(hip, seq_n, npast, ring_tab, window, ids, H, Hkv, pool_blocks, bps=0):
+    L = hip.lib()
+    info = hip.PlanInfo()
+    keep = [np.ascontiguousarray(seq_n, np.int32), np.ascontiguousarray(npast, np.int32),
+            np.ascontiguousarray(ring_tab, np.int32), np.ascontiguousarray(ids, np.int32)]
+    args = (len(seq_n), keep[0].ctypes.data, keep[1].ctypes.data, keep[2].ctypes.data,
+            keep[2].shape[1], pool_blocks, window, keep[3].ctypes.data, H, Hkv, bps)
+    rc = L.lgmlh_plan_ring(*args, None, 0, C.byref(info))
+    if rc:
+        return rc, None, None
+    buf = np.zeros(info.bytes, np.uint8)
+    rc = L.lgmlh_plan_ring(*args, buf.ctypes.data, buf.nbytes, C.byref(info))
+    return rc, info, buf
+
+
+def test_ring_plan_maps_positions_into_the_rings(hip):
+    """lgmlh_plan_ring: position p of sequence s goes to ring_tab[s, (p / 64)
+    % R] * 64 + p % 64 (rows_swa = p % ring, transformer.lua:2469-2476), and
+    each query group's runs cover the logical blocks from its window's start
+    to its last position exactly once."""
+    W, R = 100, 3  # 192 ring cells: a pass of up to 93 tokens
+    ring_tab = np.array([[7, 2, 5], [0, 9, 4], [1, 3, 8]], np.int32)
+    seq_n, npast = [1, 40, 93], [1000, 37, 0]
+    ids = np.arange(sum(seq_n), dtype=np.int32)
+    rc, info, buf = plan_ring(hip, seq_n, npast, ring_tab, W, ids, 8, 4, 10, bps=1)
+    assert rc == 0 and info.window == W and info.ring == R and info.max_blocks == R
+    cells = arr(buf, info.off_cells, info.n_tokens, np.int64)
+    t = 0
+    for s, (n, p0) in enumerate(zip(seq_n, npast)):
+        for j in range(n):
+            p = p0 + j
+            assert cells[t] == ring_tab[s, (p // 64) % R] * 64 + p % 64
+            t += 1
+    assert list(arr(buf, info.off_block_tab, 9, np.int32)) == list(ring_tab.reshape(-1))
+    items = arr(buf, info.off_items, 4 * info.n_items, np.int32).reshape(-1, 4)
+    runs = {}
+    for s, tok0, nt, blk in items:
+        runs.setdefault((int(s), int(tok0), int(nt) & 31), []).append((blk & 0xffff, blk >> 16))
+    offs = np.cumsum([0] + seq_n)
+    for (s, tok0, nt), rr in runs.items():
+        rr.sort()
+        pf = npast[s] + tok0 - offs[s]
+        pl = pf + nt - 1
+        assert rr[0][0] == max(0, pf - W + 1) // 64 and rr[-1][1] == pl // 64 + 1
+        assert all(rr[i][1] == rr[i + 1][0] for i in range(len(rr) - 1))
+        assert len({hi - lo for lo, hi in rr[:-1]}) <= 1  # runs of equal length
+    # every token is in exactly one group
+    assert sorted(t0 + k for (_, t0, nt) in runs for k in range(nt)) == list(range(sum(seq_n)))
+
+
+def test_ring_plan_errors(hip):
+    tab = np.array([[0, 1]], np.int32)
+    # 2 blocks = 128 cells: window 100 leaves room for 29 tokens in one pass
+    assert plan_ring(hip, [29], [500], tab, 100, np.zeros(29), 4, 2, 4)[0] == 0
+    assert plan_ring(hip, [30], [500], tab, 100, np.zeros(30), 4, 2, 4)[0] == hip.ERANGE
+    assert "ring" in hip.last_error()
+    # ring blocks outside the pool
+    assert plan_ring(hip, [1], [70], np.array([[0, 4]], np.int32), 100, [0], 4, 2, 4)[0] == \
+        hip.ERANGE
+    # no window
+    assert plan_ring(hip, [1], [0], tab, 0, [0], 4, 2, 4)[0] == hip.EINVAL
