@@ -19,6 +19,12 @@ qwen3moe (48 layers, d 2048, 32 / 4 heads, head 128, 128 experts of width
 U[256, 8192]: tokens are grouped by expert for the grouped Q4_K expert
 products.
 
+--workload c4: a Gemma-4-style model (26 layers,
+d 2560, 8 / 4 heads of 256, 5 sliding-window layers with a 1024-token ring
+per slot to 1 global layer, GeGLU FFN 10240, vocab 262144 tied, Q8_0), 32
+slots with contexts U[1024, 16384] decoding 128 steps (no joins: every
+budget outlasts the run).
+
 value = decoded tokens / wall seconds of the K timed steps (inputs resident
 in HBM; the per-step host plan upload and the 64 sampled ids read back are
 inside; no instrumentation). roofline = the paged attention kernel (the
@@ -41,7 +47,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--seed", type=int, default=20261201)
-    ap.add_argument("--slots", type=int, default=64)
+    ap.add_argument("--slots", type=int, default=0, help="slots (0 = the workload's)")
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2")
     ap.add_argument("--bps", type=int, default=0, help="KV blocks per attention work item (0 = auto)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -58,6 +64,11 @@ WORKLOADS = {
                metric="decode tok/s, 64 ragged seqs, Llama-3-8B-shape Q4_K; paged-attn HBM GB/s %",
                text="C2: Llama-3-8B shape, Q4_K_M, f16 KV, 64 ragged slots, prompts U[128,4096], "
                     "continuous batching (budgets U[64,2048], joins prefilled in 512-token chunks)"),
+    "c4": dict(prompt=(1024, 16384), slots=32, joins=False,
+               metric="decode tok/s, 32 slots, Gemma-4-style SWA ring Q8_0; paged-attn HBM GB/s %",
+               text="C4: Gemma-4-style, 26 layers (5 sliding-window 1024-token rings per slot : 1 "
+                    "global), d 2560, 8/4 heads of 256, GeGLU 10240, vocab 262144 tied, Q8_0, f16 "
+                    "KV, 32 slots, contexts U[1024,16384], decode only (no joins)"),
     "c5": dict(prompt=(256, 8192),
                metric="decode tok/s, 64 ragged seqs, 30B-A3B-shape MoE Q4_K; paged-attn HBM GB/s %",
                text="C5: 30B-A3B-shaped qwen3moe, 128 experts x 768, top-8 softmax routing, Q4_K, "
@@ -77,20 +88,22 @@ def log(args, *a):
 
 def cpu_baseline(hp, contexts, seed, args):
     """The C oracle on one decode step of the workload's shape: 1 of the
-    n_layer layers plus the output head, 64 sequences at the workload's
-    contexts (synthetic KV), timed on the host cores; scaled to a full step."""
+    n_layer layers plus the output head (a sliding and a global layer, for
+    a gemma shape), all sequences at the workload's contexts (synthetic KV),
+    timed on the host cores; scaled to a full step."""
     import numpy as np
 
+    from lgml_amd import workload
     from oracle import core, models
 
     E, V = hp["n_embd"], hp["n_vocab"]
     threads = core.threads()
-    ohp, w = models.build(args.workload, seed=seed, n_layer=1, init="normal")
-    om = core.OracleModel(ohp, w)
     S = len(contexts)
     B = 64
     nbs = [(c + 1 + B - 1) // B for c in contexts]
-    n_cells = sum(nbs) * B
+    gemma = bool(hp.get("gemma"))
+    R = workload.ring_blocks(hp, 1) if gemma else 0
+    n_cells = max(sum(nbs), S * R) * B
     row = hp["n_head_kv"] * hp["head_dim"]
     rng = np.random.default_rng(seed)
     kp = [rng.integers(0x3000, 0x3c00, size=(n_cells, row), dtype=np.uint16)]
@@ -100,26 +113,44 @@ def cpu_baseline(hp, contexts, seed, args):
     for i, nb in enumerate(nbs):
         bt[i, :nb] = np.arange(o, o + nb)
         o += nb
+    rt = np.arange(S * R, dtype=np.int32).reshape(S, R) if gemma else None
     ids = rng.integers(0, V, size=S).astype(np.int32)
-    b = core.BatchDesc([1] * S, contexts, bt, B, ids, list(range(S)))
+    b = core.BatchDesc([1] * S, contexts, bt, B, ids, list(range(S)), ring_tab=rt)
+
+    def one_layer(shape):
+        """Mean seconds of a 1-layer pass (embeddings, layer, head), repeated
+        until ~8 s of samples; the model's output matrix."""
+        ohp, w = models.build(shape, seed=seed, n_layer=1, init="normal")
+        om = core.OracleModel(ohp, w)
+        reps, t_all = 0, 0.0
+        while reps < 2 or (t_all < 8.0 and reps < 20):
+            t0 = time.time()
+            om.forward(kp, vp, b)
+            t_all += time.time() - t0
+            reps += 1
+        return t_all / reps, reps, t_all, w["output"]
+
+    kinds = [("layer", args.workload, hp["n_layer"])]
+    if gemma:
+        n_glob = sum(1 - workload.gemma_layer(hp, il)["swa"] for il in range(hp["n_layer"]))
+        kinds = [("sliding layer", args.workload, hp["n_layer"] - n_glob),
+                 ("global layer", dict(models.SHAPES[args.workload], swa_period=1), n_glob)]
+    passes = [one_layer(shape) for _, shape, _ in kinds]
+    out = passes[0][3]
     x = rng.standard_normal((S, E)).astype(np.float32)
     t0 = time.time()
-    core.mul_mat(w["output"][1], w["output"][0], V, E, x)
+    core.mul_mat(out[1], out[0], V, E, x)
     t_head = time.time() - t0
-    # the 1-layer pass (embeddings, layer, head) repeated until ~8 s of samples
-    reps, t_all = 0, 0.0
-    while reps < 3 or (t_all < 8.0 and reps < 20):
-        t0 = time.time()
-        om.forward(kp, vp, b)
-        t_all += time.time() - t0
-        reps += 1
-    t_layer = max(t_all / reps - t_head, 1e-9)
-    t_step = t_head + hp["n_layer"] * t_layer
+    t_step = t_head
+    parts = []
+    for (name, _, n), (t_pass, reps, t_all, _) in zip(kinds, passes):
+        t_layer = max(t_pass - t_head, 1e-9)
+        t_step += n * t_layer
+        parts.append("%d x %s (%.2f s; %d passes, %.1f s)" % (n, name, t_layer, reps, t_all))
     return {"value": S / t_step, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": "oracle/ (C, OpenMP) decode pass of the %s shape at %d sequences "
-                      "(contexts as the GPU run, synthetic KV) with 1 layer, %d times (%.1f s), "
-                      "output head %.1f s; step = head + %d x layer (%.2f s)" % (
-                          args.workload.upper(), S, reps, t_all, t_head, hp["n_layer"], t_layer)}
+            "sample": "oracle/ (C, OpenMP) 1-layer decode passes of the %s shape at %d sequences "
+                      "(contexts as the GPU run, synthetic KV), output head %.1f s; step = head + "
+                      "%s" % (args.workload.upper(), S, t_head, " + ".join(parts))}
 
 
 def traffic_of(path, args):
@@ -162,13 +193,20 @@ def main():
     hp = dict(workload.SHAPES[args.workload])
     ty = workload.policy(hp["wtype"], hp["n_layer"])
     rng = workload.Lcg(args.seed)
-    S = args.slots
+    S = args.slots = args.slots or wl.get("slots", 64)
     plo, phi = wl["prompt"]
-    max_ctx = phi + 2048 + 64
+    n_trace = min(args.steps, 16)
+    joins_on = wl.get("joins", True)
+    # without joins every budget outlasts the warmup, timed and traced steps
+    budget = (64, 2048) if joins_on else (args.warmup + args.steps + n_trace + 2,) * 2
+    max_ctx = phi + budget[1] + 64
     n_cells = ((S * max_ctx + 63) // 64) * 64
+    # sliding layers: a ring per slot, sized for 512-token passes
+    ring_cells = S * workload.ring_blocks(hp, engine.UBATCH) * 64 if hp.get("gemma") else 0
     log(args, "building the model on the device ...")
     t0 = time.time()
-    model = runtime.DeviceModel(hp, runtime.generated_weights(hp, args.seed, ty), n_cells)
+    model = runtime.DeviceModel(hp, runtime.generated_weights(hp, args.seed, ty), n_cells,
+                                ring_cells=ring_cells)
     torch.cuda.synchronize()
     log(args, "model ready in %.1f s; pool %d cells (%.1f GB KV)" % (
         time.time() - t0, n_cells, n_cells * 2 * 2 * hp["n_head_kv"] * hp["head_dim"] *
@@ -179,7 +217,6 @@ def main():
     for t in model.kpools + model.vpools:
         t.view(torch.float16).uniform_(-1.0, 1.0, generator=g)
 
-    n_trace = min(args.steps, 16)
     trace = runtime.EventTrace(n_trace * hp["n_layer"] * 8 + 64,
                                hip.TRACE_ATTN | hip.TRACE_GEMM | hip.TRACE_EXPERTS)
     eng = engine.Engine(model, S, blocks_per_split=args.bps)
@@ -187,7 +224,7 @@ def main():
     def new_request(prefilled):
         n = rng.int(plo, phi)
         prompt = [rng.int(0, hp["n_vocab"] - 1) for _ in range(n)]
-        r = engine.Request(prompt, rng.int(64, 2048))
+        r = engine.Request(prompt, rng.int(*budget))
         eng.submit(r)
         if prefilled:
             eng.seqs.reserve(r.seq, n)
@@ -205,7 +242,7 @@ def main():
     def step(record):
         eng.trace = trace if record else None
         got = eng.step()
-        while len(eng.active) < S:
+        while joins_on and len(eng.active) < S:
             new_request(False)
             joins[0] += 1
         return got
@@ -217,17 +254,23 @@ def main():
     decoded = prefill_tok = 0
     wbytes = workload.weight_bytes(hp, S)
     xbytes = workload.expert_bytes(hp, S)
-    kvb = 2 * hp["n_layer"] * hp["n_head_kv"] * hp["head_dim"] * 2  # K+V bytes per cell, all layers
+    cellb = 2 * hp["n_head_kv"] * hp["head_dim"] * 2  # K+V bytes per cell and layer
+    swa = list(model.swa)
 
     def bytes_of_last_step():
-        """(attention bytes per layer, step bytes) of the step just run."""
+        """(attention bytes of each layer, step bytes) of the step just run:
+        K + V of every cell a query group sees (a sliding layer: at most the
+        window - 1 + the pass's tokens), q in and out; the step adds the
+        weights and the new cells' K + V."""
         plan = eng.last_plan
-        seq_n = plan.seq_n
-        n_kv = (plan.seq_npast.astype(np.int64) + seq_n)
+        seq_n = plan.seq_n.astype(np.int64)
+        n_kv = plan.seq_npast.astype(np.int64) + seq_n
         N = int(seq_n.sum())
-        per_layer_kv = int(n_kv.sum()) * kvb // hp["n_layer"]
         qo = N * hp["n_head"] * hp["head_dim"] * 4 * 2
-        return per_layer_kv + qo, wbytes + int(n_kv.sum()) * kvb + N * kvb
+        full = int(n_kv.sum()) * cellb
+        win = int(np.minimum(n_kv, hp.get("n_swa", 0) - 1 + seq_n).sum()) * cellb
+        per_layer = [(win if sl else full) + qo for sl in swa]
+        return per_layer, wbytes + sum(per_layer) + N * cellb * len(swa)
 
     # The timed steps run without instrumentation (value, ms_per_step); the
     # kernel times come from n_trace more steps with HIP events around
@@ -254,7 +297,7 @@ def main():
     L = hp["n_layer"]
     # attention launches are recorded in step order, L per step
     n_att = len(at)
-    tot_bytes = sum(attn_bytes[i // L] for i in range(n_att))
+    tot_bytes = sum(attn_bytes[i // L][i % L] for i in range(n_att))
     attn_gbs = tot_bytes / (sum(at) / 1e3) if at else 0.0
     avg_attn_ms = sum(at) / max(n_att, 1)
     gemm_ms = (sum(gt) + sum(xt)) / n_trace
@@ -272,7 +315,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "%s weights, f16 KV, f32 accumulate" % hp["wtype"],
+        "dtype": "%s weights, f16 KV, f32 accumulate" % hp["wtype"].replace("q8_0", "Q8_0"),
         "data": "synthetic (seeded random-init weights, LCG prompts, synthetic initial KV)",
         "config": {
             "workload": wl["text"],

@@ -256,13 +256,11 @@ struct WFrag<LGMLH_Q6_K> {
 
 template <>
 struct WFrag<LGMLH_Q8_0> {
-  u32x4 qs[4];           // 8 blocks x 8 int8
-  const uint8_t *hd;     // header: d of rows 4c + i, block g at hd + 8g
+  u32x4 qs[4];           // 8 blocks x 8 int8 (the header goes through LDS)
   __device__ __forceinline__ void load(const uint8_t *ch, int lane) {
     const u32x4 *p = (const u32x4 *)(ch + 256 + lane * 64);
 #pragma unroll
     for (int i = 0; i < 4; i++) qs[i] = p[i];
-    hd = ch + 64 * (lane >> 4);
   }
   // q for k = 32g + 8c + e: (1024 + (q + 128)) - 1152, exact.
   __device__ __forceinline__ f16x8 frag(int g) const {
@@ -275,13 +273,16 @@ struct WFrag<LGMLH_Q8_0> {
 };
 
 // ---- the quantized GEMM --------------------------------------------------------
-// grid: (Npad / 64, ceil(M / WG_ROWS), splits); blockIdx.x (N tiles) varies
-// fastest so the workgroups that share a weight tile run together.
+// grid: (ceil(N / (16 NCT)), ceil(M / WG_ROWS), splits); blockIdx.x (N
+// tiles) varies fastest so the workgroups that share a weight tile run
+// together.
 //
 // Pipeline: the weight fragments and X pieces of K step sb + 1 load into
 // registers while sb computes (two register sets, two LDS X buffers, one
-// barrier per step). A split writes its partial sums; a second kernel adds
-// the splits in order (no inter-workgroup sync).
+// barrier per step). Q8_0 chunk headers (a d per row and 32-value block)
+// travel with X, global-to-LDS, and each group's d are read from LDS one
+// group ahead. A split writes its partial sums; a second kernel adds the
+// splits in order (no inter-workgroup sync).
 template <int TYPE, int NCT, bool GATHER>
 __global__ void __launch_bounds__(GEMM_THREADS)
 qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__restrict__ xs,
@@ -294,6 +295,10 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   __shared__ __align__(16) u32x4 xl_[2][X_SLOTS];
   __shared__ __align__(16) u32x4 gh_[2][64];  // group sums, hi: 8 f16 per row
   __shared__ __align__(16) u32x4 gl_[2][64];  // group sums, lo
+  // Q8_0: the 256-byte headers of every wave's chunks (wave w, tile a at
+  // slots 32 w + 16 a .. + 15)
+  constexpr int HD_SLOTS = TYPE == LGMLH_Q8_0 ? GEMM_WAVES * RT_PER_WAVE * 16 : 1;
+  __shared__ __align__(16) u32x4 hd_[2][HD_SLOTS];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int64_t NSB = K / QK_K;
@@ -344,6 +349,16 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   // group sums: lane = column (lanes past the workgroup's columns load a
   // valid row into slots that are never read)
   const uint32_t goff = (uint32_t)(xrow(lane < COLS ? lane : 0) * (K / 32));
+  // Chunk of tile a at K step sb_lo + kstep: a wave-uniform address (rows
+  // past M clamp to the last tile; they are computed but never stored).
+  const uint8_t *wt[RT_PER_WAVE];
+#pragma unroll
+  for (int a = 0; a < RT_PER_WAVE; a++) {
+    const int64_t rt = rt0 + a < MT ? rt0 + a : MT - 1;
+    wt[a] = w + (rt * NSB + sb_lo) * chunk_bytes(TYPE);
+  }
+  // Q8_0 header piece of lane < 32: tile lane / 16, bytes 16 (lane % 16)
+  const uint8_t *hsrc = wt[(lane >> 4) & 1] + 16 * (lane & 15);
   auto load_x = [&](uint32_t kstep, int buf) {  // kstep = sb - sb_lo
 #pragma unroll
     for (int j = 0; j < XJ; j++) {
@@ -359,15 +374,13 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
             (const void *)((wave == 0 ? ghi : glo) + goff + kstep * 8),
             (lds_t *)(wave == 0 ? &gh_[buf][0] : &gl_[buf][0]), 16, 0, 0);
     }
+    if constexpr (TYPE == LGMLH_Q8_0) {
+      if (lane < 32)
+        __builtin_amdgcn_global_load_lds(
+            (const void *)(hsrc + kstep * (uint32_t)chunk_bytes(TYPE)),
+            (lds_t *)&hd_[buf][wave * RT_PER_WAVE * 16], 16, 0, 0);
+    }
   };
-  // Chunk of tile a at K step sb_lo + kstep: a wave-uniform address (rows
-  // past M clamp to the last tile; they are computed but never stored).
-  const uint8_t *wt[RT_PER_WAVE];
-#pragma unroll
-  for (int a = 0; a < RT_PER_WAVE; a++) {
-    const int64_t rt = rt0 + a < MT ? rt0 + a : MT - 1;
-    wt[a] = w + (rt * NSB + sb_lo) * chunk_bytes(TYPE);
-  }
   auto load_w = [&](WFrag<TYPE>(&dst)[RT_PER_WAVE], uint32_t kstep) {
 #pragma unroll
     for (int a = 0; a < RT_PER_WAVE; a++) dst[a].load(wt[a] + kstep * (uint32_t)chunk_bytes(TYPE), lane);
@@ -418,8 +431,19 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
 #pragma unroll
       for (int ct = 0; ct < NCT; ct++) bl[ct] = __builtin_bit_cast(f16x8, xl[ct * 16 * 32 + slot]);
     };
+    // Q8_0: d of rows 4c .. 4c + 3 of tile a, block g
+    u32x2 dv[RT_PER_WAVE];
+    auto read_d = [&](int g) {
+      if constexpr (TYPE == LGMLH_Q8_0) {
+#pragma unroll
+        for (int a = 0; a < RT_PER_WAVE; a++)
+          dv[a] = *(const u32x2 *)((const uint8_t *)&hd_[buf][(wave * RT_PER_WAVE + a) * 16] +
+                                   64 * c + 8 * g);
+      }
+    };
     read_bh(0);
     read_bl(0);
+    read_d(0);
 #pragma unroll
     for (int g = 0; g < 8; g++) {
       f16x8 af[RT_PER_WAVE], af2[RT_PER_WAVE], afr[RT_PER_WAVE];
@@ -455,21 +479,31 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
           cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(TYPE == LGMLH_Q6_K ? afr[a] : af[a],
                                                               bl[ct], cm[a][ct], 0, 0, 0);
       if (g < 7) read_bl(g + 1);
+      u32x2 dg[RT_PER_WAVE];
+#pragma unroll
+      for (int a = 0; a < RT_PER_WAVE; a++) dg[a] = dv[a];
+      if (g < 7) read_d(g + 1);
       if (g == 6) after_lds();  // the last LDS reads of the step are out
       if constexpr (TYPE == LGMLH_Q8_0) {
         // one scale per 32-value block: flush every group
 #pragma unroll
         for (int a = 0; a < RT_PER_WAVE; a++) {
-          const u32x2 dv = *(const u32x2 *)(cur[a].hd + 8 * g);
 #pragma unroll
           for (int i = 0; i < 4; i++) {
-            const float d = h2f((uint16_t)(dv[i >> 1] >> (16 * (i & 1))));
+            const float d = h2f((uint16_t)(dg[a][i >> 1] >> (16 * (i & 1))));
 #pragma unroll
             for (int ct = 0; ct < NCT; ct++) {
               acc[a][ct][i] += d * cm[a][ct][i];
             }
           }
         }
+        // pin the flush here: left free, the compiler sinks every group's
+        // flush to the end of the step, keeping 8 groups of products live
+        // (spills)
+#pragma unroll
+        for (int a = 0; a < RT_PER_WAVE; a++)
+#pragma unroll
+          for (int ct = 0; ct < NCT; ct++) asm volatile("" : "+v"(acc[a][ct]));
       }
     }
     if constexpr (TYPE == LGMLH_Q4_K) {
@@ -673,10 +707,23 @@ static void launch_q(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t
   int spb = 0;
   splits = splits_for(M, K, N, &spb);
   const int64_t Npad = split_npad(N);
-  dim3 grid((unsigned)(Npad / WG_COLS), (unsigned)((M + WG_ROWS - 1) / WG_ROWS), (unsigned)splits);
-  hipLaunchKernelGGL((qgemm_kernel<TYPE, WG_COLS / 16, false>), grid, dim3(GEMM_THREADS), 0, st,
-                     (const uint8_t *)w, M, K, xs, Npad, N, y, ldy, res, splits, spb, part,
-                     Gather{});
+  // Column tiles of 64, or of 16 / 32 for a batch that small (the same sums
+  // per element: only the columns a workgroup carries change)
+  const int nct = N <= 16 ? 1 : N <= 32 ? 2 : WG_COLS / 16;
+  const int cols = 16 * nct;
+  dim3 grid((unsigned)((N + cols - 1) / cols), (unsigned)((M + WG_ROWS - 1) / WG_ROWS),
+            (unsigned)splits);
+#define LGMLH_PLAIN(NCT_)                                                                  \
+  hipLaunchKernelGGL((qgemm_kernel<TYPE, NCT_, false>), grid, dim3(GEMM_THREADS), 0, st,   \
+                     (const uint8_t *)w, M, K, xs, Npad, N, y, ldy, res, splits, spb, part, \
+                     Gather{})
+  if (nct == 1)
+    LGMLH_PLAIN(1);
+  else if (nct == 2)
+    LGMLH_PLAIN(2);
+  else
+    LGMLH_PLAIN(4);
+#undef LGMLH_PLAIN
   if (splits > 1 && !defer) {
     int64_t total = N * M;
     unsigned blocks = (unsigned)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);

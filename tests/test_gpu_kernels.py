@@ -139,7 +139,7 @@ def test_mul_mat_parity_and_batch_invariance(L, ty, MK):
     w = wf if ty == core.F32 else core.quantize(ty, wf)
     deq = wf if ty == core.F32 else core.dequantize(ty, w, K)
     x = core.fill_normal(130 * K, 0, 1, 8).reshape(130, K)
-    for N in (1, 3, 64, 70, 130):
+    for N in (1, 3, 17, 32, 64, 70, 130):  # column tiles of 16, 32 and 64
         y = run_mul_mat(L, ty, w, M, K, x[:N])
         want = core.mul_mat(core.F32, deq, M, K, x[:N])
         assert rel_err(y, want) < 2e-3, (N, rel_err(y, want))
