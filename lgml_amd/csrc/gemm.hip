@@ -277,8 +277,10 @@ struct WFrag<LGMLH_Q8_0> {
 // tiles) varies fastest so the workgroups that share a weight tile run
 // together.
 //
-// Pipeline: the weight fragments and X pieces of K step sb + 1 load into
-// registers while sb computes (two register sets, two LDS X buffers, one
+// Pipeline: the weight fragments (into registers) and X pieces (global-to-
+// LDS) of K step sb + 1 are issued at the start of step sb and load while
+// it computes (two register sets, two LDS buffers, each buffer its own LDS
+// object so that reads of one need not wait for loads into the other; one
 // barrier per step). Q8_0 chunk headers (a d per row and 32-value block)
 // travel with X, global-to-LDS, and each group's d are read from LDS one
 // group ahead. A split writes its partial sums; a second kernel adds the
@@ -291,14 +293,19 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
              float *__restrict__ part, Gather gt) {
   constexpr int COLS = NCT * 16;            // N columns per workgroup
   constexpr int X_SLOTS = COLS * 32;
-  __shared__ __align__(16) u32x4 xh_[2][X_SLOTS];
-  __shared__ __align__(16) u32x4 xl_[2][X_SLOTS];
-  __shared__ __align__(16) u32x4 gh_[2][64];  // group sums, hi: 8 f16 per row
-  __shared__ __align__(16) u32x4 gl_[2][64];  // group sums, lo
+  __shared__ __align__(16) u32x4 xh0_[X_SLOTS], xh1_[X_SLOTS];
+  __shared__ __align__(16) u32x4 xl0_[X_SLOTS], xl1_[X_SLOTS];
+  __shared__ __align__(16) u32x4 gh0_[64], gh1_[64];  // group sums, hi: 8 f16 per row
+  __shared__ __align__(16) u32x4 gl0_[64], gl1_[64];  // group sums, lo
   // Q8_0: the 256-byte headers of every wave's chunks (wave w, tile a at
   // slots 32 w + 16 a .. + 15)
   constexpr int HD_SLOTS = TYPE == LGMLH_Q8_0 ? GEMM_WAVES * RT_PER_WAVE * 16 : 1;
-  __shared__ __align__(16) u32x4 hd_[2][HD_SLOTS];
+  __shared__ __align__(16) u32x4 hd0_[HD_SLOTS], hd1_[HD_SLOTS];
+  auto XH = [&](int b) { return b ? xh1_ : xh0_; };
+  auto XL = [&](int b) { return b ? xl1_ : xl0_; };
+  auto GH = [&](int b) { return b ? gh1_ : gh0_; };
+  auto GL = [&](int b) { return b ? gl1_ : gl0_; };
+  auto HD = [&](int b) { return b ? hd1_ : hd0_; };
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int64_t NSB = K / QK_K;
@@ -364,21 +371,21 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
     for (int j = 0; j < XJ; j++) {
       const int slot0 = (wave * XJ + j) * 64;
       __builtin_amdgcn_global_load_lds((const void *)(xhi + xoff[j] + kstep * QK_K),
-                                       (lds_t *)&xh_[buf][slot0], 16, 0, 0);
+                                       (lds_t *)&XH(buf)[slot0], 16, 0, 0);
       __builtin_amdgcn_global_load_lds((const void *)(xlo + xoff[j] + kstep * QK_K),
-                                       (lds_t *)&xl_[buf][slot0], 16, 0, 0);
+                                       (lds_t *)&XL(buf)[slot0], 16, 0, 0);
     }
     if constexpr (TYPE == LGMLH_Q4_K) {
       if (wave < 2)  // wave 0: hi sums, wave 1: lo sums
         __builtin_amdgcn_global_load_lds(
             (const void *)((wave == 0 ? ghi : glo) + goff + kstep * 8),
-            (lds_t *)(wave == 0 ? &gh_[buf][0] : &gl_[buf][0]), 16, 0, 0);
+            (lds_t *)(wave == 0 ? GH(buf) : GL(buf)), 16, 0, 0);
     }
     if constexpr (TYPE == LGMLH_Q8_0) {
       if (lane < 32)
         __builtin_amdgcn_global_load_lds(
             (const void *)(hsrc + kstep * (uint32_t)chunk_bytes(TYPE)),
-            (lds_t *)&hd_[buf][wave * RT_PER_WAVE * 16], 16, 0, 0);
+            (lds_t *)&HD(buf)[wave * RT_PER_WAVE * 16], 16, 0, 0);
     }
   };
   auto load_w = [&](WFrag<TYPE>(&dst)[RT_PER_WAVE], uint32_t kstep) {
@@ -391,15 +398,15 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   // fragments of group g + 1 are read while group g multiplies; within a
   // group the products with hi go before those with lo, so no MFMA waits
   // for the one just issued.
-  auto compute = [&](const WFrag<TYPE>(&cur)[RT_PER_WAVE], int buf, auto &&after_lds) {
-    const u32x4 *xh = xh_[buf], *xl = xl_[buf];
+  auto compute = [&](const WFrag<TYPE>(&cur)[RT_PER_WAVE], int buf) {
+    const u32x4 *xh = XH(buf), *xl = XL(buf);
     f32x4 cm[RT_PER_WAVE][NCT];
-    // The group sums are read first: every LDS read of the step must be
-    // issued before the next step's global-to-LDS loads (after_lds), or the
-    // compiler, unable to tell the buffers apart, waits for those loads.
+    // The two buffers are separate LDS objects, so the compiler lets these
+    // reads run while the next step's global-to-LDS loads into the other
+    // buffer are in flight.
     f16x4 sh4[NCT], sl4[NCT];
     if constexpr (TYPE == LGMLH_Q4_K) {
-      const f16 *gh = (const f16 *)gh_[buf], *gl = (const f16 *)gl_[buf];
+      const f16 *gh = (const f16 *)GH(buf), *gl = (const f16 *)GL(buf);
 #pragma unroll
       for (int ct = 0; ct < NCT; ct++) {
         sh4[ct] = f16x4{0, 0, 0, 0};
@@ -437,7 +444,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
       if constexpr (TYPE == LGMLH_Q8_0) {
 #pragma unroll
         for (int a = 0; a < RT_PER_WAVE; a++)
-          dv[a] = *(const u32x2 *)((const uint8_t *)&hd_[buf][(wave * RT_PER_WAVE + a) * 16] +
+          dv[a] = *(const u32x2 *)((const uint8_t *)&HD(buf)[(wave * RT_PER_WAVE + a) * 16] +
                                    64 * c + 8 * g);
       }
     };
@@ -483,7 +490,6 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
 #pragma unroll
       for (int a = 0; a < RT_PER_WAVE; a++) dg[a] = dv[a];
       if (g < 7) read_d(g + 1);
-      if (g == 6) after_lds();  // the last LDS reads of the step are out
       if constexpr (TYPE == LGMLH_Q8_0) {
         // one scale per 32-value block: flush every group
 #pragma unroll
@@ -551,7 +557,8 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
                   WFrag<TYPE>(&nxt)[RT_PER_WAVE], int buf) {
     const uint32_t kn = k + 1 < nsteps ? k + 1 : k;
     load_w(nxt, kn);
-    compute(cur, buf, [&] { load_x(kn, buf ^ 1); });
+    load_x(kn, buf ^ 1);
+    compute(cur, buf);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's X loads have landed in LDS
     __syncthreads();                // ... and everyone's; buffer buf is free again
   };

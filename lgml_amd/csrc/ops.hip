@@ -156,12 +156,16 @@ __global__ void rms_norm_kernel(float *__restrict__ x, const int32_t *__restrict
 // ---- q/k norm, rope and KV store -------------------------------------------
 constexpr int QKV_V_FROM_K = 1, QKV_V_NORM = 2;
 // One workgroup per token. The row [q | k | v] is staged in LDS.
+// rms_norm of one head by one wave: f64 sum of squares, mean rounded to
+// f32, scale = 1 / sqrtf(mean + eps), v = (v * scale) * w.
 __device__ void head_rms_norm(float *v, int D, float eps, const float *w) {
+  const int lane = threadIdx.x & 63;
   double s = 0;
-  for (int i = 0; i < D; i++) s += (double)v[i] * (double)v[i];
-  float mean = (float)(s / (double)D);
-  float scale = 1.0f / sqrtf(mean + eps);
-  for (int i = 0; i < D; i++) v[i] = w ? (v[i] * scale) * w[i] : v[i] * scale;
+  for (int i = lane; i < D; i += 64) s += (double)v[i] * (double)v[i];
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  const float mean = (float)(s / (double)D);
+  const float scale = 1.0f / sqrtf(mean + eps);
+  for (int i = lane; i < D; i += 64) v[i] = w ? (v[i] * scale) * w[i] : v[i] * scale;
 }
 
 __global__ void qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int Hkv, int D,
@@ -200,11 +204,13 @@ __global__ void qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int 
     __syncthreads();
   }
   if (q_norm || k_norm || (vmode & QKV_V_NORM)) {
-    for (int h = threadIdx.x; h < H + 2 * Hkv; h += blockDim.x) {
-      if (h < H && q_norm) head_rms_norm(row + h * D, D, eps, q_norm);
-      if (h >= H && h < H + Hkv && k_norm) head_rms_norm(row + h * D, D, eps, k_norm);
-      // gemma: V rms-normed, no weight (:1782-1784)
-      if (h >= H + Hkv && (vmode & QKV_V_NORM)) head_rms_norm(row + h * D, D, eps, nullptr);
+    // one wave per head: q_norm / k_norm, and on gemma the V norm without
+    // a weight (:1782-1784)
+    const int wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (int h = wv; h < H + 2 * Hkv; h += nw) {
+      const bool is_q = h < H, is_k = !is_q && h < H + Hkv;
+      if (is_q ? !q_norm : is_k ? !k_norm : !(vmode & QKV_V_NORM)) continue;  // wave-uniform
+      head_rms_norm(row + h * D, D, eps, is_q ? q_norm : is_k ? k_norm : nullptr);
     }
     __syncthreads();
   }

@@ -19,6 +19,11 @@ shared, the best partial match is copied into a block of its own, and only
 the rest of the prompt runs. Full prompt blocks get keys as their prefill
 completes (E:publish, :1829-1841), so later requests can share them.
 
+A pass carries at most max_tokens tokens (a MoE model: 8192 / n_used,
+the picks one routing pass groups): decode tokens always go, prompt chunks
+are cut to what is left, and a request with no room waits for the next
+pass (E:flush itself is bounded by the memory budget, engine.lua:1477-1486).
+
 A model with sliding-window layers gives each slot a ring of its own in
 the ring pools (M:cache's per-slot rings, transformer.lua:575-600): slot
 i owns ring blocks i R .. i R + R - 1, R = ring_cells / 64 / n_slots, and
@@ -154,8 +159,10 @@ class Engine:
     """Slots over one pool; step() runs one batched pass (E:flush)."""
 
     def __init__(self, model, n_slots, ubatch=UBATCH, blocks_per_split=0, trace=None,
-                 prefix_cache=False):
+                 prefix_cache=False, max_tokens=None):
         self.model = model
+        nu = model.hp.get("n_used", 0) if model.hp.get("n_expert") else 0
+        self.max_tokens = max_tokens or (8192 // nu if nu else None)
         self.seqs = PoolSeqs(model)
         self.prefix_cache = prefix_cache
         self.hits = self.hit_blocks = 0
@@ -259,8 +266,19 @@ class Engine:
         """One pass over every active request; returns the requests that got
         a token. Requests whose budget is spent finish."""
         entries = []
+        left = self.max_tokens if self.max_tokens else 1 << 62
+        n_dec = sum(1 for r in self.active if r.fed >= len(r.prompt))
         for r in list(self.active):
             ids = r.pending(self.ubatch)
+            if r.fed < len(r.prompt):
+                # a prompt chunk takes what the decode tokens leave
+                room = left - n_dec
+                if room <= 0:
+                    continue
+                ids = ids[:room]
+            else:
+                n_dec -= 1
+            left -= len(ids)
             try:
                 self.seqs.reserve(r.seq, r.seq.n_past + len(ids))
             except PoolFull as e:
