@@ -203,6 +203,25 @@ int lgmlh_paged_attention(const float *q, int n_head, int n_head_kv, int head_di
     const void *kpool, const void *vpool, const lgmlh_ubatch *ub, float *out, void *workspace,
     size_t workspace_bytes, void *stream);
 
+/* graph:flash_attn(q, k, v, mask, scale, max_bias, softcap)
+ * (src/lgml.c:2121-2170) over strided K / V views with an explicit mask:
+ * the compatibility entry for attention outside the paged pool (e.g. M.attend
+ * on kv.for_flash views, kv.lua:141-147, under fill_causal / fill_mask
+ * masks, src/lgml.c:2836-2935). For query row t of head h and column j:
+ * s = scale q.k_j; with softcap > 0, s = softcap tanh(s / softcap); then
+ * s += slope_h mask[h % mask_heads][t][j] (slope 1, or ALiBi's when
+ * max_bias > 0); out = softmax(s) v. A -inf mask drops the column; a row
+ * with every column dropped gives zeros. q (H, T, D) f32; K / V element
+ * (hk, j, d) at k[hk * k_head_stride + j * k_row_stride + d] f16 (strides
+ * in elements, K 16-byte aligned with strides multiples of 8); mask
+ * (mask_heads, mask_rows >= T, n_kv) contiguous f16 or NULL; out (T, H, D)
+ * f32 (heads and tokens swapped, as the reference returns). Head h reads
+ * kv head h / (H / Hkv). D a multiple of 8 up to 256. */
+int lgmlh_flash_attn(const float *q, int n_head, int n_tokens, int head_dim, const uint16_t *k,
+    const uint16_t *v, int n_head_kv, int n_kv, int64_t k_row_stride, int64_t k_head_stride,
+    int64_t v_row_stride, int64_t v_head_stride, const uint16_t *mask, int mask_heads,
+    int mask_rows, float scale, float max_bias, float softcap, float *out, void *stream);
+
 /* ===================================================================== *
  * Weight matrix products: graph:mul_mat (src/lgml.c:1811-1839), ggml
  * convention: W (M, K) rows of `type`, X (N, K) -> Y (N, M) f32.

@@ -20,6 +20,7 @@ SYMBOLS = (
     "lgmlh_last_error", "lgmlh_abi_version", "lgmlh_row_size", "lgmlh_kv_layer_bytes",
     "lgmlh_kv_store", "lgmlh_kv_gather", "lgmlh_kv_copy_block", "lgmlh_set_rows_f16",
     "lgmlh_plan", "lgmlh_plan_bind", "lgmlh_attention_workspace", "lgmlh_paged_attention",
+    "lgmlh_flash_attn",
     "lgmlh_repacked_bytes", "lgmlh_repack", "lgmlh_dequantize", "lgmlh_mul_mat_workspace",
     "lgmlh_mul_mat", "lgmlh_get_rows", "lgmlh_rms_norm", "lgmlh_qkv_rope_store",
     "lgmlh_swiglu", "lgmlh_argmax", "lgmlh_forward_workspace", "lgmlh_forward",
@@ -122,6 +123,8 @@ def _declare(L):
         "lgmlh_plan_ring": ([i32, vp, vp, vp, i32, i64, i32, vp, i32, i32, i32, vp, sz,
                              C.POINTER(PlanInfo)], i32),
         "lgmlh_attention_workspace": ([C.POINTER(PlanInfo), i32], sz),
+        "lgmlh_flash_attn": ([vp, i32, i32, i32, vp, vp, i32, i32, i64, i64, i64, i64, vp, i32,
+                              i32, C.c_float, C.c_float, C.c_float, vp, vp], i32),
         "lgmlh_paged_attention": ([vp, i32, i32, i32, C.c_float, vp, vp, C.POINTER(Ubatch), vp,
                                    vp, sz, vp], i32),
         "lgmlh_repacked_bytes": ([i32, i64, i64], i64),

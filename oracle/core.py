@@ -90,6 +90,8 @@ def _declare(L):
                                       vp, i32]
     L.orc_paged_attention_swa.argtypes = [vp, vp, vp, i32, i32, i32, C.c_float, i32,
                                           C.POINTER(Batch), vp, i32]
+    L.orc_flash_attn.argtypes = [vp, i32, i32, i32, vp, vp, i32, i32, i64, i64, i64, i64, vp,
+                                 i32, i32, C.c_float, C.c_float, C.c_float, vp, i32]
     L.orc_set_rows_f16.argtypes = [vp, i64, i64, vp, vp, i64]
     L.orc_mul_mat.argtypes = [i32, vp, i64, i64, vp, i64, vp, i32]
     L.orc_moe_route.argtypes = [vp, i64, i32, i32, i32, i32, C.c_float, vp, vp]
@@ -278,6 +280,42 @@ def paged_attention_swa(q, kpool, vpool, H, Hkv, D, scale, window, batch, nthrea
                                        C.byref(batch.c), _p(out), nthreads or threads())
     if rc:
         raise ValueError("paged_attention_swa failed")
+    return out
+
+
+def flash_attn(q, k, v, n_head_kv, mask=None, scale=1.0, max_bias=0.0, softcap=0.0,
+               k_strides=None, v_strides=None, n_kv=None, nthreads=None):
+    """graph:flash_attn (src/lgml.c:2121-2170) on f16 K / V. q (H, T, D) f32.
+    k, v: uint16 arrays (f16 bits) holding element (hk, j, d) at [hk *
+    head_stride + j * row_stride + d] of the flattened array; strides
+    (row_stride, head_stride) default to a contiguous (Hkv, n_kv, D) layout
+    (n_kv = k.shape[-2]). mask: (mask_heads, rows, n_kv) or (rows, n_kv)
+    f16 bits, or None. Returns (T, H, D) f32."""
+    q = np.ascontiguousarray(q, np.float32)
+    H, T, D = q.shape
+    kf = np.ascontiguousarray(k).reshape(-1)
+    vf = np.ascontiguousarray(v).reshape(-1)
+    if n_kv is None:
+        n_kv = k.shape[-2]
+    if k_strides is None:
+        k_strides = (D, n_kv * D)
+    if v_strides is None:
+        v_strides = (D, n_kv * D)
+    mh, mr, mp = 0, 0, None
+    if mask is not None:
+        m = np.ascontiguousarray(mask)
+        if m.ndim == 2:
+            m = m[None]
+        mh, mr = m.shape[0], m.shape[1]
+        assert m.shape[2] == n_kv, "the mask has a column per kv row"
+        mp = m
+    out = np.zeros((T, H, D), np.float32)
+    rc = lib().orc_flash_attn(_p(q), H, T, D, _p(kf), _p(vf), n_head_kv, n_kv, k_strides[0],
+                              k_strides[1], v_strides[0], v_strides[1],
+                              _p(mp) if mp is not None else None, mh, mr, scale, max_bias,
+                              softcap, _p(out), nthreads or threads())
+    if rc:
+        raise ValueError("flash_attn failed")
     return out
 
 

@@ -733,6 +733,98 @@ attend(const float *q, const uint16_t *kpool, const uint16_t *vpool, int H, int 
 	return bad ? -1 : 0;
 }
 
+/* ALiBi slope of head h (ggml_flash_attn_ext / soft_max_ext): with
+ * n = the largest power of two <= H, m0 = 2^(-max_bias / n), m1 =
+ * 2^(-max_bias / 2 / n); heads below n take m0^(h + 1), the rest
+ * m1^(2 (h - n) + 1). 1 when max_bias is 0. */
+static float
+alibi_slope(int h, int H, float max_bias)
+{
+	if (max_bias <= 0.0f)
+		return 1.0f;
+	int n = 1;
+	while (n * 2 <= H)
+		n *= 2;
+	const float m0 = powf(2.0f, -max_bias / (float)n);
+	const float m1 = powf(2.0f, -(max_bias / 2.0f) / (float)n);
+	return h < n ? powf(m0, (float)(h + 1)) : powf(m1, (float)(2 * (h - n) + 1));
+}
+
+int
+orc_flash_attn(const float *q, int H, int T, int D, const uint16_t *k, const uint16_t *v,
+    int Hkv, int n_kv, int64_t k_rs, int64_t k_hs, int64_t v_rs, int64_t v_hs,
+    const uint16_t *mask, int mask_heads, int mask_rows, float scale, float max_bias,
+    float softcap, float *out, int n_threads)
+{
+	if (H <= 0 || Hkv <= 0 || H % Hkv || T < 0 || D <= 0 || n_kv < 0 ||
+	    (mask && (mask_heads <= 0 || H % mask_heads || mask_rows < T)) ||
+	    (!mask && max_bias > 0.0f))
+		return -1;
+	const int G = H / Hkv;
+	int bad = 0;
+
+#pragma omp parallel num_threads(nthreads(n_threads))
+	{
+		double *sc = malloc(sizeof(double) * (size_t)(n_kv + 1));
+		double *acc = malloc(sizeof(double) * (size_t)D);
+		if (!sc || !acc) {
+#pragma omp atomic write
+			bad = 1;
+		}
+#pragma omp for schedule(dynamic, 1) collapse(2)
+		for (int t = 0; t < T; t++) {
+			for (int h = 0; h < H; h++) {
+				if (!sc || !acc)
+					continue;
+				const int kh = h / G;
+				const float *qh = q + ((int64_t)h * T + t) * D;
+				const uint16_t *mr = mask ? mask + ((int64_t)(h % mask_heads) * mask_rows +
+				    t) * n_kv : NULL;
+				const float slope = alibi_slope(h, H, max_bias);
+				double mx = -INFINITY;
+				for (int j = 0; j < n_kv; j++) {
+					const float mv = mr ? orc_f16_to_f32(mr[j]) : 0.0f;
+					if (mv == -INFINITY) {
+						sc[j] = -INFINITY;
+						continue;
+					}
+					const uint16_t *kr = k + (int64_t)kh * k_hs + (int64_t)j * k_rs;
+					double a = 0;
+					for (int d = 0; d < D; d++)
+						a += (double)qh[d] * (double)orc_f16_to_f32(kr[d]);
+					a *= scale;
+					if (softcap > 0.0f)
+						a = (double)softcap * tanh(a / softcap);
+					sc[j] = a + (double)slope * mv;
+					if (sc[j] > mx)
+						mx = sc[j];
+				}
+				double sum = 0;
+				for (int j = 0; j < n_kv; j++) {
+					sc[j] = sc[j] == -INFINITY ? 0.0 : exp(sc[j] - mx);
+					sum += sc[j];
+				}
+				for (int d = 0; d < D; d++)
+					acc[d] = 0;
+				for (int j = 0; j < n_kv && sum > 0; j++) {
+					if (sc[j] == 0.0)
+						continue;
+					const uint16_t *vr = v + (int64_t)kh * v_hs + (int64_t)j * v_rs;
+					const double w = sc[j] / sum;
+					for (int d = 0; d < D; d++)
+						acc[d] += w * (double)orc_f16_to_f32(vr[d]);
+				}
+				float *o = out + ((int64_t)t * H + h) * D;
+				for (int d = 0; d < D; d++)
+					o[d] = (float)acc[d];
+			}
+		}
+		free(sc);
+		free(acc);
+	}
+	return bad ? -1 : 0;
+}
+
 int
 orc_moe_route(const float *logits, int64_t n, int n_expert, int n_used, int gating,
     int norm_topk, float scale, int32_t *ids, float *w)

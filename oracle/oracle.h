@@ -140,6 +140,21 @@ int orc_paged_attention_swa(const float *q, const uint16_t *kpool, const uint16_
     int H, int Hkv, int D, float scale, int window, const orc_batch *b, float *out,
     int n_threads);
 
+/* graph:flash_attn (src/lgml.c:2121-2170) with an explicit mask: the
+ * published algorithm of ggml_flash_attn_ext (ggml, the un-vendored
+ * subproject pinned at 0f1fa6109ad6f11d51dc0ab6f8e599258a393e1c). For
+ * query row t of head h and column j: s = scale * q.k_j; with softcap > 0
+ * s = softcap * tanh(s / softcap); then s += slope_h * mask[h % mask_heads]
+ * [t][j] (slope 1, or ALiBi's with max_bias > 0). A -inf mask drops the
+ * column; a row with every column dropped gives zeros. o = softmax(s) v.
+ * q (H, T, D) f32; k, v element (hk, j, d) at [hk * hs + j * rs + d] f16;
+ * mask (mask_heads, mask_rows >= T, n_kv) f16 or NULL; out (T, H, D).
+ * Head h reads kv head h / (H / Hkv). Scores and sums in f64. */
+int orc_flash_attn(const float *q, int H, int T, int D, const uint16_t *k, const uint16_t *v,
+    int Hkv, int n_kv, int64_t k_rs, int64_t k_hs, int64_t v_rs, int64_t v_hs,
+    const uint16_t *mask, int mask_heads, int mask_rows, float scale, float max_bias,
+    float softcap, float *out, int n_threads);
+
 /* ggml_set_rows (src/lgml.c:1937-1969): dst[ids[j]] = f16(src[j]). */
 int orc_set_rows_f16(uint16_t *dst, int64_t dst_rows, int64_t row, const float *src,
     const int64_t *ids, int64_t n);

@@ -253,3 +253,18 @@ def test_ring_plan_errors(hip):
         hip.ERANGE
     # no window
     assert plan_ring(hip, [1], [0], tab, 0, [0], 4, 2, 4)[0] == hip.EINVAL
+
+
+def test_flash_attn_checks_arguments(hip):
+    """Host-side argument checks of lgmlh_flash_attn (no GPU work)."""
+    L = hip.lib()
+    d = C.c_void_p(256)
+    # head size not a multiple of 8; max_bias without a mask
+    assert L.lgmlh_flash_attn(d, 4, 1, 20, d, d, 2, 8, 20, 160, 20, 160, None, 0, 0, 1.0, 0.0,
+                              0.0, d, None) == hip.EINVAL
+    assert L.lgmlh_flash_attn(d, 4, 1, 16, d, d, 2, 8, 16, 128, 16, 128, None, 0, 0, 1.0, 8.0,
+                              0.0, d, None) == hip.EINVAL
+    assert "max_bias" in hip.last_error()
+    # mask planes must divide the heads
+    assert L.lgmlh_flash_attn(d, 4, 1, 16, d, d, 2, 8, 16, 128, 16, 128, d, 3, 1, 1.0, 0.0,
+                              0.0, d, None) == hip.EINVAL
