@@ -76,6 +76,28 @@ int lgmlh_kv_gather(const void *pool, int which, int64_t n_cells, int n_head_kv,
 int lgmlh_kv_copy_block(void *kpool, void *vpool, int64_t n_cells, int n_head_kv, int head_dim,
     int32_t src, int32_t dst, int n, void *stream);
 
+/* Bytes of one 64-cell block of one layer's K (or V): 64 * Hkv * D * 2. A
+ * pool block's cells in all layers (M.block_bytes, transformer.lua:
+ * 1036-1042) are that times the number of pool tensors. */
+int64_t lgmlh_kv_block_bytes(int n_head_kv, int head_dim);
+
+/* M.copy_block_host (transformer.lua:1044-1060) in one launch: block
+ * `block` of every pool tensor pools[0..n_pools) (a DEVICE array of the
+ * tensors' addresses, e.g. K and V of each layer in order) to host memory
+ * (out = 1) or back (out = 0), tensor p at host + p * lgmlh_kv_block_bytes.
+ * host must be device-accessible (pinned: hipHostMalloc, or device memory)
+ * and 16-byte aligned. The spill / unspill of E:spill_block / E:unspill
+ * (engine.lua:1845-1868). */
+int lgmlh_kv_block_host(void *const *pools, int n_pools, int64_t n_cells, int n_head_kv,
+    int head_dim, int32_t block, void *host, int out, void *stream);
+
+/* pool_grow (transformer.lua:831-908) on the device: a pool of old_cells
+ * into a new tensor of new_cells (both multiples of 64), cell ids kept
+ * (the block layout makes the old pool a prefix of the new); the new
+ * cells start zeroed. No host round trip. */
+int lgmlh_kv_grow(const void *old_pool, int64_t old_cells, void *new_pool, int64_t new_cells,
+    int n_head_kv, int head_dim, void *stream);
+
 /* Plain ggml_set_rows on a row-major f16 tensor: dst[ids[j]] = f16(src[j])
  * (src/lgml.c:1937-1969). h_ids is the host copy for the range check. */
 int lgmlh_set_rows_f16(uint16_t *dst, int64_t dst_rows, int64_t row, const float *src,
@@ -97,6 +119,10 @@ int32_t lgmlh_kvpool_take(void *pool, int32_t min);
 /* P:evict (kvpool.lua:139-160): the cached block of the lowest priority,
  * least recently used, deepest; it loses its key. -1 when none. */
 int32_t lgmlh_kvpool_evict(void *pool);
+/* The block the next lgmlh_kvpool_evict takes (-1 if none) and its
+ * priority, nothing changed: the on_evict moment of kvpool.lua:149-152,
+ * when the owner copies a keyed block's cells out before it loses its key. */
+int32_t lgmlh_kvpool_victim(void *pool, int32_t *prio);
 /* P:ref / P:unref / P:refs_of (kvpool.lua:165-205). */
 int lgmlh_kvpool_ref(void *pool, int32_t b, int prio);
 int lgmlh_kvpool_unref(void *pool, int32_t b);

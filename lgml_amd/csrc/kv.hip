@@ -92,9 +92,74 @@ int kv_store_strided(void *kpool, void *vpool, int64_t n_cells, int Hkv, int D, 
   return hip_check(hipGetLastError(), "kv_store");
 }
 
+// One block of every pool tensor to (out) or from host memory: pools[p]
+// is a tensor of the block layout; block b's bytes (the same count in each
+// tensor, K or V) go to host + p * block_bytes. 16 bytes per thread.
+__global__ void kv_block_host_kernel(void *const *__restrict__ pools, int64_t block_bytes,
+                                     int32_t b, uint8_t *__restrict__ host, int out) {
+  const int p = blockIdx.y;
+  uint8_t *dev = (uint8_t *)pools[p] + (int64_t)b * block_bytes;
+  uint8_t *hst = host + (int64_t)p * block_bytes;
+  for (int64_t o = 16 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x); o < block_bytes;
+       o += 16 * (int64_t)gridDim.x * blockDim.x) {
+    if (out)
+      *(u32x4 *)(hst + o) = *(const u32x4 *)(dev + o);
+    else
+      *(u32x4 *)(dev + o) = *(const u32x4 *)(hst + o);
+  }
+}
+
+__global__ void zero_kernel(u32x4 *__restrict__ p, int64_t n16) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = u32x4{0, 0, 0, 0};
+}
+
 }  // namespace lgmlh
 
 using namespace lgmlh;
+
+extern "C" int64_t lgmlh_kv_block_bytes(int n_head_kv, int head_dim) {
+  if (n_head_kv <= 0 || head_dim <= 0) return -1;
+  return (int64_t)KV_BLOCK * n_head_kv * head_dim * 2;
+}
+
+extern "C" int lgmlh_kv_block_host(void *const *pools, int n_pools, int64_t n_cells,
+                                   int n_head_kv, int head_dim, int32_t block, void *host, int out,
+                                   void *stream) {
+  const int64_t bb = lgmlh_kv_block_bytes(n_head_kv, head_dim);
+  if (!pools || !host || n_pools <= 0 || n_pools > 65535 || bb <= 0 || bb % 16 ||
+      n_cells % KV_BLOCK || block < 0 || block >= n_cells / KV_BLOCK || ((uintptr_t)host & 15)) {
+    set_error("kv_block_host: bad arguments");
+    return LGMLH_EINVAL;
+  }
+  const int64_t chunks = bb / 16;
+  const unsigned gx = (unsigned)((chunks + 255) / 256 < 64 ? (chunks + 255) / 256 : 64);
+  hipLaunchKernelGGL(kv_block_host_kernel, dim3(gx, (unsigned)n_pools), dim3(256), 0,
+                     as_stream(stream), pools, bb, block, (uint8_t *)host, out);
+  return hip_check(hipGetLastError(), "kv_block_host");
+}
+
+extern "C" int lgmlh_kv_grow(const void *old_pool, int64_t old_cells, void *new_pool,
+                             int64_t new_cells, int n_head_kv, int head_dim, void *stream) {
+  const int64_t ob = lgmlh_kv_layer_bytes(old_cells, n_head_kv, head_dim);
+  const int64_t nb = lgmlh_kv_layer_bytes(new_cells, n_head_kv, head_dim);
+  if (!old_pool || !new_pool || ob <= 0 || nb < ob || old_pool == new_pool) {
+    set_error("kv_grow: bad arguments (cells %lld -> %lld)", (long long)old_cells,
+              (long long)new_cells);
+    return LGMLH_EINVAL;
+  }
+  hipStream_t st = as_stream(stream);
+  LGMLH_TRY(hip_check(hipMemcpyAsync(new_pool, old_pool, (size_t)ob, hipMemcpyDeviceToDevice, st),
+                      "kv_grow"));
+  const int64_t n16 = (nb - ob) / 16;  // the new cells start zeroed (a fill, not a memset)
+  if (n16 > 0) {
+    const unsigned g = (unsigned)((n16 + 255) / 256 < 4096 ? (n16 + 255) / 256 : 4096);
+    hipLaunchKernelGGL(zero_kernel, dim3(g), dim3(256), 0, st, (u32x4 *)((uint8_t *)new_pool + ob),
+                       n16);
+  }
+  return hip_check(hipGetLastError(), "kv_grow");
+}
 
 extern "C" int64_t lgmlh_kv_layer_bytes(int64_t n_cells, int n_head_kv, int head_dim) {
   if (n_cells <= 0 || n_cells % KV_BLOCK || n_head_kv <= 0 || head_dim <= 0) return -1;

@@ -187,9 +187,7 @@ extern "C" int32_t lgmlh_kvpool_take(void *pool, int32_t min) {
 // kvpool.lua:139-160. Lua's pairs() visits blocks in no fixed order; this
 // scan goes by block id, so an exact tie of (prio, used, depth) goes to the
 // lowest id.
-extern "C" int32_t lgmlh_kvpool_evict(void *pool) {
-  View v;
-  if (!view_of(pool, v)) return -1;
+static int32_t victim_of(const View &v) {
   int32_t best = -1;
   for (int32_t b = 0; b < v.h->cap; b++) {
     Block *k = v.blk(b);
@@ -203,6 +201,24 @@ extern "C" int32_t lgmlh_kvpool_evict(void *pool) {
         (k->prio == o->prio && (k->used < o->used || (k->used == o->used && k->depth > o->depth))))
       best = b;
   }
+  return best;
+}
+
+// The block the next evict takes and its priority, with nothing changed:
+// the moment of kvpool.lua:149-152, where the owner of the tensors copies a
+// keyed block's cells out (on_evict) before the block loses its key.
+extern "C" int32_t lgmlh_kvpool_victim(void *pool, int32_t *prio) {
+  View v;
+  if (!view_of(pool, v)) return -1;
+  const int32_t b = victim_of(v);
+  if (b >= 0 && prio) *prio = v.blk(b)->prio;
+  return b;
+}
+
+extern "C" int32_t lgmlh_kvpool_evict(void *pool) {
+  View v;
+  if (!view_of(pool, v)) return -1;
+  const int32_t best = victim_of(v);
   if (best < 0) return -1;
   unkey(v, best);
   v.h->cached--;

@@ -24,6 +24,12 @@ the picks one routing pass groups): decode tokens always go, prompt chunks
 are cut to what is left, and a request with no room waits for the next
 pass (E:flush itself is bounded by the memory budget, engine.lua:1477-1486).
 
+With ram > 0 (and prefix_cache), keyed blocks that the pool evicts spill
+to a RAM store (E:spill_block / E:unspill, engine.lua:1843-1868; the block
+entries of prompt_cache.lua's store, :132-222): one launch copies the
+block's cells in every layer to pinned host memory, and a later request
+whose prompt key misses the pool takes them back before it attaches.
+
 A model with sliding-window layers gives each slot a ring of its own in
 the ring pools (M:cache's per-slot rings, transformer.lua:575-600): slot
 i owns ring blocks i R .. i R + R - 1, R = ring_cells / 64 / n_slots, and
@@ -59,6 +65,18 @@ class PoolSeqs:
         self.model = model
         self.alloc = kvpool.Pool(model.pool_blocks, BLOCK)
         self.pressure = pressure
+        self.on_evict = None  # on_evict(block, key, prio), kvpool.lua:149-152
+
+    def evict(self):
+        """P:evict (kvpool.lua:139-160), telling on_evict about a keyed block
+        first, while its cells and key are still there."""
+        if self.on_evict is not None:
+            v = self.alloc.victim()
+            if v is not None:
+                k = self.alloc.key_of(v[0])
+                if k is not None and k != "part":
+                    self.on_evict(v[0], k, v[1])
+        return self.alloc.evict()
 
     def new_block(self, c, min_):
         """transformer.lua:934-958 (the pool is allocated whole up front, so
@@ -67,12 +85,12 @@ class PoolSeqs:
         b = self.alloc.take(min_)
         if b is not None:
             return b
-        b = self.alloc.evict()
+        b = self.evict()
         if b is None and self.pressure is not None:
             self.pressure(self, c)
             b = self.alloc.take(min_)
             if b is None:
-                b = self.alloc.evict()
+                b = self.evict()
         return b
 
     def reserve(self, c, n):
@@ -134,6 +152,74 @@ def seq_cells(c, frm, n):
     return [c.blocks[p // BLOCK] * BLOCK + p % BLOCK for p in range(frm, frm + n)]
 
 
+class RamEntry:
+    __slots__ = ("key", "parent", "depth", "tokens", "prio", "buf", "bytes", "used")
+
+    def __init__(self, **kw):
+        for k, v in kw.items():
+            setattr(self, k, v)
+
+
+class RamStore:
+    """The spilled-block part of the prompt cache's RAM store
+    (prompt_cache.lua:132-222): entries by key under a byte budget, room
+    made by dropping the entry of the lowest priority, then the least
+    recently spilled (`before`, :132-136). Buffers are pinned host memory
+    the device reads and writes directly."""
+
+    def __init__(self, ram_bytes, alloc=None):
+        """alloc(nbytes): the buffer of a spilled block (default: pinned
+        host memory)."""
+        self.ram = int(ram_bytes)
+        self.alloc = alloc or (lambda n: torch.empty(n, dtype=torch.uint8, pin_memory=True))
+        self.blocks = {}
+        self.bytes = 0
+        self.tick = 0
+        self.stats = {"spilled": 0, "unspilled": 0, "evicted": 0}
+
+    def evict(self):
+        """P:evict (:140-176) over the block entries."""
+        if not self.blocks:
+            return False
+        lru = min(self.blocks.values(), key=lambda e: (e.prio, e.used))
+        del self.blocks[lru.key]
+        self.bytes -= lru.bytes
+        self.stats["evicted"] += 1
+        return True
+
+    def room(self, nbytes):
+        """P:room (:178-190)."""
+        if nbytes > self.ram:
+            return False
+        while self.bytes + nbytes > self.ram:
+            if not self.evict():
+                return False
+        return True
+
+    def spill(self, key, parent, depth, tokens, prio, nbytes, fill):
+        """P:spill (:195-207): fill(buf) copies the cells into a new pinned
+        buffer of nbytes."""
+        if self.ram <= 0 or key in self.blocks or not self.room(nbytes):
+            return False
+        buf = self.alloc(nbytes)
+        fill(buf)
+        self.tick += 1
+        self.blocks[key] = RamEntry(key=key, parent=parent, depth=depth, tokens=list(tokens),
+                                    prio=prio, buf=buf, bytes=nbytes, used=self.tick)
+        self.bytes += nbytes
+        self.stats["spilled"] += 1
+        return True
+
+    def unspill(self, key):
+        """P:unspill (:212-221): the entry, out of the store, or None."""
+        e = self.blocks.pop(key, None)
+        if e is None:
+            return None
+        self.bytes -= e.bytes
+        self.stats["unspilled"] += 1
+        return e
+
+
 class Request:
     def __init__(self, prompt, max_new, prio=kvpool.NORMAL):
         self.prompt = list(prompt)
@@ -159,7 +245,7 @@ class Engine:
     """Slots over one pool; step() runs one batched pass (E:flush)."""
 
     def __init__(self, model, n_slots, ubatch=UBATCH, blocks_per_split=0, trace=None,
-                 prefix_cache=False, max_tokens=None):
+                 prefix_cache=False, max_tokens=None, ram=0):
         self.model = model
         nu = model.hp.get("n_used", 0) if model.hp.get("n_expert") else 0
         self.max_tokens = max_tokens or (8192 // nu if nu else None)
@@ -186,6 +272,12 @@ class Engine:
                 raise ValueError("rings of %d cells per slot; a pass of %d tokens needs %d" % (
                     self.ring_blocks * BLOCK, ubatch, need))
         self.free_slots = list(range(n_slots))
+        # the RAM tier of evicted prompt blocks (engine.lua:618-629)
+        self.ram = RamStore(ram) if ram > 0 and prefix_cache else None
+        self.infos = {}  # key -> (parent, depth, tokens) of the blocks published here
+        self.from_ram = 0
+        if self.ram is not None:
+            self.seqs.on_evict = self.spill_block
 
     def submit(self, req):
         if len(self.active) >= self.n_slots:
@@ -199,16 +291,52 @@ class Engine:
         return req
 
     # -- prefix sharing ------------------------------------------------------
+    # -- the RAM tier --------------------------------------------------------
+    def block_host(self, b, buf, out):
+        m = self.model
+        check(hip.lib().lgmlh_kv_block_host(m.pools_dev.data_ptr(), m.n_pools, m.n_cells,
+                                            m.hp["n_head_kv"], m.hp["head_dim"], b, buf.data_ptr(),
+                                            1 if out else 0, stream()))
+
+    def spill_block(self, b, key, prio):
+        """E:spill_block (engine.lua:1843-1850): copy the cells of a keyed
+        block that the pool evicts to the RAM store."""
+        info = self.infos.pop(key, None)
+        if info is None:
+            return
+        self.ram.spill(key, info[0], info[1], info[2], prio, self.model.block_bytes_all,
+                       lambda buf: self.block_host(b, buf, True))
+
+    def unspill(self, key, last, prio):
+        """E:unspill (engine.lua:1852-1868): a spilled block back in the pool
+        after block last, published again, with one reference; or None."""
+        e = self.ram.unspill(key) if self.ram is not None else None
+        if e is None:
+            return None
+        b = self.seqs.new_block(None, None if last is None else last + 1)
+        if b is not None:
+            self.block_host(b, e.buf, False)
+            # the buffer goes with the entry: the copy must be done first
+            torch.cuda.current_stream().synchronize()
+            self.seqs.alloc.publish(b, key, e.parent, e.depth, e.tokens, max(e.prio, prio))
+            self.infos[key] = (e.parent, e.depth, e.tokens)
+            self.from_ram += 1
+        return b
+
     def cached_blocks(self, prompt, max_, prio):
         """E:cached_blocks (engine.lua:1873-1892): the cached blocks holding the
-        first full blocks of prompt (at most max_ tokens), each referenced."""
+        first full blocks of prompt (at most max_ tokens), each referenced;
+        spilled blocks come back from the RAM store."""
         alloc, blocks, keys, parent = self.seqs.alloc, [], [], ROOT_KEY
         while (len(blocks) + 1) * BLOCK <= max_:
             k = kvpool.key(parent, prompt, len(blocks) * BLOCK + 1, BLOCK)
             b = alloc.lookup(k)
-            if b is None:
-                break
-            alloc.ref(b, prio)
+            if b is not None:
+                alloc.ref(b, prio)
+            else:
+                b = self.unspill(k, blocks[-1] if blocks else None, prio)
+                if b is None:
+                    break
             blocks.append(b)
             keys.append(k)
             parent = k
@@ -253,8 +381,9 @@ class Engine:
             parent = c.keys[i - 2] if i >= 2 else ROOT_KEY
             k = kvpool.key(parent, req.prompt, (i - 1) * BLOCK + 1, BLOCK)
             c.keys.append(k)
-            alloc.publish(c.blocks[i - 1], k, parent, i,
-                          req.prompt[(i - 1) * BLOCK:i * BLOCK], c.prio)
+            toks = req.prompt[(i - 1) * BLOCK:i * BLOCK]
+            if alloc.publish(c.blocks[i - 1], k, parent, i, toks, c.prio):
+                self.infos[k] = (parent, i, list(toks))
 
     def finish(self, req):
         self.seqs.free(req.seq)

@@ -19,6 +19,7 @@ EPI_NONE, EPI_ADD = 0, 1
 SYMBOLS = (
     "lgmlh_last_error", "lgmlh_abi_version", "lgmlh_row_size", "lgmlh_kv_layer_bytes",
     "lgmlh_kv_store", "lgmlh_kv_gather", "lgmlh_kv_copy_block", "lgmlh_set_rows_f16",
+    "lgmlh_kv_block_bytes", "lgmlh_kv_block_host", "lgmlh_kv_grow", "lgmlh_kvpool_victim",
     "lgmlh_plan", "lgmlh_plan_bind", "lgmlh_attention_workspace", "lgmlh_paged_attention",
     "lgmlh_flash_attn",
     "lgmlh_repacked_bytes", "lgmlh_repack", "lgmlh_dequantize", "lgmlh_mul_mat_workspace",
@@ -116,6 +117,9 @@ def _declare(L):
         "lgmlh_kv_store": ([vp, vp, i64, i32, i32, vp, vp, vp, vp, i64, vp], i32),
         "lgmlh_kv_gather": ([vp, i32, i64, i32, i32, vp, i64, vp, vp], i32),
         "lgmlh_kv_copy_block": ([vp, vp, i64, i32, i32, C.c_int32, C.c_int32, i32, vp], i32),
+        "lgmlh_kv_block_bytes": ([i32, i32], i64),
+        "lgmlh_kv_block_host": ([vp, i32, i64, i32, i32, C.c_int32, vp, i32, vp], i32),
+        "lgmlh_kv_grow": ([vp, i64, vp, i64, i32, i32, vp], i32),
         "lgmlh_set_rows_f16": ([vp, i64, i64, vp, vp, vp, i64, vp], i32),
         "lgmlh_plan": ([i32, vp, vp, vp, i32, i64, vp, i32, i32, i32, vp, sz,
                         C.POINTER(PlanInfo)], i32),
@@ -148,6 +152,7 @@ def _declare(L):
         "lgmlh_kvpool_init": ([vp, sz, C.c_int32, C.c_int32, C.c_int32], i32),
         "lgmlh_kvpool_take": ([vp, C.c_int32], C.c_int32),
         "lgmlh_kvpool_evict": ([vp], C.c_int32),
+        "lgmlh_kvpool_victim": ([vp, C.POINTER(C.c_int32)], C.c_int32),
         "lgmlh_kvpool_ref": ([vp, C.c_int32, i32], i32),
         "lgmlh_kvpool_unref": ([vp, C.c_int32], i32),
         "lgmlh_kvpool_refs_of": ([vp, C.c_int32], C.c_int32),

@@ -63,6 +63,13 @@ class Pool:
         b = hip.lib().lgmlh_kvpool_evict(self.mem)
         return None if b < 0 else b
 
+    def victim(self):
+        """(block, prio) that the next evict takes, or None; nothing changes
+        (the on_evict moment of kvpool.lua:149-152)."""
+        prio = C.c_int32(0)
+        b = hip.lib().lgmlh_kvpool_victim(self.mem, C.byref(prio))
+        return None if b < 0 else (b, prio.value)
+
     def ref(self, b, prio=None):
         hip.check(hip.lib().lgmlh_kvpool_ref(self.mem, b, NORMAL if prio is None else prio))
 

@@ -335,6 +335,16 @@ class DeviceModel:
         self.m = m
         self.ws = None
         self.ws_bytes = 0
+        # the pool tensors of the paged layers as a device array (K, V of
+        # each layer in order), for the one-launch block copies to host
+        # memory (lgmlh_kv_block_host)
+        ptrs = []
+        for il in range(hp["n_layer"]):
+            if not self.swa[il]:
+                ptrs += [self.kpools[il].data_ptr(), self.vpools[il].data_ptr()]
+        self.n_pools = len(ptrs)
+        self.pools_dev = torch.tensor(ptrs or [0], dtype=torch.int64, device=DEV)
+        self.block_bytes_all = self.n_pools * L.lgmlh_kv_block_bytes(Hkv, D)
 
     @property
     def pool_blocks(self):

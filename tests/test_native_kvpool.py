@@ -112,7 +112,11 @@ def test_native_pool_follows_the_oracle(nkp, seed):
             m = rng.randrange(n)
             assert nat.take(m) == o.take(m), step
         elif op == "evict":
-            assert nat.evict() == o.evict(), step
+            # victim names the block evict takes (the on_evict moment)
+            v = nat.victim()
+            got = nat.evict()
+            assert got == o.evict(), step
+            assert (v[0] if v else None) == got, step
         elif op == "ref" and (held or cached):
             b = rng.choice(held + cached)
             pr = rng.choice([nkp.LOW, nkp.NORMAL, nkp.HIGH])
