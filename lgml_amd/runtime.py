@@ -111,6 +111,14 @@ def generated_weights(hp, seed, policy):
     return get
 
 
+def load_gguf(path, n_cells, ring_cells=0):
+    """A DeviceModel from a gguf file (lgml_amd.gguf.load: llama, qwen3,
+    qwen3moe, gemma4 with one head size for every layer)."""
+    from . import gguf
+    hp, w = gguf.load(path)
+    return DeviceModel(hp, w, n_cells, ring_cells)
+
+
 class Plan:
     """A planned ubatch (lgmlh_plan), copied to the device. With ring_tab
     (n_seq, ring_blocks) and window, the plan of the sliding-window layers
@@ -242,6 +250,12 @@ class DeviceModel:
         for il in range(hp["n_layer"]):
             Ly = self.layers[il]
             g = layer_info(il)
+            if not gen:
+                lw = w["layers"][il]
+                if lw.get("head_dim", D) != D or lw.get("n_head_kv", Hkv) != Hkv:
+                    raise ValueError("layer %d: head size %s / %s KV heads; the device forward "
+                                     "takes one head size and KV head count for every layer"
+                                     % (il, lw.get("head_dim"), lw.get("n_head_kv")))
             Ly.attn_norm = vec("attn_norm", il, E)
             Ly.ffn_norm = vec("ffn_norm", il, E)
             for nm in ("q_norm", "k_norm"):

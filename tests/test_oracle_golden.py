@@ -16,8 +16,9 @@ from oracle import core, models
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "ref_logits.json")
 
 
-def run_rows(arch, block_tab=None, cap=64, block=64):
-    hp, w = models.ref_tiny(arch)
+def run_rows(arch, block_tab=None, cap=64, block=64, model=None):
+    """The golden passes of arch on the tiny model (or on model = (hp, w))."""
+    hp, w = model if model is not None else models.ref_tiny(arch)
     m = core.OracleModel(hp, w)
     d = json.load(open(GOLDEN))
     ref = d["rows"][arch]
@@ -68,11 +69,11 @@ def test_greedy_stream_follows_reference(oracle_lib):
 GOLDEN_G4 = os.path.join(os.path.dirname(__file__), "golden", "ref_gemma4.json")
 
 
-def run_gemma4_rows(block=64, ring_blocks=1):
+def run_gemma4_rows(block=64, ring_blocks=1, model=None):
     """The tiny gemma4 rows: the two prompt batches, then the greedy ids.
     Global layers use a paged pool; the sliding layer a ring of
     ring_blocks blocks of `block` cells (it must hold window - 1 + 20)."""
-    hp, w = models.ref_tiny_gemma4()
+    hp, w = model if model is not None else models.ref_tiny_gemma4()
     m = core.OracleModel(hp, w)
     d = json.load(open(GOLDEN_G4))
     ref = d["rows"]["dense"]
