@@ -76,6 +76,20 @@ def test_c2_shape_reduced_depth_ragged_decode(n_layer):
     assert same, (tg, to)
 
 
+def test_c2_full_depth_32_greedy_steps():
+    """The full C2 model (32 layers, Q4_K_M, vocab 128256) on two short
+    prompts, then 32 greedy steps batched over both: logits within 2e-3 of
+    the oracle and identical greedy streams (the north star's 32-step bar at
+    the metric's own shape; the CPU oracle takes about 2 minutes here)."""
+    hp, w = models.build("c2", seed=12, init="normal")
+    prompts = [lcg_ints(3000, 8, 0, hp["n_vocab"]), lcg_ints(3001, 13, 0, hp["n_vocab"])]
+    print("c2 full depth: 2 prompts, 32 greedy steps", flush=True)
+    errs, same, tg, to, *_ = run_both(hp, w, 256, prompts, 32)
+    print("c2 full depth: max rel err %.3g" % max(errs), flush=True)
+    assert max(errs) < 2e-3, errs
+    assert same, (tg, to)
+
+
 def test_batched_pass_equals_lone_pass():
     """test_batch.lua:40-81 / test_qwen_moe.lua:466-509: a sequence decoded in
     a batch gives the same logits as decoded alone (here bit for bit)."""
