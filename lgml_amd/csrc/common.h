@@ -93,6 +93,31 @@ struct Pending {
       v[4 + e] = b[e];
     }
   }
+  // The same at (n, m0 .. m0 + 3): the values of sum8's halves, for callers
+  // that spread a row over more lanes.
+  __device__ __forceinline__ void sum4(int64_t n, int64_t m0, float (&v)[4]) const {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    f4 a = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (wts) {
+      const float *p = part + (int64_t)n * splits * cols + m0;
+      const float *wp = wts + (int64_t)n * splits;
+      for (int z = 0; z < splits; z++, p += cols) a += *(const f4 *)p * wp[z];
+    } else {
+      const float *p = part + n * cols + m0;
+      const int64_t zs = rows * cols;
+      int z = 0;
+      for (; z + 4 <= splits; z += 4, p += 4 * zs) {
+        const f4 a0 = *(const f4 *)p, a1 = *(const f4 *)(p + zs);
+        const f4 a2 = *(const f4 *)(p + 2 * zs), a3 = *(const f4 *)(p + 3 * zs);
+        a += a0;
+        a += a1;
+        a += a2;
+        a += a3;
+      }
+      for (; z < splits; z++, p += zs) a += *(const f4 *)p;
+    }
+    for (int e = 0; e < 4; e++) v[e] = a[e];
+  }
 };
 
 // Cells per KV block; the pool layout and the attention tiles assume it.

@@ -45,7 +45,9 @@ __global__ void dequant_kernel(int type, const uint8_t *__restrict__ w, int64_t 
     out[m * K + k] = row_value(type, w + m * rb, k);
 }
 
-constexpr int RMS_THREADS = 256, RMS_PIECES = 4;  // rows of up to 8192 values
+// One workgroup per row, one 8-value piece per thread (rows of up to 8192
+// values): the many loads of a row's pending split sums go out at once.
+constexpr int RMS_THREADS = 1024, RMS_PIECES = 1;
 
 // ---- rms_norm * w ----------------------------------------------------------
 // Sum of squares in f64 (as the CPU reference's ggml_float), mean rounded
@@ -155,7 +157,6 @@ __global__ void rms_norm_kernel(float *__restrict__ x, const int32_t *__restrict
 
 // ---- q/k norm, rope and KV store -------------------------------------------
 constexpr int QKV_V_FROM_K = 1, QKV_V_NORM = 2;
-// One workgroup per token. The row [q | k | v] is staged in LDS.
 // rms_norm of one head by one wave: f64 sum of squares, mean rounded to
 // f32, scale = 1 / sqrtf(mean + eps), v = (v * scale) * w.
 __device__ void head_rms_norm(float *v, int D, float eps, const float *w) {
@@ -168,58 +169,32 @@ __device__ void head_rms_norm(float *v, int D, float eps, const float *w) {
   for (int i = lane; i < D; i += 64) v[i] = w ? (v[i] * scale) * w[i] : v[i] * scale;
 }
 
-__global__ void qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int Hkv, int D,
-                                      int n_rot, int neox, float theta_scale,
-                                      const float *__restrict__ ff,
-                                      const float *__restrict__ q_norm,
-                                      const float *__restrict__ k_norm, float eps,
-                                      const int32_t *__restrict__ pos,
-                                      uint16_t *__restrict__ kp, uint16_t *__restrict__ vp,
-                                      const int64_t *__restrict__ cells,
-                                      float *__restrict__ q_out, Pending pa, Pending pb,
-                                      int vmode) {
-  extern __shared__ float row[];
-  int64_t t = blockIdx.x;
-  int W = (H + 2 * Hkv) * D;
-  const float *src = qkv + t * W;
-  // Columns [0, pa.cols) may come from pending partials pa, the rest from
-  // pb; pieces of 8 columns (W, pa.cols and pb.cols are multiples of 8).
-  for (int pc = threadIdx.x; pc < W / 8; pc += blockDim.x) {
-    const int e = 8 * pc;
-    float v[8];
-    if (pa.splits && e < pa.cols)
-      pa.sum8(t, e, v);
-    else if (pb.splits && e >= W - pb.cols)
-      pb.sum8(t, e - (W - pb.cols), v);
-    else
-#pragma unroll
-      for (int i = 0; i < 8; i++) v[i] = src[e + i];
-#pragma unroll
-    for (int i = 0; i < 8; i++) row[e + i] = v[i];
-  }
-  __syncthreads();
-  if (vmode & QKV_V_FROM_K) {
-    // no V rows: V is the raw K (transformer.lua:1779)
-    for (int e = threadIdx.x; e < Hkv * D; e += blockDim.x) row[(H + Hkv) * D + e] = row[H * D + e];
-    __syncthreads();
-  }
-  if (q_norm || k_norm || (vmode & QKV_V_NORM)) {
-    // one wave per head: q_norm / k_norm, and on gemma the V norm without
-    // a weight (:1782-1784)
-    const int wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    for (int h = wv; h < H + 2 * Hkv; h += nw) {
-      const bool is_q = h < H, is_k = !is_q && h < H + Hkv;
-      if (is_q ? !q_norm : is_k ? !k_norm : !(vmode & QKV_V_NORM)) continue;  // wave-uniform
-      head_rms_norm(row + h * D, D, eps, is_q ? q_norm : is_k ? k_norm : nullptr);
-    }
-    __syncthreads();
-  }
+// One workgroup per (token, 8 heads) and one wave per head of [q | k | v]:
+// the head's values (with the pending split sums) go to LDS, then its norm
+// (q_norm / k_norm; on gemma the V norm without a weight, :1782-1784),
+// rope for q and k heads, and the store: q to q_out, k and v to their pool
+// cell. With QKV_V_FROM_K a V head is the raw K head (transformer.lua:1779).
+constexpr int QKV_HEADS = 8;
+__global__ void __launch_bounds__(64 * QKV_HEADS)
+qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int Hkv, int D, int n_rot, int neox,
+                      float theta_scale, const float *__restrict__ ff,
+                      const float *__restrict__ q_norm, const float *__restrict__ k_norm,
+                      float eps, const int32_t *__restrict__ pos, uint16_t *__restrict__ kp,
+                      uint16_t *__restrict__ vp, const int64_t *__restrict__ cells,
+                      float *__restrict__ q_out, Pending pa, Pending pb, int vmode) {
+  extern __shared__ float lds[];
+  const int64_t t = blockIdx.x;
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int NH = H + 2 * Hkv, W = NH * D;
+  const int h = blockIdx.y * QKV_HEADS + wv;  // this wave's head
+  const int half = n_rot / 2;
+  float *cs_ = lds, *sn_ = lds + half, *v = lds + n_rot + wv * D;
+  const bool has = h < NH;  // wave-uniform
+  const bool is_q = h < H, is_k = !is_q && h < H + Hkv, is_v = h >= H + Hkv;
   // One angle per rotated pair i, shared by every head: theta_0 = pos,
   // theta_{i+1} = theta_i * base^(-2/n_rot) (a running f32 product, as the
   // CPU reference's rope cache), divided by the frequency factor.
   const int p = pos[t];
-  const int half = n_rot / 2;
-  float *cs_ = row + W, *sn_ = cs_ + half;
   for (int i = threadIdx.x; i < half; i += blockDim.x) {
     float theta = (float)p;
     for (int j = 0; j < i; j++) theta *= theta_scale;
@@ -227,24 +202,54 @@ __global__ void qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int 
     cs_[i] = cosf(tt);
     sn_[i] = sinf(tt);
   }
-  __syncthreads();
-  for (int e = threadIdx.x; e < (H + Hkv) * half; e += blockDim.x) {
-    const int h = e / half, i = e % half;
-    const double cs = (double)cs_[i], sn = (double)sn_[i];
-    float *v = row + h * D;
-    const int a = neox ? i : 2 * i, b = neox ? i + half : 2 * i + 1;
-    const double x0 = v[a], x1 = v[b];
-    v[a] = (float)(x0 * cs - x1 * sn);
-    v[b] = (float)(x0 * sn + x1 * cs);
+  if (has) {
+    // Columns of the head: [0, pa.cols) may come from pending partials pa,
+    // the rest from pb; pieces of 4 (W, pa.cols, pb.cols multiples of 8).
+    const int sh = is_v && (vmode & QKV_V_FROM_K) ? h - Hkv : h;
+    const float *src = qkv + t * W;
+    for (int pc = lane; pc < D / 4; pc += 64) {
+      const int e = sh * D + 4 * pc;
+      float x[4];
+      if (pa.splits && e < pa.cols)
+        pa.sum4(t, e, x);
+      else if (pb.splits && e >= W - pb.cols)
+        pb.sum4(t, e - (W - pb.cols), x);
+      else
+#pragma unroll
+        for (int i = 0; i < 4; i++) x[i] = src[e + i];
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[4 * pc + i] = x[i];
+    }
   }
-  __syncthreads();
-  for (int e = threadIdx.x; e < H * D; e += blockDim.x) q_out[t * H * D + e] = row[e];
-  int64_t cell = cells[t];
-  int64_t b = cell / KV_BLOCK, o = cell % KV_BLOCK;
-  for (int e = threadIdx.x; e < Hkv * D; e += blockDim.x) {
-    int h = e / D, d = e % D;
-    kp[((b * Hkv + h) * KV_BLOCK + o) * D + d] = f2h(row[H * D + e]);
-    vp[((b * Hkv + h) * (int64_t)D + d) * KV_BLOCK + o] = f2h(row[(H + Hkv) * D + e]);
+  __syncthreads();  // the angles and each wave's head
+  if (!has) return;
+  if (is_q ? q_norm != nullptr : is_k ? k_norm != nullptr : (vmode & QKV_V_NORM) != 0) {
+    head_rms_norm(v, D, eps, is_q ? q_norm : is_k ? k_norm : nullptr);
+    __builtin_amdgcn_wave_barrier();
+  }
+  if (!is_v) {
+    for (int i = lane; i < half; i += 64) {
+      const double cs = (double)cs_[i], sn = (double)sn_[i];
+      const int a = neox ? i : 2 * i, b = neox ? i + half : 2 * i + 1;
+      const double x0 = v[a], x1 = v[b];
+      v[a] = (float)(x0 * cs - x1 * sn);
+      v[b] = (float)(x0 * sn + x1 * cs);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  if (is_q) {
+    for (int d = lane; d < D; d += 64) q_out[(t * H + h) * D + d] = v[d];
+    return;
+  }
+  const int64_t cell = cells[t];
+  const int64_t b = cell / KV_BLOCK, o = cell % KV_BLOCK;
+  if (is_k) {
+    const int hk = h - H;
+    for (int d = lane; d < D; d += 64) kp[((b * Hkv + hk) * KV_BLOCK + o) * D + d] = f2h(v[d]);
+  } else {
+    const int hv = h - H - Hkv;
+    for (int d = lane; d < D; d += 64)
+      vp[((b * Hkv + hv) * (int64_t)D + d) * KV_BLOCK + o] = f2h(v[d]);
   }
 }
 
@@ -492,7 +497,8 @@ int qkv_rope_store_dev(float *qkv, int64_t n, int n_head, int n_head_kv,
                                     const int64_t *cells, float *q_out, void *stream, Pending pa,
                        Pending pb, int vmode) {
   if (!qkv || !pos || !kpool || !vpool || !cells || !q_out || n < 0 || n_head <= 0 ||
-      n_head_kv <= 0 || head_dim <= 0 || head_dim % 8 || n_rot <= 0 || n_rot > head_dim ||
+      n_head_kv <= 0 || head_dim <= 0 || head_dim % 8 || head_dim > 1024 || n_rot <= 0 ||
+      n_rot > head_dim ||
       n_rot % 2 || n_cells % KV_BLOCK || pa.cols % 8 || pb.cols % 8) {
     set_error("qkv_rope_store: bad arguments");
     return LGMLH_EINVAL;
@@ -500,12 +506,10 @@ int qkv_rope_store_dev(float *qkv, int64_t n, int n_head, int n_head_kv,
   if (n == 0) return LGMLH_OK;
   // base^(-2/n_rot) rounded to f32 on the host, as the CPU reference does.
   float theta_scale = powf(freq_base, -2.0f / (float)n_rot);
-  size_t lds = ((size_t)(n_head + 2 * n_head_kv) * head_dim + n_rot) * sizeof(float);
-  if (lds > 160 * 1024) {
-    set_error("qkv_rope_store: row too wide");
-    return LGMLH_EINVAL;
-  }
-  hipLaunchKernelGGL(qkv_rope_store_kernel, dim3((unsigned)n), dim3(512), lds,
+  const size_t lds = ((size_t)QKV_HEADS * head_dim + n_rot) * sizeof(float);
+  const int groups = (n_head + 2 * n_head_kv + QKV_HEADS - 1) / QKV_HEADS;
+  hipLaunchKernelGGL(qkv_rope_store_kernel, dim3((unsigned)n, (unsigned)groups),
+                     dim3(64 * QKV_HEADS), lds,
                      as_stream(stream), qkv, n_head, n_head_kv, head_dim, n_rot, neox,
                      theta_scale, freq_factors, q_norm, k_norm, eps, pos, (uint16_t *)kpool,
                      (uint16_t *)vpool, cells, q_out, pa, pb, vmode);
