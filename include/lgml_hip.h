@@ -185,7 +185,9 @@ typedef struct {
 } lgmlh_ubatch;
 
 /* Plan a pass. G = n_head / n_head_kv; blocks_per_split bounds the KV
- * blocks one work item reads (0 = the default, 16). The work list depends
+ * blocks one work item reads (0 = the default, 16): a query group's blocks
+ * go into the fewest such runs, of lengths that differ by at most one. The
+ * work list depends
  * only on each sequence's own length, so a sequence is computed the same
  * way alone or in any batch. With buf NULL only info is
  * filled (sizes); otherwise buf must hold info->bytes. Errors:

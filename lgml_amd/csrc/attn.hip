@@ -83,22 +83,29 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
 
   // Q fragments (B operand): Q[row][ks*32 + quad*8 .. +7] as f16 hi + lo
   // (q = hi + lo to 22 bits; K is exact f16, so S^T is f32-accurate). Kept
-  // in LDS to leave registers for the next block's tiles.
+  // in LDS to leave registers for the next block's tiles. Every lane
+  // addresses a valid row (rows past the group read its last token and are
+  // zeroed), so all pieces load together.
   {
-    const float *qr = q + ((int64_t)(tok0 + rtok) * H + rhead) * D;
+    const int qt = rvalid ? rtok : ntok - 1;
+    const float *qr = q + ((int64_t)(tok0 + qt) * H + rhead) * D;
+    f32x4 qa[2 * KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
-      f16x8 h = f16x8{0, 0, 0, 0, 0, 0, 0, 0}, lo = h;
-      if (rvalid) {
-        const f32x4 *p4 = (const f32x4 *)(qr + ks * 32 + quad * 8);
-        f32x4 a = p4[0], b = p4[1];
+      qa[2 * ks] = *(const f32x4 *)(qr + ks * 32 + quad * 8);
+      qa[2 * ks + 1] = *(const f32x4 *)(qr + ks * 32 + quad * 8 + 4);
+    }
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          h[e] = (f16)a[e];
-          lo[e] = (f16)(a[e] - (float)h[e]);
-          h[4 + e] = (f16)b[e];
-          lo[4 + e] = (f16)(b[e] - (float)h[4 + e]);
-        }
+    for (int ks = 0; ks < KS; ks++) {
+      f16x8 h, lo;
+      const f32x4 a = rvalid ? qa[2 * ks] : f32x4{0, 0, 0, 0};
+      const f32x4 b = rvalid ? qa[2 * ks + 1] : f32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        h[e] = (f16)a[e];
+        lo[e] = (f16)(a[e] - (float)h[e]);
+        h[4 + e] = (f16)b[e];
+        lo[4 + e] = (f16)(b[e] - (float)h[4 + e]);
       }
       qsh[ks * 64 + lane] = h;
       qsl[ks * 64 + lane] = lo;

@@ -5,8 +5,8 @@
 // every token (seq_cells, :1126-1133), the block tables, the logit rows
 // off + n - 1 -- into one buffer for a single host-to-device copy, and adds
 // the work list of the paged attention kernel: for every sequence, groups
-// of 16 / G query tokens, each split into runs of at most blocks_per_split
-// KV blocks, plus one merge item per group with more than one split. A
+// of 16 / G query tokens, each split into the fewest runs of at most
+// blocks_per_split KV blocks (balanced lengths), plus one merge item per group with more than one split. A
 // ring plan (sliding-window layers) maps positions into each sequence's
 // ring of blocks and starts each group's runs at its window.
 #include <string.h>
@@ -82,13 +82,13 @@ static int plan_impl(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
       const int64_t pf = (int64_t)seq_npast[s] + g0, pl = (int64_t)seq_npast[s] + ge - 1;
       int b0 = ring ? (int)((pf - window + 1 > 0 ? pf - window + 1 : 0) / B) : 0;
       int nbg = (int)(pl / B + 1);
-      int ns = (nbg - b0 + bps - 1) / bps;
-      // ring plans: runs of equal length (a window is a fixed span)
-      int run = ring ? (nbg - b0 + ns - 1) / ns : bps;
+      // the fewest runs of at most bps blocks, of lengths that differ by at
+      // most one (the longest run bounds the kernel's time)
+      const int len = nbg - b0, ns = (len + bps - 1) / bps;
       int first = (int)(items.size() / 4);
       int mg = ns > 1 ? (int)(merge.size() / 4) + 1 : 0;
       for (int j = 0; j < ns; j++) {
-        int lo = b0 + j * run, hi = b0 + (j + 1) * run < nbg ? b0 + (j + 1) * run : nbg;
+        const int lo = b0 + (int)((int64_t)j * len / ns), hi = b0 + (int)((int64_t)(j + 1) * len / ns);
         items.push_back(s);
         items.push_back(off + g0);
         items.push_back((ge - g0) | (mg << 5));
