@@ -101,6 +101,52 @@ __device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
   return a > b || (a == b && ia < ib);
 }
 
+// Reductions over the 16 lanes of a lane group (one DPP row) by a butterfly
+// of row permutes: lane ^ 1, lane ^ 2 (quad permutes), then the mirrors
+// within 8 and within 16 lanes. Every lane ends with the same result.
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float row_max(float v) {
+  v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+  v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+  v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+  return fmaxf(v, dpp_f<DPP_MIRROR>(v));
+}
+// Partner sums: a + b at one lane, b + a at its partner (equal), so every
+// lane holds the same sum.
+__device__ __forceinline__ float row_sum(float v) {
+  v += dpp_f<DPP_XOR1>(v);
+  v += dpp_f<DPP_XOR2>(v);
+  v += dpp_f<DPP_HALF_MIRROR>(v);
+  return v + dpp_f<DPP_MIRROR>(v);
+}
+// The best (value, index) of the row. NaN values never win (better() is
+// false both ways), so the order is total over the candidates and every
+// pairing gives the same winner.
+template <int CTRL>
+__device__ __forceinline__ void best_step(float &bv, int &bi) {
+  const float ov = dpp_f<CTRL>(bv);
+  const int oi = dpp_i<CTRL>(bi);
+  if (better(ov, oi, bv, bi)) {
+    bv = ov;
+    bi = oi;
+  }
+}
+__device__ __forceinline__ void row_best(float &bv, int &bi) {
+  best_step<DPP_XOR1>(bv, bi);
+  best_step<DPP_XOR2>(bv, bi);
+  best_step<DPP_HALF_MIRROR>(bv, bi);
+  best_step<DPP_MIRROR>(bv, bi);
+}
+
 // Routing of token t by the 16 lanes sub = 0..15 of a lane group (lane
 // holds experts sub + 16 i, i < PER): logits l = sum of the nz partial
 // rows (in order); probs = soft_max (f32: max, exp, sum over the group in a
@@ -108,7 +154,7 @@ __device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
 // monotone) as ids, largest first, ties to the smaller index
 // (argsort_top_k); weights = probs of the ids, / max(sum, 6.103515625e-5)
 // when norm_topk (transformer.lua:2003-2005), times scale (:2006-2008).
-// Tokens t >= T run along (their lanes take part in the shuffles) and
+// Tokens t >= T run along (their lanes take part in the row permutes) and
 // write nothing.
 template <int PER>
 __device__ void route_token(const float *__restrict__ part, int nz, int64_t T, int64_t t, int NE,
@@ -116,18 +162,39 @@ __device__ void route_token(const float *__restrict__ part, int nz, int64_t T, i
                             int32_t *__restrict__ ids, float *__restrict__ wts,
                             int32_t *ids_lds) {
   const bool live = t < T;
+  const int64_t tt = live ? t : 0;
   float l[PER], p[PER];
 #pragma unroll
   for (int i = 0; i < PER; i++) l[i] = 0.0f;
-  // split sums in split order; the loads of a split are independent
-#pragma unroll 8
-  for (int z = 0; z < nz; z++) {
-    const float *pz = part + ((int64_t)z * T + (live ? t : 0)) * NE;
+  // Split sums in split order. Every lane loads an in-range address
+  // (experts past NE read expert 0 and are dropped below), ZB splits at a
+  // time, so the loads of a batch are in flight together.
+  constexpr int ZB = PER <= 8 ? 4 : PER <= 16 ? 2 : 1;
+  // (32-bit element offsets: the partials of a pass stay far below 2^30
+  // floats, and the loads then share one 64-bit base)
+  auto load = [&](int z, float (&v)[PER]) {
+    const uint32_t row = (uint32_t)(((int64_t)z * T + tt) * NE);
 #pragma unroll
     for (int i = 0; i < PER; i++) {
       const int e = sub + 16 * i;
-      if (e < NE) l[i] += pz[e];
+      v[i] = part[row + (uint32_t)(e < NE ? e : 0)];
     }
+  };
+  int z = 0;
+  for (; z + ZB <= nz; z += ZB) {
+    float v[ZB][PER];
+#pragma unroll
+    for (int zz = 0; zz < ZB; zz++) load(z + zz, v[zz]);
+#pragma unroll
+    for (int zz = 0; zz < ZB; zz++)
+#pragma unroll
+      for (int i = 0; i < PER; i++) l[i] += v[zz][i];
+  }
+  for (; z < nz; z++) {
+    float v[PER];
+    load(z, v);
+#pragma unroll
+    for (int i = 0; i < PER; i++) l[i] += v[i];
   }
   float mx = -INFINITY;
 #pragma unroll
@@ -135,7 +202,7 @@ __device__ void route_token(const float *__restrict__ part, int nz, int64_t T, i
     if (sub + 16 * i >= NE) l[i] = -INFINITY;
     mx = fmaxf(mx, l[i]);
   }
-  for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  mx = row_max(mx);
   if (gating == LGMLH_GATING_SOFTMAX) {
     float s = 0.0f;
 #pragma unroll
@@ -143,21 +210,19 @@ __device__ void route_token(const float *__restrict__ part, int nz, int64_t T, i
       p[i] = sub + 16 * i < NE ? expf(l[i] - mx) : 0.0f;
       s += p[i];
     }
-    for (int o = 1; o < 16; o <<= 1) s += __shfl_xor(s, o);
+    s = row_sum(s);
 #pragma unroll
     for (int i = 0; i < PER; i++) p[i] = p[i] / s;
   } else {
 #pragma unroll
     for (int i = 0; i < PER; i++) p[i] = 1.0f / (1.0f + expf(-l[i]));
   }
+  // Round j picks the j-th id; lane sub == j keeps it. Every lane adds the
+  // weights in pick order (the norm_topk sum).
   uint32_t taken = 0;
-  int sel[MOE_MAX_USED];
-  float w[MOE_MAX_USED];
-#pragma unroll
-  for (int j = 0; j < MOE_MAX_USED; j++) {
-    sel[j] = 0;
-    w[j] = 0.0f;
-    if (j >= n_used) continue;
+  int my_sel = 0;
+  float my_w = 0.0f, wsum = 0.0f;
+  for (int j = 0; j < n_used; j++) {
     float bv = -INFINITY;
     int bi = 0x7fffffff;
 #pragma unroll
@@ -168,14 +233,7 @@ __device__ void route_token(const float *__restrict__ part, int nz, int64_t T, i
         bi = e;
       }
     }
-    for (int o = 1; o < 16; o <<= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const int oi = __shfl_xor(bi, o);
-      if (better(ov, oi, bv, bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
+    row_best(bv, bi);
     // every lane of the group holds the winner now (none when the logits
     // are NaN: expert 0 then, so ids stay in range); its owner marks it
     // and sends its prob
@@ -188,29 +246,20 @@ __device__ void route_token(const float *__restrict__ part, int nz, int64_t T, i
         pw = p[i];
       }
     // from lane (bi % 16) of this group
-    w[j] = __shfl(pw, (int)(__lane_id() & ~15u) + (bi & 15));
-    sel[j] = bi;
-  }
-  if (norm_topk) {
-    float s = 0.0f;
-#pragma unroll
-    for (int j = 0; j < MOE_MAX_USED; j++)
-      if (j < n_used) s += w[j];
-    s = fmaxf(s, 6.103515625e-5f);
-#pragma unroll
-    for (int j = 0; j < MOE_MAX_USED; j++) w[j] = w[j] / s;
-  }
-  if (scale != 1.0f)
-#pragma unroll
-    for (int j = 0; j < MOE_MAX_USED; j++) w[j] = w[j] * scale;
-  if (!live) return;
-#pragma unroll
-  for (int j = 0; j < MOE_MAX_USED; j++)
-    if (j < n_used && sub == j) {
-      ids[t * n_used + j] = sel[j];
-      wts[t * n_used + j] = w[j];
-      if (ids_lds) ids_lds[t * n_used + j] = sel[j];
+    const float w = __shfl(pw, (int)(__lane_id() & ~15u) + (bi & 15));
+    wsum += w;
+    if (sub == j) {
+      my_sel = bi;
+      my_w = w;
     }
+  }
+  if (norm_topk) my_w = my_w / fmaxf(wsum, 6.103515625e-5f);
+  if (scale != 1.0f) my_w = my_w * scale;
+  if (live && sub < n_used) {
+    ids[t * n_used + sub] = my_sel;
+    wts[t * n_used + sub] = my_w;
+    if (ids_lds) ids_lds[t * n_used + sub] = my_sel;
+  }
 }
 
 // ---- grouping of the picks by expert ------------------------------------------
@@ -293,7 +342,7 @@ __device__ void group_picks(GroupLds &lds, int P, int NE, const GroupOut &go) {
     const int e = p < hi ? lds.ids[p] : -1;
     int rank = 0, tot = 0;
     for (int l2 = 0; l2 < 64; l2++) {
-      const int e2 = __shfl(e, l2);
+      const int e2 = __builtin_amdgcn_readlane(e, l2);  // lane l2's expert, to every lane
       const int same = e2 == e ? 1 : 0;
       tot += same;
       rank += l2 < lane ? same : 0;
