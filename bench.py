@@ -27,7 +27,10 @@ budget outlasts the run).
 
 value = decoded tokens / wall seconds of the K timed steps (inputs resident
 in HBM; the per-step host plan upload and the 64 sampled ids read back are
-inside; no instrumentation). roofline = the paged attention kernel (the
+inside; no instrumentation). The engine runs ahead by one pass (the next
+pass is planned and queued before the previous one's tokens are read back;
+decode tokens go from pass to pass on the device); --sync reads every pass
+back before the next. roofline = the paged attention kernel (the
 dominant kernel: ~80% of the step's bytes): its algorithmic bytes (K + V of
 every visible cell, q in, out) per launch over its duration, timed with HIP
 events on the pass's stream during min(K, 16) further steps, against
@@ -52,6 +55,8 @@ def parse():
     ap.add_argument("--bps", type=int, default=0, help="KV blocks per attention work item (0 = auto)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quiet", action="store_true")
+    ap.add_argument("--sync", action="store_true",
+                    help="read each pass's tokens back before launching the next (no run-ahead)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES, 8 times (the known-size kernel "
                          "that scales the FETCH_SIZE / WRITE_SIZE counters); prints nothing")
@@ -219,7 +224,7 @@ def main():
 
     trace = runtime.EventTrace(n_trace * hp["n_layer"] * 8 + 64,
                                hip.TRACE_ATTN | hip.TRACE_GEMM | hip.TRACE_EXPERTS)
-    eng = engine.Engine(model, S, blocks_per_split=args.bps)
+    eng = engine.Engine(model, S, blocks_per_split=args.bps, run_ahead=not args.sync)
 
     def new_request(prefilled):
         n = rng.int(plo, phi)
@@ -239,16 +244,28 @@ def main():
     contexts0 = [r.seq.n_past for r in eng.active]
     joins = [0]
 
-    def step(record):
-        eng.trace = trace if record else None
-        got = eng.step()
+    def top_up():
         while joins_on and len(eng.active) < S:
             new_request(False)
             joins[0] += 1
+
+    def step(record):
+        """One engine step; (requests that got a token, whether a pass was
+        read back: a run-ahead engine's first step after a drain reads none)."""
+        eng.trace = trace if record else None
+        done = eng.passes
+        got = eng.step()
+        top_up()
+        return got, eng.passes > done
+
+    def drain():
+        got = eng.drain()
+        top_up()
         return got
 
     for _ in range(args.warmup):
         step(False)
+    drain()
     torch.cuda.synchronize()
     trace.reset()
     decoded = prefill_tok = 0
@@ -257,12 +274,11 @@ def main():
     cellb = 2 * hp["n_head_kv"] * hp["head_dim"] * 2  # K+V bytes per cell and layer
     swa = list(model.swa)
 
-    def bytes_of_last_step():
-        """(attention bytes of each layer, step bytes) of the step just run:
-        K + V of every cell a query group sees (a sliding layer: at most the
-        window - 1 + the pass's tokens), q in and out; the step adds the
-        weights and the new cells' K + V."""
-        plan = eng.last_plan
+    def bytes_of(plan):
+        """(attention bytes of each layer, step bytes) of a pass: K + V of
+        every cell a query group sees (a sliding layer: at most the window
+        - 1 + the pass's tokens), q in and out; the step adds the weights and
+        the new cells' K + V."""
         seq_n = plan.seq_n.astype(np.int64)
         n_kv = plan.seq_npast.astype(np.int64) + seq_n
         N = int(seq_n.sum())
@@ -279,18 +295,28 @@ def main():
     joins[0] = 0
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        got = step(False)
+    # every pass launched in the timed region is read back in it (the
+    # run-ahead engine's last one by the drain)
+    for i in range(args.steps + 1):
+        if i < args.steps:
+            got, read = step(False)
+        else:
+            n0 = eng.passes
+            got = drain()
+            read = eng.passes > n0
+        if not read:
+            continue
         seq_n = eng.last_plan.seq_n
         decoded += len(got)
         prefill_tok += int(seq_n[seq_n > 1].sum())
-        step_bytes.append(bytes_of_last_step()[1])
+        step_bytes.append(bytes_of(eng.last_plan)[1])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     attn_bytes = []
     for _ in range(n_trace):
         step(True)
-        attn_bytes.append(bytes_of_last_step()[0])
+        attn_bytes.append(bytes_of(eng.launched_plan)[0])
+    drain()
     at = trace.times_ms(hip.TRACE_ATTN)
     gt = trace.times_ms(hip.TRACE_GEMM)
     xt = trace.times_ms(hip.TRACE_EXPERTS)
@@ -322,6 +348,7 @@ def main():
             "slots": S, "seed": args.seed, "decoded_tokens": decoded,
             "prefill_tokens": prefill_tok, "joins": joins[0],
             "mean_context": float(np.mean(contexts0)),
+            "engine": "sync" if args.sync else "run-ahead",
         },
         "roofline": {
             "bound": "hbm", "kernel": "paged_attn_kernel + merge_kernel (per layer)",

@@ -230,12 +230,23 @@ class Request:
         self.fed = 0       # prompt tokens run so far
         self.err = None
         self.done = False
+        # run-ahead engines: sampled tokens of passes not yet read back, the
+        # (pass, row) holding the latest one on the device, and whether the
+        # request takes part in no further pass
+        self.n_inflight = 0
+        self.tok_src = None
+        self.finishing = False
 
     def pending(self, ubatch):
         """The ids of this request's next pass: a prompt chunk or one token."""
         if self.fed < len(self.prompt):
             return self.prompt[self.fed:self.fed + ubatch]
         return [self.out[-1]]
+
+
+class _Pass:
+    """A pass in flight (run-ahead engines)."""
+    __slots__ = ("plan", "logits", "ids_dev", "ids_host", "event", "entries")
 
 
 ROOT_KEY = "lgml:"  # E:root_key (engine.lua:1823-1825) without adapters
@@ -245,8 +256,11 @@ class Engine:
     """Slots over one pool; step() runs one batched pass (E:flush)."""
 
     def __init__(self, model, n_slots, ubatch=UBATCH, blocks_per_split=0, trace=None,
-                 prefix_cache=False, max_tokens=None, ram=0):
+                 prefix_cache=False, max_tokens=None, ram=0, run_ahead=False):
         self.model = model
+        self.run_ahead = run_ahead
+        self._inflight = None
+        self.launched_plan = None
         nu = model.hp.get("n_used", 0) if model.hp.get("n_expert") else 0
         self.max_tokens = max_tokens or (8192 // nu if nu else None)
         self.seqs = PoolSeqs(model)
@@ -393,7 +407,142 @@ class Engine:
 
     def step(self):
         """One pass over every active request; returns the requests that got
-        a token. Requests whose budget is spent finish."""
+        a token. Requests whose budget is spent finish.
+
+        A run-ahead engine launches the next pass first and then reads back
+        the one launched by the previous call: it returns that pass's
+        requests (last_plan, last_entries and last_logits are that pass's),
+        and a decode token goes from one pass to the next on the device. The
+        passes' contents do not depend on the sampled values (budgets end
+        requests), so only the joining of new requests lags one pass; each
+        sequence's results are the same (they do not depend on the batch)."""
+        if not self.run_ahead:
+            return self._step_sync()
+        nxt = self._launch()
+        got = self._complete(self._inflight) if self._inflight is not None else []
+        self._inflight = nxt
+        return got
+
+    def drain(self):
+        """Read back the pass in flight (run-ahead engines); its requests."""
+        p, self._inflight = self._inflight, None
+        return self._complete(p) if p is not None else []
+
+    def _launch(self):
+        """Plan and queue one pass from the launched state (positions and
+        prompt progress advance at launch); None when nothing runs."""
+        entries = []
+        left = self.max_tokens if self.max_tokens else 1 << 62
+        n_dec = sum(1 for r in self.active if not r.finishing and r.fed >= len(r.prompt))
+        for r in list(self.active):
+            if r.finishing:
+                continue
+            src = None
+            if r.fed < len(r.prompt):
+                room = left - n_dec
+                if room <= 0:
+                    continue
+                ids = r.prompt[r.fed:r.fed + min(self.ubatch, room)]
+            else:
+                n_dec -= 1
+                if r.tok_src is not None:
+                    ids, src = [0], r.tok_src  # the token is still on the device
+                else:
+                    ids = [r.out[-1]]
+            left -= len(ids)
+            try:
+                self.seqs.reserve(r.seq, r.seq.n_past + len(ids))
+            except PoolFull as e:
+                r.err = str(e)
+                if r.n_inflight:
+                    r.finishing = True
+                else:
+                    self.finish(r)
+                continue
+            entries.append((r, ids, src))
+        if not entries:
+            return None
+        seq_n = [len(ids) for _, ids, _ in entries]
+        npast = [r.seq.n_past for r, _, _ in entries]
+        mb = max(len(r.seq.blocks) for r, _, _ in entries)
+        bt = np.full((len(entries), mb), -1, np.int32)
+        for i, (r, _, _) in enumerate(entries):
+            bt[i, :len(r.seq.blocks)] = r.seq.blocks
+        ids = np.concatenate([np.asarray(x, np.int32) for _, x, _ in entries])
+        ring_tab = None
+        if self.ring_blocks:
+            R = self.ring_blocks
+            ring_tab = np.array([np.arange(r.slot * R, (r.slot + 1) * R) for r, _, _ in entries],
+                                np.int32)
+        plan = self.model.plan(seq_n, npast, bt, ids, self.bps, ring_tab=ring_tab)
+        # decode tokens still on the device: copied into the plan's ids
+        # (and the ring plan's) from the previous pass's samples
+        off = np.cumsum([0] + seq_n[:-1])
+        dst = [int(off[i]) for i, (_, _, src) in enumerate(entries) if src is not None]
+        if dst:
+            srcs = [src for _, _, src in entries if src is not None]
+            prev = srcs[0][0]
+            assert all(p_ is prev for p_, _ in srcs), "device tokens come from one pass"
+            rows = np.array([row for _, row in srcs], np.int64)
+            di = torch.from_numpy(np.array(dst, np.int64)).pin_memory().to("cuda", non_blocking=True)
+            ri = torch.from_numpy(rows).pin_memory().to("cuda", non_blocking=True)
+            vals = prev.ids_dev.index_select(0, ri)
+            plan.dev_ids().index_copy_(0, di, vals)
+            if plan.ring is not None:
+                plan.ring.dev_ids().index_copy_(0, di, vals)
+        self.launched_plan = plan
+        logits = self.model.forward(plan, trace=self.trace)
+        n = len(entries)
+        p = _Pass()
+        p.plan, p.logits = plan, logits
+        p.ids_dev = torch.empty(n, dtype=torch.int32, device="cuda")
+        check(hip.lib().lgmlh_argmax(logits.data_ptr(), n, self.model.hp["n_vocab"],
+                                     p.ids_dev.data_ptr(), stream()))
+        p.ids_host = torch.empty(n, dtype=torch.int32, pin_memory=True)
+        p.ids_host.copy_(p.ids_dev, non_blocking=True)
+        p.event = torch.cuda.Event()
+        p.event.record()
+        p.entries = []
+        for row, (r, x, _) in enumerate(entries):
+            r.seq.n_past += len(x)
+            prompt = r.fed < len(r.prompt)
+            sampled = True
+            if prompt:
+                r.fed += len(x)
+                sampled = r.fed >= len(r.prompt)  # mid-prompt chunk: not sampled
+            if sampled:
+                r.n_inflight += 1
+                r.tok_src = (p, row)
+                if len(r.out) + r.n_inflight >= r.max_new:
+                    r.finishing = True
+            p.entries.append((r, len(x), prompt, sampled))
+        return p
+
+    def _complete(self, p):
+        """Read back a launched pass: its sampled tokens, prefix-cache keys of
+        its prompt chunks, and the requests that end with it."""
+        p.event.synchronize()
+        toks = p.ids_host.numpy()
+        self.last_plan, self.last_logits = p.plan, p.logits
+        self.last_entries = [r for r, _, _, _ in p.entries]
+        self.passes += 1
+        self.rows += len(p.entries)
+        self.tokens += sum(n for _, n, _, _ in p.entries)
+        got = []
+        for row, (r, _, prompt, sampled) in enumerate(p.entries):
+            if prompt and self.prefix_cache:
+                self.publish(r)
+            if sampled:
+                r.out.append(int(toks[row]))
+                r.n_inflight -= 1
+                if r.tok_src is not None and r.tok_src[0] is p:
+                    r.tok_src = None
+                got.append(r)
+            if r.finishing and r.n_inflight == 0 and not r.done:
+                self.finish(r)
+        return got
+
+    def _step_sync(self):
         entries = []
         left = self.max_tokens if self.max_tokens else 1 << 62
         n_dec = sum(1 for r in self.active if r.fed >= len(r.prompt))
@@ -430,7 +579,7 @@ class Engine:
             ring_tab = np.array([np.arange(r.slot * R, (r.slot + 1) * R) for r, _ in entries],
                                 np.int32)
         plan = self.model.plan(seq_n, npast, bt, ids, self.bps, ring_tab=ring_tab)
-        self.last_plan = plan
+        self.last_plan = self.launched_plan = plan
         self.last_entries = [r for r, _ in entries]
         logits = self.model.forward(plan, trace=self.trace)
         self.last_logits = logits

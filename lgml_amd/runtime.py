@@ -148,14 +148,23 @@ class Plan:
                     int(pool_blocks), int(window), ptr(self.ids), n_head, n_head_kv,
                     blocks_per_split)
         check(fn(*args, None, 0, C.byref(self.info)))
-        self.host = np.zeros(self.info.bytes, np.uint8)
+        # pinned host memory: the upload is an asynchronous copy on the
+        # stream, so the host does not wait for the work queued before it
+        self._pinned = torch.empty(self.info.bytes, dtype=torch.uint8, pin_memory=True)
+        self.host = self._pinned.numpy()
         check(fn(*args, ptr(self.host), self.host.nbytes, C.byref(self.info)))
-        self.dev = torch.from_numpy(self.host).to(DEV)
+        self.dev = self._pinned.to(DEV, non_blocking=True)
         self.ub = hip.Ubatch()
         check(L.lgmlh_plan_bind(C.byref(self.info), self.dev.data_ptr(), C.byref(self.ub)))
 
     def host_array(self, off, n, dtype):
         return self.host[off:off + n * np.dtype(dtype).itemsize].view(dtype)
+
+    def dev_ids(self):
+        """The pass's token ids on the device (int32), as the forward reads
+        them."""
+        n = self.info.n_tokens
+        return self.dev[self.info.off_ids:self.info.off_ids + 4 * n].view(torch.int32)
 
     @property
     def cells(self):
