@@ -24,6 +24,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "split.h"
 
 namespace lgmlh {
 
@@ -55,7 +56,7 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
                   const int32_t *__restrict__ items, const int32_t *__restrict__ seq_off,
                   const int32_t *__restrict__ seq_npast, const int32_t *__restrict__ block_tab,
                   int max_blocks, int ring, int window, float *__restrict__ out,
-                  float *__restrict__ part) {
+                  f16 *__restrict__ planes, int64_t npad, float *__restrict__ part) {
   constexpr int KS = D / 32;   // MFMA k-steps over D
   constexpr int DT = D / 16;   // d tiles of the output
   __shared__ __align__(16) uint16_t plh[ROWS * P_STRIDE];  // P as f16 hi
@@ -237,9 +238,30 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
     if (rvalid) {
       // o / l, as the merge divides: a token's output does not depend on
       // whether its group was split (the grouping follows chunk boundaries)
-      float *orow = out + ((int64_t)(tok0 + rtok) * H + rhead) * D;
+      const int64_t n = tok0 + rtok;
+      if (planes) {
+        // split planes of the output product's X: the lanes of a row hold
+        // 8 values of each 32-value group (d tiles 2g and 2g + 1)
+        const int64_t K = (int64_t)H * D, k0 = (int64_t)rhead * D;
 #pragma unroll
-      for (int dt = 0; dt < DT; dt++) *(f32x4 *)(orow + dt * 16 + quad * 4) = o[dt] / l;
+        for (int g = 0; g < DT / 2; g++) {
+          float s = 0.0f;
+#pragma unroll
+          for (int h2 = 0; h2 < 2; h2++) {
+            const f32x4 y = o[2 * g + h2] / l;
+            const float v[4] = {y[0], y[1], y[2], y[3]};
+            split_store4(planes, npad, K, n, k0 + (2 * g + h2) * 16 + quad * 4, v);
+            s += v[0] + v[1] + v[2] + v[3];
+          }
+          s += __shfl_xor(s, 16);
+          s += __shfl_xor(s, 32);
+          if (quad == 0) split_store_gsum(planes, npad, K, n, (k0 >> 5) + g, s);
+        }
+      } else {
+        float *orow = out + (n * H + rhead) * D;
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) *(f32x4 *)(orow + dt * 16 + quad * 4) = o[dt] / l;
+      }
     }
     return;
   }
@@ -264,7 +286,7 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
 template <int D>
 __global__ void __launch_bounds__(64)
 merge_kernel(const int32_t *__restrict__ merge, int H, int Hkv, const float *__restrict__ part,
-             float *__restrict__ out) {
+             float *__restrict__ out, f16 *__restrict__ planes, int64_t npad) {
   constexpr int WMAX = 64;  // splits whose weights are kept in LDS
   __shared__ float wsh[WMAX * ROWS], lsh[2 * ROWS];
   const int lane = threadIdx.x, mg = blockIdx.x, kvh = blockIdx.y;
@@ -305,7 +327,22 @@ merge_kernel(const int32_t *__restrict__ merge, int H, int Hkv, const float *__r
                                 : exp2f(p0[sp * pstride + ROWS * D + r] - lsh[ROWS + r]);
       acc += *(const f32x4 *)(p0 + sp * pstride + r * D + d0) * w;
     }
-    *(f32x4 *)(out + ((int64_t)(tok0 + r / G) * H + kvh * G + r % G) * D + d0) = acc / lsh[r];
+    const f32x4 y = acc / lsh[r];
+    const int64_t n = tok0 + r / G, k = (int64_t)(kvh * G + r % G) * D + d0;
+    if (planes) {
+      // 8 lanes hold a 32-value group (D / 4 is a multiple of 8, so groups
+      // of 8 lanes leave the loop together)
+      const int64_t K = (int64_t)H * D;
+      const float v[4] = {y[0], y[1], y[2], y[3]};
+      split_store4(planes, npad, K, n, k, v);
+      float s = v[0] + v[1] + v[2] + v[3];
+      s += __shfl_xor(s, 1);
+      s += __shfl_xor(s, 2);
+      s += __shfl_xor(s, 4);
+      if ((e4 & 7) == 0) split_store_gsum(planes, npad, K, n, k >> 5, s);
+    } else {
+      *(f32x4 *)(out + n * H * D + k) = y;
+    }
   }
 }
 
@@ -320,28 +357,32 @@ extern "C" size_t lgmlh_attention_workspace(const lgmlh_plan_info *info, int hea
 
 template <int D>
 static void launch_attn(const float *q, int H, int Hkv, float scale_log2, const void *kp,
-                        const void *vp, const lgmlh_ubatch *ub, float *out, float *part,
-                        hipStream_t st) {
+                        const void *vp, const lgmlh_ubatch *ub, float *out, f16 *planes,
+                        int64_t npad, float *part, hipStream_t st) {
   if (ub->ring > 0)
     hipLaunchKernelGGL((paged_attn_kernel<D, true>), dim3(ub->n_items, Hkv), dim3(64), 0, st, q,
                        H, Hkv, scale_log2, (const uint16_t *)kp, (const uint16_t *)vp, ub->items,
                        ub->seq_off, ub->seq_npast, ub->block_tab, ub->max_blocks, ub->ring,
-                       ub->window, out, part);
+                       ub->window, out, planes, npad, part);
   else
     hipLaunchKernelGGL((paged_attn_kernel<D, false>), dim3(ub->n_items, Hkv), dim3(64), 0, st, q,
                        H, Hkv, scale_log2, (const uint16_t *)kp, (const uint16_t *)vp, ub->items,
                        ub->seq_off, ub->seq_npast, ub->block_tab, ub->max_blocks, 0, 0, out,
-                       part);
+                       planes, npad, part);
   if (ub->n_merge > 0)
     hipLaunchKernelGGL(merge_kernel<D>, dim3(ub->n_merge, Hkv), dim3(64), 0, st, ub->merge, H,
-                       Hkv, part, out);
+                       Hkv, part, out, planes, npad);
 }
 
-extern "C" int lgmlh_paged_attention(const float *q, int n_head, int n_head_kv, int head_dim,
-                                     float scale, const void *kpool, const void *vpool,
-                                     const lgmlh_ubatch *ub, float *out, void *workspace,
-                                     size_t workspace_bytes, void *stream) {
-  if (!q || !kpool || !vpool || !ub || !out || n_head_kv <= 0 || n_head % n_head_kv) {
+namespace lgmlh {
+// The attention output as f32 rows (out) or, with planes set, as the split
+// planes (rows padded to npad) of the output product's X.
+int paged_attention_dev(const float *q, int n_head, int n_head_kv, int head_dim, float scale,
+                        const void *kpool, const void *vpool, const lgmlh_ubatch *ub, float *out,
+                        f16 *planes, int64_t npad, void *workspace, size_t workspace_bytes,
+                        hipStream_t st) {
+  if (!q || !kpool || !vpool || !ub || !(out || planes) || n_head_kv <= 0 ||
+      n_head % n_head_kv) {
     set_error("paged_attention: bad arguments");
     return LGMLH_EINVAL;
   }
@@ -357,14 +398,27 @@ extern "C" int lgmlh_paged_attention(const float *q, int n_head, int n_head_kv, 
   }
   if (ub->n_items == 0) return LGMLH_OK;
   float sl = scale * LOG2E;
-  hipStream_t st = as_stream(stream);
+  float *part = (float *)workspace;
   switch (head_dim) {
-    case 64: launch_attn<64>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, (float *)workspace, st); break;
-    case 128: launch_attn<128>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, (float *)workspace, st); break;
-    case 256: launch_attn<256>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, (float *)workspace, st); break;
+    case 64: launch_attn<64>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, planes, npad, part, st); break;
+    case 128: launch_attn<128>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, planes, npad, part, st); break;
+    case 256: launch_attn<256>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, planes, npad, part, st); break;
     default:
       set_error("paged_attention: head_dim %d not supported (64, 128, 256)", head_dim);
       return LGMLH_EINVAL;
   }
   return hip_check(hipGetLastError(), "paged_attention");
+}
+}  // namespace lgmlh
+
+extern "C" int lgmlh_paged_attention(const float *q, int n_head, int n_head_kv, int head_dim,
+                                     float scale, const void *kpool, const void *vpool,
+                                     const lgmlh_ubatch *ub, float *out, void *workspace,
+                                     size_t workspace_bytes, void *stream) {
+  if (!out) {
+    set_error("paged_attention: bad arguments");
+    return LGMLH_EINVAL;
+  }
+  return paged_attention_dev(q, n_head, n_head_kv, head_dim, scale, kpool, vpool, ub, out,
+                             nullptr, 0, workspace, workspace_bytes, as_stream(stream));
 }

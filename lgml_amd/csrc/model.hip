@@ -18,6 +18,10 @@ int mul_mat_split(int type, const void *w, int64_t M, int64_t K, const f16 *xs, 
 int mul_mat_f32(const float *w, int64_t M, int64_t K, const float *x, int64_t N, float *y,
                 int64_t ldy, const float *residual, hipStream_t st);
 int split_x(const void *x, int xtype, int64_t N, int64_t K, f16 *xs, hipStream_t st);
+int paged_attention_dev(const float *q, int n_head, int n_head_kv, int head_dim, float scale,
+                        const void *kpool, const void *vpool, const lgmlh_ubatch *ub, float *out,
+                        f16 *planes, int64_t npad, void *workspace, size_t workspace_bytes,
+                        hipStream_t st);
 int rms_norm_dev(float *x, const int32_t *rows, int64_t n_rows, int64_t n, float eps,
                  const float *w, float *out, f16 *planes, hipStream_t st, Pending pend,
                  bool writeback);
@@ -291,11 +295,14 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
                                  L.swa ? m->ring_cells : m->n_cells, lub->cells, q, st, p_qk, p_v,
                                  vmode));
     {
+      // a quantized output product takes its X as split planes, written by
+      // the attention (and merge) kernels themselves
       Span sp(trace, LGMLH_TRACE_ATTN, st);
-      LGMLH_TRY(lgmlh_paged_attention(q, (int)z.H, (int)z.Hkv, (int)z.D, scale, L.kpool,
-                                      L.vpool, lub, att, aws, z.attn_ws, st));
+      const bool oq = isq(L.wo_type);
+      LGMLH_TRY(paged_attention_dev(q, (int)z.H, (int)z.Hkv, (int)z.D, scale, L.kpool, L.vpool,
+                                    lub, oq ? nullptr : att, oq ? xs : nullptr, split_npad(z.N),
+                                    aws, z.attn_ws, st));
     }
-    if (isq(L.wo_type)) LGMLH_TRY(split_x(att, LGMLH_F32, z.N, z.H * z.D, xs, st));
     LGMLH_TRY(out_product(L.wo_type, L.wo, z.H * z.D, att, L.post_attn_norm, 0.0f, p_o));
     if (L.gate_inp) {
       // routed experts (transformer.lua:2054-2068, M.moe :1989-2027): x +=

@@ -49,4 +49,28 @@ __device__ __forceinline__ void split_store8(f16 *__restrict__ planes, int64_t N
   }
 }
 
+// Stores 4 values of row n at columns k0..k0+3 (k0 % 4 == 0), hi and lo;
+// the group sum goes separately (split_store_gsum).
+__device__ __forceinline__ void split_store4(f16 *__restrict__ planes, int64_t Npad, int64_t K,
+                                             int64_t n, int64_t k0, const float (&v)[4]) {
+  f16x4 h, l;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    h[e] = (f16)v[e];
+    l[e] = (f16)(v[e] - (float)h[e]);
+  }
+  f16 *hp = planes + n * K + k0;
+  *(f16x4 *)hp = h;
+  *(f16x4 *)(hp + Npad * K) = l;
+}
+
+// Stores the sum s of group g (columns 32 g .. 32 g + 31) of row n.
+__device__ __forceinline__ void split_store_gsum(f16 *__restrict__ planes, int64_t Npad,
+                                                 int64_t K, int64_t n, int64_t g, float s) {
+  f16 *gp = planes + 2 * Npad * K + n * (K / 32) + g;
+  const f16 sh = (f16)s;
+  gp[0] = sh;
+  gp[Npad * (K / 32)] = (f16)(s - (float)sh);
+}
+
 }  // namespace lgmlh
