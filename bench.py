@@ -57,6 +57,8 @@ def parse():
     ap.add_argument("--quiet", action="store_true")
     ap.add_argument("--sync", action="store_true",
                     help="read each pass's tokens back before launching the next (no run-ahead)")
+    ap.add_argument("--streams", type=int, default=0,
+                    help="1, or 2: a pass as two halves at once on two streams (0 = the workload's)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES, 8 times (the known-size kernel "
                          "that scales the FETCH_SIZE / WRITE_SIZE counters); prints nothing")
@@ -224,7 +226,9 @@ def main():
 
     trace = runtime.EventTrace(n_trace * hp["n_layer"] * 8 + 64,
                                hip.TRACE_ATTN | hip.TRACE_GEMM | hip.TRACE_EXPERTS)
-    eng = engine.Engine(model, S, blocks_per_split=args.bps, run_ahead=not args.sync)
+    n_streams = 1 if args.sync else (args.streams or wl.get("streams", 1))
+    eng = engine.Engine(model, S, blocks_per_split=args.bps, run_ahead=not args.sync,
+                        streams=n_streams)
 
     def new_request(prefilled):
         n = rng.int(plo, phi)
@@ -306,13 +310,18 @@ def main():
             read = eng.passes > n0
         if not read:
             continue
-        seq_n = eng.last_plan.seq_n
         decoded += len(got)
-        prefill_tok += int(seq_n[seq_n > 1].sum())
-        step_bytes.append(bytes_of(eng.last_plan)[1])
+        for pl in eng.last_plans:  # a pass split over two streams has two plans
+            seq_n = pl.seq_n
+            prefill_tok += int(seq_n[seq_n > 1].sum())
+        step_bytes.append(sum(bytes_of(pl)[1] for pl in eng.last_plans)
+                          - wbytes * (len(eng.last_plans) - 1))
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    # the traced steps run as one pass on one stream: the events time the
+    # attention kernels themselves, with nothing else running beside them
     attn_bytes = []
+    eng.n_streams = 1
     for _ in range(n_trace):
         step(True)
         attn_bytes.append(bytes_of(eng.launched_plan)[0])
@@ -348,7 +357,8 @@ def main():
             "slots": S, "seed": args.seed, "decoded_tokens": decoded,
             "prefill_tokens": prefill_tok, "joins": joins[0],
             "mean_context": float(np.mean(contexts0)),
-            "engine": "sync" if args.sync else "run-ahead",
+            "engine": "sync" if args.sync else "run-ahead, %d stream%s" % (
+                n_streams, "s" if n_streams > 1 else ""),
         },
         "roofline": {
             "bound": "hbm", "kernel": "paged_attn_kernel + merge_kernel (per layer)",

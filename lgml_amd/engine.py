@@ -244,9 +244,17 @@ class Request:
         return [self.out[-1]]
 
 
-class _Pass:
-    """A pass in flight (run-ahead engines)."""
+class _Half:
+    """The part of a pass in flight that runs on one stream (run-ahead
+    engines): its plan, logits, sampled ids (device, pinned host) and the
+    event after their copy."""
     __slots__ = ("plan", "logits", "ids_dev", "ids_host", "event", "entries")
+
+
+class _Pass:
+    """A pass in flight: its halves (one, or two on two streams) and its
+    entries (request, tokens, prompt chunk?, sampled?) in pass order."""
+    __slots__ = ("halves", "entries")
 
 
 ROOT_KEY = "lgml:"  # E:root_key (engine.lua:1823-1825) without adapters
@@ -256,11 +264,20 @@ class Engine:
     """Slots over one pool; step() runs one batched pass (E:flush)."""
 
     def __init__(self, model, n_slots, ubatch=UBATCH, blocks_per_split=0, trace=None,
-                 prefix_cache=False, max_tokens=None, ram=0, run_ahead=False):
+                 prefix_cache=False, max_tokens=None, ram=0, run_ahead=False, streams=1):
         self.model = model
         self.run_ahead = run_ahead
+        if streams not in (1, 2) or (streams == 2 and not run_ahead):
+            raise ValueError("streams: 1, or 2 with run_ahead")
+        # streams=2: a pass runs as two halves (alternate entries) at once,
+        # the second on a side stream of default priority
+        self.n_streams = streams
+        self._side = torch.cuda.Stream() if streams == 2 else None
         self._inflight = None
         self.launched_plan = None
+        self.launched_plans = []
+        self.last_plans = []
+        self._last_halves = None
         nu = model.hp.get("n_used", 0) if model.hp.get("n_expert") else 0
         self.max_tokens = max_tokens or (8192 // nu if nu else None)
         self.seqs = PoolSeqs(model)
@@ -462,6 +479,46 @@ class Engine:
             entries.append((r, ids, src))
         if not entries:
             return None
+        groups = [entries]
+        if self.n_streams == 2 and len(entries) >= 2:
+            groups = [entries[0::2], entries[1::2]]
+        main = torch.cuda.current_stream()
+        if len(groups) > 1:
+            # the side stream starts after all the work queued so far
+            ev = torch.cuda.Event()
+            ev.record(main)
+            self._side.wait_event(ev)
+        p = _Pass()
+        p.halves, p.entries = [], []
+        for gi, ents in enumerate(groups):
+            st = main if gi == 0 else self._side
+            with torch.cuda.stream(st):
+                p.halves.append(self._launch_half(ents, gi, main))
+        if len(groups) > 1:
+            # and the main stream goes on after both halves
+            ev = torch.cuda.Event()
+            ev.record(self._side)
+            main.wait_event(ev)
+        self.launched_plans = [h.plan for h in p.halves]
+        self.launched_plan = self.launched_plans[0]
+        for h in p.halves:
+            for row, (r, x, _) in enumerate(h.entries):
+                r.seq.n_past += len(x)
+                prompt = r.fed < len(r.prompt)
+                sampled = True
+                if prompt:
+                    r.fed += len(x)
+                    sampled = r.fed >= len(r.prompt)  # mid-prompt chunk: not sampled
+                if sampled:
+                    r.n_inflight += 1
+                    r.tok_src = (h, row)
+                    if len(r.out) + r.n_inflight >= r.max_new:
+                        r.finishing = True
+                p.entries.append((r, len(x), prompt, sampled, h, row))
+        return p
+
+    def _launch_half(self, entries, slot, main):
+        """Plan and queue the entries on the current stream."""
         seq_n = [len(ids) for _, ids, _ in entries]
         npast = [r.seq.n_past for r, _, _ in entries]
         mb = max(len(r.seq.blocks) for r, _, _ in entries)
@@ -478,69 +535,76 @@ class Engine:
         # decode tokens still on the device: copied into the plan's ids
         # (and the ring plan's) from the previous pass's samples
         off = np.cumsum([0] + seq_n[:-1])
-        dst = [int(off[i]) for i, (_, _, src) in enumerate(entries) if src is not None]
-        if dst:
-            srcs = [src for _, _, src in entries if src is not None]
-            prev = srcs[0][0]
-            assert all(p_ is prev for p_, _ in srcs), "device tokens come from one pass"
-            rows = np.array([row for _, row in srcs], np.int64)
+        by_src = {}
+        for i, (_, _, src) in enumerate(entries):
+            if src is not None:
+                by_src.setdefault(id(src[0]), (src[0], [], []))
+                by_src[id(src[0])][1].append(int(off[i]))
+                by_src[id(src[0])][2].append(src[1])
+        cur = torch.cuda.current_stream()
+        for h, dst, rows in by_src.values():
             di = torch.from_numpy(np.array(dst, np.int64)).pin_memory().to("cuda", non_blocking=True)
-            ri = torch.from_numpy(rows).pin_memory().to("cuda", non_blocking=True)
-            vals = prev.ids_dev.index_select(0, ri)
+            ri = torch.from_numpy(np.array(rows, np.int64)).pin_memory().to("cuda", non_blocking=True)
+            h.ids_dev.record_stream(cur)  # the source may come from the other stream
+            vals = h.ids_dev.index_select(0, ri)
             plan.dev_ids().index_copy_(0, di, vals)
             if plan.ring is not None:
                 plan.ring.dev_ids().index_copy_(0, di, vals)
-        self.launched_plan = plan
-        logits = self.model.forward(plan, trace=self.trace)
+        logits = self.model.forward(plan, trace=self.trace, slot=slot)
         n = len(entries)
-        p = _Pass()
-        p.plan, p.logits = plan, logits
-        p.ids_dev = torch.empty(n, dtype=torch.int32, device="cuda")
+        h = _Half()
+        h.plan, h.logits, h.entries = plan, logits, entries
+        h.ids_dev = torch.empty(n, dtype=torch.int32, device="cuda")
         check(hip.lib().lgmlh_argmax(logits.data_ptr(), n, self.model.hp["n_vocab"],
-                                     p.ids_dev.data_ptr(), stream()))
-        p.ids_host = torch.empty(n, dtype=torch.int32, pin_memory=True)
-        p.ids_host.copy_(p.ids_dev, non_blocking=True)
-        p.event = torch.cuda.Event()
-        p.event.record()
-        p.entries = []
-        for row, (r, x, _) in enumerate(entries):
-            r.seq.n_past += len(x)
-            prompt = r.fed < len(r.prompt)
-            sampled = True
-            if prompt:
-                r.fed += len(x)
-                sampled = r.fed >= len(r.prompt)  # mid-prompt chunk: not sampled
-            if sampled:
-                r.n_inflight += 1
-                r.tok_src = (p, row)
-                if len(r.out) + r.n_inflight >= r.max_new:
-                    r.finishing = True
-            p.entries.append((r, len(x), prompt, sampled))
-        return p
+                                     h.ids_dev.data_ptr(), stream()))
+        h.ids_host = torch.empty(n, dtype=torch.int32, pin_memory=True)
+        h.ids_host.copy_(h.ids_dev, non_blocking=True)
+        h.event = torch.cuda.Event()
+        h.event.record()
+        return h
 
     def _complete(self, p):
         """Read back a launched pass: its sampled tokens, prefix-cache keys of
         its prompt chunks, and the requests that end with it."""
-        p.event.synchronize()
-        toks = p.ids_host.numpy()
-        self.last_plan, self.last_logits = p.plan, p.logits
-        self.last_entries = [r for r, _, _, _ in p.entries]
+        toks = {}
+        for h in p.halves:
+            h.event.synchronize()
+            toks[id(h)] = h.ids_host.numpy()
+        self.last_plans = [h.plan for h in p.halves]
+        self.last_plan = self.last_plans[0]
+        self._last_halves = p.halves
+        self._last_logits = None
+        self.last_entries = [r for r, _, _, _, _, _ in p.entries]
         self.passes += 1
         self.rows += len(p.entries)
-        self.tokens += sum(n for _, n, _, _ in p.entries)
+        self.tokens += sum(n for _, n, _, _, _, _ in p.entries)
         got = []
-        for row, (r, _, prompt, sampled) in enumerate(p.entries):
+        for r, _, prompt, sampled, h, row in p.entries:
             if prompt and self.prefix_cache:
                 self.publish(r)
             if sampled:
-                r.out.append(int(toks[row]))
+                r.out.append(int(toks[id(h)][row]))
                 r.n_inflight -= 1
-                if r.tok_src is not None and r.tok_src[0] is p:
+                if r.tok_src is not None and r.tok_src[0] is h:
                     r.tok_src = None
                 got.append(r)
             if r.finishing and r.n_inflight == 0 and not r.done:
                 self.finish(r)
         return got
+
+    @property
+    def last_logits(self):
+        """Logits of the last pass read back, rows in last_entries order."""
+        if self._last_logits is None and self._last_halves:
+            hs = self._last_halves
+            self._last_logits = hs[0].logits if len(hs) == 1 else torch.cat(
+                [h.logits for h in hs])
+        return self._last_logits
+
+    @last_logits.setter
+    def last_logits(self, v):
+        self._last_logits = v
+        self._last_halves = None
 
     def _step_sync(self):
         entries = []
@@ -580,6 +644,7 @@ class Engine:
                                 np.int32)
         plan = self.model.plan(seq_n, npast, bt, ids, self.bps, ring_tab=ring_tab)
         self.last_plan = self.launched_plan = plan
+        self.last_plans = self.launched_plans = [plan]
         self.last_entries = [r for r, _ in entries]
         logits = self.model.forward(plan, trace=self.trace)
         self.last_logits = logits

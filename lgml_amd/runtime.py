@@ -358,6 +358,7 @@ class DeviceModel:
         self.m = m
         self.ws = None
         self.ws_bytes = 0
+        self._side_ws = {}  # workspaces of passes run concurrently on other streams
         # the pool tensors of the paged layers as a device array (K, V of
         # each layer in order), for the one-launch block copies to host
         # memory (lgmlh_kv_block_host)
@@ -389,31 +390,39 @@ class DeviceModel:
                           ring_tab=ring_tab, window=self.hp["n_swa"])
         return p
 
-    def workspace(self, plan, n_out):
+    def workspace(self, plan, n_out, slot=0):
+        """The forward's workspace; slot > 0: one of its own, for a pass that
+        runs at the same time as slot 0's on another stream."""
         need = hip.lib().lgmlh_forward_workspace(
             C.byref(self.m), C.byref(plan.info),
             C.byref(plan.ring.info) if plan.ring is not None else None, n_out)
+        if slot:
+            ws = self._side_ws.get(slot)
+            if ws is None or ws.numel() < need:
+                ws = self._side_ws[slot] = _empty(need)
+            return ws, ws.numel()
         if need > self.ws_bytes:
             self.ws = _empty(need)
             self.ws_bytes = need
-        return self.ws
+        return self.ws, self.ws_bytes
 
-    def forward(self, plan, out_rows=None, logits=None, trace=None):
+    def forward(self, plan, out_rows=None, logits=None, trace=None, slot=0):
         """Logits (n_out, vocab) f32 on the device for out_rows (ubatch token
-        indices; default the last token of each sequence). trace: an
-        EventTrace to time launch groups with HIP events."""
+        indices; default the last token of each sequence), on the current
+        stream. trace: an EventTrace to time launch groups with HIP events.
+        slot: the workspace (see workspace())."""
         if out_rows is None:
             n_out, rows = plan.info.n_seq, None
         else:
             rows = torch.as_tensor(np.ascontiguousarray(out_rows, np.int32)).to(DEV)
             n_out = rows.numel()
-        ws = self.workspace(plan, n_out)
+        ws, ws_bytes = self.workspace(plan, n_out, slot)
         if logits is None:
             logits = torch.empty((n_out, self.hp["n_vocab"]), dtype=torch.float32, device=DEV)
         check(hip.lib().lgmlh_forward(C.byref(self.m), C.byref(plan.ub),
                                       C.byref(plan.ring.ub) if plan.ring is not None else None,
                                       ptr(rows), n_out, logits.data_ptr(), ws.data_ptr(),
-                                      self.ws_bytes,
+                                      ws_bytes,
                                       C.byref(trace.c) if trace is not None else None, stream()))
         return logits
 

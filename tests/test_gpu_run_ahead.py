@@ -8,7 +8,9 @@ sequence's results do not depend on its batch), and end after exactly its
 budget. Covered: prompt chunks mixed into decode passes, budgets that end
 requests at different passes, slots taken by queued requests, prefix
 sharing (blocks published as their pass is read back), and a model with
-sliding-window rings (the ring plan's ids take the device tokens too).
+sliding-window rings (the ring plan's ids take the device tokens too); and
+the same with each pass run as two halves at once on two streams (a half's
+decode tokens may come from either half of the previous pass).
 """
 import numpy as np
 import pytest
@@ -21,12 +23,12 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 
-def serve(gm, prompts, budgets, n_slots, run_ahead, ubatch=64, prefix_cache=False):
+def serve(gm, prompts, budgets, n_slots, run_ahead, ubatch=64, prefix_cache=False, streams=1):
     """All requests through one engine, queued ones joining as slots free;
     per request its (token, logits) samples in order."""
     from lgml_amd import engine
     eng = engine.Engine(gm, n_slots, ubatch=ubatch, prefix_cache=prefix_cache,
-                        run_ahead=run_ahead)
+                        run_ahead=run_ahead, streams=streams)
     reqs = [engine.Request(p, b) for p, b in zip(prompts, budgets)]
     queue = list(reqs)
     got = {id(r): [] for r in reqs}
@@ -77,6 +79,10 @@ def test_run_ahead_equals_sync_with_joins_and_prefix_sharing():
         b = serve(runtime.DeviceModel(hp, w, 64 * 64), prompts, budgets, 3, True,
                   prefix_cache=pc)
         same(a, b)
+        print("run-ahead on two streams vs sync, prefix_cache=%s" % pc, flush=True)
+        c = serve(runtime.DeviceModel(hp, w, 64 * 64), prompts, budgets, 3, True,
+                  prefix_cache=pc, streams=2)
+        same(a, c)
 
 
 def test_run_ahead_equals_sync_with_rings():
@@ -93,3 +99,7 @@ def test_run_ahead_equals_sync_with_rings():
     b = serve(runtime.DeviceModel(hp, w, 2048, ring_cells=2 * R * 64), prompts, budgets, 2,
               True)
     same(a, b)
+    print("run-ahead on two streams vs sync, rings", flush=True)
+    c = serve(runtime.DeviceModel(hp, w, 2048, ring_cells=2 * R * 64), prompts, budgets, 2,
+              True, streams=2)
+    same(a, c)
