@@ -170,6 +170,33 @@ struct Span {
     if (slot >= 0) (void)hipEventRecord((hipEvent_t)t->events[2 * slot + 1], st);
   }
 };
+
+// A side stream (default priority) and two events per host thread and
+// device, for a product that runs beside another product of the same pass;
+// null when any of them cannot be made (the caller stays on its stream).
+struct Side {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+  bool failed = false;
+};
+Side *side_of() {
+  constexpr int MAX_DEV = 16;
+  static thread_local Side sides[MAX_DEV];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return nullptr;
+  Side &sd = sides[dev];
+  if (sd.failed) return nullptr;
+  if (!sd.s) {
+    if (hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&sd.join, hipEventDisableTiming) != hipSuccess) {
+      (void)hipGetLastError();
+      sd.failed = true;
+      return nullptr;
+    }
+  }
+  return &sd;
+}
 }  // namespace
 
 extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
@@ -238,16 +265,21 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
   // (quantized weights); the producer wrote the form(s) the weights take.
   // A quantized product split over K leaves its partial sums pending (pd):
   // the next kernel that reads y adds them in order, then the residual.
+  auto gemm_on = [&](hipStream_t s, int type, const void *w, int64_t M, int64_t K,
+                     const float *xf, int64_t N, float *y, int64_t ldy, const float *res,
+                     float *part, size_t part_bytes, Pending &pd) -> int {
+    Span sp(trace, LGMLH_TRACE_GEMM, s);
+    pd = Pending{};
+    if (type == LGMLH_F32) return mul_mat_f32((const float *)w, M, K, xf, N, y, ldy, res, s);
+    int splits = 0;
+    int rc = mul_mat_split(type, w, M, K, xs, N, y, ldy, res, part, part_bytes, s, &splits);
+    if (rc == LGMLH_OK && splits > 1) pd = Pending{part, splits, N, M};
+    return rc;
+  };
   auto gemm = [&](int type, const void *w, int64_t M, int64_t K, const float *xf, int64_t N,
                   float *y, int64_t ldy, const float *res, float *part, size_t part_bytes,
                   Pending &pd) -> int {
-    Span sp(trace, LGMLH_TRACE_GEMM, st);
-    pd = Pending{};
-    if (type == LGMLH_F32) return mul_mat_f32((const float *)w, M, K, xf, N, y, ldy, res, st);
-    int splits = 0;
-    int rc = mul_mat_split(type, w, M, K, xs, N, y, ldy, res, part, part_bytes, st, &splits);
-    if (rc == LGMLH_OK && splits > 1) pd = Pending{part, splits, N, M};
-    return rc;
+    return gemm_on(st, type, w, M, K, xf, N, y, ldy, res, part, part_bytes, pd);
   };
   auto isq = [](int type) { return type != LGMLH_F32; };
   // A product whose output goes to the residual stream x: added into x by
@@ -278,12 +310,26 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
     // x += the previous layer's down product, then attn_norm
     LGMLH_TRY(rms_norm_dev(x, nullptr, z.N, z.E, m->eps, L.attn_norm, qin_f ? xn : nullptr,
                            qin_q ? xs : nullptr, st, p_down, true));
+    // A V matrix of its own type (a more_bits layer's Q6_K) is a small
+    // product that leaves most CUs idle: it runs on a side stream beside
+    // the q|k product (not while tracing, whose events time one stream).
+    p_v = Pending{};
+    Side *sd = v_sep && !trace ? side_of() : nullptr;
+    if (sd) {
+      LGMLH_TRY(hip_check(hipEventRecord(sd->fork, st), "forward: fork"));
+      LGMLH_TRY(hip_check(hipStreamWaitEvent(sd->s, sd->fork, 0), "forward: fork"));
+      LGMLH_TRY(gemm_on(sd->s, L.wv_type, L.wv, z.W - L.wqkv_rows, z.E, xn, z.N,
+                        qkv + L.wqkv_rows, z.W, nullptr, gws_v, z.gemm_ws_v, p_v));
+      LGMLH_TRY(hip_check(hipEventRecord(sd->join, sd->s), "forward: join"));
+    }
     LGMLH_TRY(gemm(L.wqkv_type, L.wqkv, L.wqkv_rows, z.E, xn, z.N, qkv, z.W, nullptr, gws,
                    z.gemm_ws, p_qk));
-    p_v = Pending{};
-    if (v_sep)
+    if (sd) {
+      LGMLH_TRY(hip_check(hipStreamWaitEvent(st, sd->join, 0), "forward: join"));
+    } else if (v_sep) {
       LGMLH_TRY(gemm(L.wv_type, L.wv, z.W - L.wqkv_rows, z.E, xn, z.N, qkv + L.wqkv_rows, z.W,
                      nullptr, gws_v, z.gemm_ws_v, p_v));
+    }
     // a sliding layer keeps its K / V in the sequences' rings (rows_swa,
     // transformer.lua:2469-2476) and attends through the ring plan
     const lgmlh_ubatch *lub = L.swa ? ub_ring : ub;
