@@ -376,8 +376,13 @@ class DeviceModel:
 
     def plan(self, seq_n, seq_npast, block_tab, ids, blocks_per_split=0, ring_tab=None):
         """The pass's plan; with sliding layers also its ring plan (.ring)
-        over ring_tab (n_seq, ring blocks), the sequences' rings."""
+        over ring_tab (n_seq, ring blocks), the sequences' rings.
+        blocks_per_split 0: 32 KV blocks per attention work item for heads
+        of 256 (their kernel holds one wave per SIMD: fewer, longer items
+        stay within one round of waves), the plan's default (16) else."""
         ids = np.ascontiguousarray(ids, np.int32)
+        if not blocks_per_split and self.hp["head_dim"] >= 256:
+            blocks_per_split = 32
         if len(ids) and (ids.min() < 0 or ids.max() >= self.hp["n_vocab"]):
             raise ValueError("token id out of range [0, %d)" % self.hp["n_vocab"])
         p = Plan(seq_n, seq_npast, block_tab, ids, self.hp["n_head"], self.hp["n_head_kv"],
