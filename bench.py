@@ -53,6 +53,8 @@ def parse():
     ap.add_argument("--slots", type=int, default=0, help="slots (0 = the workload's)")
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2")
     ap.add_argument("--bps", type=int, default=0, help="KV blocks per attention work item (0 = auto)")
+    ap.add_argument("--ring-bps", type=int, default=0,
+                    help="KV blocks per work item through the sliding-window rings (0 = auto)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quiet", action="store_true")
     ap.add_argument("--sync", action="store_true",
@@ -214,6 +216,7 @@ def main():
     t0 = time.time()
     model = runtime.DeviceModel(hp, runtime.generated_weights(hp, args.seed, ty), n_cells,
                                 ring_cells=ring_cells)
+    model.ring_blocks_per_split = args.ring_bps
     torch.cuda.synchronize()
     log(args, "model ready in %.1f s; pool %d cells (%.1f GB KV)" % (
         time.time() - t0, n_cells, n_cells * 2 * 2 * hp["n_head_kv"] * hp["head_dim"] *

@@ -374,13 +374,18 @@ class DeviceModel:
     def pool_blocks(self):
         return self.n_cells // 64
 
+    ring_blocks_per_split = 0  # the ring plans' run length (0: as blocks_per_split)
+
     def plan(self, seq_n, seq_npast, block_tab, ids, blocks_per_split=0, ring_tab=None):
         """The pass's plan; with sliding layers also its ring plan (.ring)
         over ring_tab (n_seq, ring blocks), the sequences' rings.
-        blocks_per_split 0: 32 KV blocks per attention work item for heads
-        of 256 (their kernel holds one wave per SIMD: fewer, longer items
-        stay within one round of waves), the plan's default (16) else."""
+        blocks_per_split 0: for heads of 256 (their kernel holds one wave per
+        SIMD), runs of 32 KV blocks over the paged pool (fewer, longer items
+        stay within one round of waves) and the plan's default, 16, through
+        the rings (a window's few blocks over more waves); 16 for both
+        else."""
         ids = np.ascontiguousarray(ids, np.int32)
+        ring_bps = self.ring_blocks_per_split or blocks_per_split
         if not blocks_per_split and self.hp["head_dim"] >= 256:
             blocks_per_split = 32
         if len(ids) and (ids.min() < 0 or ids.max() >= self.hp["n_vocab"]):
@@ -391,7 +396,7 @@ class DeviceModel:
             if ring_tab is None:
                 raise ValueError("the model has sliding-window layers: pass ring_tab")
             p.ring = Plan(seq_n, seq_npast, ring_tab, ids, self.hp["n_head"],
-                          self.hp["n_head_kv"], self.ring_cells // 64, blocks_per_split,
+                          self.hp["n_head_kv"], self.ring_cells // 64, ring_bps,
                           ring_tab=ring_tab, window=self.hp["n_swa"])
         return p
 
