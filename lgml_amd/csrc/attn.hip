@@ -282,7 +282,7 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
 // item, splits, first token, tokens), one wave per (group, KV head). Lane
 // r < rows finds its row's max M, the split weights w = exp2(m - M) and
 // L = sum l w; then every lane adds the split outputs of 4 columns at a
-// time, weighted, in split order.
+// time (up to 4 such positions per round), weighted, in split order.
 template <int D>
 __global__ void __launch_bounds__(64)
 merge_kernel(const int32_t *__restrict__ merge, int H, int Hkv, const float *__restrict__ part,
@@ -295,53 +295,90 @@ merge_kernel(const int32_t *__restrict__ merge, int H, int Hkv, const float *__r
   const int G = H / Hkv, nrows = ntok * G;
   const float *p0 = part + ((int64_t)first * Hkv + kvh) * Partial<D>::floats;
   const int64_t pstride = (int64_t)Hkv * Partial<D>::floats;  // from one split to the next
+  // Loads go out in rounds: the m and l of 8 splits, then 4 splits of 4
+  // output positions per lane (addresses clamped into range; the values
+  // past the last split are dropped), so a merge takes a few round trips.
   if (lane < nrows) {
+    const float *ml = p0 + ROWS * D + lane;
     float M = -INFINITY;
-    for (int sp = 0; sp < ns; sp++) M = fmaxf(M, p0[sp * pstride + ROWS * D + lane]);
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+      float mv[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) mv[i] = ml[(int64_t)min(s0 + i, ns - 1) * pstride];
+#pragma unroll
+      for (int i = 0; i < 8; i++) M = fmaxf(M, mv[i]);  // repeats of the last split: same max
+    }
     float L = 0.0f;
-    for (int sp = 0; sp < ns; sp++) {
-      const float w = exp2f(p0[sp * pstride + ROWS * D + lane] - M);  // 0 for a split that saw no cell
-      L += p0[sp * pstride + ROWS * D + ROWS + lane] * w;
-      if (sp < WMAX) wsh[sp * ROWS + lane] = w;
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+      float mv[8], lv[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const int64_t o = (int64_t)min(s0 + i, ns - 1) * pstride;
+        mv[i] = ml[o];
+        lv[i] = ml[o + ROWS];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+        if (s0 + i < ns) {
+          const float w = exp2f(mv[i] - M);  // 0 for a split that saw no cell
+          L += lv[i] * w;
+          if (s0 + i < WMAX) wsh[(s0 + i) * ROWS + lane] = w;
+        }
     }
     lsh[lane] = L;
     lsh[ROWS + lane] = M;
   }
   __syncthreads();
-  for (int e4 = lane; e4 < nrows * (D / 4); e4 += 64) {
-    const int r = e4 / (D / 4), d0 = 4 * (e4 % (D / 4));
-    f32x4 acc = f32x4{0, 0, 0, 0};
-    int sp = 0;
-    for (; sp + 4 <= ns && sp + 4 <= WMAX; sp += 4) {
-      const f32x4 a0 = *(const f32x4 *)(p0 + sp * pstride + r * D + d0);
-      const f32x4 a1 = *(const f32x4 *)(p0 + (sp + 1) * pstride + r * D + d0);
-      const f32x4 a2 = *(const f32x4 *)(p0 + (sp + 2) * pstride + r * D + d0);
-      const f32x4 a3 = *(const f32x4 *)(p0 + (sp + 3) * pstride + r * D + d0);
-      acc += a0 * wsh[sp * ROWS + r];
-      acc += a1 * wsh[(sp + 1) * ROWS + r];
-      acc += a2 * wsh[(sp + 2) * ROWS + r];
-      acc += a3 * wsh[(sp + 3) * ROWS + r];
+  const int n4 = nrows * (D / 4);
+  for (int base = 0; base < n4; base += 4 * 64) {
+    int rr[4], dd[4];
+    f32x4 acc[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+      const int e4 = min(base + lane + 64 * jj, n4 - 1);
+      rr[jj] = e4 / (D / 4);
+      dd[jj] = 4 * (e4 % (D / 4));
+      acc[jj] = f32x4{0, 0, 0, 0};
     }
-    for (; sp < ns; sp++) {
-      const float w = sp < WMAX ? wsh[sp * ROWS + r]
-                                : exp2f(p0[sp * pstride + ROWS * D + r] - lsh[ROWS + r]);
-      acc += *(const f32x4 *)(p0 + sp * pstride + r * D + d0) * w;
+    for (int sp = 0; sp < ns; sp += 4) {
+      f32x4 a[4][4];
+#pragma unroll
+      for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          a[jj][i] = *(const f32x4 *)(p0 + (int64_t)min(sp + i, ns - 1) * pstride + rr[jj] * D +
+                                      dd[jj]);
+#pragma unroll
+      for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (sp + i < ns) {
+            const int z = sp + i, r = rr[jj];
+            const float w = z < WMAX ? wsh[z * ROWS + r]
+                                     : exp2f(p0[z * pstride + ROWS * D + r] - lsh[ROWS + r]);
+            acc[jj] += a[jj][i] * w;
+          }
     }
-    const f32x4 y = acc / lsh[r];
-    const int64_t n = tok0 + r / G, k = (int64_t)(kvh * G + r % G) * D + d0;
-    if (planes) {
-      // 8 lanes hold a 32-value group (D / 4 is a multiple of 8, so groups
-      // of 8 lanes leave the loop together)
-      const int64_t K = (int64_t)H * D;
-      const float v[4] = {y[0], y[1], y[2], y[3]};
-      split_store4(planes, npad, K, n, k, v);
-      float s = v[0] + v[1] + v[2] + v[3];
-      s += __shfl_xor(s, 1);
-      s += __shfl_xor(s, 2);
-      s += __shfl_xor(s, 4);
-      if ((e4 & 7) == 0) split_store_gsum(planes, npad, K, n, k >> 5, s);
-    } else {
-      *(f32x4 *)(out + n * H * D + k) = y;
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+      const int e4 = base + lane + 64 * jj;
+      if (e4 >= n4) continue;  // groups of 8 lanes (D / 4 is a multiple of 8) leave together
+      const int r = rr[jj], d0 = dd[jj];
+      const f32x4 y = acc[jj] / lsh[r];
+      const int64_t n = tok0 + r / G, k = (int64_t)(kvh * G + r % G) * D + d0;
+      if (planes) {
+        // 8 lanes hold a 32-value group
+        const int64_t K = (int64_t)H * D;
+        const float v[4] = {y[0], y[1], y[2], y[3]};
+        split_store4(planes, npad, K, n, k, v);
+        float s = v[0] + v[1] + v[2] + v[3];
+        s += __shfl_xor(s, 1);
+        s += __shfl_xor(s, 2);
+        s += __shfl_xor(s, 4);
+        if ((e4 & 7) == 0) split_store_gsum(planes, npad, K, n, k >> 5, s);
+      } else {
+        *(f32x4 *)(out + n * H * D + k) = y;
+      }
     }
   }
 }

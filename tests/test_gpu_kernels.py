@@ -237,6 +237,20 @@ def test_paged_attention_parity(L, H, Hkv, D):
         assert e < 2e-3 and e < 1e-4, (bps, e)
 
 
+def test_paged_attention_more_splits_than_kept_weights(L):
+    """A group split into more runs (68) than the merge keeps weights for in
+    LDS (64): the last runs' weights are recomputed from m and M."""
+    H, Hkv, D = 8, 2, 128
+    seqs = [(1, 4300), (3, 4400)]
+    q, kpool, vpool, bt = make_attn_case(H, Hkv, D, seqs, seed=77, n_cells=16384)
+    got, plan = gpu_attention(L, q, kpool, vpool, H, Hkv, D, seqs, bt, 1, n_cells=16384)
+    b = core.BatchDesc([n for n, _ in seqs], [p for _, p in seqs], bt, 64,
+                       np.zeros(len(q), np.int32), [])
+    want = core.paged_attention(q, kpool, vpool, H, Hkv, D, 1.0 / np.sqrt(D), b)
+    assert np.isfinite(got).all()
+    assert rel_err(got.reshape(len(q) * H, D), want.reshape(len(q) * H, D)) < 1e-4
+
+
 def test_paged_attention_alone_equals_batched(L):
     H, Hkv, D = 32, 8, 128
     seqs = [(1, 100), (1, 2000), (9, 700), (1, 5)]
