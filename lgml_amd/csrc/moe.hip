@@ -382,6 +382,18 @@ route_kernel(const float *__restrict__ part, int nz, int64_t T, int NE, int n_us
   group_picks(lds, (int)(T * n_used), NE, go);
 }
 
+// Routing alone over many workgroups: 16 tokens per workgroup of 256
+// threads (no LDS), so the tokens spread over the CUs.
+template <int PER>
+__global__ void __launch_bounds__(256)
+route_many_kernel(const float *__restrict__ part, int nz, int64_t T, int NE, int n_used,
+                  int gating, int norm_topk, float scale, int32_t *__restrict__ ids,
+                  float *__restrict__ wts) {
+  const int64_t t = (int64_t)blockIdx.x * 16 + threadIdx.x / 16;
+  route_token<PER>(part, nz, T, t, NE, n_used, gating, norm_topk, scale, threadIdx.x & 15, ids,
+                   wts, nullptr);
+}
+
 // Grouping of given ids (graph:mul_mat_id's ids). Picks whose id is outside
 // [0, NE) join no expert; their Y rows (M values) are written as zeros.
 __global__ void __launch_bounds__(ROUTE_THREADS)
@@ -488,15 +500,35 @@ int moe_route_dev(const float *part, int nz, int64_t T, int NE, int n_used, int 
   if (T == 0) return LGMLH_OK;
   GroupOut g = go ? *go : GroupOut{nullptr, nullptr, nullptr, 16};
   const int grp = go ? 1 : 0;
+  // Up to 16 tokens: routing and grouping in one workgroup (one launch).
+  // More: the routing spreads over workgroups of 16 tokens (one per CU
+  // instead of 16 waves sharing one), then one workgroup groups the picks
+  // (two launches; the same ids and order).
+  if (T <= 16) {
+    if (NE <= 128)
+      hipLaunchKernelGGL(route_kernel<8>, dim3(1), dim3(ROUTE_THREADS), 0, st, part, nz, T, NE,
+                         n_used, gating, norm_topk, scale, ids, wts, grp, g);
+    else if (NE <= 256)
+      hipLaunchKernelGGL(route_kernel<16>, dim3(1), dim3(ROUTE_THREADS), 0, st, part, nz, T, NE,
+                         n_used, gating, norm_topk, scale, ids, wts, grp, g);
+    else
+      hipLaunchKernelGGL(route_kernel<32>, dim3(1), dim3(ROUTE_THREADS), 0, st, part, nz, T, NE,
+                         n_used, gating, norm_topk, scale, ids, wts, grp, g);
+    return hip_check(hipGetLastError(), "moe route");
+  }
+  const dim3 grid((unsigned)((T + 15) / 16));
   if (NE <= 128)
-    hipLaunchKernelGGL(route_kernel<8>, dim3(1), dim3(ROUTE_THREADS), 0, st, part, nz, T, NE,
-                       n_used, gating, norm_topk, scale, ids, wts, grp, g);
+    hipLaunchKernelGGL(route_many_kernel<8>, grid, dim3(256), 0, st, part, nz, T, NE, n_used,
+                       gating, norm_topk, scale, ids, wts);
   else if (NE <= 256)
-    hipLaunchKernelGGL(route_kernel<16>, dim3(1), dim3(ROUTE_THREADS), 0, st, part, nz, T, NE,
-                       n_used, gating, norm_topk, scale, ids, wts, grp, g);
+    hipLaunchKernelGGL(route_many_kernel<16>, grid, dim3(256), 0, st, part, nz, T, NE, n_used,
+                       gating, norm_topk, scale, ids, wts);
   else
-    hipLaunchKernelGGL(route_kernel<32>, dim3(1), dim3(ROUTE_THREADS), 0, st, part, nz, T, NE,
-                       n_used, gating, norm_topk, scale, ids, wts, grp, g);
+    hipLaunchKernelGGL(route_many_kernel<32>, grid, dim3(256), 0, st, part, nz, T, NE, n_used,
+                       gating, norm_topk, scale, ids, wts);
+  if (grp)
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(ROUTE_THREADS), 0, st, ids,
+                       (int)(T * n_used), NE, g, nullptr, (int64_t)0);
   return hip_check(hipGetLastError(), "moe route");
 }
 
