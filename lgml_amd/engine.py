@@ -580,6 +580,8 @@ class Engine:
         self.tokens += sum(n for _, n, _, _, _, _ in p.entries)
         got = []
         for r, _, prompt, sampled, h, row in p.entries:
+            if r.done:
+                continue  # ended at launch (a pool-full reserve) with only a prompt chunk in flight
             if prompt and self.prefix_cache:
                 self.publish(r)
             if sampled:

@@ -23,9 +23,11 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 
-def serve(gm, prompts, budgets, n_slots, run_ahead, ubatch=64, prefix_cache=False, streams=1):
+def serve(gm, prompts, budgets, n_slots, run_ahead, ubatch=64, prefix_cache=False, streams=1,
+          expect_err=()):
     """All requests through one engine, queued ones joining as slots free;
-    per request its (token, logits) samples in order."""
+    per request its (token, logits) samples in order. Requests whose index
+    is in expect_err must end with "kv pool full"."""
     from lgml_amd import engine
     eng = engine.Engine(gm, n_slots, ubatch=ubatch, prefix_cache=prefix_cache,
                         run_ahead=run_ahead, streams=streams)
@@ -49,9 +51,12 @@ def serve(gm, prompts, budgets, n_slots, run_ahead, ubatch=64, prefix_cache=Fals
         passes += 1
         assert passes < 1000
     record(eng.drain())
-    for r in reqs:
-        assert r.done and r.err is None and len(r.out) == r.max_new, (r.err, len(r.out))
-    return [got[id(r)] for r in reqs]
+    for i, r in enumerate(reqs):
+        if i in expect_err:
+            assert r.done and r.err and "kv pool full" in r.err, r.err
+        else:
+            assert r.done and r.err is None and len(r.out) == r.max_new, (r.err, len(r.out))
+    return [got[id(r)] for i, r in enumerate(reqs) if i not in expect_err]
 
 
 def same(a, b):
@@ -103,3 +108,18 @@ def test_run_ahead_equals_sync_with_rings():
     c = serve(runtime.DeviceModel(hp, w, 2048, ring_cells=2 * R * 64), prompts, budgets, 2,
               True, streams=2)
     same(a, c)
+
+
+def test_run_ahead_pool_full_mid_prompt():
+    """A prompt longer than the pool fails alone while its earlier chunks
+    are still in flight; the other requests sample as with the synchronous
+    engine."""
+    from lgml_amd import runtime
+    hp, w = models.build("c2", seed=13, n_layer=2, init="normal")
+    V = hp["n_vocab"]
+    prompts = [lcg_ints(6200, 100, 0, V), lcg_ints(6201, 800, 0, V), lcg_ints(6202, 30, 0, V)]
+    budgets = [5, 3, 6]
+    print("run-ahead vs sync, a prompt longer than the pool", flush=True)
+    a = serve(runtime.DeviceModel(hp, w, 12 * 64), prompts, budgets, 2, False, expect_err=(1,))
+    b = serve(runtime.DeviceModel(hp, w, 12 * 64), prompts, budgets, 2, True, expect_err=(1,))
+    same(a, b)
