@@ -33,9 +33,9 @@ decode tokens go from pass to pass on the device); --sync reads every pass
 back before the next. roofline = the paged attention kernel (the
 dominant kernel: ~80% of the step's bytes): its algorithmic bytes (K + V of
 every visible cell, q in, out) per launch over its duration, timed with HIP
-events on the pass's stream during min(K, 16) further steps, against
-8 TB/s. cpu_baseline = the C oracle (oracle/) timed on a bounded sample of
-the same step on the host cores.
+events on the pass's stream during min(K, 16) further steps (the decode
+passes among them), against 8 TB/s. cpu_baseline = the C oracle (oracle/)
+timed on a bounded sample of the same step on the host cores.
 """
 import argparse
 import json
@@ -323,23 +323,36 @@ def main():
     wall = time.perf_counter() - t0
     # the traced steps run as one pass on one stream: the events time the
     # attention kernels themselves, with nothing else running beside them
-    attn_bytes = []
+    attn_bytes, decode_pass = [], []
     eng.n_streams = 1
     for _ in range(n_trace):
         step(True)
-        attn_bytes.append(bytes_of(eng.launched_plan)[0])
+        pl = eng.launched_plan
+        attn_bytes.append(bytes_of(pl)[0])
+        decode_pass.append(bool((pl.seq_n <= 1).all()))
     drain()
-    at = trace.times_ms(hip.TRACE_ATTN)
-    gt = trace.times_ms(hip.TRACE_GEMM)
-    xt = trace.times_ms(hip.TRACE_EXPERTS)
-    L = hp["n_layer"]
-    # attention launches are recorded in step order, L per step
+
+    def per_pass(ts):
+        """The recorded spans of one kind, split by pass (the same number
+        of launches of a kind in every pass)."""
+        k = len(ts) // n_trace
+        return [ts[i * k:(i + 1) * k] for i in range(n_trace)]
+    # The kernel figures come from the decode passes among the traced ones:
+    # a joining prompt's 512-token chunk is a prefill pass, another regime
+    # (its attention reads each block once per group of 16 / G tokens).
+    keep = [i for i in range(n_trace) if decode_pass[i]]
+    if len(keep) < n_trace // 2:
+        keep = list(range(n_trace))
+    at_p = per_pass(trace.times_ms(hip.TRACE_ATTN))
+    gt_p = per_pass(trace.times_ms(hip.TRACE_GEMM))
+    xt_p = per_pass(trace.times_ms(hip.TRACE_EXPERTS))
+    at = [t for i in keep for t in at_p[i]]
     n_att = len(at)
-    tot_bytes = sum(attn_bytes[i // L][i % L] for i in range(n_att))
+    tot_bytes = sum(sum(attn_bytes[i][:len(at_p[i])]) for i in keep)
     attn_gbs = tot_bytes / (sum(at) / 1e3) if at else 0.0
     avg_attn_ms = sum(at) / max(n_att, 1)
-    gemm_ms = (sum(gt) + sum(xt)) / n_trace
-    exp_ms = sum(xt) / n_trace
+    gemm_ms = sum(sum(gt_p[i]) + sum(xt_p[i]) for i in keep) / len(keep)
+    exp_ms = sum(sum(xt_p[i]) for i in keep) / len(keep)
     ms_step = wall * 1e3 / args.steps
     step_gbs = sum(step_bytes) / wall
     result = {
@@ -372,8 +385,8 @@ def main():
         "step_roofline": {
             "bytes_per_step": sum(step_bytes) / len(step_bytes),
             "achieved_GBps": step_gbs / 1e9, "frac": step_gbs / HBM_PEAK,
-            "gemm_ms_per_step": gemm_ms, "attn_ms_per_step": sum(at) / n_trace,
-            "traced_steps": n_trace,
+            "gemm_ms_per_step": gemm_ms, "attn_ms_per_step": sum(at) / len(keep),
+            "traced_steps": len(keep),
             "gemm_GBps": wbytes / (gemm_ms / 1e3) / 1e9 if gemm_ms else None,
         },
     }
