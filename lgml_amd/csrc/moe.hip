@@ -33,23 +33,26 @@ constexpr int MOE_MAX_PICKS = 8192;   // picks of one pass (LDS)
 
 // ---- router logits: split-K f32 product -------------------------------------
 // part[z][n][e] = sum over k in [256 z, 256 z + 256) of W[e][k] x[n][k], in
-// k order (fmaf). A workgroup takes 16 experts x 64 tokens of one K chunk;
-// thread t owns expert t % 16 for tokens t / 16 + 16 j (j < 4).
+// k order (fmaf). A workgroup takes 16 experts x TOK tokens of one K chunk;
+// thread t owns expert t % 16 for tokens t / 16 + 16 j (j < TOK / 16).
+// TOK is 64, or 16 for a batch of at most 64 tokens (four times the
+// workgroups; each sum is the same fmaf chain either way).
 constexpr int ROUTER_KC = 256;
-constexpr int ROUTER_TOK = 64;
 constexpr int ROUTER_LD = ROUTER_KC + 4;  // row pitch (floats): 16-byte rows, no bank conflicts
+template <int TOK>
 __global__ void __launch_bounds__(256)
 router_part_kernel(const float *__restrict__ w, int NE, int64_t K, const float *__restrict__ x,
                    int64_t N, float *__restrict__ part) {
+  constexpr int TJ = TOK / 16;  // tokens per thread
   __shared__ __align__(16) float ws_[16 * ROUTER_LD];
-  __shared__ __align__(16) float xs_[ROUTER_TOK * ROUTER_LD];
+  __shared__ __align__(16) float xs_[TOK * ROUTER_LD];
   const int t = threadIdx.x, e = t & 15, tq = t >> 4;
-  const int64_t e0 = (int64_t)blockIdx.x * 16, n0 = (int64_t)blockIdx.z * ROUTER_TOK;
+  const int64_t e0 = (int64_t)blockIdx.x * 16, n0 = (int64_t)blockIdx.z * TOK;
   const int64_t k0 = (int64_t)blockIdx.y * ROUTER_KC;
   // 16-byte loads, all issued before the first LDS store: float4 i of a
   // row of ROUTER_KC / 4 (K % 4 == 0)
   constexpr int Q = ROUTER_KC / 4;
-  constexpr int WJ = 16 * Q / 256, XJ = ROUTER_TOK * Q / 256;
+  constexpr int WJ = 16 * Q / 256, XJ = TOK * Q / 256;
   f32x4 wv_[WJ], xv_[XJ];
 #pragma unroll
   for (int j = 0; j < WJ; j++) {
@@ -74,13 +77,15 @@ router_part_kernel(const float *__restrict__ w, int NE, int64_t K, const float *
     *(f32x4 *)&xs_[(i / Q) * ROUTER_LD + 4 * (i % Q)] = xv_[j];
   }
   __syncthreads();
-  float acc[4] = {0, 0, 0, 0};
+  float acc[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; j++) acc[j] = 0.0f;
   const float *wr = ws_ + e * ROUTER_LD;
 #pragma unroll 4
   for (int c = 0; c < ROUTER_KC; c += 4) {
     const f32x4 wv = *(const f32x4 *)(wr + c);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int j = 0; j < TJ; j++) {
       const f32x4 xv = *(const f32x4 *)(xs_ + (tq + 16 * j) * ROUTER_LD + c);
       acc[j] = fmaf(wv[0], xv[0], acc[j]);
       acc[j] = fmaf(wv[1], xv[1], acc[j]);
@@ -89,7 +94,7 @@ router_part_kernel(const float *__restrict__ w, int NE, int64_t K, const float *
     }
   }
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
+  for (int j = 0; j < TJ; j++) {
     const int64_t n = n0 + tq + 16 * j;
     if (e0 + e < NE && n < N) part[((int64_t)blockIdx.y * N + n) * NE + e0 + e] = acc[j];
   }
@@ -473,9 +478,12 @@ int router_logits(const float *w, int NE, int64_t K, const float *x, int64_t T, 
     set_error("moe router: K %lld is not a multiple of 4", (long long)K);
     return LGMLH_EINVAL;
   }
-  dim3 grid((unsigned)((NE + 15) / 16), (unsigned)router_splits(K),
-            (unsigned)((T + ROUTER_TOK - 1) / ROUTER_TOK));
-  hipLaunchKernelGGL(router_part_kernel, grid, dim3(256), 0, st, w, NE, K, x, T, part);
+  const int tok = T <= 64 ? 16 : 64;
+  dim3 grid((unsigned)((NE + 15) / 16), (unsigned)router_splits(K), (unsigned)((T + tok - 1) / tok));
+  if (tok == 16)
+    hipLaunchKernelGGL(router_part_kernel<16>, grid, dim3(256), 0, st, w, NE, K, x, T, part);
+  else
+    hipLaunchKernelGGL(router_part_kernel<64>, grid, dim3(256), 0, st, w, NE, K, x, T, part);
   return hip_check(hipGetLastError(), "moe router");
 }
 
