@@ -336,7 +336,8 @@ int lgmlh_rms_norm(const float *x, int64_t n_rows, int64_t n, float eps, const f
 /* The qkv tail (transformer.lua:1776-1788): optional per-head rms_norm with
  * q_norm / k_norm, rope (graph:rope, src/lgml.c:2004-2081: mode normal or
  * neox, freq factors), then the KV store of k and v at cells. q is roped
- * in place. qkv is (n, (H + 2 Hkv) * D) f32 with [q | k | v] per row. */
+ * in place. qkv is (n, (H + 2 Hkv) * D) f32 with [q | k | v] per row. A
+ * cell outside [0, n_cells) is not written (cells are device data here). */
 int lgmlh_qkv_rope_store(float *qkv, int64_t n, int n_head, int n_head_kv, int head_dim,
     int n_rot, int neox, float freq_base, const float *freq_factors, const float *q_norm,
     const float *k_norm, float eps, const int32_t *pos, void *kpool, void *vpool,

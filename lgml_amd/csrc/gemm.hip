@@ -719,13 +719,15 @@ static void launch_q(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t
   splits = splits_for(M, K, N, &spb);
   const int64_t Npad = split_npad(N);
   // Column tiles of 64, or of 16 / 32 for a batch that small (the same sums
-  // per element: only the columns a workgroup carries change). A product
-  // with fewer than 200 workgroups of rows and splits takes tiles of 16:
-  // more workgroups, and for Q4_K / Q6_K two per CU (C5's dense products
-  // 6.81 -> 6.49 ms per step, C4's Q8_0 ones 1.96 -> 1.85; at 256, C2's
-  // gate|up, 224 workgroups, lost 20%).
+  // per element: only the columns a workgroup carries change). A decode-
+  // sized product (N <= 64) with fewer than 200 workgroups of rows and
+  // splits takes tiles of 16: more workgroups, and for Q4_K / Q6_K two per
+  // CU (C5's dense products 6.81 -> 6.49 ms per step, C4's Q8_0 ones 1.96
+  // -> 1.85; at 256, C2's gate|up, 224 workgroups, lost 20%). A prefill-
+  // sized batch keeps wide tiles, so each weight fragment is dequantized
+  // once for 64 columns.
   int nct = N <= 16 ? 1 : N <= 32 ? 2 : WG_COLS / 16;
-  if ((int64_t)((M + WG_ROWS - 1) / WG_ROWS) * splits < 200) nct = 1;
+  if (N <= 64 && (int64_t)((M + WG_ROWS - 1) / WG_ROWS) * splits < 200) nct = 1;
   const int cols = 16 * nct;
   dim3 grid((unsigned)((N + cols - 1) / cols), (unsigned)((M + WG_ROWS - 1) / WG_ROWS),
             (unsigned)splits);

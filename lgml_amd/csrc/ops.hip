@@ -181,7 +181,8 @@ qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int Hkv, int D, int 
                       const float *__restrict__ q_norm, const float *__restrict__ k_norm,
                       float eps, const int32_t *__restrict__ pos, uint16_t *__restrict__ kp,
                       uint16_t *__restrict__ vp, const int64_t *__restrict__ cells,
-                      float *__restrict__ q_out, Pending pa, Pending pb, int vmode) {
+                      int64_t n_cells, float *__restrict__ q_out, Pending pa, Pending pb,
+                      int vmode) {
   extern __shared__ float lds[];
   const int64_t t = blockIdx.x;
   const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -242,6 +243,7 @@ qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int Hkv, int D, int 
     return;
   }
   const int64_t cell = cells[t];
+  if (cell < 0 || cell >= n_cells) return;  // a cell outside the pool is never written
   const int64_t b = cell / KV_BLOCK, o = cell % KV_BLOCK;
   if (is_k) {
     const int hk = h - H;
@@ -307,10 +309,13 @@ __global__ void softcap_kernel(float *__restrict__ x, int64_t n, float cap) {
 }
 
 // ---- argmax: first index of the maximum --------------------------------------
-// First index of the row maximum (strict >, src/sample.c:914-925). Each
-// thread scans its strided slice (float4 loads when rows are 16-byte
-// aligned), then the candidates meet in a fixed-order tree that keeps the
-// smaller index on ties.
+// src/sample.c:914-925: m = x[0], then x[i] replaces it only when x[i] > m.
+// So a NaN at index 0 gives 0 (nothing compares greater than it), a NaN
+// elsewhere is never taken, and ties keep the first index. Here: each
+// thread scans its strided slice for the first maximum of its non-NaN
+// values (float4 loads when rows are 16-byte aligned), the candidates meet
+// in a fixed-order tree that keeps the smaller index on ties, and a NaN at
+// index 0 decides the row alone.
 constexpr int ARGMAX_THREADS = 1024;
 __device__ __forceinline__ void amax_take(float &bv, int64_t &bi, float v, int64_t i) {
   if (i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi))) {
@@ -326,13 +331,13 @@ argmax_kernel(const float *__restrict__ x, int64_t n, int32_t *__restrict__ out)
   const int64_t r = blockIdx.x;
   const float *xr = x + r * n;
   float best = 0.0f;
-  int64_t idx = -1;
+  int64_t idx = -1;  // no candidate yet (NaN values never become one)
   if ((n & 3) == 0 && (((uintptr_t)x) & 15) == 0) {
     for (int64_t q = tid; q < n / 4; q += ARGMAX_THREADS) {
       const f32x4 v = ((const f32x4 *)xr)[q];
 #pragma unroll
       for (int e = 0; e < 4; e++)
-        if (idx < 0 || v[e] > best) {
+        if (v[e] == v[e] && (idx < 0 || v[e] > best)) {
           best = v[e];
           idx = 4 * q + e;
         }
@@ -340,7 +345,7 @@ argmax_kernel(const float *__restrict__ x, int64_t n, int32_t *__restrict__ out)
   } else {
     for (int64_t i = tid; i < n; i += ARGMAX_THREADS) {
       const float v = xr[i];
-      if (idx < 0 || v > best) {
+      if (v == v && (idx < 0 || v > best)) {
         best = v;
         idx = i;
       }
@@ -360,7 +365,8 @@ argmax_kernel(const float *__restrict__ x, int64_t n, int32_t *__restrict__ out)
     float b = sv[0];
     int64_t bi = si[0];
     for (int k = 1; k < ARGMAX_THREADS / 64; k++) amax_take(b, bi, sv[k], si[k]);
-    out[r] = (int32_t)bi;
+    const float x0 = n > 0 ? xr[0] : 0.0f;
+    out[r] = x0 != x0 || bi < 0 ? 0 : (int32_t)bi;
   }
 }
 
@@ -512,7 +518,7 @@ int qkv_rope_store_dev(float *qkv, int64_t n, int n_head, int n_head_kv,
                      dim3(64 * QKV_HEADS), lds,
                      as_stream(stream), qkv, n_head, n_head_kv, head_dim, n_rot, neox,
                      theta_scale, freq_factors, q_norm, k_norm, eps, pos, (uint16_t *)kpool,
-                     (uint16_t *)vpool, cells, q_out, pa, pb, vmode);
+                     (uint16_t *)vpool, cells, n_cells, q_out, pa, pb, vmode);
   return hip_check(hipGetLastError(), "qkv_rope_store");
 }
 }  // namespace lgmlh

@@ -11,7 +11,7 @@
 // ring of blocks and starts each group's runs at its window.
 #include <string.h>
 
-#include <vector>
+#include <utility>
 
 #include "common.h"
 
@@ -73,34 +73,42 @@ static int plan_impl(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
   // A fixed default: the split points of a sequence must not depend on the
   // rest of the batch (a sequence gives the same bits alone or batched).
   const int bps = blocks_per_split ? blocks_per_split : 16;
-  std::vector<int32_t> items, merge;
-  for (int s = 0, off = 0; s < n_seq; off += seq_n[s], s++) {
-    for (int g0 = 0; g0 < seq_n[s]; g0 += T) {
-      int ge = g0 + T < seq_n[s] ? g0 + T : seq_n[s];
-      // logical blocks [b0, nbg): from the window of the group's first
-      // token (ring plans) or from 0, to the group's last position
-      const int64_t pf = (int64_t)seq_npast[s] + g0, pl = (int64_t)seq_npast[s] + ge - 1;
-      int b0 = ring ? (int)((pf - window + 1 > 0 ? pf - window + 1 : 0) / B) : 0;
-      int nbg = (int)(pl / B + 1);
-      // the fewest runs of at most bps blocks, of lengths that differ by at
-      // most one (the longest run bounds the kernel's time)
-      const int len = nbg - b0, ns = (len + bps - 1) / bps;
-      int first = (int)(items.size() / 4);
-      int mg = ns > 1 ? (int)(merge.size() / 4) + 1 : 0;
-      for (int j = 0; j < ns; j++) {
-        const int lo = b0 + (int)((int64_t)j * len / ns), hi = b0 + (int)((int64_t)(j + 1) * len / ns);
-        items.push_back(s);
-        items.push_back(off + g0);
-        items.push_back((ge - g0) | (mg << 5));
-        items.push_back(lo | (hi << 16));
-      }
-      if (ns > 1) {
-        merge.push_back(first);
-        merge.push_back(ns);
-        merge.push_back(off + g0);
-        merge.push_back(ge - g0);
+  // The work list is walked twice with no allocation: once to count the
+  // items and merges (the buffer layout), once to write them into buf.
+  // emit(item index, item[4], merge[4] or NULL, merge index) gets each run;
+  // a group of more than one run passes its merge with its first run.
+  auto walk = [&](auto &&emit) {
+    int64_t n_items = 0, n_merge = 0;
+    for (int s = 0, off = 0; s < n_seq; off += seq_n[s], s++) {
+      for (int g0 = 0; g0 < seq_n[s]; g0 += T) {
+        const int ge = g0 + T < seq_n[s] ? g0 + T : seq_n[s];
+        // logical blocks [b0, nbg): from the window of the group's first
+        // token (ring plans) or from 0, to the group's last position
+        const int64_t pf = (int64_t)seq_npast[s] + g0, pl = (int64_t)seq_npast[s] + ge - 1;
+        const int b0 = ring ? (int)((pf - window + 1 > 0 ? pf - window + 1 : 0) / B) : 0;
+        const int nbg = (int)(pl / B + 1);
+        // the fewest runs of at most bps blocks, of lengths that differ by
+        // at most one (the longest run bounds the kernel's time)
+        const int len = nbg - b0, ns = (len + bps - 1) / bps;
+        const uint32_t mg = ns > 1 ? (uint32_t)n_merge + 1 : 0;
+        for (int j = 0; j < ns; j++) {
+          const uint32_t lo = (uint32_t)(b0 + (int)((int64_t)j * len / ns));
+          const uint32_t hi = (uint32_t)(b0 + (int)((int64_t)(j + 1) * len / ns));
+          const int32_t item[4] = {s, off + g0, (int32_t)((uint32_t)(ge - g0) | (mg << 5)),
+                                   (int32_t)(lo | (hi << 16))};
+          const int32_t mrg[4] = {(int32_t)n_items, ns, off + g0, ge - g0};
+          emit(n_items, item, j == 0 && ns > 1 ? mrg : nullptr, n_merge);
+          n_items++;
+        }
+        if (ns > 1) n_merge++;
       }
     }
+    return std::make_pair(n_items, n_merge);
+  };
+  const auto counts = walk([](int64_t, const int32_t *, const int32_t *, int64_t) {});
+  if (counts.first > INT32_MAX / 8 || counts.second > INT32_MAX / 8) {
+    set_error("plan: too many work items");
+    return LGMLH_EINVAL;
   }
   lgmlh_plan_info in;
   memset(&in, 0, sizeof in);
@@ -108,8 +116,8 @@ static int plan_impl(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
   in.n_tokens = (int32_t)N;
   in.max_blocks = max_blocks;
   in.block = B;
-  in.n_items = (int32_t)(items.size() / 4);
-  in.n_merge = (int32_t)(merge.size() / 4);
+  in.n_items = (int32_t)counts.first;
+  in.n_merge = (int32_t)counts.second;
   in.rows = 16;
   in.n_head_kv = n_head_kv;
   in.window = ring ? window : 0;
@@ -122,8 +130,8 @@ static int plan_impl(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
   in.off_npast = o;        o = align16(o + 4 * (int64_t)n_seq);
   in.off_block_tab = o;    o = align16(o + 4 * (int64_t)n_seq * max_blocks);
   in.off_logit_rows = o;   o = align16(o + 4 * (int64_t)n_seq);
-  in.off_items = o;        o = align16(o + 4 * (int64_t)items.size());
-  in.off_merge = o;        o = align16(o + 4 * (int64_t)merge.size());
+  in.off_items = o;        o = align16(o + 16 * (int64_t)in.n_items);
+  in.off_merge = o;        o = align16(o + 16 * (int64_t)in.n_merge);
   in.bytes = o;
   *info = in;
   if (!buf) return LGMLH_OK;
@@ -152,8 +160,11 @@ static int plan_impl(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
   }
   psoff[n_seq] = (int32_t)t;
   memcpy(b + in.off_block_tab, block_tab, 4 * (size_t)n_seq * max_blocks);
-  if (!items.empty()) memcpy(b + in.off_items, items.data(), 4 * items.size());
-  if (!merge.empty()) memcpy(b + in.off_merge, merge.data(), 4 * merge.size());
+  int32_t *pit = (int32_t *)(b + in.off_items), *pmg = (int32_t *)(b + in.off_merge);
+  walk([&](int64_t i, const int32_t *item, const int32_t *mrg, int64_t m) {
+    memcpy(pit + 4 * i, item, 16);
+    if (mrg) memcpy(pmg + 4 * m, mrg, 16);
+  });
   return LGMLH_OK;
 }
 

@@ -96,6 +96,11 @@ def _declare(L):
     L.orc_mul_mat.argtypes = [i32, vp, i64, i64, vp, i64, vp, i32]
     L.orc_moe_route.argtypes = [vp, i64, i32, i32, i32, i32, C.c_float, vp, vp]
     L.orc_mul_mat_id.argtypes = [i32, vp, i64, i64, i64, vp, i64, vp, i64, i32, vp, i32]
+    L.orc_splitmix64.argtypes = [C.POINTER(C.c_uint64)]
+    L.orc_splitmix64.restype = C.c_uint64
+    L.orc_rms_norm.argtypes = [vp, vp, i64, i64, C.c_float, vp]
+    L.orc_rope.argtypes = [vp, i64, i32, i32, i32, i32, C.c_float, vp, vp]
+    L.orc_glu.argtypes = [vp, vp, vp, i64, i32]
     L.orc_argmax.argtypes = [vp, i64]
     L.orc_argmax.restype = C.c_int32
 
@@ -231,6 +236,41 @@ def mul_mat_id(t, w, n_expert, M, K, x, ids, nthreads=None):
                             nthreads or threads()) != 0:
         raise ValueError("mul_mat_id failed")
     return y
+
+
+def splitmix64(seed, n):
+    """n raw splitmix64 draws from seed (src/lgml.c:3064-3079)."""
+    s = C.c_uint64(seed & (2**64 - 1))
+    return [int(lib().orc_splitmix64(C.byref(s))) for _ in range(n)]
+
+
+def rms_norm(x, eps, w=None):
+    """graph:rms_norm (src/lgml.c:1633) of each row of x (rows, n), times w."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    wv = None if w is None else np.ascontiguousarray(w, np.float32)
+    lib().orc_rms_norm(_p(x), _p(y), x.shape[0], x.shape[1], eps,
+                       None if wv is None else _p(wv))
+    return y
+
+
+def rope(x, n_heads, D, n_rot, neox, base, pos, ff=None):
+    """graph:rope (src/lgml.c:2004-2081) of rows (rows, n_heads * D) at pos."""
+    y = np.ascontiguousarray(x, np.float32).copy()
+    pos = np.ascontiguousarray(pos, np.int32)
+    ffv = None if ff is None else np.ascontiguousarray(ff, np.float32)
+    lib().orc_rope(_p(y), y.shape[0], n_heads, D, n_rot, int(neox), base,
+                   None if ffv is None else _p(ffv), _p(pos))
+    return y
+
+
+def glu(g, u, gelu=False):
+    """silu(g) u, or gelu(g) u (transformer.lua:2048), elementwise."""
+    g = np.ascontiguousarray(g, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    out = np.empty_like(g)
+    lib().orc_glu(_p(g), _p(u), _p(out), g.size, int(bool(gelu)))
+    return out
 
 
 def argmax(v):

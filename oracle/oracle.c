@@ -66,6 +66,13 @@ splitmix64(uint64_t *x)
 	return z ^ (z >> 31);
 }
 
+/* One raw draw, for tests against splitmix64's published outputs. */
+uint64_t
+orc_splitmix64(uint64_t *state)
+{
+	return splitmix64(state);
+}
+
 static double
 unit01(uint64_t *x)
 {
@@ -1019,6 +1026,36 @@ static double
 gelu(double x)
 {
 	return 0.5 * x * (1.0 + tanh(0.7978845608028654 * (x + 0.044715 * x * x * x)));
+}
+
+/* The ops of the forward exported one by one, for tests of the device's
+ * standalone entry points: rms_norm_row over rows (graph:rms_norm,
+ * src/lgml.c:1633), rope_row over rows of heads at positions (graph:rope,
+ * src/lgml.c:2004-2081), and the GLU of ffn (transformer.lua:2048:
+ * silu(g) u, or gemma's gelu(g) u) in f64, rounded once. */
+void
+orc_rms_norm(const float *x, float *y, int64_t rows, int64_t n, float eps, const float *w)
+{
+	for (int64_t r = 0; r < rows; r++)
+		rms_norm_row(x + r * n, y + r * n, n, eps, w);
+}
+
+void
+orc_rope(float *x, int64_t rows, int n_heads, int D, int n_rot, int neox, float base,
+    const float *ff, const int32_t *pos)
+{
+	for (int64_t r = 0; r < rows; r++)
+		rope_row(x + r * n_heads * D, n_heads, D, n_rot, neox, base, ff, pos[r]);
+}
+
+void
+orc_glu(const float *g, const float *u, float *out, int64_t n, int use_gelu)
+{
+	for (int64_t i = 0; i < n; i++) {
+		double gv = g[i];
+		double a = use_gelu ? gelu(gv) : gv / (1.0 + exp(-gv));
+		out[i] = (float)(a * (double)u[i]);
+	}
 }
 
 /* transformer.lua:2285-2365 (forward) with qkv (:1754-1789), the batched

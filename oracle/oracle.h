@@ -35,6 +35,8 @@ void orc_lcg_fill(uint64_t *state, float *out, int64_t n, double lo, double hi);
  * Box-Muller "normal" fill (two draws per value, cos branch). */
 void orc_fill_normal(uint64_t *seed, float *out, int64_t n, double mean, double sd);
 void orc_fill_uniform(uint64_t *seed, float *out, int64_t n, double a, double b);
+/* One raw splitmix64 draw (the state advanced in place). */
+uint64_t orc_splitmix64(uint64_t *state);
 /* orc_fill_normal's values for a fresh seed, in parallel; and the same
  * values quantized row by row (rows x cols) into `type`. */
 void orc_gen_normal(uint64_t seed, float *out, int64_t n, double mean, double sd, int n_threads);
@@ -180,6 +182,15 @@ int orc_moe_route(const float *logits, int64_t n, int n_expert, int n_used, int 
 int orc_mul_mat_id(int type, const void *w, int64_t n_expert, int64_t M, int64_t K,
     const float *x, int64_t U, const int32_t *ids, int64_t T, int n_used, float *y,
     int n_threads);
+
+/* The forward's row ops, one by one: rms_norm of rows of n values
+ * (graph:rms_norm, src/lgml.c:1633; w may be NULL); rope of rows of
+ * n_heads x D at pos[r] (graph:rope, src/lgml.c:2004-2081; ff may be NULL);
+ * silu(g) u or, with use_gelu, gelu(g) u (transformer.lua:2048). */
+void orc_rms_norm(const float *x, float *y, int64_t rows, int64_t n, float eps, const float *w);
+void orc_rope(float *x, int64_t rows, int n_heads, int D, int n_rot, int neox, float base,
+    const float *ff, const int32_t *pos);
+void orc_glu(const float *g, const float *u, float *out, int64_t n, int use_gelu);
 
 /* Greedy first-max argmax (src/sample.c:914-925). */
 int32_t orc_argmax(const float *v, int64_t n);

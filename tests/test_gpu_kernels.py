@@ -129,23 +129,33 @@ def run_mul_mat(L, ty, w, M, K, x, xtype=None):
     return y.cpu().numpy()
 
 
+# Column tiles per workgroup (gemm.hip launch_q): 16 for N <= 16, 32 for
+# N <= 32, else 64; but a product of N <= 64 with fewer than 200 workgroups
+# of row tiles x K splits takes 16. The small shapes run the 16-column
+# kernel at N <= 64 and the 64-column one at N = 70 and 130; the large
+# ones, (25600, 1024) = 100 row tiles x 2 splits and (51200, 256) = 200 x
+# 1, run the 32- and 64-column kernels at N = 17 / 32 and 64 / 130.
 @pytest.mark.parametrize("ty", [core.Q4_K, core.Q6_K, core.Q8_0, core.F32])
-@pytest.mark.parametrize("MK", [(512, 1024), (256, 4096), (48, 768)])
+@pytest.mark.parametrize("MK", [(512, 1024), (256, 4096), (48, 768), (25600, 1024),
+                                (51200, 256)])
 def test_mul_mat_parity_and_batch_invariance(L, ty, MK):
     M, K = MK
     if ty != core.F32 and K % 256:
         pytest.skip("quantized K must be a multiple of 256")
+    big = M * K > 4_000_000
+    if big and ty == core.F32:
+        pytest.skip("the column tiles are a quantized-product choice")
     wf = core.fill_normal(M * K, 0, 0.02, 7).reshape(M, K)
     w = wf if ty == core.F32 else core.quantize(ty, wf)
     deq = wf if ty == core.F32 else core.dequantize(ty, w, K)
     x = core.fill_normal(130 * K, 0, 1, 8).reshape(130, K)
-    for N in (1, 3, 17, 32, 64, 70, 130):  # column tiles of 16, 32 and 64
+    for N in ((17, 32, 64, 130) if big else (1, 3, 17, 32, 64, 70, 130)):
         y = run_mul_mat(L, ty, w, M, K, x[:N])
         want = core.mul_mat(core.F32, deq, M, K, x[:N])
         assert rel_err(y, want) < 2e-3, (N, rel_err(y, want))
         assert rel_err(y, want) < 1e-5, (N, rel_err(y, want))
-        if N == 130:
-            for j in (0, 63, 64, 129):
+        if N in (32, 130):  # a 16-column launch alone, the 32- / 64-column one batched
+            for j in ((0, 63, 64, 129) if N == 130 else (0, 16, 31)):
                 alone = run_mul_mat(L, ty, w, M, K, x[j:j + 1])
                 assert np.array_equal(alone[0].view(np.uint32), y[j].view(np.uint32)), j
 

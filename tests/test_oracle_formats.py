@@ -45,6 +45,39 @@ def test_lcg_sequence(oracle_lib):
         assert r.next() == (x >> 11) / 2.0**53
 
 
+# splitmix64's published outputs (Vigna's splitmix64.c, the generator that
+# seeds xoshiro): seed 1234567 and seed 0 (0xe220a8397b1dcdaf first).
+SPLITMIX_1234567 = [6457827717110365317, 3203168211198807973, 9817491932198370423,
+                    4593380528125082431, 16408922859458223821]
+SPLITMIX_0 = [0xe220a8397b1dcdaf]
+
+
+def test_splitmix64_published_vectors(oracle_lib):
+    assert core.splitmix64(1234567, 5) == SPLITMIX_1234567
+    assert core.splitmix64(0, 1) == SPLITMIX_0
+
+
+def test_fill_normal_is_box_muller_of_the_draws(oracle_lib):
+    # tensor:fill("normal", mean, sd, seed) (src/lgml.c:3130-3136): value i
+    # takes draws 2i+1, 2i+2 as u = (draw >> 11) / 2^53 and is
+    # mean + sd sqrt(-2 ln u1) cos(2 pi u2), in double, stored as f32.
+    # The draws come from the splitmix64 pinned above; math.log / math.cos
+    # (the platform libm) give the closed form.
+    import math
+    for seed, mean, sd in ((1234567, 0.0, 0.02), (0, 1.5, 3.0), (20261201, -0.25, 1.0)):
+        n = 64
+        draws = core.splitmix64(seed, 2 * n)
+        got = core.fill_normal(n, mean, sd, seed)
+        par = core.gen_normal(n, mean, sd, seed)
+        for i in range(n):
+            u1 = (draws[2 * i] >> 11) / 2.0**53
+            u2 = (draws[2 * i + 1] >> 11) / 2.0**53
+            want = np.float32(mean + sd * math.sqrt(-2.0 * math.log(u1 if u1 > 0 else 1e-300)) *
+                              math.cos(6.283185307179586 * u2))
+            assert got[i] == want, (seed, i)
+            assert par[i] == want, (seed, i)  # the parallel generator: same values
+
+
 def test_splitmix_normal_statistics(oracle_lib):
     v = core.fill_normal(200_000, 0.0, 0.02, 99)
     assert abs(float(v.mean())) < 2e-4
