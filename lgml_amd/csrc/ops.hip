@@ -272,7 +272,12 @@ __global__ void swiglu_kernel(const float *__restrict__ gu, int64_t n, int64_t F
     int64_t r = e / F, c = e % F;
     double g = pend.splits ? pend.sum(r, c) : gu[r * 2 * F + c];
     double u = pend.splits ? pend.sum(r, F + c) : gu[r * 2 * F + F + c];
-    out[e] = (OutT)(float)(glu_act(g, gelu) * u);
+    float v = (float)(glu_act(g, gelu) * u);
+    // An f16 output is f16 of this f32 value. Left free, the compiler folds
+    // the two conversions into one f64 -> f16 rounding, which differs at
+    // f16 ties (rounding an arbitrary f64 value twice is not innocuous).
+    asm volatile("" : "+v"(v));
+    out[e] = (OutT)v;
   }
 }
 

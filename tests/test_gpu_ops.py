@@ -46,7 +46,8 @@ def argmax_dev(L, x):
     from lgml_amd import hip
     x = np.ascontiguousarray(x, np.float32)
     out = torch.empty(x.shape[0], dtype=torch.int32, device="cuda")
-    hip.check(L.lgmlh_argmax(dev(x).data_ptr(), x.shape[0], x.shape[1], out.data_ptr(), st()))
+    xd = dev(x)  # held: a freed temporary's memory goes to the next upload
+    hip.check(L.lgmlh_argmax(xd.data_ptr(), x.shape[0], x.shape[1], out.data_ptr(), st()))
     return out.cpu().numpy().tolist()
 
 
@@ -108,8 +109,9 @@ def test_set_rows_f16_bit_exact(L):
     src[0, :len(edge)] = edge
     ids = rng.choice(rows, n, replace=False).astype(np.int64)
     dst = torch.zeros((rows, row), dtype=torch.int16, device="cuda")
-    hip.check(L.lgmlh_set_rows_f16(dst.data_ptr(), rows, row, dev(src).data_ptr(),
-                                   dev(ids).data_ptr(), ids.ctypes.data, n, st()))
+    dsrc, dids = dev(src), dev(ids)
+    hip.check(L.lgmlh_set_rows_f16(dst.data_ptr(), rows, row, dsrc.data_ptr(), dids.data_ptr(),
+                                   ids.ctypes.data, n, st()))
     got = dst.cpu().numpy().view(np.uint16)
     want = np.zeros((rows, row), np.uint16)
     want[ids] = src.astype(np.float16).view(np.uint16)
@@ -119,12 +121,13 @@ def test_set_rows_f16_bit_exact(L):
     assert np.array_equal(got, ora)
     bad = ids.copy()
     bad[5] = rows
-    rc = L.lgmlh_set_rows_f16(dst.data_ptr(), rows, row, dev(src).data_ptr(),
-                              dev(bad).data_ptr(), bad.ctypes.data, n, st())
+    dbad = dev(bad)
+    rc = L.lgmlh_set_rows_f16(dst.data_ptr(), rows, row, dsrc.data_ptr(), dbad.data_ptr(),
+                              bad.ctypes.data, n, st())
     assert rc == hip.ERANGE
     bad[5] = -1
-    assert L.lgmlh_set_rows_f16(dst.data_ptr(), rows, row, dev(src).data_ptr(),
-                                dev(bad).data_ptr(), bad.ctypes.data, n, st()) == hip.ERANGE
+    assert L.lgmlh_set_rows_f16(dst.data_ptr(), rows, row, dsrc.data_ptr(), dbad.data_ptr(),
+                                bad.ctypes.data, n, st()) == hip.ERANGE
     assert np.array_equal(dst.cpu().numpy().view(np.uint16), want)  # nothing written
 
 
@@ -137,18 +140,19 @@ def test_rms_norm_f32_and_f16(L, n):
     w = rng.uniform(0.5, 1.5, n).astype(np.float32)
     want = core.rms_norm(x, 1e-6, w)
     out = torch.empty((rows, n), dtype=torch.float32, device="cuda")
-    hip.check(L.lgmlh_rms_norm(dev(x).data_ptr(), rows, n, 1e-6, dev(w).data_ptr(),
-                               out.data_ptr(), hip.F32, st()))
+    dx, dw = dev(x), dev(w)
+    hip.check(L.lgmlh_rms_norm(dx.data_ptr(), rows, n, 1e-6, dw.data_ptr(), out.data_ptr(),
+                               hip.F32, st()))
     got = out.cpu().numpy()
     assert rel_err(got, want) < 1e-6
     o16 = torch.empty((rows, n), dtype=torch.float16, device="cuda")
-    hip.check(L.lgmlh_rms_norm(dev(x).data_ptr(), rows, n, 1e-6, dev(w).data_ptr(),
-                               o16.data_ptr(), hip.F16, st()))
+    hip.check(L.lgmlh_rms_norm(dx.data_ptr(), rows, n, 1e-6, dw.data_ptr(), o16.data_ptr(),
+                               hip.F16, st()))
     g16 = o16.cpu().numpy().view(np.uint16).astype(np.int32)
     w16 = got.astype(np.float16).view(np.uint16).astype(np.int32)
     assert np.array_equal(g16, w16)  # f16 of the kernel's own f32 values
     # without a weight
-    hip.check(L.lgmlh_rms_norm(dev(x).data_ptr(), rows, n, 1e-5, None, out.data_ptr(), hip.F32,
+    hip.check(L.lgmlh_rms_norm(dx.data_ptr(), rows, n, 1e-5, None, out.data_ptr(), hip.F32,
                                st()))
     assert rel_err(out.cpu().numpy(), core.rms_norm(x, 1e-5)) < 1e-6
 
@@ -163,11 +167,12 @@ def test_swiglu_geglu(L, gelu):
     want = core.glu(gu[:, :F], gu[:, F:], gelu)
     fn = L.lgmlh_geglu if gelu else L.lgmlh_swiglu
     out = torch.empty((n, F), dtype=torch.float32, device="cuda")
-    hip.check(fn(dev(gu).data_ptr(), n, F, out.data_ptr(), hip.F32, st()))
+    dgu = dev(gu)
+    hip.check(fn(dgu.data_ptr(), n, F, out.data_ptr(), hip.F32, st()))
     got = out.cpu().numpy()
     assert rel_err(got, want) < 1e-6
     o16 = torch.empty((n, F), dtype=torch.float16, device="cuda")
-    hip.check(fn(dev(gu).data_ptr(), n, F, o16.data_ptr(), hip.F16, st()))
+    hip.check(fn(dgu.data_ptr(), n, F, o16.data_ptr(), hip.F16, st()))
     assert np.array_equal(o16.cpu().numpy().view(np.uint16),
                           got.astype(np.float16).view(np.uint16))
 
@@ -199,9 +204,9 @@ def test_qkv_rope_store(L, shape):
     dq = dev(qkv)
     keep = [dev(a) if a is not None else None for a in (ff, qn, kn)]
     p = [t.data_ptr() if t is not None else None for t in keep]
-    dc = dev(cells)
+    dc, dpos = dev(cells), dev(pos)
     hip.check(L.lgmlh_qkv_rope_store(dq.data_ptr(), n, H, Hkv, D, D, int(neox), base, p[0], p[1],
-                                     p[2], eps, dev(pos).data_ptr(), kp.data_ptr(), vp.data_ptr(),
+                                     p[2], eps, dpos.data_ptr(), kp.data_ptr(), vp.data_ptr(),
                                      n_cells, dc.data_ptr(), q_out.data_ptr(), st()))
     q = qkv[:, :H * D].reshape(n * H, D)
     k = qkv[:, H * D:(H + Hkv) * D].reshape(n * Hkv, D)
@@ -231,9 +236,9 @@ def test_qkv_rope_store(L, shape):
     for which, pool in ((0, kp), (1, vp)):
         sel = others[::7]
         out = torch.empty((len(sel), Hkv * D), dtype=torch.int16, device="cuda")
-        hip.check(L.lgmlh_kv_gather(pool.data_ptr(), which, n_cells, Hkv, D,
-                                    dev(sel.astype(np.int64)).data_ptr(), len(sel),
-                                    out.data_ptr(), st()))
+        dsel = dev(sel.astype(np.int64))
+        hip.check(L.lgmlh_kv_gather(pool.data_ptr(), which, n_cells, Hkv, D, dsel.data_ptr(),
+                                    len(sel), out.data_ptr(), st()))
         assert not out.cpu().numpy().any()
 
 
@@ -254,13 +259,14 @@ def test_get_rows(L, ty):
     ids = rng.integers(0, rows, n).astype(np.int32)
     ids[:3] = [0, rows - 1, 0]
     out = torch.empty((n, cols), dtype=torch.float32, device="cuda")
-    dt = dev(table)
-    hip.check(L.lgmlh_get_rows(ty, dt.data_ptr(), rows, cols, dev(ids).data_ptr(), ids.ctypes.data,
+    dt, dids = dev(table), dev(ids)
+    hip.check(L.lgmlh_get_rows(ty, dt.data_ptr(), rows, cols, dids.data_ptr(), ids.ctypes.data,
                                n, out.data_ptr(), st()))
     assert np.array_equal(out.cpu().numpy().view(np.uint32), deq[ids].view(np.uint32))
     bad = ids.copy()
     bad[9] = rows
-    assert L.lgmlh_get_rows(ty, dt.data_ptr(), rows, cols, dev(bad).data_ptr(), bad.ctypes.data,
+    dbad = dev(bad)
+    assert L.lgmlh_get_rows(ty, dt.data_ptr(), rows, cols, dbad.data_ptr(), bad.ctypes.data,
                             n, out.data_ptr(), st()) == hip.ERANGE
 
 
