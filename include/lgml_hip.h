@@ -279,6 +279,18 @@ int lgmlh_mul_mat(int type, const void *w, int64_t M, int64_t K, const void *x, 
     int64_t N, float *y, int epi, const float *residual, void *workspace, size_t ws_bytes,
     void *stream);
 
+/* lgmlh_mul_mat without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, serving loops that forbid
+ * hipMalloc). It has no counterpart in the reference. The workspace lives
+ * in a static device array of lgmlh_mul_mat_noalloc_limit() bytes (32 MiB)
+ * that each GPU holds until the process ends; a product whose
+ * lgmlh_mul_mat_workspace exceeds it fails with LGMLH_ENOMEM. Calls that
+ * overlap on one GPU (other streams or threads) race for the array.
+ * Results are those of lgmlh_mul_mat, bit for bit. */
+size_t lgmlh_mul_mat_noalloc_limit(void);
+int lgmlh_mul_mat_noalloc(int type, const void *w, int64_t M, int64_t K, const void *x,
+    int xtype, int64_t N, float *y, int epi, const float *residual, void *stream);
+
 /* ===================================================================== *
  * Routed experts (qwen3moe): the router of M.moe (transformer.lua:
  * 1989-2027) and graph:mul_mat_id (src/ops_nn.c:322-362) with the weighted

@@ -21,6 +21,8 @@
 // N, so a row gives the same bits alone or batched. K is split over
 // workgroups when M alone gives too few (split count from M and K only);
 // the splits are added in a fixed order by a second kernel.
+#include <mutex>
+
 #include "common.h"
 #include "quant.h"
 #include "split.h"
@@ -929,4 +931,65 @@ extern "C" int lgmlh_mul_mat(int type, const void *w, int64_t M, int64_t K, cons
   LGMLH_TRY(split_x(x, xtype, N, K, xs, st));
   return mul_mat_split(type, w, M, K, xs, N, y, M, res, (float *)((char *)workspace + xb),
                        ws_bytes - xb, st, nullptr);
+}
+
+// ---- the entry point that allocates nothing -----------------------------------
+// lgmlh_mul_mat_noalloc runs lgmlh_mul_mat's kernels with their workspace
+// (the split X planes and the split-K partial sums) in `scratch`, a
+// file-scope device array, instead of a caller's workspace: for callers
+// that cannot allocate (code under HIP graph capture, serving loops that
+// forbid hipMalloc). Every GPU the library runs on holds its own copy of
+// the array until the process ends. In host code `scratch` names a host
+// stand-in, never a device address: the device address comes from
+// hipGetSymbolAddress, once per device with that device current, and only
+// that address reaches kernels. Nothing in the workspace needs to start at
+// zero (every byte a kernel reads was written by the same call), so no call
+// clears it. Calls that overlap on one GPU (two streams, two threads) race
+// for the array.
+namespace lgmlh {
+constexpr size_t SCRATCH_BYTES = size_t(32) << 20;  // 32 MiB per GPU
+static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+
+// The device address of this device's scratch, or nullptr (error set).
+static void *scratch_ptr() {
+  constexpr int MAX_DEV = 64;
+  static std::mutex mu;
+  static void *ptrs[MAX_DEV];
+  int dev = 0;
+  if (hip_check(hipGetDevice(&dev), "mul_mat_noalloc: device") != LGMLH_OK) return nullptr;
+  if (dev < 0 || dev >= MAX_DEV) {
+    set_error("mul_mat_noalloc: device %d past the %d this library tracks", dev, MAX_DEV);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void *p = nullptr;
+    if (hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "mul_mat_noalloc: scratch") !=
+        LGMLH_OK)
+      return nullptr;
+    ptrs[dev] = p;
+  }
+  return ptrs[dev];
+}
+}  // namespace lgmlh
+
+extern "C" size_t lgmlh_mul_mat_noalloc_limit(void) { return SCRATCH_BYTES; }
+
+extern "C" int lgmlh_mul_mat_noalloc(int type, const void *w, int64_t M, int64_t K,
+                                     const void *x, int xtype, int64_t N, float *y, int epi,
+                                     const float *residual, void *stream) {
+  if (type != LGMLH_F32 && (M <= 0 || K <= 0 || N < 0 || K % QK_K)) {
+    set_error("mul_mat_noalloc: bad shape (M %lld, K %lld, N %lld)", (long long)M,
+              (long long)K, (long long)N);
+    return LGMLH_EINVAL;
+  }
+  const size_t need = type == LGMLH_F32 ? 0 : workspace_for(type, M, K, N);
+  if (need > SCRATCH_BYTES) {
+    set_error("mul_mat_noalloc: this product needs %zu bytes of workspace; the static scratch "
+              "holds %zu (use lgmlh_mul_mat with a workspace)", need, SCRATCH_BYTES);
+    return LGMLH_ENOMEM;
+  }
+  void *ws = scratch_ptr();
+  if (!ws) return LGMLH_EHIP;
+  return lgmlh_mul_mat(type, w, M, K, x, xtype, N, y, epi, residual, ws, SCRATCH_BYTES, stream);
 }

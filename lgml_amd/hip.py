@@ -31,6 +31,7 @@ SYMBOLS = (
     "lgmlh_kvpool_longest_kid", "lgmlh_kvpool_set_cap", "lgmlh_kvpool_stats", "lgmlh_block_key",
     "lgmlh_gen_normal", "lgmlh_moe_route", "lgmlh_mul_mat_id_workspace", "lgmlh_mul_mat_id",
     "lgmlh_moe_sum", "lgmlh_plan_ring", "lgmlh_geglu", "lgmlh_softcap",
+    "lgmlh_mul_mat_noalloc_limit", "lgmlh_mul_mat_noalloc",
 )
 GATING_SOFTMAX, GATING_SIGMOID = 1, 2
 TRACE_ATTN, TRACE_GEMM, TRACE_EXPERTS = 1, 2, 4
@@ -136,6 +137,8 @@ def _declare(L):
         "lgmlh_dequantize": ([i32, vp, i64, i64, vp, vp], i32),
         "lgmlh_mul_mat_workspace": ([i32, i64, i64, i64], sz),
         "lgmlh_mul_mat": ([i32, vp, i64, i64, vp, i32, i64, vp, i32, vp, vp, sz, vp], i32),
+        "lgmlh_mul_mat_noalloc_limit": ([], sz),
+        "lgmlh_mul_mat_noalloc": ([i32, vp, i64, i64, vp, i32, i64, vp, i32, vp, vp], i32),
         "lgmlh_get_rows": ([i32, vp, i64, i64, vp, vp, i64, vp, vp], i32),
         "lgmlh_rms_norm": ([vp, i64, i64, C.c_float, vp, vp, i32, vp], i32),
         "lgmlh_qkv_rope_store": ([vp, i64, i32, i32, i32, i32, i32, C.c_float, vp, vp, vp,
