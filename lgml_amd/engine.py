@@ -6,9 +6,8 @@ copy-on-write of a shared partial block, here a device block copy),
 share (:1116-1123), seq_cells (:1126-1133) -- over the native pool
 bookkeeping (lgml_amd.kvpool). Engine.flush restates E:flush
 (lua/lgml/engine.lua:1423-1506): the pending decode steps and prompt
-chunks of all slots run as one pass, blocks are taken for each entry in
-arrival order first, and an entry that gets no block fails alone with
-"kv pool full". Prompts go in chunks of at most ubatch tokens
+chunks of all slots run as one pass, and blocks are taken for each entry
+in arrival order first (a full pool: see below). Prompts go in chunks of at most ubatch tokens
 (E:prefill_batched, :2213-2255, ubatch 512, :57). Greedy sampling is the
 first maximum (src/sample.c:914-925) on the device.
 
@@ -34,6 +33,22 @@ A model with sliding-window layers gives each slot a ring of its own in
 the ring pools (M:cache's per-slot rings, transformer.lua:575-600): slot
 i owns ring blocks i R .. i R + R - 1, R = ring_cells / 64 / n_slots, and
 a request holds a slot from submit to finish.
+
+A full pool makes a request wait, not end (E:flush, E:victim, E:preempt,
+engine.lua:1193-1243,1410-1448): when an entry gets no block, a running
+request of lower priority (the lowest, the least recently started) lets
+its cells go and the entry runs in a later pass; with no such request,
+the entry's own request lets its cells go and waits, unless it runs
+alone (then its reply ends with "kv pool full"). A request that lets its
+cells go publishes the keys of its blocks (E:publish_tail, :1906-1918),
+gives up its slot and waits; when another request ends it takes a slot
+again, attaches what is still cached of its tokens (pool or RAM store)
+and runs the rest. The reference's E:pool_pressure (:1122-1140) first
+takes the cells of idle slots; here a request that ends gives its blocks
+back at once (keyed ones stay cached and are evicted first), so no idle
+slot holds cells. Paged-pool models only: a sliding-window ring cannot
+be rebuilt from cached blocks (the reference checkpoints it), so there a
+full pool ends the request.
 """
 import ctypes as C
 
@@ -227,9 +242,15 @@ class Request:
         self.prio = prio
         self.out = []
         self.seq = None
-        self.fed = 0       # prompt tokens run so far
+        # the tokens to run before decoding: the prompt, or after a wait the
+        # tokens so far and the rest (E:preempt's toks)
+        self.feed = list(prompt)
+        self.fed = 0       # feed tokens run so far
         self.err = None
         self.done = False
+        self.preempt = False  # lets its cells go at the next chance
+        self.started = 0      # submit order (E:victim: the least recently started)
+        self.waits = 0        # times it let its cells go
         # run-ahead engines: sampled tokens of passes not yet read back, the
         # (pass, row) holding the latest one on the device, and whether the
         # request takes part in no further pass
@@ -239,9 +260,17 @@ class Request:
 
     def pending(self, ubatch):
         """The ids of this request's next pass: a prompt chunk or one token."""
-        if self.fed < len(self.prompt):
-            return self.prompt[self.fed:self.fed + ubatch]
+        if self.fed < len(self.feed):
+            return self.feed[self.fed:self.fed + ubatch]
         return [self.out[-1]]
+
+    def history(self):
+        """(the tokens whose cells the sequence holds, the tokens that did
+        not run) with no pass in flight: the feed run so far and the fed
+        samples; the rest of the feed, or the last sample."""
+        if self.fed < len(self.feed):
+            return self.feed[:self.fed], self.feed[self.fed:]
+        return self.feed + self.out[:-1], self.out[-1:]
 
 
 class _Half:
@@ -307,6 +336,13 @@ class Engine:
         self.ram = RamStore(ram) if ram > 0 and prefix_cache else None
         self.infos = {}  # key -> (parent, depth, tokens) of the blocks published here
         self.from_ram = 0
+        # requests that let their cells go, in the order they did, and the
+        # counts of E:preempt (engine.lua:1203-1206)
+        self.waiting = []
+        self.preemptions = 0
+        self.waits = {}
+        self._ended = 0     # requests that ended since the waiting ones last tried
+        self._submitted = 0
         if self.ram is not None:
             self.seqs.on_evict = self.spill_block
 
@@ -315,6 +351,8 @@ class Engine:
             raise RuntimeError("no free slot")
         req.slot = self.free_slots.pop(0)
         req.seq = Seq(self.seqs, req.prio)
+        self._submitted += 1
+        req.started = self._submitted
         self.active.append(req)
         if self.prefix_cache:
             req.fed = self.attach(req)
@@ -376,7 +414,7 @@ class Engine:
     def attach(self, req):
         """E:attach_blocks (engine.lua:2038-2077) for a new request: returns
         the number of prompt tokens already in the cache."""
-        prompt, c, alloc = req.prompt, req.seq, self.seqs.alloc
+        prompt, c, alloc = req.feed, req.seq, self.seqs.alloc
         max_ = len(prompt) - 1  # at least one prompt token must run
         blocks, keys = self.cached_blocks(prompt, max_, c.prio)
         try:
@@ -406,13 +444,18 @@ class Engine:
     def publish(self, req):
         """E:publish (engine.lua:1829-1841): keys for the full prompt blocks
         of the request that have none yet."""
+        self.publish_tokens(req, req.feed)
+
+    def publish_tokens(self, req, tokens):
+        """Keys for the full blocks of the sequence's tokens (a prefix of
+        tokens) that have none yet."""
         c, alloc = req.seq, self.seqs.alloc
-        upto = min(c.n_past, len(req.prompt)) // BLOCK
+        upto = min(c.n_past, len(tokens)) // BLOCK
         for i in range(len(c.keys) + 1, upto + 1):
             parent = c.keys[i - 2] if i >= 2 else ROOT_KEY
-            k = kvpool.key(parent, req.prompt, (i - 1) * BLOCK + 1, BLOCK)
+            k = kvpool.key(parent, tokens, (i - 1) * BLOCK + 1, BLOCK)
             c.keys.append(k)
-            toks = req.prompt[(i - 1) * BLOCK:i * BLOCK]
+            toks = tokens[(i - 1) * BLOCK:i * BLOCK]
             if alloc.publish(c.blocks[i - 1], k, parent, i, toks, c.prio):
                 self.infos[k] = (parent, i, list(toks))
 
@@ -421,6 +464,82 @@ class Engine:
         self.free_slots.append(req.slot)
         req.done = True
         self.active.remove(req)
+        self._ended += 1
+
+    # -- a full pool ------------------------------------------------------------
+    def victim(self, req):
+        """E:victim (engine.lua:1410-1420): a running request of lower
+        priority than req whose cells can go: the lowest priority, the least
+        recently started first; or None."""
+        best = None
+        for q in self.active:
+            if (q is not req and not q.preempt and not q.finishing and q.prio < req.prio and
+                    (best is None or (q.prio, q.started) < (best.prio, best.started))):
+                best = q
+        return best
+
+    def on_full(self, req, err):
+        """An entry of req got no block (E:flush, engine.lua:1436-1448, and
+        the callers of E:preempt, :2230-2233,3178-3187): a running request of
+        lower priority lets its cells go and req runs in a later pass; with
+        none, req itself lets its cells go and waits, or, alone or on a model
+        with rings, its reply ends. Returns True when req ended."""
+        v = self.victim(req)
+        if v is not None:
+            v.preempt = True
+            return False
+        running = sum(1 for q in self.active if not q.preempt and not q.finishing)
+        if running < 2 or self.ring_blocks:
+            req.err = str(err)
+            return True
+        req.preempt = True
+        return False
+
+    def publish_tail(self, req, tokens):
+        """E:publish_tail (engine.lua:1906-1918): keys for the full blocks of
+        the sequence's tokens, and the partial-block marker of its last
+        block, so that the request finds its cells again."""
+        c, alloc = req.seq, self.seqs.alloc
+        self.publish_tokens(req, tokens)
+        n = min(c.n_past, len(tokens))
+        i = n // BLOCK  # the partial block's index (0-based)
+        if n % BLOCK and i < len(c.blocks) and len(c.keys) == i:
+            alloc.publish_part(c.blocks[i], c.keys[i - 1] if i else ROOT_KEY, i + 1,
+                               tokens[i * BLOCK:n], c.prio)
+
+    def let_go(self, req):
+        """E:preempt (engine.lua:1193-1243), with no pass of req in flight: it
+        publishes its blocks' keys, lets its cells and slot go and waits;
+        its feed becomes its tokens so far and the rest."""
+        hist, rest = req.history()
+        assert req.seq.n_past == len(hist), (req.seq.n_past, len(hist))
+        self.publish_tail(req, hist)
+        self.seqs.free(req.seq)
+        self.free_slots.append(req.slot)
+        self.active.remove(req)
+        req.seq, req.slot = None, None
+        req.feed, req.fed = hist + rest, 0
+        req.preempt = req.finishing = False
+        req.tok_src = None
+        req.waits += 1
+        self.waiting.append(req)
+        self.preemptions += 1
+        self.waits[req.prio] = self.waits.get(req.prio, 0) + 1
+
+    def resume(self):
+        """The waiting requests take a slot again once another request has
+        ended (E:preempt's wait, engine.lua:1223-1242): each attaches what is
+        still cached of its tokens and runs the rest."""
+        if not self.waiting or not self._ended:
+            return
+        self._ended = 0
+        while self.waiting and self.free_slots:
+            req = self.waiting.pop(0)
+            req.slot = self.free_slots.pop(0)
+            req.seq = Seq(self.seqs, req.prio)
+            self.active.append(req)
+            req.fed = self.attach(req)
+            req.seq.n_past = req.fed
 
     def step(self):
         """One pass over every active request; returns the requests that got
@@ -448,18 +567,24 @@ class Engine:
     def _launch(self):
         """Plan and queue one pass from the launched state (positions and
         prompt progress advance at launch); None when nothing runs."""
+        # requests that must let their cells go do so once nothing of theirs
+        # is in flight; then the waiting ones may come back
+        for r in [q for q in self.active if q.preempt and not q.finishing and not q.n_inflight]:
+            self.let_go(r)
+        self.resume()
         entries = []
         left = self.max_tokens if self.max_tokens else 1 << 62
-        n_dec = sum(1 for r in self.active if not r.finishing and r.fed >= len(r.prompt))
+        n_dec = sum(1 for r in self.active
+                    if not r.finishing and not r.preempt and r.fed >= len(r.feed))
         for r in list(self.active):
-            if r.finishing:
+            if r.finishing or r.preempt:
                 continue
             src = None
-            if r.fed < len(r.prompt):
+            if r.fed < len(r.feed):
                 room = left - n_dec
                 if room <= 0:
                     continue
-                ids = r.prompt[r.fed:r.fed + min(self.ubatch, room)]
+                ids = r.feed[r.fed:r.fed + min(self.ubatch, room)]
             else:
                 n_dec -= 1
                 if r.tok_src is not None:
@@ -470,13 +595,18 @@ class Engine:
             try:
                 self.seqs.reserve(r.seq, r.seq.n_past + len(ids))
             except PoolFull as e:
-                r.err = str(e)
-                if r.n_inflight:
-                    r.finishing = True
-                else:
-                    self.finish(r)
+                if self.on_full(r, e):
+                    if r.n_inflight:
+                        r.finishing = True
+                    else:
+                        self.finish(r)
                 continue
             entries.append((r, ids, src))
+        # a request whose cells must go drops out of the pass (E:flush,
+        # engine.lua:1450-1456)
+        entries = [e for e in entries if not e[0].preempt]
+        for r in [q for q in self.active if q.preempt and not q.finishing and not q.n_inflight]:
+            self.let_go(r)
         if not entries:
             return None
         groups = [entries]
@@ -504,11 +634,11 @@ class Engine:
         for h in p.halves:
             for row, (r, x, _) in enumerate(h.entries):
                 r.seq.n_past += len(x)
-                prompt = r.fed < len(r.prompt)
+                prompt = r.fed < len(r.feed)
                 sampled = True
                 if prompt:
                     r.fed += len(x)
-                    sampled = r.fed >= len(r.prompt)  # mid-prompt chunk: not sampled
+                    sampled = r.fed >= len(r.feed)  # mid-prompt chunk: not sampled
                 if sampled:
                     r.n_inflight += 1
                     r.tok_src = (h, row)
@@ -582,8 +712,8 @@ class Engine:
         for r, _, prompt, sampled, h, row in p.entries:
             if r.done:
                 continue  # ended at launch (a pool-full reserve) with only a prompt chunk in flight
-            if prompt and self.prefix_cache:
-                self.publish(r)
+            if prompt and self.prefix_cache and r.seq is not None:
+                self.publish(r)  # (a request that let its cells go has no sequence)
             if sampled:
                 r.out.append(int(toks[id(h)][row]))
                 r.n_inflight -= 1
@@ -609,12 +739,15 @@ class Engine:
         self._last_halves = None
 
     def _step_sync(self):
+        self.resume()
         entries = []
         left = self.max_tokens if self.max_tokens else 1 << 62
-        n_dec = sum(1 for r in self.active if r.fed >= len(r.prompt))
+        n_dec = sum(1 for r in self.active if r.fed >= len(r.feed))
         for r in list(self.active):
+            if r.preempt:
+                continue
             ids = r.pending(self.ubatch)
-            if r.fed < len(r.prompt):
+            if r.fed < len(r.feed):
                 # a prompt chunk takes what the decode tokens leave
                 room = left - n_dec
                 if room <= 0:
@@ -626,10 +759,15 @@ class Engine:
             try:
                 self.seqs.reserve(r.seq, r.seq.n_past + len(ids))
             except PoolFull as e:
-                r.err = str(e)
-                self.finish(r)
+                if self.on_full(r, e):
+                    self.finish(r)
                 continue
             entries.append((r, ids))
+        # the requests whose cells go drop out of the pass and wait (E:flush,
+        # engine.lua:1450-1456)
+        for r in [q for q in self.active if q.preempt]:
+            self.let_go(r)
+        entries = [(r, ids) for r, ids in entries if r.seq is not None]
         if not entries:
             return []
         seq_n = [len(ids) for _, ids in entries]
@@ -661,11 +799,11 @@ class Engine:
         got = []
         for (r, x), tok in zip(entries, nxt):
             r.seq.n_past += len(x)
-            if r.fed < len(r.prompt):
+            if r.fed < len(r.feed):
                 r.fed += len(x)
                 if self.prefix_cache:
                     self.publish(r)
-                if r.fed < len(r.prompt):
+                if r.fed < len(r.feed):
                     continue  # mid-prompt chunk: its logits are not sampled
             r.out.append(int(tok))
             got.append(r)

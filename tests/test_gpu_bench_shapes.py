@@ -1,0 +1,141 @@
+"""Parity at the benchmark's own shapes: one decode pass of the forward at
+full width against the oracle, with the same synthetic KV on both sides.
+
+- C2: 64 slots at the bench's LCG contexts U[128, 4096]
+  (bench.py's draw order and seed), Llama-3-8B width, Q4_K_M, 1 layer.
+- C5: 64 slots at contexts U[256, 8192], the 30B-A3B-shaped
+  qwen3moe width (128 experts of 768, top-8), Q4_K, 1 layer.
+- C4: 32 slots at contexts U[1024, 16384], the Gemma-4-style
+  width (heads of 256, Q8_0, vocab 262144, softcap), a sliding layer (its
+  1024-token window through each slot's ring) and a global layer.
+
+Every cell a pass reads holds the same random f16 K / V on both sides (the
+device pools are written through lgmlh_kv_store from the oracle's f16
+values, exact). Logits must be within 2e-3 max relative error of the
+oracle's and the greedy ids identical.
+"""
+import numpy as np
+import pytest
+
+from oracle import core, models
+from tests.gpu_util import Schedule, rel_err
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def bench_contexts(seed, S, lo, hi, V):
+    """bench.py's initial requests: per slot a prompt length U[lo, hi], its
+    ids, a budget and the part of it left (the same LCG draws)."""
+    from lgml_amd import workload
+    rng = workload.Lcg(seed)
+    out = []
+    for _ in range(S):
+        n = rng.int(lo, hi)
+        for _ in range(n):
+            rng.int(0, V - 1)
+        b = rng.int(64, 2048)
+        rng.int(1, b)
+        out.append(n)
+    return out
+
+
+def fill_both(L, gm, kp, vp, layer, cells, rng, ring):
+    """Random f16 K / V at cells of a layer, in the oracle pools and (through
+    lgmlh_kv_store) the device pools."""
+    from lgml_amd import hip
+    row = kp[layer].shape[1]
+    k = rng.uniform(-1, 1, (len(cells), row)).astype(np.float16)
+    v = rng.uniform(-1, 1, (len(cells), row)).astype(np.float16)
+    kp[layer][cells] = k.view(np.uint16)
+    vp[layer][cells] = v.view(np.uint16)
+    kd = torch.from_numpy(k.astype(np.float32)).cuda()
+    vd = torch.from_numpy(v.astype(np.float32)).cuda()
+    cd = torch.from_numpy(cells.astype(np.int64)).cuda()
+    n = gm.ring_cells if ring else gm.n_cells
+    hip.check(L.lgmlh_kv_store(gm.kpools[layer].data_ptr(), gm.vpools[layer].data_ptr(), n,
+                               gm.hp["n_head_kv"], gm.hp["head_dim"], kd.data_ptr(), vd.data_ptr(),
+                               cd.data_ptr(), cells.ctypes.data, len(cells),
+                               torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+
+
+def decode_pass(hp, w, contexts, seed, ring_blocks=0):
+    from lgml_amd import hip, runtime
+    L = hip.lib()
+    S = len(contexts)
+    nbs = [(c + 1 + 63) // 64 for c in contexts]
+    n_cells = sum(nbs) * 64
+    ring_cells = S * ring_blocks * 64
+    cap = max(n_cells, ring_cells)
+    gm = runtime.DeviceModel(hp, w, n_cells, ring_cells=ring_cells)
+    om = core.OracleModel(hp, w)
+    row = hp["n_head_kv"] * hp["head_dim"]
+    kp = [np.zeros((cap, row), np.uint16) for _ in range(hp["n_layer"])]
+    vp = [np.zeros((cap, row), np.uint16) for _ in range(hp["n_layer"])]
+    sch = Schedule(n_cells // 64, S)
+    for s, c in enumerate(contexts):
+        sch.grow(s, c + 1)
+    bt = sch.table(list(range(S)))
+    rt = None
+    if ring_blocks:
+        rt = np.arange(S * ring_blocks, dtype=np.int32).reshape(S, ring_blocks)
+    rng = np.random.default_rng(seed)
+    swa = gm.swa
+    for il in range(hp["n_layer"]):
+        if swa[il]:
+            # the ring cells of the window's positions (p % ring)
+            win = hp["n_swa"]
+            cells = []
+            for s, c in enumerate(contexts):
+                for p in range(max(0, c - win + 1), c):
+                    cells.append(rt[s, (p // 64) % ring_blocks] * 64 + p % 64)
+            fill_both(L, gm, kp, vp, il, np.array(cells, np.int64), rng, True)
+        else:
+            cells = np.concatenate([np.arange(c) + 0 for c in contexts])
+            cells = np.concatenate([bt[s, np.arange(c) // 64] * 64 + np.arange(c) % 64
+                                    for s, c in enumerate(contexts)]).astype(np.int64)
+            fill_both(L, gm, kp, vp, il, cells, rng, False)
+    ids = rng.integers(0, hp["n_vocab"], S).astype(np.int32)
+    plan = gm.plan([1] * S, contexts, bt, ids, ring_tab=rt)
+    lg = gm.forward(plan).cpu().numpy()
+    b = core.BatchDesc([1] * S, contexts, bt, 64, ids, plan.logit_rows, ring_tab=rt)
+    lo = om.forward(kp, vp, b)
+    return lg, lo
+
+
+def check(lg, lo, name):
+    err = rel_err(lg, lo)
+    ga = [int(np.argmax(r)) for r in lg]
+    oa = [core.argmax(r) for r in lo]
+    print("%s: %d rows, max rel err %.3g" % (name, len(lg), err), flush=True)
+    assert err < 2e-3, err
+    assert ga == oa
+
+
+def test_c2_bench_shape_decode_pass():
+    hp, w = models.build("c2", seed=41, n_layer=1, init="normal")
+    ctx = bench_contexts(20261201, 64, 128, 4096, hp["n_vocab"])
+    assert 128 <= min(ctx) and max(ctx) <= 4096
+    lg, lo = decode_pass(hp, w, ctx, 42)
+    check(lg, lo, "c2 width, 64 slots")
+
+
+def test_c5_bench_shape_decode_pass():
+    hp, w = models.build("c5", seed=51, n_layer=1, init="normal")
+    ctx = bench_contexts(20261201, 64, 256, 8192, hp["n_vocab"])
+    lg, lo = decode_pass(hp, w, ctx, 52)
+    check(lg, lo, "c5 width, 64 slots")
+
+
+def test_c4_bench_shape_decode_pass():
+    from lgml_amd import workload
+    # layer 0 slides (1024-token window through the rings), layer 1 is global
+    shape = dict(models.SHAPES["c4"], swa_period=2)
+    hp, w = models.build(shape, seed=61, n_layer=2, init="normal")
+    hp["n_swa"] = shape["n_swa"]
+    ctx = bench_contexts(20261201, 32, 1024, 16384, hp["n_vocab"])
+    R = workload.ring_blocks(hp, 1)
+    lg, lo = decode_pass(hp, w, ctx, 62, ring_blocks=R)
+    check(lg, lo, "c4 width, 32 slots, sliding + global")
