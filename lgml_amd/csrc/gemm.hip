@@ -146,9 +146,6 @@ __device__ __forceinline__ f16x2 fma2(f16x2 a, f16 s, f16 c) {
 __device__ __forceinline__ f16x8 cat4(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
   return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
-__device__ __forceinline__ f16 byte_f16(uint32_t w, int k) {
-  return (f16)(float)((w >> (8 * k)) & 0xffu);
-}
 
 template <int TYPE>
 struct WFrag;
@@ -158,13 +155,13 @@ struct WFrag<LGMLH_Q4_K> {
   u32x4 dm;               // d | dmin << 16 of rows 4c + i, i = 0..3
   uint32_t s0, s1, s2;    // the 12 scale bytes of row r
   u32x4 qs[2];            // 4 pieces of 8 bytes
-  __device__ __forceinline__ void load(const uint8_t *ch, int lane) {
-    dm = *(const u32x4 *)(ch + 16 * (lane >> 4));
-    const uint32_t *sp = (const uint32_t *)(ch + 64 + 12 * (lane & 15));
+  __device__ __forceinline__ void load(const uint8_t *ch, uint32_t lane) {
+    dm = *(const u32x4 *)(ch + 16u * (lane >> 4));
+    const uint32_t *sp = (const uint32_t *)(ch + 64u + 12u * (lane & 15));
     s0 = sp[0];
     s1 = sp[1];
     s2 = sp[2];
-    const u32x4 *p = (const u32x4 *)(ch + 256 + lane * 32);
+    const u32x4 *p = (const u32x4 *)(ch + 256u + lane * 32u);
     qs[0] = p[0];
     qs[1] = p[1];
   }
@@ -178,25 +175,33 @@ struct WFrag<LGMLH_Q4_K> {
   __device__ __forceinline__ uint32_t m47() const {
     return ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
   }
-  // sc_g * q for k = 32g + 8c + e, e = 0..7 (<= 945, exact). scb holds the
-  // scales of g's half (sc03 or sc47). Low nibbles: (1024 + q) sc - 1024 sc;
-  // high nibbles kept in place: (1024 + 16 q) sc / 16 - 64 sc.
-  __device__ __forceinline__ f16x8 frag(int g, uint32_t scb) const {
+  // The multipliers of groups 2j (low nibbles) and 2j + 1 (high nibbles):
+  // s = {sc_2j, sc_2j+1 / 16}, cc = {-1024 sc_2j, -64 sc_2j+1} (all exact
+  // in f16), from the scale bytes of g's half (sc03 or sc47) by one
+  // permute and packed f16 arithmetic.
+  __device__ __forceinline__ void pair(int j, uint32_t scb, f16x2 &s, f16x2 &cc) const {
+    const f16x2 sc = biased(scb, (j & 1) ? SEL_23 : SEL_01) - f16x2{(f16)1024.0f, (f16)1024.0f};
+    s = sc * f16x2{(f16)1.0f, (f16)0.0625f};
+    cc = sc * f16x2{(f16)-1024.0f, (f16)-64.0f};
+  }
+  // sc_g * q for k = 32g + 8c + e, e = 0..7 (<= 945, exact), with s / cc
+  // of g's pair. Low nibbles: (1024 + q) sc - 1024 sc; high nibbles kept
+  // in place: (1024 + 16 q) sc / 16 - 64 sc.
+  __device__ __forceinline__ f16x8 frag(int g, f16x2 sp, f16x2 cp) const {
     const int j = g >> 1;
     const uint32_t w0 = qs[j >> 1][2 * (j & 1)], w1 = qs[j >> 1][2 * (j & 1) + 1];
-    const f16 scf = byte_f16(scb, g & 3);
     uint32_t n0, n1;
     f16 s, cc;
     if (g & 1) {
       n0 = w0 & 0xF0F0F0F0u;
       n1 = w1 & 0xF0F0F0F0u;
-      s = scf * (f16)0.0625f;
-      cc = scf * (f16)-64.0f;
+      s = sp[1];
+      cc = cp[1];
     } else {
       n0 = w0 & 0x0F0F0F0Fu;
       n1 = w1 & 0x0F0F0F0Fu;
-      s = scf;
-      cc = scf * (f16)-1024.0f;
+      s = sp[0];
+      cc = cp[0];
     }
     return cat4(fma2(biased(n0, SEL_01), s, cc), fma2(biased(n0, SEL_23), s, cc),
                 fma2(biased(n1, SEL_01), s, cc), fma2(biased(n1, SEL_23), s, cc));
@@ -217,10 +222,10 @@ struct WFrag<LGMLH_Q6_K> {
   u32x4 scl;       // the 16 int8 scales of row r
   u32x4 ql[2];     // ql pieces (h, tb), index 2h + tb
   u32x4 qh;        // qh pieces h
-  __device__ __forceinline__ void load(const uint8_t *ch, int lane) {
-    d4 = *(const u32x2 *)(ch + 8 * (lane >> 4));
-    scl = *(const u32x4 *)(ch + 32 + 16 * (lane & 15));
-    const u32x4 *p = (const u32x4 *)(ch + 288 + lane * 48);
+  __device__ __forceinline__ void load(const uint8_t *ch, uint32_t lane) {
+    d4 = *(const u32x2 *)(ch + 8u * (lane >> 4));
+    scl = *(const u32x4 *)(ch + 32u + 16u * (lane & 15));
+    const u32x4 *p = (const u32x4 *)(ch + 288u + lane * 48u);
     ql[0] = p[0];
     ql[1] = p[1];
     qh = p[2];
@@ -259,8 +264,8 @@ struct WFrag<LGMLH_Q6_K> {
 template <>
 struct WFrag<LGMLH_Q8_0> {
   u32x4 qs[4];           // 8 blocks x 8 int8 (the header goes through LDS)
-  __device__ __forceinline__ void load(const uint8_t *ch, int lane) {
-    const u32x4 *p = (const u32x4 *)(ch + 256 + lane * 64);
+  __device__ __forceinline__ void load(const uint8_t *ch, uint32_t lane) {
+    const u32x4 *p = (const u32x4 *)(ch + 256u + lane * 64u);
 #pragma unroll
     for (int i = 0; i < 4; i++) qs[i] = p[i];
   }
@@ -353,11 +358,13 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   constexpr int XJ = X_SLOTS / (GEMM_WAVES * 64);  // NCT
   const f16 *xhi = xs + n0 * K + sb_lo * QK_K, *xlo = xhi + Npad * K;
   const f16 *ghi = xs + 2 * Npad * K + n0 * (K / 32) + sb_lo * 8, *glo = ghi + Npad * (K / 32);
+  // byte offsets of a lane's pieces from the plane's K step (the planes
+  // stay under 4 GiB: checked at launch)
   uint32_t xoff[XJ];
 #pragma unroll
   for (int j = 0; j < XJ; j++) {
     const int sl = (wave * XJ + j) * 64 + lane, n = sl >> 5, kp = (sl & 31) ^ (n & 15);
-    xoff[j] = (uint32_t)(xrow(n) * K + kp * 8);
+    xoff[j] = (uint32_t)(xrow(n) * K + kp * 8) * 2u;
   }
   // group sums: lane = column (lanes past the workgroup's columns load a
   // valid row into slots that are never read)
@@ -376,10 +383,13 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
 #pragma unroll
     for (int j = 0; j < XJ; j++) {
       const int slot0 = (wave * XJ + j) * 64;
-      __builtin_amdgcn_global_load_lds((const void *)(xhi + xoff[j] + kstep * QK_K),
-                                       (lds_t *)&XH(buf)[slot0], 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void *)(xlo + xoff[j] + kstep * QK_K),
-                                       (lds_t *)&XL(buf)[slot0], 16, 0, 0);
+      // a wave-uniform base plus a 32-bit lane offset (no 64-bit adds per lane)
+      const uint8_t *bh = (const uint8_t *)(xhi + kstep * QK_K);
+      const uint8_t *bl = (const uint8_t *)(xlo + kstep * QK_K);
+      __builtin_amdgcn_global_load_lds((const void *)(bh + xoff[j]), (lds_t *)&XH(buf)[slot0],
+                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void *)(bl + xoff[j]), (lds_t *)&XL(buf)[slot0],
+                                       16, 0, 0);
     }
     if constexpr (TYPE == LGMLH_Q4_K) {
       if (wave < 2)  // wave 0: hi sums, wave 1: lo sums
@@ -396,7 +406,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   };
   auto load_w = [&](WFrag<TYPE>(&dst)[RT_PER_WAVE], uint32_t kstep) {
 #pragma unroll
-    for (int a = 0; a < RT_PER_WAVE; a++) dst[a].load(wt[a] + kstep * (uint32_t)chunk_bytes(TYPE), lane);
+    for (int a = 0; a < RT_PER_WAVE; a++) dst[a].load(wt[a] + kstep * (uint32_t)chunk_bytes(TYPE), (uint32_t)lane);
   };
   const uint32_t sh6 = 8u * (uint32_t)(c >> 1);
 
@@ -457,13 +467,20 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
     read_bh(0);
     read_bl(0);
     read_d(0);
+    f16x2 sp[RT_PER_WAVE], cp[RT_PER_WAVE];  // Q4_K: multipliers of g's pair
 #pragma unroll
     for (int g = 0; g < 8; g++) {
       f16x8 af[RT_PER_WAVE], af2[RT_PER_WAVE], afr[RT_PER_WAVE];
+      if constexpr (TYPE == LGMLH_Q4_K) {
+        if ((g & 1) == 0) {
+#pragma unroll
+          for (int a = 0; a < RT_PER_WAVE; a++) cur[a].pair(g >> 1, scb[a][g >> 2], sp[a], cp[a]);
+        }
+      }
 #pragma unroll
       for (int a = 0; a < RT_PER_WAVE; a++) {
         if constexpr (TYPE == LGMLH_Q4_K)
-          af[a] = cur[a].frag(g, scb[a][g >> 2]);
+          af[a] = cur[a].frag(g, sp[a], cp[a]);
         else if constexpr (TYPE == LGMLH_Q6_K)
           cur[a].frag(g, sh6, af[a], af2[a], afr[a]);
         else
@@ -534,7 +551,8 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
           f32x4 mn = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sh4[ct], f32x4{0, 0, 0, 0}, 0, 0, 0);
           mn = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sl4[ct], mn, 0, 0, 0);
 #pragma unroll
-          for (int i = 0; i < 4; i++) acc[a][ct][i] += dd[i] * cm[a][ct][i] - dm[i] * mn[i];
+          for (int i = 0; i < 4; i++)
+            acc[a][ct][i] = fmaf(-dm[i], mn[i], fmaf(dd[i], cm[a][ct][i], acc[a][ct][i]));
         }
       }
     } else if constexpr (TYPE == LGMLH_Q6_K) {

@@ -44,7 +44,7 @@ def serve(gm, prompts, budgets, n_slots, run_ahead, ubatch=64, prefix_cache=Fals
                 got[id(r)].append((r.out[-1], lg[i].copy()))
 
     passes = 0
-    while queue or eng.active:
+    while queue or eng.active or eng.waiting:
         while queue and len(eng.active) < n_slots:
             eng.submit(queue.pop(0))
         record(eng.step())
@@ -111,9 +111,10 @@ def test_run_ahead_equals_sync_with_rings():
 
 
 def test_run_ahead_pool_full_mid_prompt():
-    """A prompt longer than the pool fails alone while its earlier chunks
-    are still in flight; the other requests sample as with the synchronous
-    engine."""
+    """A prompt longer than the pool waits while other requests run (its
+    earlier chunks may still be in flight when the pool fills) and, once
+    alone, ends with "kv pool full" (engine.lua:2229-2234); the other
+    requests sample as with the synchronous engine."""
     from lgml_amd import runtime
     hp, w = models.build("c2", seed=13, n_layer=2, init="normal")
     V = hp["n_vocab"]
