@@ -28,7 +28,10 @@ inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s);
 
 // Split-K partial sums of a product not yet reduced: part[z][n][m] for
 // z < splits, n < rows, m < cols (cols = the product's M). The consumer
-// adds them in order z = 0, 1, ... (then the residual, if any).
+// adds them in the canonical order: runs of `group` consecutive partials
+// first (a run's sum starts from its first partial), then the runs in
+// order from 0, then the residual, if any. (group 2: one partial per K
+// split, the splits pair up; group 1: one per pair, already added.)
 // With wts set, the terms are the expert outputs of a token's picks
 // instead: part[n][z][m] times wts[n][z] for the splits = n_used picks.
 // With post set (gemma post norms), the consumer adds rms_norm(sum) * post
@@ -41,6 +44,7 @@ struct Pending {
   const float *wts = nullptr;
   const float *post = nullptr;
   float scale = 0.0f;
+  int group = 1;
   __device__ __forceinline__ float sum(int64_t n, int64_t m) const {
     float v = 0.0f;
     if (wts) {
@@ -48,11 +52,17 @@ struct Pending {
         v += part[((int64_t)n * splits + z) * cols + m] * wts[(int64_t)n * splits + z];
       return v;
     }
-    for (int z = 0; z < splits; z++) v += part[((int64_t)z * rows + n) * cols + m];
+    const int64_t zs = rows * cols;
+    const float *p = part + n * cols + m;
+    for (int z = 0; z < splits; z += group) {
+      float g = p[z * zs];
+      for (int i = 1; i < group && z + i < splits; i++) g += p[(z + i) * zs];
+      v += g;
+    }
     return v;
   }
   // The sums at (n, m0 .. m0 + 7), m0 % 4 == 0 and cols % 4 == 0: 16-byte
-  // loads, four splits in flight, added in split order.
+  // loads, up to four partials in flight, added in the canonical order.
   __device__ __forceinline__ void sum8(int64_t n, int64_t m0, float (&v)[8]) const {
     typedef float f4 __attribute__((ext_vector_type(4)));
     f4 a = {0.0f, 0.0f, 0.0f, 0.0f}, b = a;
@@ -65,28 +75,47 @@ struct Pending {
         a += a0 * wz;
         b += b0 * wz;
       }
-      for (int e = 0; e < 4; e++) {
-        v[e] = a[e];
-        v[4 + e] = b[e];
+    } else {
+      const float *p = part + n * cols + m0;
+      const int64_t zs = rows * cols;
+      int z = 0;
+      if (group == 2) {
+        for (; z + 4 <= splits; z += 4, p += 4 * zs) {
+          const f4 a0 = *(const f4 *)p, b0 = *(const f4 *)(p + 4);
+          const f4 a1 = *(const f4 *)(p + zs), b1 = *(const f4 *)(p + zs + 4);
+          const f4 a2 = *(const f4 *)(p + 2 * zs), b2 = *(const f4 *)(p + 2 * zs + 4);
+          const f4 a3 = *(const f4 *)(p + 3 * zs), b3 = *(const f4 *)(p + 3 * zs + 4);
+          a += a0 + a1;
+          b += b0 + b1;
+          a += a2 + a3;
+          b += b2 + b3;
+        }
+        for (; z + 2 <= splits; z += 2, p += 2 * zs) {
+          const f4 a0 = *(const f4 *)p, b0 = *(const f4 *)(p + 4);
+          const f4 a1 = *(const f4 *)(p + zs), b1 = *(const f4 *)(p + zs + 4);
+          a += a0 + a1;
+          b += b0 + b1;
+        }
+      } else {
+        for (; z + 4 <= splits; z += 4, p += 4 * zs) {
+          const f4 a0 = *(const f4 *)p, b0 = *(const f4 *)(p + 4);
+          const f4 a1 = *(const f4 *)(p + zs), b1 = *(const f4 *)(p + zs + 4);
+          const f4 a2 = *(const f4 *)(p + 2 * zs), b2 = *(const f4 *)(p + 2 * zs + 4);
+          const f4 a3 = *(const f4 *)(p + 3 * zs), b3 = *(const f4 *)(p + 3 * zs + 4);
+          a += a0;
+          b += b0;
+          a += a1;
+          b += b1;
+          a += a2;
+          b += b2;
+          a += a3;
+          b += b3;
+        }
       }
-      return;
-    }
-    const float *p = part + n * cols + m0;
-    const int64_t zs = rows * cols;
-    int z = 0;
-    for (; z + 4 <= splits; z += 4, p += 4 * zs) {
-      const f4 a0 = *(const f4 *)p, b0 = *(const f4 *)(p + 4);
-      const f4 a1 = *(const f4 *)(p + zs), b1 = *(const f4 *)(p + zs + 4);
-      const f4 a2 = *(const f4 *)(p + 2 * zs), b2 = *(const f4 *)(p + 2 * zs + 4);
-      const f4 a3 = *(const f4 *)(p + 3 * zs), b3 = *(const f4 *)(p + 3 * zs + 4);
-      a += a0; b += b0;
-      a += a1; b += b1;
-      a += a2; b += b2;
-      a += a3; b += b3;
-    }
-    for (; z < splits; z++, p += zs) {
-      a += *(const f4 *)p;
-      b += *(const f4 *)(p + 4);
+      for (; z < splits; z++, p += zs) {  // a last run of one
+        a += *(const f4 *)p;
+        b += *(const f4 *)(p + 4);
+      }
     }
     for (int e = 0; e < 4; e++) {
       v[e] = a[e];
@@ -106,13 +135,20 @@ struct Pending {
       const float *p = part + n * cols + m0;
       const int64_t zs = rows * cols;
       int z = 0;
-      for (; z + 4 <= splits; z += 4, p += 4 * zs) {
-        const f4 a0 = *(const f4 *)p, a1 = *(const f4 *)(p + zs);
-        const f4 a2 = *(const f4 *)(p + 2 * zs), a3 = *(const f4 *)(p + 3 * zs);
-        a += a0;
-        a += a1;
-        a += a2;
-        a += a3;
+      if (group == 2) {
+        for (; z + 2 <= splits; z += 2, p += 2 * zs) {
+          const f4 a0 = *(const f4 *)p, a1 = *(const f4 *)(p + zs);
+          a += a0 + a1;
+        }
+      } else {
+        for (; z + 4 <= splits; z += 4, p += 4 * zs) {
+          const f4 a0 = *(const f4 *)p, a1 = *(const f4 *)(p + zs);
+          const f4 a2 = *(const f4 *)(p + 2 * zs), a3 = *(const f4 *)(p + 3 * zs);
+          a += a0;
+          a += a1;
+          a += a2;
+          a += a3;
+        }
       }
       for (; z < splits; z++, p += zs) a += *(const f4 *)p;
     }

@@ -300,7 +300,7 @@ template <int TYPE, int NCT, bool GATHER>
 __global__ void __launch_bounds__(GEMM_THREADS, NCT == 1 && TYPE != LGMLH_Q8_0 ? 4 : 1)
 qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__restrict__ xs,
              int64_t Npad, int64_t N, float *__restrict__ y, int64_t ldy,
-             const float *__restrict__ residual, int splits, int sb_per_split,
+             const float *__restrict__ residual, int nz, int sb_per_split, int fold,
              float *__restrict__ part, Gather gt) {
   constexpr int COLS = NCT * 16;            // N columns per workgroup
   constexpr int X_SLOTS = COLS * 32;
@@ -333,9 +333,10 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
     n0 = 0;
   }
   const int64_t rt0 = (int64_t)blockIdx.y * (WG_ROWS / 16) + wave * RT_PER_WAVE;
+  // K range: splits fold z .. fold z + fold - 1 of sb_per_split steps each
   const int z = blockIdx.z;
-  const int64_t sb_lo = (int64_t)z * sb_per_split;
-  const int64_t sb_hi = sb_lo + sb_per_split < NSB ? sb_lo + sb_per_split : NSB;
+  const int64_t sb_lo = (int64_t)z * fold * sb_per_split;
+  const int64_t sb_hi = sb_lo + fold * sb_per_split < NSB ? sb_lo + fold * sb_per_split : NSB;
   const int c = lane >> 4, r16 = lane & 15;
   // X row of column n (GATHER: of its pick; columns past count repeat the
   // first pick and are never stored)
@@ -592,59 +593,91 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
-  for (uint32_t k = 0; k < nsteps; k += 2) {
-    step(k, w0, w1, 0);
-    if (k + 1 < nsteps) step(k + 1, w1, w0, 1);
-  }
-
   // acc[a][ct][i] = Y[n0 + ct*16 + lane%16][(rt0+a)*16 + 4*(lane/16) + i]
   // (GATHER: Y row = the pick of column ct*16 + lane%16)
-  float *dst = splits == 1 ? y : part + (int64_t)z * N * M;
-  const int64_t ld = splits == 1 ? ldy : M;
+  float *const out = nz == 1 ? y : part + (int64_t)z * N * M;
+  const int64_t ld_out = nz == 1 ? ldy : M;
+  // The first split of a folded pair waits in part (y may be the
+  // residual). Compiled for the wide Q4_K / Q6_K tiles only: elsewhere the
+  // registers it holds would spill.
+  constexpr bool CAN_FOLD = NCT == 4 && !GATHER && TYPE != LGMLH_Q8_0;
+  float *const pair = CAN_FOLD ? part + (int64_t)z * N * M : nullptr;
   // A lane's 4 values are consecutive rows of one output column: one
   // 16-byte store when the layout allows (4-byte stores spread over 16
-  // columns cost the launch about 6 us more).
-  const bool res = splits == 1 && residual;
-  const bool vec = (ld & 3) == 0 && ((uintptr_t)dst & 15) == 0 &&
-                   (!res || ((ldy & 3) == 0 && ((uintptr_t)residual & 15) == 0));
+  // columns cost the launch about 6 us more). add: the sum is the pair's
+  // first split (each lane reads back only what it stored) + acc; res: the
+  // residual goes on last.
+  auto emit = [&](float *dst, int64_t ld, bool add, bool res) {
+    const bool vec = (ld & 3) == 0 && ((uintptr_t)dst & 15) == 0 &&
+                     (!add || ((M & 3) == 0 && ((uintptr_t)pair & 15) == 0)) &&
+                     (!res || ((ldy & 3) == 0 && ((uintptr_t)residual & 15) == 0));
 #pragma unroll
-  for (int a = 0; a < RT_PER_WAVE; a++)
+    for (int a = 0; a < RT_PER_WAVE; a++)
 #pragma unroll
-    for (int ct = 0; ct < NCT; ct++) {
-      int64_t n = n0 + ct * 16 + r16;
-      int64_t m = (rt0 + a) * 16 + 4 * c;
-      if constexpr (GATHER) {
-        if (ct * 16 + r16 >= count) continue;
-        n = gt.sorted[first + ct * 16 + r16];
-      } else if (n >= N) {
-        continue;
-      }
-      if (vec && m + 3 < M) {
-        f32x4 v = acc[a][ct];
-        if (res) v += *(const f32x4 *)(residual + n * ldy + m);
-        *(f32x4 *)(dst + n * ld + m) = v;
-        continue;
-      }
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-        if (m + i < M) {
-          float v = acc[a][ct][i];
-          if (res) v += residual[n * ldy + m + i];
-          dst[n * ld + m + i] = v;
+      for (int ct = 0; ct < NCT; ct++) {
+        int64_t n = n0 + ct * 16 + r16;
+        int64_t m = (rt0 + a) * 16 + 4 * c;
+        if constexpr (GATHER) {
+          if (ct * 16 + r16 >= count) continue;
+          n = gt.sorted[first + ct * 16 + r16];
+        } else if (n >= N) {
+          continue;
         }
+        if (vec && m + 3 < M) {
+          f32x4 v = acc[a][ct];
+          if (add) v = *(volatile f32x4 *)(pair + n * M + m) + v;
+          if (res) v += *(const f32x4 *)(residual + n * ldy + m);
+          *(f32x4 *)(dst + n * ld + m) = v;
+          continue;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (m + i < M) {
+            float v = acc[a][ct][i];
+            if (add) v = *(volatile float *)(pair + n * M + m + i) + v;
+            if (res) v += residual[n * ldy + m + i];
+            dst[n * ld + m + i] = v;
+          }
+      }
+  };
+  // A folded pair: the first split's sum is stored at its last step and
+  // the accumulators start again from 0, so each split is the same sum as
+  // in a workgroup of its own.
+  const uint32_t split_end =
+      CAN_FOLD && fold > 1 && nsteps > (uint32_t)sb_per_split ? sb_per_split : 0;
+  auto boundary = [&](uint32_t k) {
+    if (CAN_FOLD && k + 1 == split_end) {
+      emit(pair, M, false, false);
+#pragma unroll
+      for (int a = 0; a < RT_PER_WAVE; a++)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ct++) acc[a][ct] = f32x4{0, 0, 0, 0};
     }
+  };
+  for (uint32_t k = 0; k < nsteps; k += 2) {
+    step(k, w0, w1, 0);
+    boundary(k);
+    if (k + 1 < nsteps) {
+      step(k + 1, w1, w0, 1);
+      boundary(k + 1);
+    }
+  }
+  if (CAN_FOLD && split_end)
+    emit(out, ld_out, true, nz == 1 && residual);
+  else
+    emit(out, ld_out, false, nz == 1 && residual);
 }
 
-// The splits of a split-K product, added in order 0..splits-1.
-__global__ void splitk_reduce_kernel(const float *__restrict__ part, int splits, int64_t N,
-                                     int64_t M, float *__restrict__ y, int64_t ldy,
+// The partial sums of a split-K product, added in the canonical order
+// (Pending::sum): pairs of splits, then the pairs in order, then the
+// residual.
+__global__ void splitk_reduce_kernel(Pending pd, float *__restrict__ y, int64_t ldy,
                                      const float *__restrict__ residual) {
-  int64_t total = N * M;
+  const int64_t total = pd.rows * pd.cols, M = pd.cols;
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * blockDim.x) {
     int64_t n = e / M, m = e % M;
-    float v = 0.0f;
-    for (int zz = 0; zz < splits; zz++) v += part[(int64_t)zz * total + e];
+    float v = pd.sum(n, m);
     if (residual) v += residual[n * ldy + m];
     y[n * ldy + m] = v;
   }
@@ -700,8 +733,11 @@ f32gemm_kernel(const float *__restrict__ w, int64_t M, int64_t K, const float *_
 
 // K splits depend on M and K only, never on N: each output element is then
 // the same sum in the same order for any batch size. Returns the number of
-// splits actually launched (each of sb_per_split K steps, the last may be
-// shorter).
+// splits (each of sb_per_split K steps, the last may be shorter). Their
+// sums add up in a fixed association: consecutive pairs (SPLIT_PAIR) first,
+// then the pairs in order, so that a workgroup may run both splits of a
+// pair itself (see launch_q) with the same result.
+constexpr int SPLIT_PAIR = 2;
 int splits_for(int64_t M, int64_t K, int64_t N, int *sb_per_split = nullptr) {
   (void)N;
   const int64_t NSB = K / QK_K;
@@ -731,12 +767,15 @@ size_t workspace_for(int type, int64_t M, int64_t K, int64_t N) {
   return align256(split_bytes(N, K)) + partial_bytes(type, M, K, N);
 }
 
+// Launch a quantized product; returns the partials it leaves in part (0:
+// the product is in y) and, in *group, how many consecutive partials make a
+// pair sum (2: one per split; 1: one per folded pair).
 template <int TYPE>
-static void launch_q(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t N, float *y,
-                     int64_t ldy, const float *res, int splits, float *part, bool defer,
-                     hipStream_t st) {
+static int launch_q(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t N, float *y,
+                    int64_t ldy, const float *res, float *part, bool defer, hipStream_t st,
+                    int *group) {
   int spb = 0;
-  splits = splits_for(M, K, N, &spb);
+  const int splits = splits_for(M, K, N, &spb);
   const int64_t Npad = split_npad(N);
   // Column tiles of 64, or of 16 / 32 for a batch that small (the same sums
   // per element: only the columns a workgroup carries change). A decode-
@@ -749,12 +788,22 @@ static void launch_q(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t
   int nct = N <= 16 ? 1 : N <= 32 ? 2 : WG_COLS / 16;
   if (N <= 64 && (int64_t)((M + WG_ROWS - 1) / WG_ROWS) * splits < 200) nct = 1;
   const int cols = 16 * nct;
+  const int64_t tiles = ((N + cols - 1) / cols) * ((M + WG_ROWS - 1) / WG_ROWS);
+  // With workgroups to spare (two rounds of CUs or more), a workgroup runs
+  // both splits of a pair: half the partial sums (none for a product of
+  // two splits) to write and read back. Same sums either way.
+  const int fold = splits > 1 && nct == 4 && TYPE != LGMLH_Q8_0 &&
+                           tiles * ((splits + 1) / SPLIT_PAIR) >= 512
+                       ? SPLIT_PAIR
+                       : 1;
+  const int nz = (splits + fold - 1) / fold;
+  *group = fold == 1 ? SPLIT_PAIR : 1;
   dim3 grid((unsigned)((N + cols - 1) / cols), (unsigned)((M + WG_ROWS - 1) / WG_ROWS),
-            (unsigned)splits);
+            (unsigned)nz);
 #define LGMLH_PLAIN(NCT_)                                                                  \
   hipLaunchKernelGGL((qgemm_kernel<TYPE, NCT_, false>), grid, dim3(GEMM_THREADS), 0, st,   \
-                     (const uint8_t *)w, M, K, xs, Npad, N, y, ldy, res, splits, spb, part, \
-                     Gather{})
+                     (const uint8_t *)w, M, K, xs, Npad, N, y, ldy, res, nz, spb, fold,    \
+                     part, Gather{})
   if (nct == 1)
     LGMLH_PLAIN(1);
   else if (nct == 2)
@@ -762,23 +811,25 @@ static void launch_q(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t
   else
     LGMLH_PLAIN(4);
 #undef LGMLH_PLAIN
-  if (splits > 1 && !defer) {
+  if (nz > 1 && !defer) {
     int64_t total = N * M;
     unsigned blocks = (unsigned)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, st, part, splits, N, M,
-                       y, ldy, res);
+    Pending pd{part, nz, N, M};
+    pd.group = *group;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, st, pd, y, ldy, res);
   }
+  return nz > 1 ? nz : 0;
 }
 
 // Quantized product on split X (split.h layout for N rows of K). part holds
 // the split-K partial sums (partial_bytes). With `deferred` given, a split
-// product leaves its partials in part ([splits][N][M], added in order by
-// the consumer, which also adds the residual) and *deferred = splits;
-// otherwise the splits are reduced here (*deferred = 0).
+// product leaves its partials in part and *deferred describes them (added
+// in the canonical order by the consumer, Pending::sum, which also adds the
+// residual); otherwise they are reduced here (*deferred stays empty).
 int mul_mat_split(int type, const void *w, int64_t M, int64_t K, const f16 *xs, int64_t N,
                   float *y, int64_t ldy, const float *residual, float *part, size_t part_bytes,
-                  hipStream_t st, int *deferred) {
-  if (deferred) *deferred = 0;
+                  hipStream_t st, Pending *deferred) {
+  if (deferred) *deferred = Pending{};
   if (!w || !xs || !y || M <= 0 || K <= 0 || N < 0 || ldy < M || K % QK_K) {
     set_error("mul_mat: bad arguments (M %lld, K %lld)", (long long)M, (long long)K);
     return LGMLH_EINVAL;
@@ -790,15 +841,19 @@ int mul_mat_split(int type, const void *w, int64_t M, int64_t K, const f16 *xs, 
     return LGMLH_ENOMEM;
   }
   const bool defer = deferred && splits > 1;
+  int nz = 0, group = 1;
   switch (type) {
-    case LGMLH_Q4_K: launch_q<LGMLH_Q4_K>(w, M, K, xs, N, y, ldy, residual, splits, part, defer, st); break;
-    case LGMLH_Q6_K: launch_q<LGMLH_Q6_K>(w, M, K, xs, N, y, ldy, residual, splits, part, defer, st); break;
-    case LGMLH_Q8_0: launch_q<LGMLH_Q8_0>(w, M, K, xs, N, y, ldy, residual, splits, part, defer, st); break;
+    case LGMLH_Q4_K: nz = launch_q<LGMLH_Q4_K>(w, M, K, xs, N, y, ldy, residual, part, defer, st, &group); break;
+    case LGMLH_Q6_K: nz = launch_q<LGMLH_Q6_K>(w, M, K, xs, N, y, ldy, residual, part, defer, st, &group); break;
+    case LGMLH_Q8_0: nz = launch_q<LGMLH_Q8_0>(w, M, K, xs, N, y, ldy, residual, part, defer, st, &group); break;
     default:
       set_error("mul_mat: type %d not supported", type);
       return LGMLH_EINVAL;
   }
-  if (defer) *deferred = splits;
+  if (defer && nz > 1) {
+    *deferred = Pending{part, nz, N, M};
+    deferred->group = group;
+  }
   return hip_check(hipGetLastError(), "mul_mat");
 }
 
@@ -809,7 +864,7 @@ static void launch_grouped(const void *w, int64_t M, int64_t K, const f16 *xs, i
   dim3 grid((unsigned)max_tiles, (unsigned)((M + WG_ROWS - 1) / WG_ROWS), 1);
   hipLaunchKernelGGL((qgemm_kernel<TYPE, NCT, true>), grid, dim3(GEMM_THREADS), 0, st,
                      (const uint8_t *)w, M, K, xs, Npad, (int64_t)0, y, M, (const float *)nullptr,
-                     1, NSB, (float *)nullptr, gt);
+                     1, NSB, 1, (float *)nullptr, gt);
 }
 
 // Grouped product (mul_mat_id): for each column tile of the grouping (see

@@ -14,7 +14,7 @@ namespace lgmlh {
 
 int mul_mat_split(int type, const void *w, int64_t M, int64_t K, const f16 *xs, int64_t N,
                   float *y, int64_t ldy, const float *residual, float *part, size_t part_bytes,
-                  hipStream_t st, int *deferred);
+                  hipStream_t st, Pending *deferred);
 int mul_mat_f32(const float *w, int64_t M, int64_t K, const float *x, int64_t N, float *y,
                 int64_t ldy, const float *residual, hipStream_t st);
 int split_x(const void *x, int xtype, int64_t N, int64_t K, f16 *xs, hipStream_t st);
@@ -264,17 +264,14 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
   // A product on X given as f32 rows (f32 weights) or as split planes xs
   // (quantized weights); the producer wrote the form(s) the weights take.
   // A quantized product split over K leaves its partial sums pending (pd):
-  // the next kernel that reads y adds them in order, then the residual.
+  // the next kernel that reads y adds them in the canonical order, then the residual.
   auto gemm_on = [&](hipStream_t s, int type, const void *w, int64_t M, int64_t K,
                      const float *xf, int64_t N, float *y, int64_t ldy, const float *res,
                      float *part, size_t part_bytes, Pending &pd) -> int {
     Span sp(trace, LGMLH_TRACE_GEMM, s);
     pd = Pending{};
     if (type == LGMLH_F32) return mul_mat_f32((const float *)w, M, K, xf, N, y, ldy, res, s);
-    int splits = 0;
-    int rc = mul_mat_split(type, w, M, K, xs, N, y, ldy, res, part, part_bytes, s, &splits);
-    if (rc == LGMLH_OK && splits > 1) pd = Pending{part, splits, N, M};
-    return rc;
+    return mul_mat_split(type, w, M, K, xs, N, y, ldy, res, part, part_bytes, s, &pd);
   };
   auto gemm = [&](int type, const void *w, int64_t M, int64_t K, const float *xf, int64_t N,
                   float *y, int64_t ldy, const float *res, float *part, size_t part_bytes,

@@ -160,6 +160,44 @@ def test_mul_mat_parity_and_batch_invariance(L, ty, MK):
                 assert np.array_equal(alone[0].view(np.uint32), y[j].view(np.uint32)), j
 
 
+# At prefill sizes a workgroup runs both K splits of a pair (gemm.hip
+# launch_q: Q4_K / Q6_K with 64-column tiles and at least 512 workgroups of
+# pairs); its sums are the same as with one workgroup per split, bit for
+# bit. (4096, 4096): 8 splits, 4 pairs; (4096, 3584): 7 splits, the last
+# pair a single split; (16384, 1024): 2 splits, one pair, written straight
+# to y (and, with the residual, over it in place).
+@pytest.mark.parametrize("ty", [core.Q4_K, core.Q6_K])
+@pytest.mark.parametrize("MK", [(4096, 4096), (4096, 3584), (16384, 1024)])
+def test_mul_mat_folded_split_pairs(L, ty, MK):
+    from lgml_amd import hip
+    M, K = MK
+    N = 576
+    wf = core.fill_normal(M * K, 0, 0.02, 17).reshape(M, K)
+    w = core.quantize(ty, wf)
+    x = core.fill_normal(N * K, 0, 1, 18).reshape(N, K)
+    y = run_mul_mat(L, ty, w, M, K, x)
+    y130 = run_mul_mat(L, ty, w, M, K, x[:130])  # one workgroup per split
+    assert np.array_equal(y[:130].view(np.uint32), y130.view(np.uint32))
+    alone = run_mul_mat(L, ty, w, M, K, x[N - 1:N])
+    assert np.array_equal(alone[0].view(np.uint32), y[N - 1].view(np.uint32))
+    rows = [0, 65, 300, N - 1]
+    want = core.mul_mat(core.F32, core.dequantize(ty, w, K), M, K, x[rows])
+    assert rel_err(y[rows], want) < 1e-5, rel_err(y[rows], want)
+    # the residual added in place (y is the residual)
+    nb = L.lgmlh_repacked_bytes(ty, M, K)
+    rp = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    wd = dev(w)
+    hip.check(L.lgmlh_repack(ty, M, K, wd.data_ptr(), rp.data_ptr(), st()))
+    res = core.fill_normal(N * M, 0, 1, 19).reshape(N, M)
+    yd = dev(res.copy())
+    ws_n = L.lgmlh_mul_mat_workspace(ty, M, K, N)
+    ws = torch.zeros(max(ws_n, 1), dtype=torch.uint8, device="cuda")
+    xd = dev(x)
+    hip.check(L.lgmlh_mul_mat(ty, rp.data_ptr(), M, K, xd.data_ptr(), hip.F32, N, yd.data_ptr(),
+                              hip.EPI_ADD, yd.data_ptr(), ws.data_ptr(), ws_n, st()))
+    assert np.array_equal(yd.cpu().numpy(), (y + res).astype(np.float32))
+
+
 def test_mul_mat_f32_input_and_residual(L):
     from lgml_amd import hip
     M, K, N = 512, 1024, 9
