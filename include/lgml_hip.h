@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define LGMLH_ABI_VERSION 4
+#define LGMLH_ABI_VERSION 5
 
 enum {
 	LGMLH_OK = 0,
@@ -167,6 +167,10 @@ typedef struct {
 	int64_t off_ids, off_pos, off_cells, off_seq_off, off_npast, off_block_tab, off_logit_rows,
 	    off_items, off_merge;
 	int32_t window, ring;  /* a ring plan (lgmlh_plan_ring): window, ring blocks; else 0 */
+	/* items [0, n_single) are query groups on their own; the rest come in
+	 * shared runs of consecutive items, {first item, count} at off_shared */
+	int32_t n_single, n_shared;
+	int64_t off_shared;
 } lgmlh_plan_info;
 
 typedef struct {
@@ -182,14 +186,18 @@ typedef struct {
 	const int32_t *items;      /* [n_items * 4] attention work items */
 	const int32_t *merge;      /* [n_merge * 4] split-merge groups */
 	int32_t window, ring;      /* ring plans: the window and the ring's blocks; else 0 */
+	int32_t n_single, n_shared;
+	const int32_t *shared;     /* [n_shared * 2] {first item, count} of each shared run */
 } lgmlh_ubatch;
 
 /* Plan a pass. G = n_head / n_head_kv; blocks_per_split bounds the KV
  * blocks one work item reads (0 = the default, 16): a query group's blocks
- * go into the fewest such runs, of lengths that differ by at most one. The
- * work list depends
- * only on each sequence's own length, so a sequence is computed the same
- * way alone or in any batch. With buf NULL only info is
+ * go into the fewest such runs, of lengths that differ by at most one. A
+ * sequence with several query groups in the pass (a prompt chunk) takes
+ * them in sets of up to 8 consecutive groups with the runs of the set's
+ * last token, so that one workgroup reads each block once for the set. The
+ * work list depends only on each sequence's own tokens, so a sequence is
+ * computed the same way alone or in any batch. With buf NULL only info is
  * filled (sizes); otherwise buf must hold info->bytes. Errors:
  * LGMLH_ERANGE when a block id that a position needs is outside
  * [0, pool_blocks) (the fill_blocks "position ... is in no column" error,

@@ -46,6 +46,60 @@ struct Partial {
   static constexpr int floats = ROWS * D + 2 * ROWS;
 };
 
+// The end of a work item: lane holds O^T[d = dt*16 + quad*4 + i][row].
+// A group in one run writes o / l (as the merge divides: a token's output
+// does not depend on whether its group was split) to out or, with planes,
+// to the split planes of the output product's X; a run of a split group
+// writes its partial state (rows in use only) for the merge.
+template <int D>
+__device__ __forceinline__ void finish_item(const f32x4 (&o)[D / 16], float m, float l, int mg,
+                                            bool rvalid, int tok0, int rtok, int rhead, int ntok,
+                                            int G, int row, int quad, int item, int kvh, int Hkv,
+                                            int H, float *__restrict__ out,
+                                            f16 *__restrict__ planes, int64_t npad,
+                                            float *__restrict__ part) {
+  constexpr int DT = D / 16;
+  if (mg < 0) {
+    if (rvalid) {
+      const int64_t n = tok0 + rtok;
+      if (planes) {
+        // split planes of the output product's X: the lanes of a row hold
+        // 8 values of each 32-value group (d tiles 2g and 2g + 1)
+        const int64_t K = (int64_t)H * D, k0 = (int64_t)rhead * D;
+#pragma unroll
+        for (int g = 0; g < DT / 2; g++) {
+          float s = 0.0f;
+#pragma unroll
+          for (int h2 = 0; h2 < 2; h2++) {
+            const f32x4 y = o[2 * g + h2] / l;
+            const float v[4] = {y[0], y[1], y[2], y[3]};
+            split_store4(planes, npad, K, n, k0 + (2 * g + h2) * 16 + quad * 4, v);
+            s += v[0] + v[1] + v[2] + v[3];
+          }
+          s += __shfl_xor(s, 16);
+          s += __shfl_xor(s, 32);
+          if (quad == 0) split_store_gsum(planes, npad, K, n, (k0 >> 5) + g, s);
+        }
+      } else {
+        float *orow = out + (n * H + rhead) * D;
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) *(f32x4 *)(orow + dt * 16 + quad * 4) = o[dt] / l;
+      }
+    }
+    return;
+  }
+  const int nrows = ntok * G;
+  float *pp = part + ((int64_t)item * Hkv + kvh) * Partial<D>::floats;
+  if (row < nrows) {
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) *(f32x4 *)(pp + row * D + dt * 16 + quad * 4) = o[dt];
+    if (quad == 0) {
+      pp[ROWS * D + row] = m;
+      pp[ROWS * D + ROWS + row] = l;
+    }
+  }
+}
+
 // RING: a sliding-window plan. Items hold logical block ranges; logical
 // block b of sequence s is ring entry b % ring, and row position p sees
 // positions p - window + 1 .. p only.
@@ -233,49 +287,212 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
     __asm__ volatile("" ::: "memory");  // the P reads before the next block's writes
   }
 
-  // Lane holds O^T[d = dt*16 + quad*4 + i][row].
-  if (mg < 0) {
-    if (rvalid) {
-      // o / l, as the merge divides: a token's output does not depend on
-      // whether its group was split (the grouping follows chunk boundaries)
-      const int64_t n = tok0 + rtok;
-      if (planes) {
-        // split planes of the output product's X: the lanes of a row hold
-        // 8 values of each 32-value group (d tiles 2g and 2g + 1)
-        const int64_t K = (int64_t)H * D, k0 = (int64_t)rhead * D;
+  finish_item<D>(o, m, l, mg, rvalid, tok0, rtok, rhead, ntok, G, row, quad, item, kvh, Hkv, H,
+                 out, planes, npad, part);
+}
+
+// Shared runs (a prompt chunk's query groups in sets, lgmlh_plan): one
+// workgroup of SHARED_WAVES waves per (run, KV head), wave w on item
+// first + w (w < n). Each K / V block of the run is loaded once into LDS
+// (global-to-LDS, the next block's loads in flight while this one is
+// used) and every wave reads its MFMA fragments from there: the context
+// of a chunk is read once per set instead of once per group. The
+// arithmetic of a wave is the per-item kernel's (same fragments, same
+// order), so an item gives the same bits in either kernel. A block past a
+// wave's last position is skipped (it would add nothing).
+// LDS slots of 16 B: K slot (r, c) = row r (cell), chunk c of D / 8 holds
+// the pool's chunk c ^ swk(r); V slot (r, c) = row r (d), chunk c of 8
+// (cells) holds chunk c ^ swv(r): a 16-row fragment read touches every
+// bank once.
+constexpr int SHARED_WAVES = ATTN_SHARED;
+
+template <int D>
+__device__ __forceinline__ int swk(int r) {
+  return D / 8 >= 16 ? (r & 15) : ((r >> 1) & 7);
+}
+__device__ __forceinline__ int swv(int r) { return (r >> 1) & 7; }
+
+template <int D>
+__global__ void __launch_bounds__(64 * SHARED_WAVES)
+paged_attn_shared_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
+                         const uint16_t *__restrict__ kpool, const uint16_t *__restrict__ vpool,
+                         const int32_t *__restrict__ items, const int32_t *__restrict__ shared,
+                         const int32_t *__restrict__ seq_off, const int32_t *__restrict__ seq_npast,
+                         const int32_t *__restrict__ block_tab, int max_blocks,
+                         float *__restrict__ out, f16 *__restrict__ planes, int64_t npad,
+                         float *__restrict__ part) {
+  constexpr int KS = D / 32, DT = D / 16;
+  constexpr int TILE = 64 * D;             // f16 of one K (or V) tile
+  constexpr int KC = D / 8;                // 16-byte chunks per K row
+  constexpr int LOADS = TILE / 8 / (64 * SHARED_WAVES);  // per lane and tile
+  __shared__ __align__(16) uint16_t kb0[TILE], kb1[TILE], vb0[TILE], vb1[TILE];
+  __shared__ __align__(16) uint16_t plh_[SHARED_WAVES][ROWS * P_STRIDE];
+  __shared__ __align__(16) uint16_t pll_[SHARED_WAVES][ROWS * P_STRIDE];
+  typedef __attribute__((address_space(3))) void lds_t;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int first = shared[2 * blockIdx.x], n = shared[2 * blockIdx.x + 1];
+  const int kvh = blockIdx.y;
+  const int G = H / Hkv;
+  const bool active = wave < n;
+  const int item = first + (active ? wave : 0);
+  const int s = items[4 * first + 0];
+  const int blo = items[4 * first + 3] & 0xffff;
+  const int bhi = (items[4 * first + 3] >> 16) & 0xffff;
+  const int tok0 = items[4 * item + 1];
+  const int ntok = items[4 * item + 2] & 31;
+  const int mg = (items[4 * item + 2] >> 5) - 1;
+  uint16_t *plh = plh_[wave], *pll = pll_[wave];
+
+  const int row = lane & 15, quad = lane >> 4;
+  const int rtok = row / G;
+  const int rhead = kvh * G + row % G;
+  const bool rvalid = rtok < ntok;
+  const int p_first = seq_npast[s] + (tok0 - seq_off[s]);
+  const int p_row = p_first + rtok;
+  const int p_last = p_first + ntok - 1;  // the wave's last position
+
+  // Q fragments in registers: Q[row][ks*32 + quad*8 .. +7] as f16 hi + lo
+  f16x8 qh[KS], ql[KS];
+  {
+    const int qt = rvalid ? rtok : ntok - 1;
+    const float *qr = q + ((int64_t)(tok0 + qt) * H + rhead) * D;
 #pragma unroll
-        for (int g = 0; g < DT / 2; g++) {
-          float s = 0.0f;
+    for (int ks = 0; ks < KS; ks++) {
+      const f32x4 a = rvalid ? *(const f32x4 *)(qr + ks * 32 + quad * 8) : f32x4{0, 0, 0, 0};
+      const f32x4 b = rvalid ? *(const f32x4 *)(qr + ks * 32 + quad * 8 + 4) : f32x4{0, 0, 0, 0};
 #pragma unroll
-          for (int h2 = 0; h2 < 2; h2++) {
-            const f32x4 y = o[2 * g + h2] / l;
-            const float v[4] = {y[0], y[1], y[2], y[3]};
-            split_store4(planes, npad, K, n, k0 + (2 * g + h2) * 16 + quad * 4, v);
-            s += v[0] + v[1] + v[2] + v[3];
-          }
-          s += __shfl_xor(s, 16);
-          s += __shfl_xor(s, 32);
-          if (quad == 0) split_store_gsum(planes, npad, K, n, (k0 >> 5) + g, s);
-        }
-      } else {
-        float *orow = out + (n * H + rhead) * D;
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++) *(f32x4 *)(orow + dt * 16 + quad * 4) = o[dt] / l;
+      for (int e = 0; e < 4; e++) {
+        qh[ks][e] = (f16)a[e];
+        ql[ks][e] = (f16)(a[e] - (float)qh[ks][e]);
+        qh[ks][4 + e] = (f16)b[e];
+        ql[ks][4 + e] = (f16)(b[e] - (float)qh[ks][4 + e]);
       }
     }
-    return;
   }
-  // A split: its partial state, rows in use only.
-  const int nrows = ntok * G;
-  float *pp = part + ((int64_t)item * Hkv + kvh) * Partial<D>::floats;
-  if (row < nrows) {
+
+  f32x4 o[DT];
 #pragma unroll
-    for (int dt = 0; dt < DT; dt++) *(f32x4 *)(pp + row * D + dt * 16 + quad * 4) = o[dt];
-    if (quad == 0) {
-      pp[ROWS * D + row] = m;
-      pp[ROWS * D + ROWS + row] = l;
+  for (int i = 0; i < DT; i++) o[i] = f32x4{0, 0, 0, 0};
+  float m = -INFINITY, l = 0.0f;
+
+  const int32_t *bt = block_tab + (int64_t)s * max_blocks;
+  // Global-to-LDS loads of block blk into buffer buf: load j of this lane
+  // fills slot (j * SHARED_WAVES + wave) * 64 + lane of each tile.
+  auto load = [&](int blk, int buf) {
+    const int64_t base = ((int64_t)bt[blk] * Hkv + kvh) * TILE;
+    uint16_t *kd = buf ? kb1 : kb0, *vd = buf ? vb1 : vb0;
+#pragma unroll
+    for (int j = 0; j < LOADS; j++) {
+      const int slot0 = (j * SHARED_WAVES + wave) * 64, sl = slot0 + lane;
+      const int kr = sl / KC, kc = (sl % KC) ^ swk<D>(sl / KC);
+      const int vr = sl / 8, vc = (sl % 8) ^ swv(sl / 8);
+      __builtin_amdgcn_global_load_lds((const void *)(kpool + base + kr * D + kc * 8),
+                                       (lds_t *)(kd + slot0 * 8), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void *)(vpool + base + vr * 64 + vc * 8),
+                                       (lds_t *)(vd + slot0 * 8), 16, 0, 0);
     }
+  };
+  if (blo < bhi) {
+    load(blo, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
   }
+  for (int blk = blo; blk < bhi; blk++) {
+    const int buf = (blk - blo) & 1;
+    if (blk + 1 < bhi) load(blk + 1, buf ^ 1);  // into the buffer freed by the last barrier
+    const int cbase = blk * 64;
+    if (active && cbase <= p_last) {
+      const uint16_t *kt = buf ? kb1 : kb0, *vt = buf ? vb1 : vb0;
+      // S^T[cell][row] for 4 tiles of 16 cells, K fragments from LDS
+      f32x4 st[4];
+#pragma unroll
+      for (int ct = 0; ct < 4; ct++) {
+        const int r = ct * 16 + row;
+        f16x8 kf[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++)
+          kf[ks] = load_f16x8(kt + (r * KC + ((ks * 4 + quad) ^ swk<D>(r))) * 8);
+        f32x4 acc = f32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+          acc = mfma16(kf[ks], qh[ks], acc);
+          acc = mfma16(kf[ks], ql[ks], acc);
+        }
+        st[ct] = acc;
+      }
+      const bool full = cbase + 63 <= p_first;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int ct = 0; ct < 4; ct++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int p = cbase + ct * 16 + quad * 4 + i;
+          const bool vis = full || p <= p_row;
+          const float v = (rvalid && vis) ? st[ct][i] * scale_log2 : -INFINITY;
+          st[ct][i] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m, mx);
+      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+      float rs = 0.0f;
+#pragma unroll
+      for (int ct = 0; ct < 4; ct++) {
+        uint16_t ph[4], pq[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float pv = __builtin_amdgcn_exp2f(st[ct][i] - m_use);  // exp2(-inf) = 0
+          rs += pv;
+          const f16 hv = (f16)pv;
+          ph[i] = __builtin_bit_cast(uint16_t, hv);
+          pq[i] = f2h(pv - (float)hv);
+        }
+        const u32x2 wh = u32x2{(uint32_t)ph[0] | ((uint32_t)ph[1] << 16),
+                               (uint32_t)ph[2] | ((uint32_t)ph[3] << 16)};
+        const u32x2 wl = u32x2{(uint32_t)pq[0] | ((uint32_t)pq[1] << 16),
+                               (uint32_t)pq[2] | ((uint32_t)pq[3] << 16)};
+        *(u32x2 *)(plh + row * P_STRIDE + ct * 16 + quad * 4) = wh;
+        *(u32x2 *)(pll + row * P_STRIDE + ct * 16 + quad * 4) = wl;
+      }
+      rs += __shfl_xor(rs, 16);
+      rs += __shfl_xor(rs, 32);
+      if (__builtin_amdgcn_ballot_w64(m_new != m)) {
+        const float alpha = __builtin_amdgcn_exp2f(m - m_use);  // 0 when m is -inf
+        l *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) o[dt] *= alpha;
+      }
+      l += rs;
+      m = m_new;
+      // a wave's LDS operations complete in order: the P writes before the reads
+      __asm__ volatile("" ::: "memory");
+      f16x8 pfh[2], pfl[2];
+#pragma unroll
+      for (int kc = 0; kc < 2; kc++) {
+        pfh[kc] = load_f16x8(plh + row * P_STRIDE + kc * 32 + quad * 8);
+        pfl[kc] = load_f16x8(pll + row * P_STRIDE + kc * 32 + quad * 8);
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; dt++) {
+        const int r = dt * 16 + row;
+#pragma unroll
+        for (int kc = 0; kc < 2; kc++) {
+          const f16x8 vf = load_f16x8(vt + (r * 8 + ((kc * 4 + quad) ^ swv(r))) * 8);
+          o[dt] = mfma16(vf, pfh[kc], o[dt]);
+          o[dt] = mfma16(vf, pfl[kc], o[dt]);
+        }
+      }
+      __asm__ volatile("" ::: "memory");  // the P reads before the next block's writes
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of blk + 1 have landed
+    __syncthreads();                // ... and everyone's; buffer buf is free again
+  }
+  if (!active) return;
+  finish_item<D>(o, m, l, mg, rvalid, tok0, rtok, rhead, ntok, G, row, quad, item, kvh, Hkv, H,
+                 out, planes, npad, part);
 }
 
 // Fixed-order merge of the splits of one token group (merge group: first
@@ -291,10 +508,11 @@ merge_kernel(const int32_t *__restrict__ merge, int H, int Hkv, const float *__r
   __shared__ float wsh[WMAX * ROWS], lsh[2 * ROWS];
   const int lane = threadIdx.x, mg = blockIdx.x, kvh = blockIdx.y;
   const int first = merge[4 * mg + 0], ns = merge[4 * mg + 1];
-  const int tok0 = merge[4 * mg + 2], ntok = merge[4 * mg + 3];
+  const int tok0 = merge[4 * mg + 2], ntok = merge[4 * mg + 3] & 0xff;
+  const int stride = merge[4 * mg + 3] >> 8;  // items from one split to the next
   const int G = H / Hkv, nrows = ntok * G;
   const float *p0 = part + ((int64_t)first * Hkv + kvh) * Partial<D>::floats;
-  const int64_t pstride = (int64_t)Hkv * Partial<D>::floats;  // from one split to the next
+  const int64_t pstride = (int64_t)stride * Hkv * Partial<D>::floats;
   // Loads go out in rounds: the m and l of 8 splits, then 4 splits of 4
   // output positions per lane (addresses clamped into range; the values
   // past the last split are dropped), so a merge takes a few round trips.
@@ -397,15 +615,24 @@ static void launch_attn(const float *q, int H, int Hkv, float scale_log2, const 
                         const void *vp, const lgmlh_ubatch *ub, float *out, f16 *planes,
                         int64_t npad, float *part, hipStream_t st) {
   if (ub->ring > 0)
-    hipLaunchKernelGGL((paged_attn_kernel<D, true>), dim3(ub->n_items, Hkv), dim3(64), 0, st, q,
-                       H, Hkv, scale_log2, (const uint16_t *)kp, (const uint16_t *)vp, ub->items,
-                       ub->seq_off, ub->seq_npast, ub->block_tab, ub->max_blocks, ub->ring,
-                       ub->window, out, planes, npad, part);
-  else
-    hipLaunchKernelGGL((paged_attn_kernel<D, false>), dim3(ub->n_items, Hkv), dim3(64), 0, st, q,
-                       H, Hkv, scale_log2, (const uint16_t *)kp, (const uint16_t *)vp, ub->items,
-                       ub->seq_off, ub->seq_npast, ub->block_tab, ub->max_blocks, 0, 0, out,
-                       planes, npad, part);
+    hipLaunchKernelGGL((paged_attn_kernel<D, true>), dim3(ub->n_single, Hkv), dim3(64), 0, st,
+                       q, H, Hkv, scale_log2, (const uint16_t *)kp, (const uint16_t *)vp,
+                       ub->items, ub->seq_off, ub->seq_npast, ub->block_tab, ub->max_blocks,
+                       ub->ring, ub->window, out, planes, npad, part);
+  // heads of 256 run the shared runs' items with the per-item kernel too
+  else if (const int n1 = D <= 128 ? ub->n_single : ub->n_items; n1 > 0)
+    hipLaunchKernelGGL((paged_attn_kernel<D, false>), dim3(n1, Hkv), dim3(64), 0, st,
+                       q, H, Hkv, scale_log2, (const uint16_t *)kp, (const uint16_t *)vp,
+                       ub->items, ub->seq_off, ub->seq_npast, ub->block_tab, ub->max_blocks, 0,
+                       0, out, planes, npad, part);
+  if (ub->ring == 0 && ub->n_shared > 0) {
+    if constexpr (D <= 128)
+      hipLaunchKernelGGL(paged_attn_shared_kernel<D>, dim3(ub->n_shared, Hkv),
+                         dim3(64 * SHARED_WAVES), 0, st, q, H, Hkv, scale_log2,
+                         (const uint16_t *)kp, (const uint16_t *)vp, ub->items, ub->shared,
+                         ub->seq_off, ub->seq_npast, ub->block_tab, ub->max_blocks, out, planes,
+                         npad, part);
+  }
   if (ub->n_merge > 0)
     hipLaunchKernelGGL(merge_kernel<D>, dim3(ub->n_merge, Hkv), dim3(64), 0, st, ub->merge, H,
                        Hkv, part, out, planes, npad);

@@ -158,6 +158,9 @@ struct Pending {
 
 // Cells per KV block; the pool layout and the attention tiles assume it.
 constexpr int KV_BLOCK = 64;
+// Query groups per shared attention run (lgmlh_plan's sets; the waves of
+// the shared attention kernel).
+constexpr int ATTN_SHARED = 8;
 
 __device__ __forceinline__ float h2f(uint16_t h) {
   return (float)__builtin_bit_cast(f16, h);

@@ -6,9 +6,19 @@
 // off + n - 1 -- into one buffer for a single host-to-device copy, and adds
 // the work list of the paged attention kernel: for every sequence, groups
 // of 16 / G query tokens, each split into the fewest runs of at most
-// blocks_per_split KV blocks (balanced lengths), plus one merge item per group with more than one split. A
-// ring plan (sliding-window layers) maps positions into each sequence's
-// ring of blocks and starts each group's runs at its window.
+// blocks_per_split KV blocks (balanced lengths), plus one merge item per
+// group with more than one split. A ring plan (sliding-window layers) maps
+// positions into each sequence's ring of blocks and starts each group's
+// runs at its window.
+//
+// A sequence with more than one query group in the pass (a prompt chunk)
+// has its groups in shared sets of up to SHARED consecutive groups that
+// take the same runs (those of the set's last token; blocks past a
+// group's own last position are masked for it and change nothing): the
+// shared attention kernel reads each K / V block once per set into LDS
+// for all its groups. Items are ordered so that items [0, n_single) are
+// groups on their own (decode tokens, ring plans) and every shared run is
+// n consecutive items, listed in `shared` as {first item, n}.
 #include <string.h>
 
 #include <utility>
@@ -17,6 +27,7 @@
 
 namespace lgmlh {
 static int64_t align16(int64_t x) { return (x + 15) & ~int64_t(15); }
+constexpr int SHARED = ATTN_SHARED;  // query groups per shared set
 }  // namespace lgmlh
 
 using namespace lgmlh;
@@ -74,39 +85,61 @@ static int plan_impl(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
   // rest of the batch (a sequence gives the same bits alone or batched).
   const int bps = blocks_per_split ? blocks_per_split : 16;
   // The work list is walked twice with no allocation: once to count the
-  // items and merges (the buffer layout), once to write them into buf.
-  // emit(item index, item[4], merge[4] or NULL, merge index) gets each run;
-  // a group of more than one run passes its merge with its first run.
-  auto walk = [&](auto &&emit) {
-    int64_t n_items = 0, n_merge = 0;
-    for (int s = 0, off = 0; s < n_seq; off += seq_n[s], s++) {
-      for (int g0 = 0; g0 < seq_n[s]; g0 += T) {
-        const int ge = g0 + T < seq_n[s] ? g0 + T : seq_n[s];
-        // logical blocks [b0, nbg): from the window of the group's first
-        // token (ring plans) or from 0, to the group's last position
-        const int64_t pf = (int64_t)seq_npast[s] + g0, pl = (int64_t)seq_npast[s] + ge - 1;
-        const int b0 = ring ? (int)((pf - window + 1 > 0 ? pf - window + 1 : 0) / B) : 0;
-        const int nbg = (int)(pl / B + 1);
-        // the fewest runs of at most bps blocks, of lengths that differ by
-        // at most one (the longest run bounds the kernel's time)
-        const int len = nbg - b0, ns = (len + bps - 1) / bps;
-        const uint32_t mg = ns > 1 ? (uint32_t)n_merge + 1 : 0;
-        for (int j = 0; j < ns; j++) {
-          const uint32_t lo = (uint32_t)(b0 + (int)((int64_t)j * len / ns));
-          const uint32_t hi = (uint32_t)(b0 + (int)((int64_t)(j + 1) * len / ns));
-          const int32_t item[4] = {s, off + g0, (int32_t)((uint32_t)(ge - g0) | (mg << 5)),
-                                   (int32_t)(lo | (hi << 16))};
-          const int32_t mrg[4] = {(int32_t)n_items, ns, off + g0, ge - g0};
-          emit(n_items, item, j == 0 && ns > 1 ? mrg : nullptr, n_merge);
-          n_items++;
-        }
-        if (ns > 1) n_merge++;
-      }
-    }
-    return std::make_pair(n_items, n_merge);
+  // items, merges and shared runs (the buffer layout), once to write them
+  // into buf. emit(item index, item[4], merge[4] or NULL, merge index,
+  // shared[2] or NULL, shared index) gets each item; the first item of a
+  // group with more than one run passes the group's merge (its runs are
+  // `stride` items apart: the set's size), the first item of a shared run
+  // passes the run's entry.
+  struct Counts {
+    int64_t items = 0, merges = 0, single = 0, shared = 0;
   };
-  const auto counts = walk([](int64_t, const int32_t *, const int32_t *, int64_t) {});
-  if (counts.first > INT32_MAX / 8 || counts.second > INT32_MAX / 8) {
+  auto walk = [&](auto &&emit) {
+    Counts n;
+    for (int phase = 0; phase < 2; phase++) {  // 0: groups on their own, 1: shared sets
+      for (int s = 0, off = 0; s < n_seq; off += seq_n[s], s++) {
+        const int ng = (seq_n[s] + T - 1) / T;  // query groups of s
+        const int W = ring || ng < 2 ? 1 : SHARED;
+        if ((W > 1) != (phase == 1)) continue;
+        for (int sg = 0; sg < ng; sg += W) {
+          const int nm = ng - sg < W ? ng - sg : W;  // groups in the set
+          const int g0 = sg * T, ge = (sg + nm) * T < seq_n[s] ? (sg + nm) * T : seq_n[s];
+          // logical blocks [b0, nbg): from the window of the set's first
+          // token (ring plans) or from 0, to the set's last position
+          const int64_t pf = (int64_t)seq_npast[s] + g0, pl = (int64_t)seq_npast[s] + ge - 1;
+          const int b0 = ring ? (int)((pf - window + 1 > 0 ? pf - window + 1 : 0) / B) : 0;
+          const int nbg = (int)(pl / B + 1);
+          // the fewest runs of at most bps blocks, of lengths that differ
+          // by at most one (the longest run bounds the kernel's time)
+          const int len = nbg - b0, ns = (len + bps - 1) / bps;
+          const int64_t first = n.items;
+          for (int j = 0; j < ns; j++) {
+            const uint32_t lo = (uint32_t)(b0 + (int)((int64_t)j * len / ns));
+            const uint32_t hi = (uint32_t)(b0 + (int)((int64_t)(j + 1) * len / ns));
+            const int32_t sh[2] = {(int32_t)n.items, nm};
+            for (int m = 0; m < nm; m++) {
+              const int t0 = g0 + m * T, te = t0 + T < seq_n[s] ? t0 + T : seq_n[s];
+              const uint32_t mg = ns > 1 ? (uint32_t)(n.merges + m) + 1 : 0;
+              const int32_t item[4] = {s, off + t0, (int32_t)((uint32_t)(te - t0) | (mg << 5)),
+                                       (int32_t)(lo | (hi << 16))};
+              const int32_t mrg[4] = {(int32_t)(first + m), ns, off + t0,
+                                      (int32_t)((uint32_t)(te - t0) | ((uint32_t)nm << 8))};
+              emit(n.items, item, j == 0 && ns > 1 ? mrg : nullptr, n.merges + m,
+                   W > 1 && m == 0 ? sh : nullptr, n.shared);
+              n.items++;
+            }
+            if (W > 1) n.shared++;
+          }
+          if (ns > 1) n.merges += nm;
+        }
+      }
+      if (phase == 0) n.single = n.items;
+    }
+    return n;
+  };
+  const Counts counts = walk([](int64_t, const int32_t *, const int32_t *, int64_t,
+                                const int32_t *, int64_t) {});
+  if (counts.items > INT32_MAX / 8 || counts.merges > INT32_MAX / 8) {
     set_error("plan: too many work items");
     return LGMLH_EINVAL;
   }
@@ -116,8 +149,10 @@ static int plan_impl(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
   in.n_tokens = (int32_t)N;
   in.max_blocks = max_blocks;
   in.block = B;
-  in.n_items = (int32_t)counts.first;
-  in.n_merge = (int32_t)counts.second;
+  in.n_items = (int32_t)counts.items;
+  in.n_merge = (int32_t)counts.merges;
+  in.n_single = (int32_t)counts.single;
+  in.n_shared = (int32_t)counts.shared;
   in.rows = 16;
   in.n_head_kv = n_head_kv;
   in.window = ring ? window : 0;
@@ -132,6 +167,7 @@ static int plan_impl(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
   in.off_logit_rows = o;   o = align16(o + 4 * (int64_t)n_seq);
   in.off_items = o;        o = align16(o + 16 * (int64_t)in.n_items);
   in.off_merge = o;        o = align16(o + 16 * (int64_t)in.n_merge);
+  in.off_shared = o;       o = align16(o + 8 * (int64_t)in.n_shared);
   in.bytes = o;
   *info = in;
   if (!buf) return LGMLH_OK;
@@ -161,9 +197,12 @@ static int plan_impl(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
   psoff[n_seq] = (int32_t)t;
   memcpy(b + in.off_block_tab, block_tab, 4 * (size_t)n_seq * max_blocks);
   int32_t *pit = (int32_t *)(b + in.off_items), *pmg = (int32_t *)(b + in.off_merge);
-  walk([&](int64_t i, const int32_t *item, const int32_t *mrg, int64_t m) {
+  int32_t *psh = (int32_t *)(b + in.off_shared);
+  walk([&](int64_t i, const int32_t *item, const int32_t *mrg, int64_t m, const int32_t *sh,
+           int64_t k) {
     memcpy(pit + 4 * i, item, 16);
     if (mrg) memcpy(pmg + 4 * m, mrg, 16);
+    if (sh) memcpy(psh + 2 * k, sh, 8);
   });
   return LGMLH_OK;
 }
@@ -212,6 +251,9 @@ extern "C" int lgmlh_plan_bind(const lgmlh_plan_info *info, const void *dev, lgm
   ub->logit_rows = (const int32_t *)(b + info->off_logit_rows);
   ub->items = (const int32_t *)(b + info->off_items);
   ub->merge = (const int32_t *)(b + info->off_merge);
+  ub->n_single = info->n_single;
+  ub->n_shared = info->n_shared;
+  ub->shared = (const int32_t *)(b + info->off_shared);
   ub->window = info->window;
   ub->ring = info->ring;
   return LGMLH_OK;

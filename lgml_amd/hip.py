@@ -49,7 +49,8 @@ class PlanInfo(C.Structure):
                [(n, C.c_int64) for n in ("bytes", "off_ids", "off_pos", "off_cells", "off_seq_off",
                                          "off_npast", "off_block_tab", "off_logit_rows",
                                          "off_items", "off_merge")] + \
-               [("window", C.c_int32), ("ring", C.c_int32)]
+               [("window", C.c_int32), ("ring", C.c_int32), ("n_single", C.c_int32),
+                ("n_shared", C.c_int32), ("off_shared", C.c_int64)]
 
 
 class Ubatch(C.Structure):
@@ -57,7 +58,8 @@ class Ubatch(C.Structure):
                                          "n_merge", "rows", "n_head_kv")] + \
                [(n, C.c_void_p) for n in ("ids", "pos", "cells", "seq_off", "seq_npast",
                                           "block_tab", "logit_rows", "items", "merge")] + \
-               [("window", C.c_int32), ("ring", C.c_int32)]
+               [("window", C.c_int32), ("ring", C.c_int32), ("n_single", C.c_int32),
+                ("n_shared", C.c_int32), ("shared", C.c_void_p)]
 
 
 class Layer(C.Structure):

@@ -35,7 +35,7 @@ def test_exports_every_declared_symbol(hip):
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing
     assert sorted(hip.SYMBOLS) == names
-    assert L.lgmlh_abi_version() == 4
+    assert L.lgmlh_abi_version() == 5
 
 
 def test_struct_layouts_match_the_header(hip, tmp_path):
@@ -170,15 +170,41 @@ def test_plan_packs_like_fill_batch(hip):
         runs.sort()
         assert runs[0][0] == 0 and all(runs[i][1] == runs[i + 1][0] for i in range(len(runs) - 1))
     assert info.n_merge == sum(1 for r in seen.values() if len(r) > 1)
-    # one merge group per split token group (numbered from 1), 0 for one split
+    # one merge group per split token group (numbered from 1), 0 for one split;
+    # its runs are `stride` items apart, in order
     mg = arr(buf, info.off_merge, 4 * info.n_merge, np.int32).reshape(-1, 4)
     for key, runs in seen.items():
         (g,) = groups[key]
         if len(runs) == 1:
             assert g == 0
         else:
-            first, ns, tok0, nt = mg[g - 1]
+            first, ns, tok0, f = mg[g - 1]
             assert ns == len(runs) and tok0 == key[1]
+            stride = f >> 8
+            got = [(items[first + j * stride][3] & 0xffff, items[first + j * stride][3] >> 16)
+                   for j in range(ns)]
+            assert all(items[first + j * stride][1] == tok0 for j in range(ns))
+            assert got == sorted(runs)
+    # the decode token's items come first (on their own); the chunk's 18
+    # groups of 4 tokens come in shared sets of 8, 8, 2 with the runs of
+    # each set's last token
+    assert info.n_single == len(seen[(0, 0)])
+    assert all(items[i][0] == 0 for i in range(info.n_single))
+    sh = arr(buf, info.off_shared, 2 * info.n_shared, np.int32).reshape(-1, 2)
+    covered = []
+    for first, n in sh:
+        assert 1 <= n <= 8
+        blk = {int(items[first + m][3]) for m in range(n)}
+        assert len(blk) == 1 and all(items[first + m][0] == 1 for m in range(n))
+        assert [items[first + m][1] for m in range(n)] == [items[first][1] + 4 * m
+                                                          for m in range(n)]
+        covered += range(first, first + n)
+    assert sorted(covered) == list(range(info.n_single, info.n_items))
+    for (s, tok0), runs in seen.items():
+        if s == 1:
+            set0 = 1 + ((tok0 - 1) // 32) * 32
+            last = min(set0 + 32, 71) - 1  # the set's last token
+            assert max(hi for _, hi in runs) == (150 + last - 1) // 64 + 1
 
 
 def test_plan_errors(hip):

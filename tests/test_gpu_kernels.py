@@ -285,6 +285,31 @@ def test_paged_attention_parity(L, H, Hkv, D):
         assert e < 2e-3 and e < 1e-4, (bps, e)
 
 
+@pytest.mark.parametrize("H,Hkv,D", [(32, 8, 128), (32, 4, 128), (4, 2, 64)])
+def test_paged_attention_prompt_chunks(L, H, Hkv, D):
+    """Prompt chunks run in shared sets of 8 query groups (one workgroup
+    reads each K / V block once for the set, lgmlh_plan): a 512-token chunk
+    deep in its prompt, sets cut short (37 and 40 tokens), a decode token
+    beside them; runs of 16 blocks and of 3 (merges of interleaved items)."""
+    seqs = [(512, 2500), (1, 700), (37, 3000), (40, 63)]
+    q, kpool, vpool, bt = make_attn_case(H, Hkv, D, seqs, seed=H + Hkv + D, n_cells=16384)
+    for bps in (0, 3):
+        got, plan = gpu_attention(L, q, kpool, vpool, H, Hkv, D, seqs, bt, bps, n_cells=16384)
+        assert plan.info.n_shared > 0 and plan.info.n_single > 0
+        b = core.BatchDesc([n for n, _ in seqs], [p for _, p in seqs], bt, 64,
+                           np.zeros(len(q), np.int32), [])
+        want = core.paged_attention(q, kpool, vpool, H, Hkv, D, 1.0 / np.sqrt(D), b)
+        assert np.isfinite(got).all()
+        e = rel_err(got.reshape(len(q) * H, D), want.reshape(len(q) * H, D))
+        assert e < 1e-4, (bps, e)
+        off = 0
+        for i, (n, p) in enumerate(seqs):  # alone: the same bits
+            alone, _ = gpu_attention(L, q[off:off + n], kpool, vpool, H, Hkv, D, [(n, p)],
+                                     bt[i:i + 1], bps, n_cells=16384)
+            assert np.array_equal(alone.view(np.uint32), got[off:off + n].view(np.uint32)), i
+            off += n
+
+
 def test_paged_attention_more_splits_than_kept_weights(L):
     """A group split into more runs (68) than the merge keeps weights for in
     LDS (64): the last runs' weights are recomputed from m and M."""
