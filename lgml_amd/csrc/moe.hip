@@ -457,8 +457,10 @@ __global__ void moe_sum_kernel(const float *__restrict__ y, const float *__restr
 static size_t a256(size_t b) { return (b + 255) & ~size_t(255); }
 
 // Column tile width for P picks over NE experts: 64 once an expert averages
-// 32 picks (prefill), else 16.
-int moe_tile_cols(int64_t P, int NE) { return P >= 32 * (int64_t)NE ? 64 : 16; }
+// 128 picks, else 16. (A 512-token prefill pass of C5 gives an expert about
+// 36 picks: in 64-column tiles those are half empty, and 16-column ones,
+// two workgroups per CU, made C5's mixed phase 9% faster.)
+int moe_tile_cols(int64_t P, int NE) { return P >= 128 * (int64_t)NE ? 64 : 16; }
 
 // An upper bound of the tiles of a grouping: sum over experts of
 // ceil(c_e / tc) <= (P + (tc - 1) * min(NE, P)) / tc, and <= P.

@@ -5,8 +5,8 @@ Routing (lgmlh_moe_route): ids bit-exact on the same logits (ties to the
 smaller index), weights within 1e-6. Grouped expert products
 (lgmlh_mul_mat_id): within 2e-3 max relative error of the oracle's f64
 result (they meet 1e-5: exact weights, f16 hi + lo activations), every
-weight type, U = 1 and U = n_used, the decode (16-column) and prefill
-(64-column) groupings, an expert picked twice by one token, ids out of range
+weight type, U = 1 and U = n_used, the 16-column groupings (decode and
+prefill passes) and the 64-column one (over 128 picks per expert), an expert picked twice by one token, ids out of range
 (rows of zeros). A pick's row is the same bits alone or in any batch. Whole
 C5-shaped passes at reduced depth (2 of 48 layers, full width) on ragged
 batches: logits within 2e-3, identical greedy ids, batched == lone.
@@ -87,7 +87,7 @@ def run_id(L, ty, w_dev, NE, M, K, x, ids):
 
 
 @pytest.mark.parametrize("ty", [core.Q4_K, core.Q6_K, core.Q8_0, core.F32])
-@pytest.mark.parametrize("T,U", [(64, 1), (64, 8), (600, 1)])
+@pytest.mark.parametrize("T,U", [(64, 1), (64, 8), (600, 1), (2100, 1)])
 def test_mul_mat_id_matches_oracle(L, ty, T, U):
     NE, k = 128, 8
     M, K = (256, 512) if ty != core.F32 else (64, 96)
