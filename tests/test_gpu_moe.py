@@ -6,7 +6,8 @@ smaller index), weights within 1e-6. Grouped expert products
 (lgmlh_mul_mat_id): within 2e-3 max relative error of the oracle's f64
 result (they meet 1e-5: exact weights, f16 hi + lo activations), every
 weight type, U = 1 and U = n_used, the 16-column groupings (decode and
-prefill passes) and the 64-column one (over 128 picks per expert), an expert picked twice by one token, ids out of range
+prefill passes) and the 64-column one (128 picks per expert and more:
+16 experts), an expert picked twice by one token, ids out of range
 (rows of zeros). A pick's row is the same bits alone or in any batch. Whole
 C5-shaped passes at reduced depth (2 of 48 layers, full width) on ragged
 batches: logits within 2e-3, identical greedy ids, batched == lone.
@@ -87,9 +88,10 @@ def run_id(L, ty, w_dev, NE, M, K, x, ids):
 
 
 @pytest.mark.parametrize("ty", [core.Q4_K, core.Q6_K, core.Q8_0, core.F32])
-@pytest.mark.parametrize("T,U", [(64, 1), (64, 8), (600, 1), (2100, 1)])
-def test_mul_mat_id_matches_oracle(L, ty, T, U):
-    NE, k = 128, 8
+# (300, 1, 16): 2400 picks over 16 experts, the 64-column grouping
+@pytest.mark.parametrize("T,U,NE", [(64, 1, 128), (64, 8, 128), (600, 1, 128), (300, 1, 16)])
+def test_mul_mat_id_matches_oracle(L, ty, T, U, NE):
+    k = 8
     M, K = (256, 512) if ty != core.F32 else (64, 96)
     rng = np.random.default_rng(ty * 1000 + T + U)
     wf = (rng.standard_normal((NE * M, K)) * 0.02).astype(np.float32)
