@@ -84,6 +84,10 @@ def parse():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES, 8 times (the known-size kernel "
                          "that scales the FETCH_SIZE / WRITE_SIZE counters); prints nothing")
+    ap.add_argument("--product", default="", metavar="TYPE:MxK:N",
+                    help="only run one weight product (q4 / q6 / q8, M x K weights, N rows), "
+                         "5 times after 2 untimed calls: the subject of the products' counter "
+                         "passes; prints its mean time")
     return ap.parse_args()
 
 
@@ -248,6 +252,43 @@ def product_flops(hp, n_tokens, n_out):
     return 2.0 * (per_tok * n_tokens + V * E * n_out)
 
 
+def product_only(spec):
+    """One weight product of seeded random weights (lgmlh_gen_normal, as the
+    benched models) on N(0, 1) rows, run 2 + 5 times."""
+    import torch
+    from lgml_amd import hip
+    L = hip.lib()
+    name, mk, n = spec.split(":")
+    ty = {"q4": hip.Q4_K, "q6": hip.Q6_K, "q8": hip.Q8_0}[name]
+    M, K = (int(v) for v in mk.split("x"))
+    N = int(n)
+    st = torch.cuda.current_stream().cuda_stream
+    raw = torch.empty(L.lgmlh_row_size(ty, K) * M, dtype=torch.uint8, device="cuda")
+    hip.check(L.lgmlh_gen_normal(20261201, ty, M, K, 0.0, 0.02, raw.data_ptr(), st))
+    w = torch.empty(L.lgmlh_repacked_bytes(ty, M, K), dtype=torch.uint8, device="cuda")
+    hip.check(L.lgmlh_repack(ty, M, K, raw.data_ptr(), w.data_ptr(), st))
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1)
+    x = torch.randn(N, K, device="cuda", generator=g)
+    y = torch.empty(N, M, device="cuda")
+    nb = L.lgmlh_mul_mat_workspace(ty, M, K, N)
+    ws = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda")
+
+    def call():
+        hip.check(L.lgmlh_mul_mat(ty, w.data_ptr(), M, K, x.data_ptr(), hip.F32, N, y.data_ptr(),
+                                  hip.EPI_NONE, None, ws.data_ptr(), nb, st))
+    call()
+    call()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        call()
+    e1.record()
+    torch.cuda.synchronize()
+    print("product %s: %.1f us" % (spec, e0.elapsed_time(e1) * 1e3 / 5))
+    return 0
+
+
 def main():
     args = parse()
     if args.calibrate_copy:
@@ -260,6 +301,8 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         return 0
+    if args.product:
+        return product_only(args.product)
     if args.gpus != 1:
         print("bench.py measures one GPU: every GPU box here has one, and the multi-GPU "
               "sharding of this path is design only (see DESIGN.md); run with --gpus 1",
