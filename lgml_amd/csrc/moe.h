@@ -11,6 +11,8 @@ struct GroupOut {
   int4 *tiles;        // {expert, first, count, 0} per column tile
   int32_t *n_tiles;   // [1] tiles in use
   int tile_cols;      // 16 or 64
+  int32_t *rank;      // [P] scratch of the many-workgroup grouping
+  int32_t *counts;    // [chunks][NE] scratch of the many-workgroup grouping
 };
 
 int moe_tile_cols(int64_t P, int NE);

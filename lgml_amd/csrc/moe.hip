@@ -100,6 +100,63 @@ router_part_kernel(const float *__restrict__ w, int NE, int64_t K, const float *
   }
 }
 
+// The same partials for a prefill-sized batch: a workgroup takes 64
+// experts x 64 tokens of one K chunk, thread t experts t % 16 + 16 i and
+// tokens t / 16 + 16 j (i, j < 4), so each K fragment read from LDS feeds
+// four products. Each sum is the same fmaf chain in k order.
+__global__ void __launch_bounds__(256)
+router_tile_kernel(const float *__restrict__ w, int NE, int64_t K, const float *__restrict__ x,
+                   int64_t N, float *__restrict__ part) {
+  constexpr int TE = 64, TT = 64, Q = ROUTER_KC / 4;
+  __shared__ __align__(16) float ws_[TE * ROUTER_LD];
+  __shared__ __align__(16) float xs_[TT * ROUTER_LD];
+  const int t = threadIdx.x, ei = t & 15, ti = t >> 4;
+  const int64_t e0 = (int64_t)blockIdx.x * TE, n0 = (int64_t)blockIdx.z * TT;
+  const int64_t k0 = (int64_t)blockIdx.y * ROUTER_KC;
+  for (int i = t; i < TE * Q; i += 256) {
+    const int r = i / Q, c4 = 4 * (i % Q);
+    f32x4 v = f32x4{0, 0, 0, 0};
+    if (e0 + r < NE && k0 + c4 < K) v = *(const f32x4 *)(w + (e0 + r) * K + k0 + c4);
+    *(f32x4 *)&ws_[r * ROUTER_LD + c4] = v;
+  }
+  for (int i = t; i < TT * Q; i += 256) {
+    const int r = i / Q, c4 = 4 * (i % Q);
+    f32x4 v = f32x4{0, 0, 0, 0};
+    if (n0 + r < N && k0 + c4 < K) v = *(const f32x4 *)(x + (n0 + r) * K + k0 + c4);
+    *(f32x4 *)&xs_[r * ROUTER_LD + c4] = v;
+  }
+  __syncthreads();
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = 0.0f;
+#pragma unroll 2
+  for (int c = 0; c < ROUTER_KC; c += 4) {
+    f32x4 wv[4], xv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) wv[i] = *(const f32x4 *)(ws_ + (ei + 16 * i) * ROUTER_LD + c);
+#pragma unroll
+    for (int j = 0; j < 4; j++) xv[j] = *(const f32x4 *)(xs_ + (ti + 16 * j) * ROUTER_LD + c);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        acc[i][j] = fmaf(wv[i][0], xv[j][0], acc[i][j]);
+        acc[i][j] = fmaf(wv[i][1], xv[j][1], acc[i][j]);
+        acc[i][j] = fmaf(wv[i][2], xv[j][2], acc[i][j]);
+        acc[i][j] = fmaf(wv[i][3], xv[j][3], acc[i][j]);
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int64_t e = e0 + ei + 16 * i, n = n0 + ti + 16 * j;
+      if (e < NE && n < N) part[((int64_t)blockIdx.y * N + n) * NE + e] = acc[i][j];
+    }
+}
+
 // ---- picks and weights ---------------------------------------------------------
 // (value, index) order of the top-k: larger value first, then smaller index.
 __device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
@@ -416,6 +473,132 @@ group_kernel(const int32_t *__restrict__ ids, int P, int NE, GroupOut go, float 
   group_picks(lds, P, NE, go);
 }
 
+// Grouping over many workgroups, for thousands of picks: chunks of
+// GROUP_CHUNK picks. group_count_kernel ranks each pick among the picks of
+// its chunk with the same expert (stable) and counts the chunk's picks per
+// expert; group_place_kernel adds the counts of the chunks before its own
+// and the experts before each expert, and places its picks. The result is
+// the one-workgroup grouping's: expert-major, pick order within an expert.
+constexpr int GROUP_CHUNK = 256;
+constexpr int GROUP_ONE = 1024;  // picks grouped by one workgroup
+
+__global__ void __launch_bounds__(GROUP_CHUNK)
+group_count_kernel(const int32_t *__restrict__ ids, int P, int NE, GroupOut go,
+                   float *__restrict__ y, int64_t M) {
+  __shared__ int32_t cnt[GROUP_CHUNK / 64][MOE_MAX_EXPERTS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i < (GROUP_CHUNK / 64) * MOE_MAX_EXPERTS; i += GROUP_CHUNK)
+    (&cnt[0][0])[i] = 0;
+  const int p = blockIdx.x * GROUP_CHUNK + tid;
+  int e = p < P ? ids[p] : -1;
+  if (p < P && (e < 0 || e >= NE)) {
+    e = -1;  // no expert: its Y row is zeros
+    if (y)
+      for (int64_t m = 0; m < M; m++) y[(int64_t)p * M + m] = 0.0f;
+  }
+  // rank among the wave's earlier lanes with the same expert
+  int rank = 0;
+  for (int l2 = 0; l2 < 64; l2++) {
+    const int e2 = __builtin_amdgcn_readlane(e, l2);
+    rank += (l2 < lane && e2 == e) ? 1 : 0;
+  }
+  __syncthreads();
+  if (e >= 0) atomicAdd(&cnt[wave][e], 1);  // counts: order-free
+  __syncthreads();
+  if (p < P) {
+    // the pick's expert and rank in its chunk (-1: no expert)
+    for (int w2 = 0; w2 < wave && e >= 0; w2++) rank += cnt[w2][e];
+    go.rank[p] = e >= 0 ? (e << 16) | rank : -1;
+  }
+  for (int ee = tid; ee < NE; ee += GROUP_CHUNK) {
+    int c = 0;
+#pragma unroll
+    for (int w2 = 0; w2 < GROUP_CHUNK / 64; w2++) c += cnt[w2][ee];
+    go.counts[(int64_t)blockIdx.x * NE + ee] = c;
+  }
+}
+
+__global__ void __launch_bounds__(GROUP_CHUNK)
+group_place_kernel(int P, int NE, GroupOut go) {
+  __shared__ int32_t base[MOE_MAX_EXPERTS];
+  __shared__ int32_t off[MOE_MAX_EXPERTS + 1], toff[MOE_MAX_EXPERTS + 1];
+  __shared__ int32_t wsum[2][GROUP_CHUNK / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int C = (P + GROUP_CHUNK - 1) / GROUP_CHUNK, c0 = blockIdx.x;
+  // experts tid, tid + GROUP_CHUNK (NE <= 512): their totals and the picks
+  // of the chunks before this one
+  constexpr int EPT = MOE_MAX_EXPERTS / GROUP_CHUNK;
+  int tot[EPT], pre[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    const int e = tid + j * GROUP_CHUNK;
+    tot[j] = pre[j] = 0;
+    if (e < NE)
+      for (int c = 0; c < C; c++) {
+        const int v = go.counts[(int64_t)c * NE + e];
+        tot[j] += v;
+        pre[j] += c < c0 ? v : 0;
+      }
+  }
+  // exclusive scans over the experts of the totals and of the tile counts:
+  // expert e = tid + j GROUP_CHUNK, scanned in e order
+  int run_c = 0, run_t = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    const int e = tid + j * GROUP_CHUNK;
+    const int nt = (tot[j] + go.tile_cols - 1) / go.tile_cols;
+    int ci = tot[j], ti = nt;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int a = __shfl_up(ci, o), b = __shfl_up(ti, o);
+      if (lane >= o) {
+        ci += a;
+        ti += b;
+      }
+    }
+    if (lane == 63) {
+      wsum[0][wave] = ci;
+      wsum[1][wave] = ti;
+    }
+    __syncthreads();
+    int cw = run_c, tw = run_t;
+    for (int w2 = 0; w2 < wave; w2++) {
+      cw += wsum[0][w2];
+      tw += wsum[1][w2];
+    }
+    for (int w2 = 0; w2 < GROUP_CHUNK / 64; w2++) {
+      run_c += wsum[0][w2];
+      run_t += wsum[1][w2];
+    }
+    if (e < NE) {
+      off[e] = cw + ci - tot[j];
+      toff[e] = tw + ti - nt;
+      base[e] = off[e] + pre[j];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    off[NE] = run_c;
+    toff[NE] = run_t;
+    if (c0 == 0) *go.n_tiles = run_t;
+  }
+  __syncthreads();
+  const int p = c0 * GROUP_CHUNK + tid;
+  if (p < P) {
+    const int v = go.rank[p];
+    if (v >= 0) go.sorted[base[v >> 16] + (v & 0xffff)] = p;
+  }
+  if (c0 != 0) return;
+  // the tile list, expert by expert
+  for (int e = tid; e < NE; e += GROUP_CHUNK) {
+    const int c = off[e + 1] - off[e];
+    for (int i = 0, t = toff[e]; i * go.tile_cols < c; i++, t++) {
+      const int first = off[e] + i * go.tile_cols;
+      const int n = c - i * go.tile_cols < go.tile_cols ? c - i * go.tile_cols : go.tile_cols;
+      go.tiles[t] = int4{e, first, n, 0};
+    }
+  }
+}
+
 // ---- f32 experts: one workgroup per (pick, 256 rows), k in order ---------------
 __global__ void __launch_bounds__(256)
 f32_id_kernel(const float *__restrict__ w, int NE, int64_t M, int64_t K,
@@ -480,6 +663,11 @@ int router_logits(const float *w, int NE, int64_t K, const float *x, int64_t T, 
     set_error("moe router: K %lld is not a multiple of 4", (long long)K);
     return LGMLH_EINVAL;
   }
+  if (T > 64 && NE >= 64) {  // prefill-sized: 64 x 64 tiles
+    dim3 grid((unsigned)((NE + 63) / 64), (unsigned)router_splits(K), (unsigned)((T + 63) / 64));
+    hipLaunchKernelGGL(router_tile_kernel, grid, dim3(256), 0, st, w, NE, K, x, T, part);
+    return hip_check(hipGetLastError(), "moe router");
+  }
   const int tok = T <= 64 ? 16 : 64;
   dim3 grid((unsigned)((NE + 15) / 16), (unsigned)router_splits(K), (unsigned)((T + tok - 1) / tok));
   if (tok == 16)
@@ -502,13 +690,16 @@ static int check_route(int64_t T, int NE, int n_used, int gating) {
   return LGMLH_OK;
 }
 
+static void launch_group(const int32_t *ids, int P, int NE, const GroupOut &g, float *y,
+                         int64_t M, hipStream_t st);
+
 // Picks, weights and (with go) the grouping, from nz router partials.
 int moe_route_dev(const float *part, int nz, int64_t T, int NE, int n_used, int gating,
                   int norm_topk, float scale, int32_t *ids, float *wts, const GroupOut *go,
                   hipStream_t st) {
   LGMLH_TRY(check_route(T, NE, n_used, gating));
   if (T == 0) return LGMLH_OK;
-  GroupOut g = go ? *go : GroupOut{nullptr, nullptr, nullptr, 16};
+  GroupOut g = go ? *go : GroupOut{nullptr, nullptr, nullptr, 16, nullptr, nullptr};
   const int grp = go ? 1 : 0;
   // Up to 16 tokens: routing and grouping in one workgroup (one launch).
   // More: the routing spreads over workgroups of 16 tokens (one per CU
@@ -536,15 +727,17 @@ int moe_route_dev(const float *part, int nz, int64_t T, int NE, int n_used, int 
   else
     hipLaunchKernelGGL(route_many_kernel<32>, grid, dim3(256), 0, st, part, nz, T, NE, n_used,
                        gating, norm_topk, scale, ids, wts);
-  if (grp)
-    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(ROUTE_THREADS), 0, st, ids,
-                       (int)(T * n_used), NE, g, nullptr, (int64_t)0);
+  if (grp) launch_group(ids, (int)(T * n_used), NE, g, nullptr, 0, st);
   return hip_check(hipGetLastError(), "moe route");
 }
 
-// Workspace of a grouping of P picks: sorted, tiles, count.
+// Workspace of a grouping of P picks: sorted, tiles, count, and the
+// many-workgroup grouping's ranks and chunk counts.
+static int64_t group_chunks(int64_t P) { return (P + GROUP_CHUNK - 1) / GROUP_CHUNK; }
+
 size_t group_bytes(int64_t P, int NE, int tc) {
-  return a256((size_t)P * 4) + a256((size_t)moe_max_tiles(P, NE, tc) * 16) + 256;
+  return a256((size_t)P * 4) + a256((size_t)moe_max_tiles(P, NE, tc) * 16) + 256 +
+         a256((size_t)P * 4) + a256((size_t)group_chunks(P) * NE * 4);
 }
 
 GroupOut group_carve(void *ws, int64_t P, int NE, int tc) {
@@ -555,8 +748,26 @@ GroupOut group_carve(void *ws, int64_t P, int NE, int tc) {
   g.tiles = (int4 *)b;
   b += a256((size_t)moe_max_tiles(P, NE, tc) * 16);
   g.n_tiles = (int32_t *)b;
+  b += 256;
+  g.rank = (int32_t *)b;
+  b += a256((size_t)P * 4);
+  g.counts = (int32_t *)b;
   g.tile_cols = tc;
   return g;
+}
+
+// The grouping of P picks: one workgroup for a few (decode), chunked over
+// many workgroups for a prefill pass's thousands (the same sorted order
+// and tiles either way).
+static void launch_group(const int32_t *ids, int P, int NE, const GroupOut &g, float *y, int64_t M,
+                         hipStream_t st) {
+  if (P <= GROUP_ONE) {
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(ROUTE_THREADS), 0, st, ids, P, NE, g, y, M);
+    return;
+  }
+  const unsigned C = (unsigned)group_chunks(P);
+  hipLaunchKernelGGL(group_count_kernel, dim3(C), dim3(GROUP_CHUNK), 0, st, ids, P, NE, g, y, M);
+  hipLaunchKernelGGL(group_place_kernel, dim3(C), dim3(GROUP_CHUNK), 0, st, P, NE, g);
 }
 
 // Y (P, M) of the experts of the picks; x is f32 (T * U rows, f32
@@ -639,8 +850,7 @@ extern "C" int lgmlh_mul_mat_id(int type, const void *w, int64_t n_expert, int64
   const int NE = (int)n_expert;
   const int tc = moe_tile_cols(P, NE);
   GroupOut go = group_carve(workspace, P, NE, tc);
-  hipLaunchKernelGGL(group_kernel, dim3(1), dim3(ROUTE_THREADS), 0, st, ids,
-                     (int)P, NE, go, y, M);
+  launch_group(ids, (int)P, NE, go, y, M, st);
   LGMLH_TRY(hip_check(hipGetLastError(), "mul_mat_id group"));
   f16 *xs = nullptr;
   if (type != LGMLH_F32) {
