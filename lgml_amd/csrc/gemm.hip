@@ -321,7 +321,23 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int64_t NSB = K / QK_K;
   const int64_t MT = (M + 15) / 16;
-  int64_t n0 = (int64_t)blockIdx.x * COLS;
+  // Tile order for the wide tiles: the dispatcher deals workgroups round-
+  // robin to the 8 XCDs, each with its own L2, so the tiles are renumbered
+  // to give consecutive tiles (the column tiles of one row block, which
+  // read the same weights) to one XCD. Which workgroup computes a tile
+  // changes, not how (prefill products 4% faster; no gain for 16-column
+  // tiles).
+  uint32_t bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+  if constexpr (NCT == 4 && !GATHER) {
+    const uint32_t gx = gridDim.x, gy = gridDim.y, total = gx * gy * gridDim.z;
+    const uint32_t L = bx + gx * (by + gy * bz);
+    const uint32_t xcd = L & 7u, per = total >> 3, rem = total & 7u;
+    const uint32_t t = xcd * per + (xcd < rem ? xcd : rem) + (L >> 3);
+    bx = t % gx;
+    by = (t / gx) % gy;
+    bz = t / (gx * gy);
+  }
+  int64_t n0 = (int64_t)bx * COLS;
   int first = 0, count = 0;
   if constexpr (GATHER) {
     // tiles past the ones in use leave at once (the whole workgroup)
@@ -332,9 +348,9 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
     count = tl.z;
     n0 = 0;
   }
-  const int64_t rt0 = (int64_t)blockIdx.y * (WG_ROWS / 16) + wave * RT_PER_WAVE;
+  const int64_t rt0 = (int64_t)by * (WG_ROWS / 16) + wave * RT_PER_WAVE;
   // K range: splits fold z .. fold z + fold - 1 of sb_per_split steps each
-  const int z = blockIdx.z;
+  const int z = (int)bz;
   const int64_t sb_lo = (int64_t)z * fold * sb_per_split;
   const int64_t sb_hi = sb_lo + fold * sb_per_split < NSB ? sb_lo + fold * sb_per_split : NSB;
   const int c = lane >> 4, r16 = lane & 15;
