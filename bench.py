@@ -84,6 +84,11 @@ def parse():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES, 8 times (the known-size kernel "
                          "that scales the FETCH_SIZE / WRITE_SIZE counters); prints nothing")
+    ap.add_argument("--read-probe", type=int, default=0, metavar="BYTES",
+                    help="only time a plain streaming read (f32 row sums of BYTES of f16 in "
+                         "rows of 4096) and a device copy of BYTES, 10 times each after 2 "
+                         "untimed: the practical HBM ceilings the kernels' GB/s compare with; "
+                         "prints both")
     ap.add_argument("--product", default="", metavar="TYPE:MxK:N",
                     help="only run one weight product (q4 / q6 / q8, M x K weights, N rows), "
                          "5 times after 2 untimed calls: the subject of the products' counter "
@@ -289,8 +294,36 @@ def product_only(spec):
     return 0
 
 
+def read_probe(nbytes):
+    """The practical HBM ceilings on this box: a streaming read (torch's f32
+    row sums of f16 rows of 4096 values: 5.9-6.4 TB/s, where one sum over
+    the whole buffer reaches only 3.6) and a device copy, each of nbytes,
+    timed with events over 10 runs after 2 untimed ones."""
+    import torch
+    a = torch.empty(nbytes // 2, dtype=torch.float16, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    rows = a.view(-1, 4096)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for name, fn, moved in (("read", lambda: rows.sum(1, dtype=torch.float32), nbytes),
+                            ("copy", lambda: b.copy_(a), 2 * nbytes)):
+        fn()
+        fn()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(10):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / 10
+        print("%s of %d B: %.1f us, %.0f GB/s (bytes moved %d)" % (name, nbytes, us, moved / us / 1e3,
+                                                                  moved))
+    return 0
+
+
 def main():
     args = parse()
+    if args.read_probe:
+        return read_probe(args.read_probe)
     if args.calibrate_copy:
         import torch
         n = args.calibrate_copy // 4
