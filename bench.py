@@ -338,7 +338,7 @@ def main():
         return product_only(args.product)
     if args.gpus != 1:
         print("bench.py measures one GPU: every GPU box here has one, and the multi-GPU "
-              "sharding of this path is design only (see DESIGN.md); run with --gpus 1",
+              "sharding of this path is design only; run with --gpus 1",
               file=sys.stderr)
         return 2
     import numpy as np
