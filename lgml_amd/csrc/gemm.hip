@@ -29,9 +29,10 @@
 
 namespace lgmlh {
 
-constexpr int GEMM_WAVES = 8;      // waves per workgroup
-constexpr int GEMM_THREADS = GEMM_WAVES * 64;
+constexpr int GEMM_WAVES = 8;      // waves per workgroup (4 for Q4_K wide tiles: gemm_waves)
 constexpr int RT_PER_WAVE = 2;     // 16-row tiles per wave
+// Rows of an 8-wave workgroup: the unit in which the K-split count and the
+// tiling rules count row tiles (fixed, so the splits do not depend on N).
 constexpr int WG_ROWS = GEMM_WAVES * RT_PER_WAVE * 16;  // 256
 constexpr int WG_COLS = 64;        // N columns per workgroup of a plain product (4 tiles)
 // X in LDS: per plane NCT * 16 rows x 32 pieces of 8 f16 (16 B), piece kp
@@ -280,15 +281,16 @@ struct WFrag<LGMLH_Q8_0> {
 };
 
 // ---- the quantized GEMM --------------------------------------------------------
-// grid: (ceil(N / (16 NCT)), ceil(M / WG_ROWS), splits); blockIdx.x (N
-// tiles) varies fastest so the workgroups that share a weight tile run
-// together.
+// grid: (ceil(N / (16 NCT)), ceil(M / rows per workgroup), splits);
+// blockIdx.x (N tiles) varies fastest so the workgroups that share a
+// weight tile run together (the wide tiles renumber them per XCD).
 //
 // Pipeline: the weight fragments (into registers) and X pieces (global-to-
 // LDS) of K step sb + 1 are issued at the start of step sb and load while
 // it computes (two register sets, two LDS buffers, each buffer its own LDS
 // object so that reads of one need not wait for loads into the other; one
-// barrier per step). Q8_0 chunk headers (a d per row and 32-value block)
+// barrier per step; with one buffer, the X loads follow the step's
+// products and a barrier). Q8_0 chunk headers (a d per row and 32-value block)
 // travel with X, global-to-LDS, and each group's d are read from LDS one
 // group ahead. A split writes its partial sums; a second kernel adds the
 // splits in order (no inter-workgroup sync).
@@ -296,26 +298,41 @@ struct WFrag<LGMLH_Q8_0> {
 // products of at most 16 columns): registers capped at 128 so that two
 // workgroups share a CU, twice the weight loads in flight (C5's expert
 // products 5.18 -> 4.42 ms per step). Q8_0 would spill under the cap.
+// Q4_K with 64-column tiles: workgroups of 4 waves (128 rows) with one X
+// buffer (66 KB of LDS), so that two share a CU; one's waits for its next
+// K step (the X loads, the barriers) are filled by the other's products
+// (C2's Q4_K shapes at N = 576: 4-15% faster, gate|up at N = 64 6%; the
+// mixed phase 3228 -> 3397 tok/s). A tile's sums do not depend on the
+// workgroup shape: each 16-row tile takes the same fragments in the same
+// K steps.
+__host__ __device__ constexpr int gemm_waves(int type, int nct) {
+  return nct == 4 && type == LGMLH_Q4_K ? 4 : GEMM_WAVES;
+}
 template <int TYPE, int NCT, bool GATHER>
-__global__ void __launch_bounds__(GEMM_THREADS, NCT == 1 && TYPE != LGMLH_Q8_0 ? 4 : 1)
+__global__ void __launch_bounds__(gemm_waves(TYPE, NCT) * 64,
+                                  NCT == 1 && TYPE != LGMLH_Q8_0   ? 4
+                                  : NCT == 4 && TYPE == LGMLH_Q4_K ? 2
+                                                                   : 1)
 qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__restrict__ xs,
              int64_t Npad, int64_t N, float *__restrict__ y, int64_t ldy,
              const float *__restrict__ residual, int nz, int sb_per_split, int fold,
              float *__restrict__ part, Gather gt) {
+  constexpr int WVS = gemm_waves(TYPE, NCT);  // waves per workgroup
+  constexpr bool ONEBUF = WVS < GEMM_WAVES;     // one X buffer
   constexpr int COLS = NCT * 16;            // N columns per workgroup
   constexpr int X_SLOTS = COLS * 32;
-  __shared__ __align__(16) u32x4 xh0_[X_SLOTS], xh1_[X_SLOTS];
-  __shared__ __align__(16) u32x4 xl0_[X_SLOTS], xl1_[X_SLOTS];
+  __shared__ __align__(16) u32x4 xh0_[X_SLOTS], xh1_[ONEBUF ? 1 : X_SLOTS];
+  __shared__ __align__(16) u32x4 xl0_[X_SLOTS], xl1_[ONEBUF ? 1 : X_SLOTS];
   __shared__ __align__(16) u32x4 gh0_[64], gh1_[64];  // group sums, hi: 8 f16 per row
   __shared__ __align__(16) u32x4 gl0_[64], gl1_[64];  // group sums, lo
   // Q8_0: the 256-byte headers of every wave's chunks (wave w, tile a at
   // slots 32 w + 16 a .. + 15)
-  constexpr int HD_SLOTS = TYPE == LGMLH_Q8_0 ? GEMM_WAVES * RT_PER_WAVE * 16 : 1;
+  constexpr int HD_SLOTS = TYPE == LGMLH_Q8_0 ? WVS * RT_PER_WAVE * 16 : 1;
   __shared__ __align__(16) u32x4 hd0_[HD_SLOTS], hd1_[HD_SLOTS];
-  auto XH = [&](int b) { return b ? xh1_ : xh0_; };
-  auto XL = [&](int b) { return b ? xl1_ : xl0_; };
-  auto GH = [&](int b) { return b ? gh1_ : gh0_; };
-  auto GL = [&](int b) { return b ? gl1_ : gl0_; };
+  auto XH = [&](int b) { return b && !ONEBUF ? xh1_ : xh0_; };
+  auto XL = [&](int b) { return b && !ONEBUF ? xl1_ : xl0_; };
+  auto GH = [&](int b) { return b && !ONEBUF ? gh1_ : gh0_; };
+  auto GL = [&](int b) { return b && !ONEBUF ? gl1_ : gl0_; };
   auto HD = [&](int b) { return b ? hd1_ : hd0_; };
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -352,7 +369,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
     count = tl.z;
     n0 = 0;
   }
-  const int64_t rt0 = (int64_t)by * (WG_ROWS / 16) + wave * RT_PER_WAVE;
+  const int64_t rt0 = (int64_t)by * (WVS * RT_PER_WAVE) + wave * RT_PER_WAVE;
   // K range: splits fold z .. fold z + fold - 1 of sb_per_split steps each
   const int z = (int)bz;
   const int64_t sb_lo = (int64_t)z * fold * sb_per_split;
@@ -376,7 +393,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   // l of load j writes slot s = 64 (XJ w + j) + l, which holds piece
   // kp = (s % 32) ^ (row & 15) of row s / 32.
   typedef __attribute__((address_space(3))) void lds_t;
-  constexpr int XJ = X_SLOTS / (GEMM_WAVES * 64);  // NCT
+  constexpr int XJ = X_SLOTS / (WVS * 64);  // NCT
   const f16 *xhi = xs + n0 * K + sb_lo * QK_K, *xlo = xhi + Npad * K;
   const f16 *ghi = xs + 2 * Npad * K + n0 * (K / 32) + sb_lo * 8, *glo = ghi + Npad * (K / 32);
   // byte offsets of a lane's pieces from the plane's K step (the planes
@@ -602,10 +619,19 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
                   WFrag<TYPE>(&nxt)[RT_PER_WAVE], int buf) {
     const uint32_t kn = k + 1 < nsteps ? k + 1 : k;
     load_w(nxt, kn);
-    load_x(kn, buf ^ 1);
-    compute(cur, buf);
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's X loads have landed in LDS
-    __syncthreads();                // ... and everyone's; buffer buf is free again
+    if constexpr (ONEBUF) {
+      // one buffer: the next step's X goes in once every wave has read it
+      compute(cur, 0);
+      __syncthreads();
+      load_x(kn, 0);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    } else {
+      load_x(kn, buf ^ 1);
+      compute(cur, buf);
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's X loads have landed in LDS
+      __syncthreads();                // ... and everyone's; buffer buf is free again
+    }
   };
   if (nsteps > 0) {
     load_w(w0, 0);
@@ -818,10 +844,12 @@ static int launch_q(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t 
                        : 1;
   const int nz = (splits + fold - 1) / fold;
   *group = fold == 1 ? SPLIT_PAIR : 1;
-  dim3 grid((unsigned)((N + cols - 1) / cols), (unsigned)((M + WG_ROWS - 1) / WG_ROWS),
+  const int wrows = gemm_waves(TYPE, nct) * RT_PER_WAVE * 16;  // rows per workgroup
+  dim3 grid((unsigned)((N + cols - 1) / cols), (unsigned)((M + wrows - 1) / wrows),
             (unsigned)nz);
 #define LGMLH_PLAIN(NCT_)                                                                  \
-  hipLaunchKernelGGL((qgemm_kernel<TYPE, NCT_, false>), grid, dim3(GEMM_THREADS), 0, st,   \
+  hipLaunchKernelGGL((qgemm_kernel<TYPE, NCT_, false>), grid, dim3(gemm_waves(TYPE, NCT_) * 64), \
+                     0, st,                                                                \
                      (const uint8_t *)w, M, K, xs, Npad, N, y, ldy, res, nz, spb, fold,    \
                      part, Gather{})
   if (nct == 1)
@@ -881,8 +909,9 @@ template <int TYPE, int NCT>
 static void launch_grouped(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t Npad,
                            const Gather &gt, int max_tiles, float *y, hipStream_t st) {
   const int NSB = (int)(K / QK_K);
-  dim3 grid((unsigned)max_tiles, (unsigned)((M + WG_ROWS - 1) / WG_ROWS), 1);
-  hipLaunchKernelGGL((qgemm_kernel<TYPE, NCT, true>), grid, dim3(GEMM_THREADS), 0, st,
+  const int wrows = gemm_waves(TYPE, NCT) * RT_PER_WAVE * 16;
+  dim3 grid((unsigned)max_tiles, (unsigned)((M + wrows - 1) / wrows), 1);
+  hipLaunchKernelGGL((qgemm_kernel<TYPE, NCT, true>), grid, dim3(gemm_waves(TYPE, NCT) * 64), 0, st,
                      (const uint8_t *)w, M, K, xs, Npad, (int64_t)0, y, M, (const float *)nullptr,
                      1, NSB, 1, (float *)nullptr, gt);
 }
