@@ -830,9 +830,12 @@ static int launch_q(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t 
   // CU (C5's dense products 6.81 -> 6.49 ms per step, C4's Q8_0 ones 1.96
   // -> 1.85; at 256, C2's gate|up, 224 workgroups, lost 20%). A prefill-
   // sized batch keeps wide tiles, so each weight fragment is dequantized
-  // once for 64 columns.
+  // once for 64 columns. Q4_K's wide tiles run two 4-wave workgroups per
+  // CU themselves, so for Q4_K the bound is 100 (C2's q|k|v and wo at 160
+  // and 128: decode +1.2%).
   int nct = N <= 16 ? 1 : N <= 32 ? 2 : WG_COLS / 16;
-  if (N <= 64 && (int64_t)((M + WG_ROWS - 1) / WG_ROWS) * splits < 200) nct = 1;
+  const int64_t small_wg = TYPE == LGMLH_Q4_K ? 100 : 200;
+  if (N <= 64 && (int64_t)((M + WG_ROWS - 1) / WG_ROWS) * splits < small_wg) nct = 1;
   const int cols = 16 * nct;
   const int64_t tiles = ((N + cols - 1) / cols) * ((M + WG_ROWS - 1) / WG_ROWS);
   // With workgroups to spare (two rounds of CUs or more), a workgroup runs

@@ -131,13 +131,15 @@ def run_mul_mat(L, ty, w, M, K, x, xtype=None):
 
 # Column tiles per workgroup (gemm.hip launch_q): 16 for N <= 16, 32 for
 # N <= 32, else 64; but a product of N <= 64 with fewer than 200 workgroups
-# of row tiles x K splits takes 16. The small shapes run the 16-column
-# kernel at N <= 64 and the 64-column one at N = 70 and 130; the large
-# ones, (25600, 1024) = 100 row tiles x 2 splits and (51200, 256) = 200 x
-# 1, run the 32- and 64-column kernels at N = 17 / 32 and 64 / 130.
+# of row tiles x K splits (Q4_K: 100) takes 16. The small shapes run the
+# 16-column kernel at N <= 64 and the 64-column one at N = 70 and 130; the
+# large ones, (25600, 1024) = 100 row tiles x 2 splits and (51200, 256) =
+# 200 x 1, run the 32- and 64-column kernels at N = 17 / 32 and 64 / 130;
+# (12800, 1024) = 50 x 2 runs Q4_K's 64-column kernel at N = 64 and the
+# others' 16-column one.
 @pytest.mark.parametrize("ty", [core.Q4_K, core.Q6_K, core.Q8_0, core.F32])
 @pytest.mark.parametrize("MK", [(512, 1024), (256, 4096), (48, 768), (25600, 1024),
-                                (51200, 256)])
+                                (51200, 256), (12800, 1024)])
 def test_mul_mat_parity_and_batch_invariance(L, ty, MK):
     M, K = MK
     if ty != core.F32 and K % 256:
