@@ -195,6 +195,25 @@ qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int Hkv, int D, int 
   // One angle per rotated pair i, shared by every head: theta_0 = pos,
   // theta_{i+1} = theta_i * base^(-2/n_rot) (a running f32 product, as the
   // CPU reference's rope cache), divided by the frequency factor.
+  // Columns of the head: [0, pa.cols) may come from pending partials pa,
+  // the rest from pb; pieces of 4 (W, pa.cols, pb.cols multiples of 8).
+  // A lane's first piece is loaded before the angles are made, so that the
+  // loads are in flight meanwhile.
+  const int sh = is_v && (vmode & QKV_V_FROM_K) ? h - Hkv : h;
+  const float *src = qkv + t * W;
+  auto piece = [&](int pc, float (&x)[4]) {
+    const int e = sh * D + 4 * pc;
+    if (pa.splits && e < pa.cols)
+      pa.sum4(t, e, x);
+    else if (pb.splits && e >= W - pb.cols)
+      pb.sum4(t, e - (W - pb.cols), x);
+    else
+#pragma unroll
+      for (int i = 0; i < 4; i++) x[i] = src[e + i];
+  };
+  float x0[4];
+  const bool first = has && lane < D / 4;
+  if (first) piece(lane, x0);
   const int p = pos[t];
   for (int i = threadIdx.x; i < half; i += blockDim.x) {
     float theta = (float)p;
@@ -203,25 +222,16 @@ qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int Hkv, int D, int 
     cs_[i] = cosf(tt);
     sn_[i] = sinf(tt);
   }
-  if (has) {
-    // Columns of the head: [0, pa.cols) may come from pending partials pa,
-    // the rest from pb; pieces of 4 (W, pa.cols, pb.cols multiples of 8).
-    const int sh = is_v && (vmode & QKV_V_FROM_K) ? h - Hkv : h;
-    const float *src = qkv + t * W;
-    for (int pc = lane; pc < D / 4; pc += 64) {
-      const int e = sh * D + 4 * pc;
-      float x[4];
-      if (pa.splits && e < pa.cols)
-        pa.sum4(t, e, x);
-      else if (pb.splits && e >= W - pb.cols)
-        pb.sum4(t, e - (W - pb.cols), x);
-      else
+  if (first)
 #pragma unroll
-        for (int i = 0; i < 4; i++) x[i] = src[e + i];
+    for (int i = 0; i < 4; i++) v[4 * lane + i] = x0[i];
+  if (has)
+    for (int pc = lane + 64; pc < D / 4; pc += 64) {  // heads of more than 256
+      float x[4];
+      piece(pc, x);
 #pragma unroll
       for (int i = 0; i < 4; i++) v[4 * pc + i] = x[i];
     }
-  }
   __syncthreads();  // the angles and each wave's head
   if (!has) return;
   if (is_q ? q_norm != nullptr : is_k ? k_norm != nullptr : (vmode & QKV_V_NORM) != 0) {
