@@ -6,7 +6,8 @@
  * (LGMLH_OK = 0, negative on error, text in lgmlh_last_error()), never
  * longjmps, and never allocates device or host memory: callers pass
  * buffers and workspaces whose sizes the *_bytes / *_workspace functions
- * report. Device pointers are HIP device addresses; `stream` is a
+ * report. (One exception, stated at lgmlh_forward: a side stream and two
+ * events, made once per host thread and device.) Device pointers are HIP device addresses; `stream` is a
  * hipStream_t (NULL = the null stream). Calls on one stream are ordered;
  * calls on different streams that share a workspace race.
  *
@@ -461,7 +462,12 @@ typedef struct {
  * (device; NULL = ub->logit_rows with n_out = n_seq). ids must be in range
  * (checked by the caller's plan, h_ids) -- the kernel reads them unchecked.
  * ub_ring: the ring plan of the same pass (lgmlh_plan_ring), needed when
- * a layer slides (NULL otherwise). trace may be NULL. */
+ * a layer slides (NULL otherwise). trace may be NULL. A layer whose V
+ * matrix has a type of its own runs that product on a side stream beside
+ * the q|k product (not while tracing): the first such pass on a host
+ * thread and device creates that stream (non-blocking, default priority)
+ * and two events, kept until the process ends; if creating them fails,
+ * the pass runs on the caller's stream alone. */
 int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub, const lgmlh_ubatch *ub_ring,
     const int32_t *out_rows, int n_out, float *logits, void *workspace, size_t ws_bytes,
     lgmlh_trace *trace, void *stream);
