@@ -325,6 +325,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   __shared__ __align__(16) u32x4 xl0_[X_SLOTS], xl1_[ONEBUF ? 1 : X_SLOTS];
   __shared__ __align__(16) u32x4 gh0_[64], gh1_[64];  // group sums, hi: 8 f16 per row
   __shared__ __align__(16) u32x4 gl0_[64], gl1_[64];  // group sums, lo
+  __shared__ __align__(16) u32x4 gz_[1];              // zeros for lanes c >= 2
   // Q8_0: the 256-byte headers of every wave's chunks (wave w, tile a at
   // slots 32 w + 16 a .. + 15)
   constexpr int HD_SLOTS = TYPE == LGMLH_Q8_0 ? WVS * RT_PER_WAVE * 16 : 1;
@@ -336,6 +337,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   auto HD = [&](int b) { return b ? hd1_ : hd0_; };
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  if (tid == 0) gz_[0] = u32x4{0, 0, 0, 0};  // read after the prologue's barrier
   const int64_t NSB = K / QK_K;
   const int64_t MT = (M + 15) / 16;
   // Tile order for the wide tiles: the dispatcher deals workgroups round-
@@ -460,15 +462,15 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
     // buffer are in flight.
     f16x4 sh4[NCT], sl4[NCT];
     if constexpr (TYPE == LGMLH_Q4_K) {
-      const f16 *gh = (const f16 *)GH(buf), *gl = (const f16 *)GL(buf);
+      // lanes c >= 2 (k past the 8 groups) read zeros: no branch per step
+      const bool gs = c < 2;
+      const f16 *gh = gs ? (const f16 *)GH(buf) + r16 * 8 + 4 * c : (const f16 *)gz_;
+      const f16 *gl = gs ? (const f16 *)GL(buf) + r16 * 8 + 4 * c : (const f16 *)gz_;
+      const int cstride = gs ? 16 * 8 : 0;
 #pragma unroll
       for (int ct = 0; ct < NCT; ct++) {
-        sh4[ct] = f16x4{0, 0, 0, 0};
-        sl4[ct] = sh4[ct];
-        if (c < 2) {
-          sh4[ct] = *(const f16x4 *)(gh + (ct * 16 + r16) * 8 + 4 * c);
-          sl4[ct] = *(const f16x4 *)(gl + (ct * 16 + r16) * 8 + 4 * c);
-        }
+        sh4[ct] = *(const f16x4 *)(gh + ct * cstride);
+        sl4[ct] = *(const f16x4 *)(gl + ct * cstride);
       }
     }
     uint32_t scb[RT_PER_WAVE][2];
