@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define LGMLH_ABI_VERSION 5
+#define LGMLH_ABI_VERSION 6
 
 enum {
 	LGMLH_OK = 0,
@@ -172,6 +172,7 @@ typedef struct {
 	 * shared runs of consecutive items, {first item, count} at off_shared */
 	int32_t n_single, n_shared;
 	int64_t off_shared;
+	int64_t off_order; /* [n_single] dispatch order of the items on their own */
 } lgmlh_plan_info;
 
 typedef struct {
@@ -189,6 +190,10 @@ typedef struct {
 	int32_t window, ring;      /* ring plans: the window and the ring's blocks; else 0 */
 	int32_t n_single, n_shared;
 	const int32_t *shared;     /* [n_shared * 2] {first item, count} of each shared run */
+	/* [n_single] the items on their own in the order the attention kernel
+	 * starts them (longest run first, then by index); NULL: index order.
+	 * Only which workgroup runs an item depends on it, not its result. */
+	const int32_t *order;
 } lgmlh_ubatch;
 
 /* Plan a pass. G = n_head / n_head_kv; blocks_per_split bounds the KV

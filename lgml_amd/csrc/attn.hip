@@ -110,7 +110,8 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
                   const int32_t *__restrict__ items, const int32_t *__restrict__ seq_off,
                   const int32_t *__restrict__ seq_npast, const int32_t *__restrict__ block_tab,
                   int max_blocks, int ring, int window, float *__restrict__ out,
-                  f16 *__restrict__ planes, int64_t npad, float *__restrict__ part) {
+                  f16 *__restrict__ planes, int64_t npad, float *__restrict__ part,
+                  const int32_t *__restrict__ order, int n_order) {
   constexpr int KS = D / 32;   // MFMA k-steps over D
   constexpr int DT = D / 16;   // d tiles of the output
   __shared__ __align__(16) uint16_t plh[ROWS * P_STRIDE];  // P as f16 hi
@@ -118,8 +119,12 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
   __shared__ __align__(16) f16x8 qsh[KS * 64], qsl[KS * 64];  // Q fragments, hi and lo
 
   const int lane = threadIdx.x;
-  const int item = blockIdx.x;
-  const int kvh = blockIdx.y;
+  // a flat grid, KV heads fastest: workgroup w runs KV head w % Hkv of
+  // slot w / Hkv, which is item order[slot] (slots past the order: item
+  // slot)
+  const int slot = (int)(blockIdx.x / (uint32_t)Hkv);
+  const int kvh = (int)(blockIdx.x % (uint32_t)Hkv);
+  const int item = order && slot < n_order ? order[slot] : slot;
   const int G = H / Hkv;
   const int s = items[4 * item + 0];
   const int tok0 = items[4 * item + 1];
@@ -614,17 +619,20 @@ template <int D>
 static void launch_attn(const float *q, int H, int Hkv, float scale_log2, const void *kp,
                         const void *vp, const lgmlh_ubatch *ub, float *out, f16 *planes,
                         int64_t npad, float *part, hipStream_t st) {
+  // one workgroup per (item, KV head), the items on their own in the
+  // plan's order
   if (ub->ring > 0)
-    hipLaunchKernelGGL((paged_attn_kernel<D, true>), dim3(ub->n_single, Hkv), dim3(64), 0, st,
-                       q, H, Hkv, scale_log2, (const uint16_t *)kp, (const uint16_t *)vp,
-                       ub->items, ub->seq_off, ub->seq_npast, ub->block_tab, ub->max_blocks,
-                       ub->ring, ub->window, out, planes, npad, part);
+    hipLaunchKernelGGL((paged_attn_kernel<D, true>), dim3((uint32_t)ub->n_single * Hkv),
+                       dim3(64), 0, st, q, H, Hkv, scale_log2, (const uint16_t *)kp,
+                       (const uint16_t *)vp, ub->items, ub->seq_off, ub->seq_npast, ub->block_tab,
+                       ub->max_blocks, ub->ring, ub->window, out, planes, npad, part, ub->order,
+                       ub->n_single);
   // heads of 256 run the shared runs' items with the per-item kernel too
   else if (const int n1 = D <= 128 ? ub->n_single : ub->n_items; n1 > 0)
-    hipLaunchKernelGGL((paged_attn_kernel<D, false>), dim3(n1, Hkv), dim3(64), 0, st,
+    hipLaunchKernelGGL((paged_attn_kernel<D, false>), dim3((uint32_t)n1 * Hkv), dim3(64), 0, st,
                        q, H, Hkv, scale_log2, (const uint16_t *)kp, (const uint16_t *)vp,
                        ub->items, ub->seq_off, ub->seq_npast, ub->block_tab, ub->max_blocks, 0,
-                       0, out, planes, npad, part);
+                       0, out, planes, npad, part, ub->order, ub->n_single);
   if (ub->ring == 0 && ub->n_shared > 0) {
     if constexpr (D <= 128)
       hipLaunchKernelGGL(paged_attn_shared_kernel<D>, dim3(ub->n_shared, Hkv),
@@ -661,6 +669,10 @@ int paged_attention_dev(const float *q, int n_head, int n_head_kv, int head_dim,
     return LGMLH_ENOMEM;
   }
   if (ub->n_items == 0) return LGMLH_OK;
+  if ((int64_t)ub->n_items * n_head_kv > (int64_t)1 << 25) {  // the per-item grid's threads
+    set_error("paged_attention: %d items x %d KV heads in one launch", ub->n_items, n_head_kv);
+    return LGMLH_EINVAL;
+  }
   float sl = scale * LOG2E;
   float *part = (float *)workspace;
   switch (head_dim) {

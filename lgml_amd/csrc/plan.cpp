@@ -18,7 +18,10 @@
 // shared attention kernel reads each K / V block once per set into LDS
 // for all its groups. Items are ordered so that items [0, n_single) are
 // groups on their own (decode tokens, ring plans) and every shared run is
-// n consecutive items, listed in `shared` as {first item, n}.
+// n consecutive items, listed in `shared` as {first item, n}. The items on
+// their own are started longest run first (`order`): every item runs as
+// one wave, all at once, so the waves that share a SIMD once the SIMDs
+// are full are the shortest ones, and they end early.
 #include <string.h>
 
 #include <utility>
@@ -168,6 +171,7 @@ static int plan_impl(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
   in.off_items = o;        o = align16(o + 16 * (int64_t)in.n_items);
   in.off_merge = o;        o = align16(o + 16 * (int64_t)in.n_merge);
   in.off_shared = o;       o = align16(o + 8 * (int64_t)in.n_shared);
+  in.off_order = o;        o = align16(o + 4 * (int64_t)in.n_single);
   in.bytes = o;
   *info = in;
   if (!buf) return LGMLH_OK;
@@ -204,6 +208,19 @@ static int plan_impl(int n_seq, const int32_t *seq_n, const int32_t *seq_npast,
     if (mrg) memcpy(pmg + 4 * m, mrg, 16);
     if (sh) memcpy(psh + 2 * k, sh, 8);
   });
+  // order: the items on their own by run length, longest first, then by
+  // index (a counting sort; runs longer than 256 blocks share a key)
+  int32_t *pord = (int32_t *)(b + in.off_order);
+  int64_t start[258];
+  memset(start, 0, sizeof start);
+  auto key = [&](int64_t i) {
+    const uint32_t r = (uint32_t)pit[4 * i + 3];
+    const int len = (int)(r >> 16) - (int)(r & 0xffff);
+    return 256 - (len < 0 ? 0 : len > 256 ? 256 : len);  // ascending key, descending length
+  };
+  for (int64_t i = 0; i < in.n_single; i++) start[key(i) + 1]++;
+  for (int k = 0; k < 257; k++) start[k + 1] += start[k];
+  for (int64_t i = 0; i < in.n_single; i++) pord[start[key(i)]++] = (int32_t)i;
   return LGMLH_OK;
 }
 
@@ -254,6 +271,7 @@ extern "C" int lgmlh_plan_bind(const lgmlh_plan_info *info, const void *dev, lgm
   ub->n_single = info->n_single;
   ub->n_shared = info->n_shared;
   ub->shared = (const int32_t *)(b + info->off_shared);
+  ub->order = (const int32_t *)(b + info->off_order);
   ub->window = info->window;
   ub->ring = info->ring;
   return LGMLH_OK;

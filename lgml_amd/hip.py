@@ -50,7 +50,7 @@ class PlanInfo(C.Structure):
                                          "off_npast", "off_block_tab", "off_logit_rows",
                                          "off_items", "off_merge")] + \
                [("window", C.c_int32), ("ring", C.c_int32), ("n_single", C.c_int32),
-                ("n_shared", C.c_int32), ("off_shared", C.c_int64)]
+                ("n_shared", C.c_int32), ("off_shared", C.c_int64), ("off_order", C.c_int64)]
 
 
 class Ubatch(C.Structure):
@@ -59,7 +59,7 @@ class Ubatch(C.Structure):
                [(n, C.c_void_p) for n in ("ids", "pos", "cells", "seq_off", "seq_npast",
                                           "block_tab", "logit_rows", "items", "merge")] + \
                [("window", C.c_int32), ("ring", C.c_int32), ("n_single", C.c_int32),
-                ("n_shared", C.c_int32), ("shared", C.c_void_p)]
+                ("n_shared", C.c_int32), ("shared", C.c_void_p), ("order", C.c_void_p)]
 
 
 class Layer(C.Structure):

@@ -383,16 +383,14 @@ class DeviceModel:
         SIMD), runs of 32 KV blocks over the paged pool (fewer, longer items
         stay within one round of waves) and the plan's default, 16, through
         the rings (a window's few blocks over more waves); else runs of 12
-        for at most 4 KV heads (half the waves per sequence of 8 heads;
-        shorter runs make up the count: C5 4584 -> 4686 tok/s, while C2's 8
-        heads are best at 16) and 16 otherwise. The run length is fixed per
-        model, so split points still depend on a sequence's own length
-        only."""
+        (with the longest runs started first, C2 decode 7263 -> 7407 tok/s
+        against 16; 10: 7383, 8: 7088). The run length is fixed per model,
+        so split points still depend on a sequence's own length only."""
         ids = np.ascontiguousarray(ids, np.int32)
         ring_bps = self.ring_blocks_per_split or blocks_per_split
         if not blocks_per_split and self.hp["head_dim"] >= 256:
             blocks_per_split = 32
-        elif not blocks_per_split and self.hp["n_head_kv"] <= 4:
+        elif not blocks_per_split:
             blocks_per_split = 12
         if len(ids) and (ids.min() < 0 or ids.max() >= self.hp["n_vocab"]):
             raise ValueError("token id out of range [0, %d)" % self.hp["n_vocab"])

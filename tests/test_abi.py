@@ -35,7 +35,7 @@ def test_exports_every_declared_symbol(hip):
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing
     assert sorted(hip.SYMBOLS) == names
-    assert L.lgmlh_abi_version() == 5
+    assert L.lgmlh_abi_version() == 6
 
 
 def test_struct_layouts_match_the_header(hip, tmp_path):
@@ -205,6 +205,34 @@ def test_plan_packs_like_fill_batch(hip):
             set0 = 1 + ((tok0 - 1) // 32) * 32
             last = min(set0 + 32, 71) - 1  # the set's last token
             assert max(hi for _, hi in runs) == (150 + last - 1) // 64 + 1
+
+
+def test_plan_order_starts_the_longest_runs_first(hip):
+    """The items on their own come in `order` by run length, longest first,
+    ties by index: a permutation of [0, n_single). Shared-run items are not
+    in it."""
+    rng = np.random.default_rng(7)
+    seq_n = [1] * 40 + [37]
+    npast = list(rng.integers(0, 64 * 30, size=40)) + [500]
+    nb = [(p + n + 63) // 64 for p, n in zip(npast, seq_n)]
+    bt = np.full((len(seq_n), max(nb)), -1, np.int32)
+    nxt = 0
+    for s, k in enumerate(nb):
+        bt[s, :k] = np.arange(nxt, nxt + k)
+        nxt += k
+    for bps in (0, 5, 12):
+        rc, info, buf = plan(hip, seq_n, npast, bt, np.zeros(sum(seq_n), np.int32), 32, 8, nxt,
+                             bps=bps)
+        assert rc == 0
+        items = arr(buf, info.off_items, 4 * info.n_items, np.int32).reshape(-1, 4)
+        order = list(arr(buf, info.off_order, info.n_single, np.int32))
+        assert sorted(order) == list(range(info.n_single))
+        length = lambda i: (int(items[i][3]) >> 16) - (int(items[i][3]) & 0xffff)
+        want = sorted(range(info.n_single), key=lambda i: (-length(i), i))
+        assert order == want
+        assert info.n_single < info.n_items  # the chunk's shared runs stay out
+        assert info.off_order >= info.off_shared + 8 * info.n_shared
+        assert info.bytes >= info.off_order + 4 * info.n_single
 
 
 def test_plan_errors(hip):
