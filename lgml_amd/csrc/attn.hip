@@ -104,7 +104,7 @@ __device__ __forceinline__ void finish_item(const f32x4 (&o)[D / 16], float m, f
 // block b of sequence s is ring entry b % ring, and row position p sees
 // positions p - window + 1 .. p only.
 template <int D, bool RING>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(64, D <= 128 ? 2 : 1)
 paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
                   const uint16_t *__restrict__ kpool, const uint16_t *__restrict__ vpool,
                   const int32_t *__restrict__ items, const int32_t *__restrict__ seq_off,
@@ -141,6 +141,25 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
   const int p_first = seq_npast[s] + (tok0 - seq_off[s]);
   const int p_row = p_first + rtok;  // last visible position of the row
 
+  const int32_t *bt = block_tab + (int64_t)s * max_blocks;
+  auto phys = [&](int blk) -> int64_t { return RING ? bt[blk % ring] : bt[blk]; };
+  auto ktile = [&](int blk) { return kpool + (phys(blk) * Hkv + kvh) * (int64_t)(64 * D); };
+  auto vtile = [&](int blk) { return vpool + (phys(blk) * Hkv + kvh) * (int64_t)(64 * D); };
+  // K rows (A operand of S^T = K Q^T) and V^T columns (A operand of
+  // O^T += V^T P^T) of one block, straight from the pool tiles.
+  f16x8 kf[4][KS], vf[DT][2];
+  auto load_k = [&](const uint16_t *kt) {
+#pragma unroll
+    for (int ct = 0; ct < 4; ct++)
+#pragma unroll
+      for (int ks = 0; ks < KS; ks++) kf[ct][ks] = load_f16x8(kt + (ct * 16 + row) * D + ks * 32 + quad * 8);
+  };
+  auto load_v = [&](const uint16_t *vt) {
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+      for (int kc = 0; kc < 2; kc++) vf[dt][kc] = load_f16x8(vt + (dt * 16 + row) * 64 + kc * 32 + quad * 8);
+  };
   // Q fragments (B operand): Q[row][ks*32 + quad*8 .. +7] as f16 hi + lo
   // (q = hi + lo to 22 bits; K is exact f16, so S^T is f32-accurate). Kept
   // in LDS to leave registers for the next block's tiles. Every lane
@@ -155,6 +174,13 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
       qa[2 * ks] = *(const f32x4 *)(qr + ks * 32 + quad * 8);
       qa[2 * ks + 1] = *(const f32x4 *)(qr + ks * 32 + quad * 8 + 4);
     }
+    // The first block's tiles go out before the Q pieces are converted,
+    // so the two loads overlap. Unconditional, so that the conversion waits
+    // for the Q pieces only (a run always has a block; block 0 of every
+    // planned sequence is a valid pool block).
+    const int b_first = blo < bhi ? blo : 0;
+    load_k(ktile(b_first));
+    load_v(vtile(b_first));
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
       f16x8 h, lo;
@@ -177,29 +203,6 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
   for (int i = 0; i < DT; i++) o[i] = f32x4{0, 0, 0, 0};
   float m = -INFINITY, l = 0.0f;
 
-  const int32_t *bt = block_tab + (int64_t)s * max_blocks;
-  auto phys = [&](int blk) -> int64_t { return RING ? bt[blk % ring] : bt[blk]; };
-  auto ktile = [&](int blk) { return kpool + (phys(blk) * Hkv + kvh) * (int64_t)(64 * D); };
-  auto vtile = [&](int blk) { return vpool + (phys(blk) * Hkv + kvh) * (int64_t)(64 * D); };
-  // K rows (A operand of S^T = K Q^T) and V^T columns (A operand of
-  // O^T += V^T P^T) of one block, straight from the pool tiles.
-  f16x8 kf[4][KS], vf[DT][2];
-  auto load_k = [&](const uint16_t *kt) {
-#pragma unroll
-    for (int ct = 0; ct < 4; ct++)
-#pragma unroll
-      for (int ks = 0; ks < KS; ks++) kf[ct][ks] = load_f16x8(kt + (ct * 16 + row) * D + ks * 32 + quad * 8);
-  };
-  auto load_v = [&](const uint16_t *vt) {
-#pragma unroll
-    for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-      for (int kc = 0; kc < 2; kc++) vf[dt][kc] = load_f16x8(vt + (dt * 16 + row) * 64 + kc * 32 + quad * 8);
-  };
-  if (blo < bhi) {
-    load_k(ktile(blo));
-    load_v(vtile(blo));
-  }
   for (int blk = blo; blk < bhi; blk++) {
     // The next block's tiles are loaded unconditionally (the last block
     // reloads its own, still in L2): straight-line code keeps the load
