@@ -23,6 +23,8 @@
 // which costs more than the second launch.)
 #include <math.h>
 
+#include <type_traits>
+
 #include "common.h"
 #include "split.h"
 
@@ -203,10 +205,14 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
   for (int i = 0; i < DT; i++) o[i] = f32x4{0, 0, 0, 0};
   float m = -INFINITY, l = 0.0f;
 
-  for (int blk = blo; blk < bhi; blk++) {
-    // The next block's tiles are loaded unconditionally (the last block
-    // reloads its own, still in L2): straight-line code keeps the load
-    // counter waits exact, so the O products do not wait for the next K.
+  // One block; NEXT: the next block's tiles are loaded meanwhile
+  // (straight-line code keeps the load counter waits exact, so the O
+  // products do not wait for the next K). Heads of up to 128 run the last
+  // block without NEXT, so no tile is loaded twice; heads of 256 (whose
+  // registers are full) load the last block's tiles again, from L2.
+  constexpr bool PEEL = D <= 128;
+  auto block = [&](int blk, auto next) __attribute__((always_inline)) {
+    constexpr bool NEXT = decltype(next)::value;
     const int nxt = blk + 1 < bhi ? blk + 1 : blk;
     // S^T[cell][row] for 4 tiles of 16 cells.
     f32x4 st[4];
@@ -220,7 +226,7 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
       }
       st[ct] = acc;
     }
-    load_k(ktile(nxt));
+    if constexpr (NEXT) load_k(ktile(nxt));
 
     // Mask and row max: lane holds cells ct*16 + quad*4 + i of its row. A
     // block that ends at or before the group's first position (and, with a
@@ -291,9 +297,12 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
         o[dt] = mfma16(vf[dt][kc], pfh[kc], o[dt]);
         o[dt] = mfma16(vf[dt][kc], pfl[kc], o[dt]);
       }
-    load_v(vtile(nxt));
+    if constexpr (NEXT) load_v(vtile(nxt));
     __asm__ volatile("" ::: "memory");  // the P reads before the next block's writes
-  }
+  };
+  for (int blk = blo; blk + (PEEL ? 1 : 0) < bhi; blk++) block(blk, std::true_type{});
+  if constexpr (PEEL)
+    if (blo < bhi) block(bhi - 1, std::false_type{});
 
   finish_item<D>(o, m, l, mg, rvalid, tok0, rtok, rhead, ntok, G, row, quad, item, kvh, Hkv, H,
                  out, planes, npad, part);
