@@ -14,6 +14,9 @@
 // f16 hi + lo pairs, so every product is f32-accurate. The loads of block
 // b + 1 are issued as soon as block b's registers are consumed (K after
 // S, V after O), so they overlap block b's softmax and products.
+// Items start longest run first (the plan's order): all of a launch's
+// waves are resident at once, and the ones that share a SIMD with an older
+// wave advance slowly until it ends, so those should be the shortest.
 //
 // The splits of a token group are merged by merge_kernel in a fixed order,
 // so results are deterministic and, since the split points depend only on
