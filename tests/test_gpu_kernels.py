@@ -247,12 +247,15 @@ def make_attn_case(H, Hkv, D, seqs, seed, n_cells=8192):
     return q, kpool, vpool, bt
 
 
-def gpu_attention(L, q, kpool_rows, vpool_rows, H, Hkv, D, seqs, bt, bps=0, n_cells=8192):
+def gpu_attention(L, q, kpool_rows, vpool_rows, H, Hkv, D, seqs, bt, bps=0, n_cells=8192,
+                  order=True):
     from lgml_amd import hip, runtime
     seq_n = [n for n, _ in seqs]
     npast = [p for _, p in seqs]
     ids = np.zeros(sum(seq_n), np.int32)
     plan = runtime.Plan(seq_n, npast, bt, ids, H, Hkv, n_cells // 64, bps)
+    if not order:
+        plan.ub.order = None  # the items on their own start in index order
     kb = L.lgmlh_kv_layer_bytes(n_cells, Hkv, D)
     kp = torch.zeros(kb, dtype=torch.uint8, device="cuda")
     vp = torch.zeros(kb, dtype=torch.uint8, device="cuda")
@@ -337,6 +340,23 @@ def test_paged_attention_alone_equals_batched(L):
                                  bt[i:i + 1], bps=2)
         assert np.array_equal(alone.view(np.uint32), got[off:off + n].view(np.uint32)), i
         off += n
+
+
+@pytest.mark.parametrize("H,Hkv,D", [(32, 8, 128), (8, 4, 256)])
+def test_paged_attention_order_changes_no_bits(L, H, Hkv, D):
+    """The plan's dispatch order (longest runs first) only changes which
+    workgroup runs an item: the same bits as index order, with runs of
+    mixed lengths and merges."""
+    seqs = [(1, 63), (1, 700), (1, 3000), (4, 1500), (1, 64), (1, 2100), (9, 400)]
+    q, kpool, vpool, bt = make_attn_case(H, Hkv, D, seqs, seed=H * D)
+    for bps in (0, 5):
+        a, plan = gpu_attention(L, q, kpool, vpool, H, Hkv, D, seqs, bt, bps)
+        b, _ = gpu_attention(L, q, kpool, vpool, H, Hkv, D, seqs, bt, bps, order=False)
+        items = plan.host_array(plan.info.off_items, 4 * plan.info.n_single, np.int32)
+        lengths = [(int(it[3]) >> 16) - (int(it[3]) & 0xffff) for it in items.reshape(-1, 4)]
+        assert len(set(lengths)) > 1  # the order is not the index order
+        assert np.isfinite(a).all()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), bps
 
 
 def test_plan_cells_and_errors(L):
