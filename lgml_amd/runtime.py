@@ -374,22 +374,26 @@ class DeviceModel:
     def pool_blocks(self):
         return self.n_cells // 64
 
-    ring_blocks_per_split = 0  # the ring plans' run length (0: as blocks_per_split)
+    ring_blocks_per_split = 0  # the ring plans' run length (0: as blocks_per_split; 12 for heads of 256)
 
     def plan(self, seq_n, seq_npast, block_tab, ids, blocks_per_split=0, ring_tab=None):
         """The pass's plan; with sliding layers also its ring plan (.ring)
         over ring_tab (n_seq, ring blocks), the sequences' rings.
         blocks_per_split 0: for heads of 256 (their kernel holds one wave per
-        SIMD), runs of 32 KV blocks over the paged pool (fewer, longer items
-        stay within one round of waves) and the plan's default, 16, through
-        the rings (a window's few blocks over more waves); else runs of 12
-        (with the longest runs started first, C2 decode 7263 -> 7407 tok/s
-        against 16; 10: 7383, 8: 7088). The run length is fixed per model,
-        so split points still depend on a sequence's own length only."""
+        SIMD), runs of 28 KV blocks over the paged pool (fewer, longer items
+        stay within one round of waves) and of 12 through the rings (a
+        window's few blocks over more waves; with the longest runs started
+        first, C4 7172 -> 7462 tok/s against 32 and 16; 24 / 26 / 30 and
+        10 / 14 are no better); else runs of 12 (C2 decode 7263 -> 7407
+        tok/s against 16; 10: 7383, 8: 7088). The run length is fixed per
+        model, so split points still depend on a sequence's own length
+        only."""
         ids = np.ascontiguousarray(ids, np.int32)
         ring_bps = self.ring_blocks_per_split or blocks_per_split
+        if not ring_bps and self.hp["head_dim"] >= 256:
+            ring_bps = 12
         if not blocks_per_split and self.hp["head_dim"] >= 256:
-            blocks_per_split = 32
+            blocks_per_split = 28
         elif not blocks_per_split:
             blocks_per_split = 12
         if len(ids) and (ids.min() < 0 or ids.max() >= self.hp["n_vocab"]):
