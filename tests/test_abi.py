@@ -295,6 +295,15 @@ def test_ring_plan_maps_positions_into_the_rings(hip):
         assert max(lens) - min(lens) <= 1 and max(lens) <= 1  # balanced runs, at most bps
     # every token is in exactly one group
     assert sorted(t0 + k for (_, t0, nt) in runs for k in range(nt)) == list(range(sum(seq_n)))
+    # ring plans have every item on its own, started longest run first
+    assert info.n_single == info.n_items and info.n_shared == 0
+    rc, info, buf = plan_ring(hip, seq_n, npast, ring_tab, W, ids, 8, 4, 10, bps=2)
+    assert rc == 0
+    items = arr(buf, info.off_items, 4 * info.n_items, np.int32).reshape(-1, 4)
+    order = list(arr(buf, info.off_order, info.n_single, np.int32))
+    length = lambda i: (int(items[i][3]) >> 16) - (int(items[i][3]) & 0xffff)
+    assert order == sorted(range(info.n_single), key=lambda i: (-length(i), i))
+    assert len({length(i) for i in range(info.n_single)}) > 1
 
 
 def test_ring_plan_errors(hip):
