@@ -226,17 +226,19 @@ def cpu_baseline(hp, contexts, seed, args):
 
 
 def traffic_of(path, args):
-    """Measured HBM bytes per attention launch (profiles/paged_attn_traffic.json),
-    when measured on this workload; else None."""
+    """Measured HBM bytes per attention launch (profiles/paged_attn_traffic.json)
+    and the algorithmic bytes of the steps they were counted on (a short run:
+    other contexts than this run's traced steps), when measured on this
+    workload; else (None, None)."""
     try:
         with open(path) as f:
             t = json.load(f)
     except (OSError, ValueError):
-        return None
+        return None, None
     if (t.get("seed") != args.seed or t.get("slots") != args.slots or
             t.get("bench_workload") != args.workload):
-        return None
-    return t.get("bytes_per_launch")
+        return None, None
+    return t.get("bytes_per_launch"), t.get("algorithmic_bytes_per_launch")
 
 
 def product_flops(hp, n_tokens, n_out):
@@ -548,6 +550,8 @@ def main():
     tot_uniq = sum(uniq_bytes[i] * len(at_p[i]) for i in keep)
     attn_gbs = tot_bytes / (sum(at) / 1e3) if at else 0.0
     avg_attn_ms = sum(at) / max(n_att, 1)
+    attn_bytes_per_launch = tot_bytes / max(n_att, 1)  # algorithmic, these steps
+    traffic = traffic_of(TRAFFIC_FILE, args)
     gemm_ms = sum(sum(gt_p[i]) + sum(xt_p[i]) for i in keep) / len(keep)
     exp_ms = sum(sum(xt_p[i]) for i in keep) / len(keep)
 
@@ -604,7 +608,9 @@ def main():
         "roofline": {
             "bound": "hbm", "kernel": "paged_attn_kernel + merge_kernel (per layer)",
             "achieved": attn_gbs / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-            "frac": attn_gbs / HBM_PEAK, "traffic": traffic_of(TRAFFIC_FILE, args),
+            "frac": attn_gbs / HBM_PEAK, "traffic": traffic[0],
+            "traffic_algorithmic_bytes": traffic[1],
+            "bytes_per_launch": attn_bytes_per_launch,
             "avg_launch_ms": avg_attn_ms, "launches": n_att,
         },
         "step_roofline": {
