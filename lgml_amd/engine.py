@@ -251,6 +251,7 @@ class Request:
         self.preempt = False  # lets its cells go at the next chance
         self.started = 0      # submit order (E:victim: the least recently started)
         self.waits = 0        # times it let its cells go
+        self.wait_mark = 0    # the engine's count of ended requests when it began to wait
         # run-ahead engines: sampled tokens of passes not yet read back, the
         # (pass, row) holding the latest one on the device, and whether the
         # request takes part in no further pass
@@ -270,7 +271,10 @@ class Request:
         samples; the rest of the feed, or the last sample."""
         if self.fed < len(self.feed):
             return self.feed[:self.fed], self.feed[self.fed:]
-        return self.feed + self.out[:-1], self.out[-1:]
+        # decoding: the feed is the prompt and a prefix of out (after a wait),
+        # all of it run; the sequence holds the prompt and every sample but
+        # the last (E:preempt's slot.tokens + rest, engine.lua:1194-1195)
+        return self.prompt + self.out[:-1], self.out[-1:]
 
 
 class _Half:
@@ -341,7 +345,7 @@ class Engine:
         self.waiting = []
         self.preemptions = 0
         self.waits = {}
-        self._ended = 0     # requests that ended since the waiting ones last tried
+        self._ended = 0     # requests that ended so far (a waiting request wakes on a later one)
         self._submitted = 0
         if self.ram is not None:
             self.seqs.on_evict = self.spill_block
@@ -522,21 +526,28 @@ class Engine:
         req.preempt = req.finishing = False
         req.tok_src = None
         req.waits += 1
+        req.wait_mark = self._ended
         self.waiting.append(req)
         self.preemptions += 1
         self.waits[req.prio] = self.waits.get(req.prio, 0) + 1
 
     def resume(self):
-        """The waiting requests take a slot again once another request has
-        ended (E:preempt's wait, engine.lua:1223-1242): each attaches what is
-        still cached of its tokens and runs the rest."""
-        if not self.waiting or not self._ended:
-            return
-        self._ended = 0
-        while self.waiting and self.free_slots:
-            req = self.waiting.pop(0)
+        """The waiting requests take a slot again, in the order they began to
+        wait, once a request has ended after they began (E:preempt's wait,
+        engine.lua:1223-1242, woken by E:slot_freed, :1284-1291): each
+        attaches what is still cached of its tokens and runs the rest. A
+        resumed request counts as started now (E:pick_slot's `best.used =
+        self.tick`, :1753), so E:victim does not pick it first again. Only
+        ends wake a waiter: a request that lets go frees cells for the one
+        that needed them, which a waiter taking them back would undo."""
+        for req in [q for q in self.waiting if self._ended > q.wait_mark]:
+            if not self.free_slots:
+                break
+            self.waiting.remove(req)
             req.slot = self.free_slots.pop(0)
             req.seq = Seq(self.seqs, req.prio)
+            self._submitted += 1
+            req.started = self._submitted
             self.active.append(req)
             req.fed = self.attach(req)
             req.seq.n_past = req.fed
