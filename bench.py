@@ -89,6 +89,10 @@ def parse():
                          "rows of 4096) and a device copy of BYTES, 10 times each after 2 "
                          "untimed: the practical HBM ceilings the kernels' GB/s compare with; "
                          "prints both")
+    ap.add_argument("--act", choices=("ggml", "exact"), default="ggml",
+                    help="arithmetic of the quantized weight products: ggml (the reference CPU "
+                         "path's: X quantized to Q8_K / Q8_0 per block, integer block dots; "
+                         "default) or exact (f32-accurate X as f16 hi + lo halves)")
     ap.add_argument("--product", default="", metavar="TYPE:MxK:N",
                     help="only run one weight product (q4 / q6 / q8, M x K weights, N rows), "
                          "5 times after 2 untimed calls: the subject of the products' counter "
@@ -189,7 +193,7 @@ def cpu_baseline(hp, contexts, seed, args):
         """Mean seconds of a 1-layer pass (embeddings, layer, head), repeated
         until ~8 s of samples; the model's output matrix."""
         ohp, w = models.build(shp, seed=seed, n_layer=1, init="normal")
-        om = core.OracleModel(ohp, w)
+        om = core.OracleModel(dict(ohp, act_quant=bool(hp.get("act_quant"))), w)
         reps, t_all = 0, 0.0
         while reps < 2 or (t_all < 8.0 and reps < 20):
             t0 = time.time()
@@ -207,7 +211,7 @@ def cpu_baseline(hp, contexts, seed, args):
     out = passes[0][3]
     x = rng.standard_normal((S, E)).astype(np.float32)
     t0 = time.time()
-    core.mul_mat(out[1], out[0], V, E, x)
+    (core.mul_mat_q8 if hp.get("act_quant") else core.mul_mat)(out[1], out[0], V, E, x)
     t_head = time.time() - t0
     t_step = t_head
     parts = []
@@ -259,9 +263,9 @@ def product_flops(hp, n_tokens, n_out):
     return 2.0 * (per_tok * n_tokens + V * E * n_out)
 
 
-def product_only(spec):
+def product_only(spec, act):
     """One weight product of seeded random weights (lgmlh_gen_normal, as the
-    benched models) on N(0, 1) rows, run 2 + 5 times."""
+    benched models) on N(0, 1) rows, run 2 + 5 times, in the arithmetic act."""
     import torch
     from lgml_amd import hip
     L = hip.lib()
@@ -282,8 +286,9 @@ def product_only(spec):
     ws = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda")
 
     def call():
-        hip.check(L.lgmlh_mul_mat(ty, w.data_ptr(), M, K, x.data_ptr(), hip.F32, N, y.data_ptr(),
-                                  hip.EPI_NONE, None, ws.data_ptr(), nb, st))
+        fn = L.lgmlh_mul_mat_ggml if act == "ggml" else L.lgmlh_mul_mat
+        hip.check(fn(ty, w.data_ptr(), M, K, x.data_ptr(), hip.F32, N, y.data_ptr(),
+                     hip.EPI_NONE, None, ws.data_ptr(), nb, st))
     call()
     call()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -292,7 +297,7 @@ def product_only(spec):
         call()
     e1.record()
     torch.cuda.synchronize()
-    print("product %s: %.1f us" % (spec, e0.elapsed_time(e1) * 1e3 / 5))
+    print("product %s (%s): %.1f us" % (spec, act, e0.elapsed_time(e1) * 1e3 / 5))
     return 0
 
 
@@ -337,7 +342,7 @@ def main():
         torch.cuda.synchronize()
         return 0
     if args.product:
-        return product_only(args.product)
+        return product_only(args.product, args.act)
     if args.gpus != 1:
         print("bench.py measures one GPU: every GPU box here has one, and the multi-GPU "
               "sharding of this path is design only; run with --gpus 1",
@@ -350,6 +355,7 @@ def main():
 
     wl = WORKLOADS[args.workload]
     hp = dict(workload.SHAPES[wl["shape"]])
+    hp["act_quant"] = args.act == "ggml"
     ty = workload.policy(hp["wtype"], hp["n_layer"])
     rng = workload.Lcg(args.seed)
     S = args.slots = args.slots or wl.get("slots", 64)
@@ -594,13 +600,18 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "%s weights, f16 KV, f32 accumulate" % hp["wtype"].replace("q8_0", "Q8_0"),
+        "dtype": "%s weights, %s, f16 KV, f32 accumulate" % (
+            hp["wtype"].replace("q8_0", "Q8_0"),
+            "X quantized per block as ggml's CPU path (Q8_%s), integer block dots" % (
+                "0" if hp["wtype"] == "q8_0" else "K") if args.act == "ggml"
+            else "f32-accurate X (f16 hi + lo)"),
         "data": "synthetic (seeded random-init weights, LCG prompts, synthetic initial KV)",
         "config": {
             "workload": wl["text"],
             "slots": S, "seed": args.seed, "decoded_tokens": decoded,
             "prefill_tokens": prefill_tok, "joins": n_joins,
             "mean_context": float(np.mean(contexts0)),
+            "act": args.act,
             "engine": "sync" if args.sync else "run-ahead, %d stream%s" % (
                 n_streams, "s" if n_streams > 1 else ""),
             "decode_only": dec,

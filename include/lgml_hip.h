@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define LGMLH_ABI_VERSION 6
+#define LGMLH_ABI_VERSION 7
 
 enum {
 	LGMLH_OK = 0,
@@ -293,6 +293,31 @@ int lgmlh_mul_mat(int type, const void *w, int64_t M, int64_t K, const void *x, 
     int64_t N, float *y, int epi, const float *residual, void *workspace, size_t ws_bytes,
     void *stream);
 
+/* Activation arithmetic of quantized products. LGMLH_ACT_EXACT: X stays
+ * f32-accurate (f16 hi + lo halves against exact integer weights).
+ * LGMLH_ACT_GGML: the reference CPU path's arithmetic [ggml mul_mat on the
+ * CPU backend]: each X row is first quantized to the weight type's
+ * vec_dot_type -- Q8_K (256-value blocks: f32 d, int8 q, 16 sums of 16) for
+ * Q4_K / Q6_K, Q8_0 (32-value blocks: f16 d, int8 q) for Q8_0 -- and the
+ * products are integer block dots scaled by d_w d_x. f32 weights take f32
+ * X in either mode. */
+enum { LGMLH_ACT_EXACT = 0, LGMLH_ACT_GGML = 1 };
+
+/* lgmlh_mul_mat in LGMLH_ACT_GGML arithmetic: graph:mul_mat
+ * (src/lgml.c:1811-1839) as the reference's CPU backend computes it.
+ * Same arguments, workspace and batch invariance as lgmlh_mul_mat. */
+int lgmlh_mul_mat_ggml(int type, const void *w, int64_t M, int64_t K, const void *x, int xtype,
+    int64_t N, float *y, int epi, const float *residual, void *workspace, size_t ws_bytes,
+    void *stream);
+/* The activation blocks of LGMLH_ACT_GGML for X (N, K) f32 and a weight
+ * of `type` (quantize_row_q8_K / quantize_row_q8_0 of ggml's CPU path, as
+ * the vec_dot_type conversion before mul_mat, src/lgml.c:1811-1839):
+ * Q4_K / Q6_K: q (N, K) int8, d (N, K / 256) f32, bsums (N, K / 16) int16;
+ * Q8_0: q (N, K) int8, d (N, K / 32) f16 bits, bsums unused (may be NULL).
+ * Device pointers. */
+int lgmlh_quantize_act(int type, const float *x, int64_t N, int64_t K, int8_t *q, void *d,
+    int16_t *bsums, void *stream);
+
 /* lgmlh_mul_mat without a workspace argument, for callers that cannot
  * allocate (code under HIP graph capture, serving loops that forbid
  * hipMalloc). It has no counterpart in the reference. The workspace lives
@@ -340,6 +365,12 @@ size_t lgmlh_mul_mat_id_workspace(int type, int64_t n_expert, int64_t M, int64_t
  * outside [0, n_expert) give rows of zeros (the reference asserts).
  * n_expert <= 512, T * n_used <= 8192. */
 int lgmlh_mul_mat_id(int type, const void *w, int64_t n_expert, int64_t M, int64_t K,
+    const void *x, int xtype, int64_t U, const int32_t *ids, int64_t T, int n_used, float *y,
+    void *workspace, size_t ws_bytes, void *stream);
+/* lgmlh_mul_mat_id in LGMLH_ACT_GGML arithmetic (ggml_mul_mat_id on the
+ * CPU backend, src/ops_nn.c:322-362): each X row quantized to the expert
+ * type's vec_dot_type, integer block dots. Same arguments and workspace. */
+int lgmlh_mul_mat_id_ggml(int type, const void *w, int64_t n_expert, int64_t M, int64_t K,
     const void *x, int xtype, int64_t U, const int32_t *ids, int64_t T, int n_used, float *y,
     void *workspace, size_t ws_bytes, void *stream);
 /* The tail of experts / sum_picks (transformer.lua:1888,1894-1910) and the
@@ -443,6 +474,9 @@ typedef struct {
 	int gemma;
 	float embd_scale, softcap;
 	int64_t ring_cells;
+	/* LGMLH_ACT_EXACT or LGMLH_ACT_GGML: the arithmetic of every quantized
+	 * weight product of the pass (the router stays f32). */
+	int act;
 } lgmlh_model;
 
 /* Workspace bytes of lgmlh_forward for a plan and n_out logit rows. Its

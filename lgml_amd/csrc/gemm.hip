@@ -207,6 +207,15 @@ struct WFrag<LGMLH_Q4_K> {
     return cat4(fma2(biased(n0, SEL_01), s, cc), fma2(biased(n0, SEL_23), s, cc),
                 fma2(biased(n1, SEL_01), s, cc), fma2(biased(n1, SEL_23), s, cc));
   }
+  // The 16x16x16 A fragment of the mins against the 16 sums of 16 values
+  // (Q8_K bsums): row r, k = 4c .. 4c + 3, sum k in group k / 2, so
+  // {m_2c, m_2c, m_2c+1, m_2c+1}.
+  __device__ __forceinline__ f16x4 mins16(int c) const {
+    const uint32_t mb = c < 2 ? m03() : m47();
+    const f16x2 k = f16x2{(f16)1024.0f, (f16)1024.0f};
+    const f16x2 a = biased(mb, (c & 1) ? SEL_23 : SEL_01) - k;
+    return f16x4{a[0], a[0], a[1], a[1]};
+  }
   // The 16x16x16 A fragment of the mins: row r, k = groups 4c .. 4c + 3
   // (zero for c >= 2).
   __device__ __forceinline__ f16x4 mins(int c) const {
@@ -308,7 +317,18 @@ struct WFrag<LGMLH_Q8_0> {
 __host__ __device__ constexpr int gemm_waves(int type, int nct) {
   return nct == 4 && type == LGMLH_Q4_K ? 4 : GEMM_WAVES;
 }
-template <int TYPE, int NCT, bool GATHER>
+//
+// Q8: X as ggml's quantized activations (split.h: Q8_K for Q4_K / Q6_K,
+// Q8_0 for Q8_0), the reference CPU path's arithmetic. The B fragments are
+// the integer q (exact in f16), so one MFMA per group replaces the hi + lo
+// pair (Q6_K: the two exact parts of sc q against q, no rounded third);
+// every block sum is an exact integer in the f32 accumulator (below 2^24
+// unless a block is extreme). Per K step the Q4_K min term is one 16x16x16
+// MFMA of the mins against the 16 sums of 16 q, and the block scales go on
+// in f32: Q4_K d_x (d_w I - dmin_w Mn), Q6_K (d_w d_x) I, Q8_0 per 32-value
+// block (d_w d_x) I. X is half the bytes to stage (no lo plane), so the
+// 4-wave Q4_K workgroups keep two X buffers.
+template <int TYPE, int NCT, bool GATHER, bool Q8>
 __global__ void __launch_bounds__(gemm_waves(TYPE, NCT) * 64,
                                   NCT == 1 && TYPE != LGMLH_Q8_0   ? 4
                                   : NCT == 4 && TYPE == LGMLH_Q4_K ? 2
@@ -318,14 +338,21 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
              const float *__restrict__ residual, int nz, int sb_per_split, int fold,
              float *__restrict__ part, Gather gt) {
   constexpr int WVS = gemm_waves(TYPE, NCT);  // waves per workgroup
-  constexpr bool ONEBUF = WVS < GEMM_WAVES;     // one X buffer
+  constexpr bool ONEBUF = WVS < GEMM_WAVES && !Q8;  // one X buffer
   constexpr int COLS = NCT * 16;            // N columns per workgroup
   constexpr int X_SLOTS = COLS * 32;
+  constexpr int XL_SLOTS = Q8 ? 1 : X_SLOTS;
+  // Q8: the X block scales of a K step: Q8_K one f32 per column (16
+  // slots); Q8_0 8 per column, [half][column][4] (128 slots)
+  constexpr int DX_SLOTS = !Q8 ? 1 : TYPE == LGMLH_Q8_0 ? 128 : 16;
   __shared__ __align__(16) u32x4 xh0_[X_SLOTS], xh1_[ONEBUF ? 1 : X_SLOTS];
-  __shared__ __align__(16) u32x4 xl0_[X_SLOTS], xl1_[ONEBUF ? 1 : X_SLOTS];
-  __shared__ __align__(16) u32x4 gh0_[64], gh1_[64];  // group sums, hi: 8 f16 per row
-  __shared__ __align__(16) u32x4 gl0_[64], gl1_[64];  // group sums, lo
+  __shared__ __align__(16) u32x4 xl0_[XL_SLOTS], xl1_[ONEBUF ? 1 : XL_SLOTS];
+  // Q4_K group sums, 8 f16 per row: hi and lo (Q8: the 16 sums of 16 q,
+  // 0..7 and 8..15)
+  __shared__ __align__(16) u32x4 gh0_[64], gh1_[64];
+  __shared__ __align__(16) u32x4 gl0_[64], gl1_[64];
   __shared__ __align__(16) u32x4 gz_[1];              // zeros for lanes c >= 2
+  __shared__ __align__(16) u32x4 dx0_[DX_SLOTS], dx1_[DX_SLOTS];
   // Q8_0: the 256-byte headers of every wave's chunks (wave w, tile a at
   // slots 32 w + 16 a .. + 15)
   constexpr int HD_SLOTS = TYPE == LGMLH_Q8_0 ? WVS * RT_PER_WAVE * 16 : 1;
@@ -335,6 +362,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   auto GH = [&](int b) { return b && !ONEBUF ? gh1_ : gh0_; };
   auto GL = [&](int b) { return b && !ONEBUF ? gl1_ : gl0_; };
   auto HD = [&](int b) { return b ? hd1_ : hd0_; };
+  auto DX = [&](int b) { return (const float *)(b ? dx1_ : dx0_); };
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   if (tid == 0) gz_[0] = u32x4{0, 0, 0, 0};  // read after the prologue's barrier
@@ -398,6 +426,12 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   constexpr int XJ = X_SLOTS / (WVS * 64);  // NCT
   const f16 *xhi = xs + n0 * K + sb_lo * QK_K, *xlo = xhi + Npad * K;
   const f16 *ghi = xs + 2 * Npad * K + n0 * (K / 32) + sb_lo * 8, *glo = ghi + Npad * (K / 32);
+  // Q8: the 16-value sums and the block scales from the K range's start
+  // (per column: xrow * K / 16, xrow * K / QB added per lane)
+  constexpr int QB = TYPE == LGMLH_Q8_0 ? 32 : QK_K;
+  const f16 *bsp = xs + q8_bs_off(Npad, K) + n0 * (K / 16) + sb_lo * 16;
+  const float *dxp = (const float *)((const char *)xs + q8_d_off(Npad, K)) + n0 * (K / QB) +
+                     sb_lo * (QK_K / QB);
   // byte offsets of a lane's pieces from the plane's K step (the planes
   // stay under 4 GiB: checked at launch)
   uint32_t xoff[XJ];
@@ -408,7 +442,9 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   }
   // group sums: lane = column (lanes past the workgroup's columns load a
   // valid row into slots that are never read)
-  const uint32_t goff = (uint32_t)(xrow(lane < COLS ? lane : 0) * (K / 32));
+  const int64_t xr_lane = xrow(lane < COLS ? lane : 0);
+  const uint32_t goff = (uint32_t)(xr_lane * (Q8 ? K / 16 : K / 32));
+  const uint32_t doff = (uint32_t)(xr_lane * (K / QB));
   // Chunk of tile a at K step sb_lo + kstep: a wave-uniform address (rows
   // past M clamp to the last tile; they are computed but never stored).
   const uint8_t *wt[RT_PER_WAVE];
@@ -428,14 +464,30 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
       const uint8_t *bl = (const uint8_t *)(xlo + kstep * QK_K);
       __builtin_amdgcn_global_load_lds((const void *)(bh + xoff[j]), (lds_t *)&XH(buf)[slot0],
                                        16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void *)(bl + xoff[j]), (lds_t *)&XL(buf)[slot0],
-                                       16, 0, 0);
+      if constexpr (!Q8)
+        __builtin_amdgcn_global_load_lds((const void *)(bl + xoff[j]), (lds_t *)&XL(buf)[slot0],
+                                         16, 0, 0);
     }
-    if constexpr (TYPE == LGMLH_Q4_K) {
+    if constexpr (TYPE == LGMLH_Q4_K && !Q8) {
       if (wave < 2)  // wave 0: hi sums, wave 1: lo sums
         __builtin_amdgcn_global_load_lds(
             (const void *)((wave == 0 ? ghi : glo) + goff + kstep * 8),
             (lds_t *)(wave == 0 ? GH(buf) : GL(buf)), 16, 0, 0);
+    }
+    if constexpr (TYPE == LGMLH_Q4_K && Q8) {
+      if (wave < 2)  // wave 0: sums 0..7 of 16 q, wave 1: sums 8..15
+        __builtin_amdgcn_global_load_lds((const void *)(bsp + goff + kstep * 16 + 8 * wave),
+                                         (lds_t *)(wave == 0 ? GH(buf) : GL(buf)), 16, 0, 0);
+    }
+    if constexpr (Q8 && TYPE != LGMLH_Q8_0) {
+      if (wave == 2)  // the d of each column (lane)
+        __builtin_amdgcn_global_load_lds((const void *)(dxp + doff + kstep),
+                                         (lds_t *)(buf ? dx1_ : dx0_), 4, 0, 0);
+    }
+    if constexpr (Q8 && TYPE == LGMLH_Q8_0) {
+      if (wave < 2)  // the d of blocks 4 wave .. 4 wave + 3 of each column (lane)
+        __builtin_amdgcn_global_load_lds((const void *)(dxp + doff + kstep * 8 + 4 * wave),
+                                         (lds_t *)((buf ? dx1_ : dx0_) + 64 * wave), 16, 0, 0);
     }
     if constexpr (TYPE == LGMLH_Q8_0) {
       if (lane < 32)
@@ -461,7 +513,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
     // reads run while the next step's global-to-LDS loads into the other
     // buffer are in flight.
     f16x4 sh4[NCT], sl4[NCT];
-    if constexpr (TYPE == LGMLH_Q4_K) {
+    if constexpr (TYPE == LGMLH_Q4_K && !Q8) {
       // lanes c >= 2 (k past the 8 groups) read zeros: no branch per step
       const bool gs = c < 2;
       const f16 *gh = gs ? (const f16 *)GH(buf) + r16 * 8 + 4 * c : (const f16 *)gz_;
@@ -472,6 +524,12 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
         sh4[ct] = *(const f16x4 *)(gh + ct * cstride);
         sl4[ct] = *(const f16x4 *)(gl + ct * cstride);
       }
+    }
+    if constexpr (TYPE == LGMLH_Q4_K && Q8) {
+      // the 16 sums of 16 q: lane c holds sums 4c .. 4c + 3 of its column
+      const f16 *gs = (const f16 *)(c < 2 ? GH(buf) : GL(buf)) + r16 * 8 + 4 * (c & 1);
+#pragma unroll
+      for (int ct = 0; ct < NCT; ct++) sh4[ct] = *(const f16x4 *)(gs + ct * 16 * 8);
     }
     uint32_t scb[RT_PER_WAVE][2];
     if constexpr (TYPE == LGMLH_Q4_K) {
@@ -490,9 +548,11 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
       for (int ct = 0; ct < NCT; ct++) bh[ct] = __builtin_bit_cast(f16x8, xh[ct * 16 * 32 + slot]);
     };
     auto read_bl = [&](int g) {
-      const int slot = r16 * 32 + ((4 * g + c) ^ r16);
+      if constexpr (!Q8) {
+        const int slot = r16 * 32 + ((4 * g + c) ^ r16);
 #pragma unroll
-      for (int ct = 0; ct < NCT; ct++) bl[ct] = __builtin_bit_cast(f16x8, xl[ct * 16 * 32 + slot]);
+        for (int ct = 0; ct < NCT; ct++) bl[ct] = __builtin_bit_cast(f16x8, xl[ct * 16 * 32 + slot]);
+      }
     };
     // Q8_0: d of rows 4c .. 4c + 3 of tile a, block g
     u32x2 dv[RT_PER_WAVE];
@@ -522,7 +582,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
         if constexpr (TYPE == LGMLH_Q4_K)
           af[a] = cur[a].frag(g, sp[a], cp[a]);
         else if constexpr (TYPE == LGMLH_Q6_K)
-          cur[a].frag(g, sh6, af[a], af2[a], afr[a]);
+          cur[a].frag(g, sh6, af[a], af2[a], afr[a]);  // afr unused with Q8
         else
           af[a] = cur[a].frag(g);
       }
@@ -542,19 +602,28 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
             cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af2[a], bh[ct], cm[a][ct], 0, 0, 0);
       }
       if (g < 7) read_bh(g + 1);
+      if constexpr (!Q8) {
 #pragma unroll
-      for (int a = 0; a < RT_PER_WAVE; a++)
+        for (int a = 0; a < RT_PER_WAVE; a++)
 #pragma unroll
-        for (int ct = 0; ct < NCT; ct++)
-          cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(TYPE == LGMLH_Q6_K ? afr[a] : af[a],
-                                                              bl[ct], cm[a][ct], 0, 0, 0);
-      if (g < 7) read_bl(g + 1);
+          for (int ct = 0; ct < NCT; ct++)
+            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                TYPE == LGMLH_Q6_K ? afr[a] : af[a], bl[ct], cm[a][ct], 0, 0, 0);
+        if (g < 7) read_bl(g + 1);
+      }
       u32x2 dg[RT_PER_WAVE];
 #pragma unroll
       for (int a = 0; a < RT_PER_WAVE; a++) dg[a] = dv[a];
       if (g < 7) read_d(g + 1);
       if constexpr (TYPE == LGMLH_Q8_0) {
-        // one scale per 32-value block: flush every group
+        // one scale per 32-value block: flush every group (Q8: times the
+        // column's d of the block, (d_w d_x) I as ggml's q8_0 dot)
+        float dxg[NCT];
+        if constexpr (Q8) {
+#pragma unroll
+          for (int ct = 0; ct < NCT; ct++)
+            dxg[ct] = DX(buf)[(g >> 2) * 256 + (ct * 16 + r16) * 4 + (g & 3)];
+        }
 #pragma unroll
         for (int a = 0; a < RT_PER_WAVE; a++) {
 #pragma unroll
@@ -562,7 +631,10 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
             const float d = h2f((uint16_t)(dg[a][i >> 1] >> (16 * (i & 1))));
 #pragma unroll
             for (int ct = 0; ct < NCT; ct++) {
-              acc[a][ct][i] += d * cm[a][ct][i];
+              if constexpr (Q8)
+                acc[a][ct][i] = fmaf(d * dxg[ct], cm[a][ct][i], acc[a][ct][i]);
+              else
+                acc[a][ct][i] += d * cm[a][ct][i];
             }
           }
         }
@@ -575,11 +647,18 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
           for (int ct = 0; ct < NCT; ct++) asm volatile("" : "+v"(acc[a][ct]));
       }
     }
+    // Q8 (Q8_K): the column's d of this K step
+    float dxs[NCT];
+    if constexpr (Q8 && TYPE != LGMLH_Q8_0) {
+#pragma unroll
+      for (int ct = 0; ct < NCT; ct++) dxs[ct] = DX(buf)[ct * 16 + r16];
+    }
     if constexpr (TYPE == LGMLH_Q4_K) {
       // min term: sum_g m_g * S_g[n] as a 16x16x16 MFMA over the 8 groups
+      // (Q8: over the 16 sums of 16 q)
 #pragma unroll
       for (int a = 0; a < RT_PER_WAVE; a++) {
-        const f16x4 am = cur[a].mins(c);
+        const f16x4 am = Q8 ? cur[a].mins16(c) : cur[a].mins(c);
         float dd[4], dm[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -589,10 +668,18 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
 #pragma unroll
         for (int ct = 0; ct < NCT; ct++) {
           f32x4 mn = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sh4[ct], f32x4{0, 0, 0, 0}, 0, 0, 0);
-          mn = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sl4[ct], mn, 0, 0, 0);
+          if constexpr (!Q8) {
+            mn = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sl4[ct], mn, 0, 0, 0);
 #pragma unroll
-          for (int i = 0; i < 4; i++)
-            acc[a][ct][i] = fmaf(-dm[i], mn[i], fmaf(dd[i], cm[a][ct][i], acc[a][ct][i]));
+            for (int i = 0; i < 4; i++)
+              acc[a][ct][i] = fmaf(-dm[i], mn[i], fmaf(dd[i], cm[a][ct][i], acc[a][ct][i]));
+          } else {
+            // d_x (d_w I - dmin_w Mn): I and Mn are exact integers
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+              acc[a][ct][i] = fmaf(dxs[ct], fmaf(dd[i], cm[a][ct][i], -(dm[i] * mn[i])),
+                                   acc[a][ct][i]);
+          }
         }
       }
     } else if constexpr (TYPE == LGMLH_Q6_K) {
@@ -603,7 +690,12 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
           // the fragments carry sc * q / 4
           const float d4 = 4.0f * h2f((uint16_t)(cur[a].d4[i >> 1] >> (16 * (i & 1))));
 #pragma unroll
-          for (int ct = 0; ct < NCT; ct++) acc[a][ct][i] += d4 * cm[a][ct][i];
+          for (int ct = 0; ct < NCT; ct++) {
+            if constexpr (Q8)
+              acc[a][ct][i] = fmaf(d4 * dxs[ct], cm[a][ct][i], acc[a][ct][i]);
+            else
+              acc[a][ct][i] += d4 * cm[a][ct][i];
+          }
         }
       }
     }
@@ -731,9 +823,10 @@ __global__ void splitk_reduce_kernel(Pending pd, float *__restrict__ y, int64_t 
   }
 }
 
-// X (f32 or f16 rows of K) -> split planes; one thread per 8 values.
+// X (f32 or f16 rows of K) -> planes of the form xf; one thread per 8 values
+// (the lanes of a 256-value block are consecutive and leave together).
 __global__ void xsplit_kernel(const void *__restrict__ x, int xtype, int64_t N, int64_t K,
-                              f16 *__restrict__ planes, int64_t Npad) {
+                              f16 *__restrict__ planes, int64_t Npad, int xf) {
   const int64_t per_row = K / 8;  // a multiple of 32: groups never straddle rows
   const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (t >= N * per_row) return;   // whole groups of 4 lanes leave together
@@ -752,7 +845,7 @@ __global__ void xsplit_kernel(const void *__restrict__ x, int xtype, int64_t N, 
 #pragma unroll
     for (int e = 0; e < 8; e++) v[e] = (float)h[e];
   }
-  split_store8(planes, Npad, K, n, k0, v);
+  act_store8(xf, planes, Npad, K, n, k0, v);
 }
 
 // ---- f32 weights: LDS-tiled VALU GEMM, sequential k order ----------------------
@@ -818,7 +911,7 @@ size_t workspace_for(int type, int64_t M, int64_t K, int64_t N) {
 // Launch a quantized product; returns the partials it leaves in part (0:
 // the product is in y) and, in *group, how many consecutive partials make a
 // pair sum (2: one per split; 1: one per folded pair).
-template <int TYPE>
+template <int TYPE, bool Q8>
 static int launch_q(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t N, float *y,
                     int64_t ldy, const float *res, float *part, bool defer, hipStream_t st,
                     int *group) {
@@ -853,7 +946,7 @@ static int launch_q(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t 
   dim3 grid((unsigned)((N + cols - 1) / cols), (unsigned)((M + wrows - 1) / wrows),
             (unsigned)nz);
 #define LGMLH_PLAIN(NCT_)                                                                  \
-  hipLaunchKernelGGL((qgemm_kernel<TYPE, NCT_, false>), grid, dim3(gemm_waves(TYPE, NCT_) * 64), \
+  hipLaunchKernelGGL((qgemm_kernel<TYPE, NCT_, false, Q8>), grid, dim3(gemm_waves(TYPE, NCT_) * 64), \
                      0, st,                                                                \
                      (const uint8_t *)w, M, K, xs, Npad, N, y, ldy, res, nz, spb, fold,    \
                      part, Gather{})
@@ -874,15 +967,28 @@ static int launch_q(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t 
   return nz > 1 ? nz : 0;
 }
 
-// Quantized product on split X (split.h layout for N rows of K). part holds
-// the split-K partial sums (partial_bytes). With `deferred` given, a split
-// product leaves its partials in part and *deferred describes them (added
-// in the canonical order by the consumer, Pending::sum, which also adds the
-// residual); otherwise they are reduced here (*deferred stays empty).
+// The X form a quantized product takes: the split planes (exact), or in
+// ggml's arithmetic the weight type's vec_dot_type (Q8_K / Q8_0).
+int xf_for(int type, int act) {
+  if (act != LGMLH_ACT_GGML || type == LGMLH_F32) return XF_SPLIT;
+  return type == LGMLH_Q8_0 ? XF_Q80 : XF_Q8K;
+}
+
+// Quantized product on X planes in the form xf (split.h, N rows of K):
+// XF_SPLIT, or xf_for(type, LGMLH_ACT_GGML). part holds the split-K partial
+// sums (partial_bytes). With `deferred` given, a split product leaves its
+// partials in part and *deferred describes them (added in the canonical
+// order by the consumer, Pending::sum, which also adds the residual);
+// otherwise they are reduced here (*deferred stays empty).
 int mul_mat_split(int type, const void *w, int64_t M, int64_t K, const f16 *xs, int64_t N,
                   float *y, int64_t ldy, const float *residual, float *part, size_t part_bytes,
-                  hipStream_t st, Pending *deferred) {
+                  hipStream_t st, Pending *deferred, int xf) {
   if (deferred) *deferred = Pending{};
+  if (xf != XF_SPLIT && xf != xf_for(type, LGMLH_ACT_GGML)) {
+    set_error("mul_mat: X form %d does not suit weight type %d", xf, type);
+    return LGMLH_EINVAL;
+  }
+  const bool q8 = xf != XF_SPLIT;
   if (!w || !xs || !y || M <= 0 || K <= 0 || N < 0 || ldy < M || K % QK_K) {
     set_error("mul_mat: bad arguments (M %lld, K %lld)", (long long)M, (long long)K);
     return LGMLH_EINVAL;
@@ -896,9 +1002,13 @@ int mul_mat_split(int type, const void *w, int64_t M, int64_t K, const f16 *xs, 
   const bool defer = deferred && splits > 1;
   int nz = 0, group = 1;
   switch (type) {
-    case LGMLH_Q4_K: nz = launch_q<LGMLH_Q4_K>(w, M, K, xs, N, y, ldy, residual, part, defer, st, &group); break;
-    case LGMLH_Q6_K: nz = launch_q<LGMLH_Q6_K>(w, M, K, xs, N, y, ldy, residual, part, defer, st, &group); break;
-    case LGMLH_Q8_0: nz = launch_q<LGMLH_Q8_0>(w, M, K, xs, N, y, ldy, residual, part, defer, st, &group); break;
+#define LGMLH_Q(T_)                                                                          \
+  (q8 ? launch_q<T_, true>(w, M, K, xs, N, y, ldy, residual, part, defer, st, &group)        \
+      : launch_q<T_, false>(w, M, K, xs, N, y, ldy, residual, part, defer, st, &group))
+    case LGMLH_Q4_K: nz = LGMLH_Q(LGMLH_Q4_K); break;
+    case LGMLH_Q6_K: nz = LGMLH_Q(LGMLH_Q6_K); break;
+    case LGMLH_Q8_0: nz = LGMLH_Q(LGMLH_Q8_0); break;
+#undef LGMLH_Q
     default:
       set_error("mul_mat: type %d not supported", type);
       return LGMLH_EINVAL;
@@ -910,13 +1020,13 @@ int mul_mat_split(int type, const void *w, int64_t M, int64_t K, const f16 *xs, 
   return hip_check(hipGetLastError(), "mul_mat");
 }
 
-template <int TYPE, int NCT>
+template <int TYPE, int NCT, bool Q8>
 static void launch_grouped(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t Npad,
                            const Gather &gt, int max_tiles, float *y, hipStream_t st) {
   const int NSB = (int)(K / QK_K);
   const int wrows = gemm_waves(TYPE, NCT) * RT_PER_WAVE * 16;
   dim3 grid((unsigned)max_tiles, (unsigned)((M + wrows - 1) / wrows), 1);
-  hipLaunchKernelGGL((qgemm_kernel<TYPE, NCT, true>), grid, dim3(gemm_waves(TYPE, NCT) * 64), 0, st,
+  hipLaunchKernelGGL((qgemm_kernel<TYPE, NCT, true, Q8>), grid, dim3(gemm_waves(TYPE, NCT) * 64), 0, st,
                      (const uint8_t *)w, M, K, xs, Npad, (int64_t)0, y, M, (const float *)nullptr,
                      1, NSB, 1, (float *)nullptr, gt);
 }
@@ -925,11 +1035,17 @@ static void launch_grouped(const void *w, int64_t M, int64_t K, const f16 *xs, i
 // Gather), Y rows of its picks = expert matrix x X rows, K unsplit. w holds
 // n_expert repacked matrices of M rows, expert_bytes apart; xs the split
 // planes of the X rows (Npad rows). tile_cols is 16 or 64, the tile width
-// the grouping was made for; max_tiles bounds the tiles in use.
+// the grouping was made for; max_tiles bounds the tiles in use. xf: the
+// planes' form (as mul_mat_split).
 int mul_mat_grouped(int type, const void *w, int64_t expert_bytes, int64_t M, int64_t K,
                     const f16 *xs, int64_t Npad, int n_used, int U, const int32_t *sorted,
                     const int4 *tiles, const int32_t *n_tiles, int max_tiles, int tile_cols,
-                    float *y, hipStream_t st) {
+                    float *y, hipStream_t st, int xf) {
+  if (xf != XF_SPLIT && xf != xf_for(type, LGMLH_ACT_GGML)) {
+    set_error("mul_mat_id: X form %d does not suit weight type %d", xf, type);
+    return LGMLH_EINVAL;
+  }
+  const bool q8 = xf != XF_SPLIT;
   if (!w || !xs || !y || M <= 0 || K <= 0 || K % QK_K || (tile_cols != 16 && tile_cols != 64)) {
     set_error("mul_mat_id: bad arguments (M %lld, K %lld)", (long long)M, (long long)K);
     return LGMLH_EINVAL;
@@ -942,9 +1058,12 @@ int mul_mat_grouped(int type, const void *w, int64_t expert_bytes, int64_t M, in
   gt.expert_bytes = expert_bytes;
   gt.n_used = n_used;
   gt.U = U;
-#define LGMLH_GROUPED(T_)                                                              \
-  (tile_cols == 16 ? launch_grouped<T_, 1>(w, M, K, xs, Npad, gt, max_tiles, y, st)    \
-                   : launch_grouped<T_, 4>(w, M, K, xs, Npad, gt, max_tiles, y, st))
+#define LGMLH_GROUPED(T_)                                                                    \
+  (tile_cols == 16                                                                           \
+       ? (q8 ? launch_grouped<T_, 1, true>(w, M, K, xs, Npad, gt, max_tiles, y, st)          \
+             : launch_grouped<T_, 1, false>(w, M, K, xs, Npad, gt, max_tiles, y, st))        \
+       : (q8 ? launch_grouped<T_, 4, true>(w, M, K, xs, Npad, gt, max_tiles, y, st)          \
+             : launch_grouped<T_, 4, false>(w, M, K, xs, Npad, gt, max_tiles, y, st)))
   switch (type) {
     case LGMLH_Q4_K: LGMLH_GROUPED(LGMLH_Q4_K); break;
     case LGMLH_Q6_K: LGMLH_GROUPED(LGMLH_Q6_K); break;
@@ -957,8 +1076,8 @@ int mul_mat_grouped(int type, const void *w, int64_t expert_bytes, int64_t M, in
   return hip_check(hipGetLastError(), "mul_mat_id");
 }
 
-// X -> split planes (xs holds split_bytes(N, K)).
-int split_x(const void *x, int xtype, int64_t N, int64_t K, f16 *xs, hipStream_t st) {
+// X -> planes of the form xf (xs holds split_bytes(N, K)).
+int split_x(const void *x, int xtype, int64_t N, int64_t K, f16 *xs, hipStream_t st, int xf) {
   if (K % QK_K || (xtype != LGMLH_F32 && xtype != LGMLH_F16)) {
     set_error("split: bad arguments");
     return LGMLH_EINVAL;
@@ -966,7 +1085,7 @@ int split_x(const void *x, int xtype, int64_t N, int64_t K, f16 *xs, hipStream_t
   int64_t total = N * (K / 8);
   if (total == 0) return LGMLH_OK;
   hipLaunchKernelGGL(xsplit_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, x,
-                     xtype, N, K, xs, split_npad(N));
+                     xtype, N, K, xs, split_npad(N), xf);
   return hip_check(hipGetLastError(), "split");
 }
 
@@ -1018,9 +1137,9 @@ extern "C" size_t lgmlh_mul_mat_workspace(int type, int64_t M, int64_t K, int64_
   return workspace_for(type, M, K, N);
 }
 
-extern "C" int lgmlh_mul_mat(int type, const void *w, int64_t M, int64_t K, const void *x,
-                             int xtype, int64_t N, float *y, int epi, const float *residual,
-                             void *workspace, size_t ws_bytes, void *stream) {
+static int mul_mat_entry(int act, int type, const void *w, int64_t M, int64_t K, const void *x,
+                         int xtype, int64_t N, float *y, int epi, const float *residual,
+                         void *workspace, size_t ws_bytes, void *stream) {
   if (epi != LGMLH_EPI_NONE && epi != LGMLH_EPI_ADD) {
     set_error("mul_mat: bad epilogue");
     return LGMLH_EINVAL;
@@ -1055,9 +1174,68 @@ extern "C" int lgmlh_mul_mat(int type, const void *w, int64_t M, int64_t K, cons
   if (N == 0) return LGMLH_OK;
   f16 *xs = (f16 *)workspace;
   size_t xb = align256(split_bytes(N, K));
-  LGMLH_TRY(split_x(x, xtype, N, K, xs, st));
+  const int xf = xf_for(type, act);
+  LGMLH_TRY(split_x(x, xtype, N, K, xs, st, xf));
   return mul_mat_split(type, w, M, K, xs, N, y, M, res, (float *)((char *)workspace + xb),
-                       ws_bytes - xb, st, nullptr);
+                       ws_bytes - xb, st, nullptr, xf);
+}
+
+extern "C" int lgmlh_mul_mat(int type, const void *w, int64_t M, int64_t K, const void *x,
+                             int xtype, int64_t N, float *y, int epi, const float *residual,
+                             void *workspace, size_t ws_bytes, void *stream) {
+  return mul_mat_entry(LGMLH_ACT_EXACT, type, w, M, K, x, xtype, N, y, epi, residual, workspace,
+                       ws_bytes, stream);
+}
+
+extern "C" int lgmlh_mul_mat_ggml(int type, const void *w, int64_t M, int64_t K, const void *x,
+                                  int xtype, int64_t N, float *y, int epi,
+                                  const float *residual, void *workspace, size_t ws_bytes,
+                                  void *stream) {
+  return mul_mat_entry(LGMLH_ACT_GGML, type, w, M, K, x, xtype, N, y, epi, residual, workspace,
+                       ws_bytes, stream);
+}
+
+// ggml's activation blocks of X (N, K) f32 for a product with weight type
+// `type`: Q8_K (q, d, bsums) for Q4_K / Q6_K, Q8_0 (q, d as f16 bits) for
+// Q8_0. One thread per 8 values.
+__global__ void act_quant_kernel(const float *__restrict__ x, int64_t N, int64_t K, int xf,
+                                 int8_t *__restrict__ q, void *__restrict__ d,
+                                 int16_t *__restrict__ bsums) {
+  const int64_t per_row = K / 8;
+  const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (t >= N * per_row) return;  // whole blocks of lanes leave together
+  const int64_t n = t / per_row, k0 = (t % per_row) * 8;
+  float v[8], qv[8], dd;
+#pragma unroll
+  for (int e = 0; e < 8; e++) v[e] = x[n * K + k0 + e];
+  if (xf == XF_Q8K) {
+    float bs;
+    q8k_block8(v, (int)((k0 >> 3) & 31), qv, dd, bs);
+    if ((k0 & 15) == 0) bsums[n * (K / 16) + (k0 >> 4)] = (int16_t)bs;
+    if ((k0 & 255) == 0) ((float *)d)[n * (K / 256) + (k0 >> 8)] = dd;
+  } else {
+    uint16_t dh;
+    q80_block8(v, qv, dd, dh);
+    if ((k0 & 31) == 0) ((uint16_t *)d)[n * (K / 32) + (k0 >> 5)] = dh;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; e++) q[n * K + k0 + e] = (int8_t)qv[e];
+}
+
+extern "C" int lgmlh_quantize_act(int type, const float *x, int64_t N, int64_t K, int8_t *q,
+                                  void *d, int16_t *bsums, void *stream) {
+  const int xf = xf_for(type, LGMLH_ACT_GGML);
+  const int64_t qb = xf == XF_Q80 ? 32 : QK_K;
+  if (xf == XF_SPLIT || !x || !q || !d || (xf == XF_Q8K && !bsums) || N < 0 || K <= 0 ||
+      K % qb) {
+    set_error("quantize_act: bad arguments (type %d, K %lld)", type, (long long)K);
+    return LGMLH_EINVAL;
+  }
+  const int64_t total = N * (K / 8);
+  if (total == 0) return LGMLH_OK;
+  hipLaunchKernelGGL(act_quant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     as_stream(stream), x, N, K, xf, q, d, bsums);
+  return hip_check(hipGetLastError(), "quantize_act");
 }
 
 // ---- the entry point that allocates nothing -----------------------------------

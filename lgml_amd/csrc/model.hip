@@ -12,21 +12,17 @@
 
 namespace lgmlh {
 
-int mul_mat_split(int type, const void *w, int64_t M, int64_t K, const f16 *xs, int64_t N,
-                  float *y, int64_t ldy, const float *residual, float *part, size_t part_bytes,
-                  hipStream_t st, Pending *deferred);
 int mul_mat_f32(const float *w, int64_t M, int64_t K, const float *x, int64_t N, float *y,
                 int64_t ldy, const float *residual, hipStream_t st);
-int split_x(const void *x, int xtype, int64_t N, int64_t K, f16 *xs, hipStream_t st);
 int paged_attention_dev(const float *q, int n_head, int n_head_kv, int head_dim, float scale,
                         const void *kpool, const void *vpool, const lgmlh_ubatch *ub, float *out,
                         f16 *planes, int64_t npad, void *workspace, size_t workspace_bytes,
                         hipStream_t st);
 int rms_norm_dev(float *x, const int32_t *rows, int64_t n_rows, int64_t n, float eps,
                  const float *w, float *out, f16 *planes, hipStream_t st, Pending pend,
-                 bool writeback);
+                 bool writeback, int xf);
 int swiglu_dev(const float *gu, int64_t n, int64_t F, float *out, f16 *planes, hipStream_t st,
-               Pending pend, int gelu);
+               Pending pend, int gelu, int xf);
 int softcap_dev(float *x, int64_t n, float cap, hipStream_t st);
 int qkv_rope_store_dev(float *qkv, int64_t n, int n_head, int n_head_kv, int head_dim, int n_rot,
                        int neox, float freq_base, const float *freq_factors, const float *q_norm,
@@ -58,14 +54,27 @@ struct Carve {
 struct Sizes {
   int64_t N, E, H, Hkv, D, F, V, W, n_out;
   size_t gemm_ws, gemm_ws_v, attn_ws, split_ws;
+  // a layer whose V product takes X in another form than its q|k product
+  // (ggml arithmetic, Q8_0 beside a K-quant): planes of its own
+  bool v_own;
   // routed experts: experts, picks per token, expert width, picks, tile width
   bool moe;
   int NE, NU, tc;
   int64_t FX, P;
 };
 
+static bool isq(int type) { return type != LGMLH_F32; }
+
+// The V product of layer L takes its X planes apart from the q|k product's.
+static bool v_own_planes(const lgmlh_model *m, const lgmlh_layer &L) {
+  return L.wv && isq(L.wv_type) && isq(L.wqkv_type) &&
+         xf_for(L.wv_type, m->act) != xf_for(L.wqkv_type, m->act);
+}
+
 static Sizes sizes_of(const lgmlh_model *m, int64_t n_tokens, int64_t n_items, int n_out) {
   Sizes z;
+  z.v_own = false;
+  for (int il = 0; il < m->n_layer; il++) z.v_own = z.v_own || v_own_planes(m, m->layers[il]);
   z.N = n_tokens;
   z.E = m->n_embd;
   z.H = m->n_head;
@@ -126,7 +135,8 @@ static size_t ws_bytes_of(const Sizes &z) {
   add(z.N * z.F * 4);        // silu(gate) * up
   add(z.n_out * z.E * 4);    // normed logit rows
   add(z.N * z.E * 4);        // a post-normed product (gemma), pending
-  add(z.split_ws);           // split planes of the current product's X
+  add(z.split_ws);           // X planes of the current product
+  if (z.v_own) add(split_bytes(z.N, z.E));  // X planes of a V product of its own form
   add(z.attn_ws);
   add(z.gemm_ws);
   add(z.gemm_ws_v);
@@ -208,6 +218,10 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
     set_error("forward: bad arguments");
     return LGMLH_EINVAL;
   }
+  if (m->act != LGMLH_ACT_EXACT && m->act != LGMLH_ACT_GGML) {
+    set_error("forward: act %d is neither LGMLH_ACT_EXACT nor LGMLH_ACT_GGML", m->act);
+    return LGMLH_EINVAL;
+  }
   for (int il = 0; il < m->n_layer; il++)
     if (m->layers[il].swa && (!ub_ring || ub_ring->ring <= 0 || ub_ring->n_tokens != ub->n_tokens ||
                               ub_ring->n_head_kv != ub->n_head_kv)) {
@@ -239,6 +253,7 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
   float *xo = (float *)cv.take(z.n_out * z.E * 4);
   float *ao = (float *)cv.take(z.N * z.E * 4);
   f16 *xs = (f16 *)cv.take(z.split_ws);
+  f16 *xs_v = z.v_own ? (f16 *)cv.take(split_bytes(z.N, z.E)) : nullptr;
   void *aws = cv.take(z.attn_ws);
   float *gws = (float *)cv.take(z.gemm_ws);
   float *gws_v = (float *)cv.take(z.gemm_ws_v);
@@ -261,24 +276,29 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
   }
   const float scale = m->attn_scale > 0 ? m->attn_scale : 1.0f / sqrtf((float)z.D);
 
-  // A product on X given as f32 rows (f32 weights) or as split planes xs
-  // (quantized weights); the producer wrote the form(s) the weights take.
-  // A quantized product split over K leaves its partial sums pending (pd):
-  // the next kernel that reads y adds them in the canonical order, then the residual.
+  // The X form of a quantized product (split planes, or ggml's Q8_K / Q8_0
+  // blocks under LGMLH_ACT_GGML).
+  auto xfo = [&](int type) { return xf_for(type, m->act); };
+  // A product on X given as f32 rows (f32 weights) or as planes (quantized
+  // weights, xs unless given); the producer wrote the form(s) the weights
+  // take. A quantized product split over K leaves its partial sums pending
+  // (pd): the next kernel that reads y adds them in the canonical order,
+  // then the residual.
   auto gemm_on = [&](hipStream_t s, int type, const void *w, int64_t M, int64_t K,
                      const float *xf, int64_t N, float *y, int64_t ldy, const float *res,
-                     float *part, size_t part_bytes, Pending &pd) -> int {
+                     float *part, size_t part_bytes, Pending &pd,
+                     const f16 *planes = nullptr) -> int {
     Span sp(trace, LGMLH_TRACE_GEMM, s);
     pd = Pending{};
     if (type == LGMLH_F32) return mul_mat_f32((const float *)w, M, K, xf, N, y, ldy, res, s);
-    return mul_mat_split(type, w, M, K, xs, N, y, ldy, res, part, part_bytes, s, &pd);
+    return mul_mat_split(type, w, M, K, planes ? planes : xs, N, y, ldy, res, part, part_bytes,
+                         s, &pd, xfo(type));
   };
   auto gemm = [&](int type, const void *w, int64_t M, int64_t K, const float *xf, int64_t N,
                   float *y, int64_t ldy, const float *res, float *part, size_t part_bytes,
                   Pending &pd) -> int {
     return gemm_on(st, type, w, M, K, xf, N, y, ldy, res, part, part_bytes, pd);
   };
-  auto isq = [](int type) { return type != LGMLH_F32; };
   // A product whose output goes to the residual stream x: added into x by
   // the GEMM (or left pending, the consumer adds it), or, with a post norm
   // or an output scale (gemma), left pending in ao: the next norm adds
@@ -302,11 +322,16 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
   for (int il = 0; il < m->n_layer; il++) {
     const lgmlh_layer &L = m->layers[il];
     const bool v_sep = L.wv != nullptr;
+    const bool v_own = v_own_planes(m, L);
     const bool qin_q = isq(L.wqkv_type) || (v_sep && isq(L.wv_type));
-    const bool qin_f = !isq(L.wqkv_type) || (v_sep && !isq(L.wv_type));
-    // x += the previous layer's down product, then attn_norm
+    const bool qin_f = !isq(L.wqkv_type) || (v_sep && !isq(L.wv_type)) || v_own;
+    // x += the previous layer's down product, then attn_norm (planes in
+    // the form of the first quantized product; a V product of another
+    // form gets its own from the f32 rows)
     LGMLH_TRY(rms_norm_dev(x, nullptr, z.N, z.E, m->eps, L.attn_norm, qin_f ? xn : nullptr,
-                           qin_q ? xs : nullptr, st, p_down, true));
+                           qin_q ? xs : nullptr, st, p_down, true,
+                           xfo(isq(L.wqkv_type) ? L.wqkv_type : L.wv_type)));
+    if (v_own) LGMLH_TRY(split_x(xn, LGMLH_F32, z.N, z.E, xs_v, st, xfo(L.wv_type)));
     // A V matrix of its own type (a more_bits layer's Q6_K) is a small
     // product that leaves most CUs idle: it runs on a side stream beside
     // the q|k product (not while tracing, whose events time one stream).
@@ -316,7 +341,8 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
       LGMLH_TRY(hip_check(hipEventRecord(sd->fork, st), "forward: fork"));
       LGMLH_TRY(hip_check(hipStreamWaitEvent(sd->s, sd->fork, 0), "forward: fork"));
       LGMLH_TRY(gemm_on(sd->s, L.wv_type, L.wv, z.W - L.wqkv_rows, z.E, xn, z.N,
-                        qkv + L.wqkv_rows, z.W, nullptr, gws_v, z.gemm_ws_v, p_v));
+                        qkv + L.wqkv_rows, z.W, nullptr, gws_v, z.gemm_ws_v, p_v,
+                        v_own ? xs_v : nullptr));
       LGMLH_TRY(hip_check(hipEventRecord(sd->join, sd->s), "forward: join"));
     }
     LGMLH_TRY(gemm(L.wqkv_type, L.wqkv, L.wqkv_rows, z.E, xn, z.N, qkv, z.W, nullptr, gws,
@@ -324,8 +350,8 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
     if (sd) {
       LGMLH_TRY(hip_check(hipStreamWaitEvent(st, sd->join, 0), "forward: join"));
     } else if (v_sep) {
-      LGMLH_TRY(gemm(L.wv_type, L.wv, z.W - L.wqkv_rows, z.E, xn, z.N, qkv + L.wqkv_rows, z.W,
-                     nullptr, gws_v, z.gemm_ws_v, p_v));
+      LGMLH_TRY(gemm_on(st, L.wv_type, L.wv, z.W - L.wqkv_rows, z.E, xn, z.N, qkv + L.wqkv_rows,
+                        z.W, nullptr, gws_v, z.gemm_ws_v, p_v, v_own ? xs_v : nullptr));
     }
     // a sliding layer keeps its K / V in the sequences' rings (rows_swa,
     // transformer.lua:2469-2476) and attends through the ring plan
@@ -337,22 +363,25 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
                                  m->eps, ub->pos, L.kpool, L.vpool,
                                  L.swa ? m->ring_cells : m->n_cells, lub->cells, q, st, p_qk, p_v,
                                  vmode));
+    // a quantized output product takes its X as split planes, written by
+    // the attention (and merge) kernels themselves; ggml's Q8 blocks are
+    // made from the f32 rows by a kernel of their own
+    const bool oq = isq(L.wo_type), o_split = oq && xfo(L.wo_type) == XF_SPLIT;
     {
-      // a quantized output product takes its X as split planes, written by
-      // the attention (and merge) kernels themselves
       Span sp(trace, LGMLH_TRACE_ATTN, st);
-      const bool oq = isq(L.wo_type);
       LGMLH_TRY(paged_attention_dev(q, (int)z.H, (int)z.Hkv, (int)z.D, scale, L.kpool, L.vpool,
-                                    lub, oq ? nullptr : att, oq ? xs : nullptr, split_npad(z.N),
-                                    aws, z.attn_ws, st));
+                                    lub, o_split ? nullptr : att, o_split ? xs : nullptr,
+                                    split_npad(z.N), aws, z.attn_ws, st));
     }
+    if (oq && !o_split)
+      LGMLH_TRY(split_x(att, LGMLH_F32, z.N, z.H * z.D, xs, st, xfo(L.wo_type)));
     LGMLH_TRY(out_product(L.wo_type, L.wo, z.H * z.D, att, L.post_attn_norm, 0.0f, p_o));
     if (L.gate_inp) {
       // routed experts (transformer.lua:2054-2068, M.moe :1989-2027): x +=
       // attention out, then ffn_norm for the router (f32) and the experts
       const bool gq = isq(L.exp_gu_type), dq = isq(L.exp_down_type);
       LGMLH_TRY(rms_norm_dev(x, nullptr, z.N, z.E, m->eps, L.ffn_norm, xn, gq ? xs : nullptr,
-                             st, p_o, true));
+                             st, p_o, true, xfo(L.exp_gu_type)));
       {
         Span sp(trace, LGMLH_TRACE_GEMM, st);
         LGMLH_TRY(router_logits(L.gate_inp, z.NE, z.E, xn, z.N, rpart, st));
@@ -362,15 +391,17 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
       {
         Span sp(trace, LGMLH_TRACE_EXPERTS, st);
         LGMLH_TRY(experts_dev(L.exp_gu_type, L.exp_gu, z.NE, 2 * z.FX, z.E, xn, xs,
-                              split_npad(z.N), 1, mids, z.N, z.NU, go, gu_e, st));
+                              split_npad(z.N), 1, mids, z.N, z.NU, go, gu_e, st,
+                              xfo(L.exp_gu_type)));
       }
       // swiglu_split on the picks' rows; their split planes replace x's
       LGMLH_TRY(swiglu_dev(gu_e, z.P, z.FX, dq ? nullptr : act_e, dq ? xs : nullptr, st,
-                           Pending{}, 0));
+                           Pending{}, 0, xfo(L.exp_down_type)));
       {
         Span sp(trace, LGMLH_TRACE_EXPERTS, st);
         LGMLH_TRY(experts_dev(L.exp_down_type, L.exp_down, z.NE, z.E, z.FX, act_e, xs,
-                              split_npad(z.P), z.NU, mids, z.N, z.NU, go, y_e, st));
+                              split_npad(z.P), z.NU, mids, z.N, z.NU, go, y_e, st,
+                              xfo(L.exp_down_type)));
       }
       // the weighted sum of the picks (g:mul, sum_picks) is added to x by
       // the next norm
@@ -380,12 +411,13 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
     // x += attention out, then ffn_norm
     LGMLH_TRY(rms_norm_dev(x, nullptr, z.N, z.E, m->eps, L.ffn_norm,
                            isq(L.wgu_type) ? nullptr : xn, isq(L.wgu_type) ? xs : nullptr, st,
-                           p_o, true));
+                           p_o, true, xfo(L.wgu_type)));
     LGMLH_TRY(gemm(L.wgu_type, L.wgu, 2 * z.F, z.E, xn, z.N, gu, 2 * z.F, nullptr, gws,
                    z.gemm_ws, p_gu));
     // SwiGLU, or GeGLU on gemma (transformer.lua:2048)
     LGMLH_TRY(swiglu_dev(gu, z.N, z.F, isq(L.wdown_type) ? nullptr : act,
-                         isq(L.wdown_type) ? xs : nullptr, st, p_gu, m->gemma));
+                         isq(L.wdown_type) ? xs : nullptr, st, p_gu, m->gemma,
+                         xfo(L.wdown_type)));
     LGMLH_TRY(out_product(L.wdown_type, L.wdown, z.F, act, L.post_ffn_norm, L.out_scale, p_down));
   }
   // head (transformer.lua:2094-2104) on the logit rows (:2349-2350); the last
@@ -393,12 +425,12 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
   if (n_out > 0) {
     const bool oq = isq(m->output_type);
     LGMLH_TRY(rms_norm_dev(x, out_rows, n_out, z.E, m->eps, m->output_norm, oq ? nullptr : xo,
-                           oq ? xs : nullptr, st, p_down, false));
+                           oq ? xs : nullptr, st, p_down, false, xfo(m->output_type)));
     // the logits are the output: a split head product is reduced here
     Span sp(trace, LGMLH_TRACE_GEMM, st);
     if (oq)
       LGMLH_TRY(mul_mat_split(m->output_type, m->output, z.V, z.E, xs, n_out, logits, z.V,
-                              nullptr, gws, z.gemm_ws, st, nullptr));
+                              nullptr, gws, z.gemm_ws, st, nullptr, xfo(m->output_type)));
     else
       LGMLH_TRY(mul_mat_f32((const float *)m->output, z.V, z.E, xo, n_out, logits, z.V, nullptr,
                             st));

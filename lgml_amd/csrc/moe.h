@@ -27,6 +27,6 @@ size_t group_bytes(int64_t P, int NE, int tc);
 GroupOut group_carve(void *ws, int64_t P, int NE, int tc);
 int experts_dev(int type, const void *w, int NE, int64_t M, int64_t K, const float *xf,
                 const f16 *xs, int64_t xnpad, int U, const int32_t *ids, int64_t T, int n_used,
-                const GroupOut &go, float *y, hipStream_t st);
+                const GroupOut &go, float *y, hipStream_t st, int xform);
 
 }  // namespace lgmlh

@@ -19,11 +19,6 @@
 
 namespace lgmlh {
 
-int mul_mat_grouped(int type, const void *w, int64_t expert_bytes, int64_t M, int64_t K,
-                    const f16 *xs, int64_t Npad, int n_used, int U, const int32_t *sorted,
-                    const int4 *tiles, const int32_t *n_tiles, int max_tiles, int tile_cols,
-                    float *y, hipStream_t st);
-int split_x(const void *x, int xtype, int64_t N, int64_t K, f16 *xs, hipStream_t st);
 
 constexpr int ROUTE_THREADS = 1024;
 constexpr int ROUTE_WAVES = ROUTE_THREADS / 64;
@@ -774,7 +769,7 @@ static void launch_group(const int32_t *ids, int P, int NE, const GroupOut &g, f
 // experts) or split planes (quantized experts, xnpad rows).
 int experts_dev(int type, const void *w, int NE, int64_t M, int64_t K, const float *xf,
                 const f16 *xs, int64_t xnpad, int U, const int32_t *ids, int64_t T, int n_used,
-                const GroupOut &go, float *y, hipStream_t st) {
+                const GroupOut &go, float *y, hipStream_t st, int xform) {
   const int64_t P = T * n_used;
   if (P == 0) return LGMLH_OK;
   if (type == LGMLH_F32) {
@@ -789,7 +784,7 @@ int experts_dev(int type, const void *w, int NE, int64_t M, int64_t K, const flo
     return LGMLH_EINVAL;
   }
   return mul_mat_grouped(type, w, eb, M, K, xs, xnpad, n_used, U, go.sorted, go.tiles, go.n_tiles,
-                         moe_max_tiles(P, NE, go.tile_cols), go.tile_cols, y, st);
+                         moe_max_tiles(P, NE, go.tile_cols), go.tile_cols, y, st, xform);
 }
 
 }  // namespace lgmlh
@@ -817,10 +812,10 @@ extern "C" size_t lgmlh_mul_mat_id_workspace(int type, int64_t n_expert, int64_t
   return b;
 }
 
-extern "C" int lgmlh_mul_mat_id(int type, const void *w, int64_t n_expert, int64_t M, int64_t K,
-                                const void *x, int xtype, int64_t U, const int32_t *ids,
-                                int64_t T, int n_used, float *y, void *workspace,
-                                size_t ws_bytes, void *stream) {
+static int mul_mat_id_entry(int act, int type, const void *w, int64_t n_expert, int64_t M,
+                            int64_t K, const void *x, int xtype, int64_t U, const int32_t *ids,
+                            int64_t T, int n_used, float *y, void *workspace, size_t ws_bytes,
+                            void *stream) {
   if (!w || !x || !ids || !y || M <= 0 || K <= 0 || T < 0 || U < 1 || n_used < 1 ||
       n_used % U || n_expert < 1 || n_expert > MOE_MAX_EXPERTS) {
     set_error("mul_mat_id: bad arguments (experts %lld, M %lld, K %lld, U %lld, used %d)",
@@ -853,12 +848,29 @@ extern "C" int lgmlh_mul_mat_id(int type, const void *w, int64_t n_expert, int64
   launch_group(ids, (int)P, NE, go, y, M, st);
   LGMLH_TRY(hip_check(hipGetLastError(), "mul_mat_id group"));
   f16 *xs = nullptr;
+  const int xform = xf_for(type, act);
   if (type != LGMLH_F32) {
     xs = (f16 *)((char *)workspace + group_bytes(P, NE, tc));
-    LGMLH_TRY(split_x(x, xtype, T * U, K, xs, st));
+    LGMLH_TRY(split_x(x, xtype, T * U, K, xs, st, xform));
   }
   return experts_dev(type, w, NE, M, K, (const float *)x, xs, split_npad(T * U), (int)U, ids, T,
-                     n_used, go, y, st);
+                     n_used, go, y, st, xform);
+}
+
+extern "C" int lgmlh_mul_mat_id(int type, const void *w, int64_t n_expert, int64_t M, int64_t K,
+                                const void *x, int xtype, int64_t U, const int32_t *ids,
+                                int64_t T, int n_used, float *y, void *workspace,
+                                size_t ws_bytes, void *stream) {
+  return mul_mat_id_entry(LGMLH_ACT_EXACT, type, w, n_expert, M, K, x, xtype, U, ids, T, n_used,
+                          y, workspace, ws_bytes, stream);
+}
+
+extern "C" int lgmlh_mul_mat_id_ggml(int type, const void *w, int64_t n_expert, int64_t M,
+                                     int64_t K, const void *x, int xtype, int64_t U,
+                                     const int32_t *ids, int64_t T, int n_used, float *y,
+                                     void *workspace, size_t ws_bytes, void *stream) {
+  return mul_mat_id_entry(LGMLH_ACT_GGML, type, w, n_expert, M, K, x, xtype, U, ids, T, n_used,
+                          y, workspace, ws_bytes, stream);
 }
 
 extern "C" int lgmlh_moe_sum(const float *y, const float *weights, int64_t T, int n_used,

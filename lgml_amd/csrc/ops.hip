@@ -59,7 +59,7 @@ template <typename OutT>
 __global__ void rms_norm_kernel(float *__restrict__ x, const int32_t *__restrict__ rows,
                                 int64_t n, float eps, const float *__restrict__ w,
                                 OutT *__restrict__ out, f16 *__restrict__ planes, int64_t npad,
-                                Pending pend, bool writeback) {
+                                Pending pend, bool writeback, int xf) {
   __shared__ double part[2][RMS_THREADS / 64];
   const int tid = threadIdx.x;
   const int64_t r = blockIdx.x;
@@ -150,7 +150,7 @@ __global__ void rms_norm_kernel(float *__restrict__ x, const int32_t *__restrict
       if (out)
 #pragma unroll
         for (int e = 0; e < 8; e++) out[r * n + 8 * pc + e] = (OutT)y[e];
-      if (planes) split_store8(planes, npad, n, r, 8 * pc, y);
+      if (planes) act_store8(xf, planes, npad, n, r, 8 * pc, y);
     }
   }
 }
@@ -294,7 +294,7 @@ __global__ void swiglu_kernel(const float *__restrict__ gu, int64_t n, int64_t F
 // The same values into split planes (F % 256 == 0); one thread per 8.
 __global__ void swiglu_split_kernel(const float *__restrict__ gu, int64_t n, int64_t F,
                                     f16 *__restrict__ planes, int64_t npad, Pending pend,
-                                    int gelu) {
+                                    int gelu, int xf) {
   const int64_t per_row = F / 8;
   const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (t >= n * per_row) return;  // whole 4-lane groups leave together
@@ -312,7 +312,7 @@ __global__ void swiglu_split_kernel(const float *__restrict__ gu, int64_t n, int
   }
 #pragma unroll
   for (int e = 0; e < 8; e++) v[e] = (float)(glu_act(g8[e], gelu) * (double)u8[e]);
-  split_store8(planes, npad, F, r, c0, v);
+  act_store8(xf, planes, npad, F, r, c0, v);
 }
 
 // ---- logit softcap: cap * tanh(x * (1 / cap)) (transformer.lua:2097-2099) ----
@@ -400,25 +400,26 @@ int get_rows_dev(int type, const void *table, int64_t n_cols, const int32_t *ids
 
 
 // rms_norm of n_rows rows (input rows[j] when rows is given) into f32 out
-// and / or split planes (planes sized for n_rows rows).
+// and / or X planes of the form xf (planes sized for n_rows rows).
 // pend: a pending product added to x first (written back to x when
 // writeback; never with rows, which may repeat).
 int rms_norm_dev(float *x, const int32_t *rows, int64_t n_rows, int64_t n, float eps,
                  const float *w, float *out, f16 *planes, hipStream_t st, Pending pend,
-                 bool writeback) {
+                 bool writeback, int xf) {
   if (n_rows == 0) return LGMLH_OK;
   if ((planes && n % 256) || n % 8 || n > 8 * RMS_THREADS * RMS_PIECES) {
     set_error("rms_norm: bad row length %lld", (long long)n);
     return LGMLH_EINVAL;
   }
   hipLaunchKernelGGL(rms_norm_kernel<float>, dim3((unsigned)n_rows), dim3(RMS_THREADS), 0, st, x, rows,
-                     n, eps, w, out, planes, split_npad(n_rows), pend, writeback && !rows);
+                     n, eps, w, out, planes, split_npad(n_rows), pend, writeback && !rows, xf);
   return hip_check(hipGetLastError(), "rms_norm");
 }
 
-// silu(g) * u (gelu(g) * u with gelu set) into f32 out and / or split planes.
+// silu(g) * u (gelu(g) * u with gelu set) into f32 out and / or X planes of
+// the form xf.
 int swiglu_dev(const float *gu, int64_t n, int64_t F, float *out, f16 *planes, hipStream_t st,
-               Pending pend, int gelu) {
+               Pending pend, int gelu, int xf) {
   if (n == 0) return LGMLH_OK;
   if (out) {
     int64_t total = n * F;
@@ -433,7 +434,7 @@ int swiglu_dev(const float *gu, int64_t n, int64_t F, float *out, f16 *planes, h
     }
     int64_t total = n * (F / 8);
     hipLaunchKernelGGL(swiglu_split_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                       st, gu, n, F, planes, split_npad(n), pend, gelu);
+                       st, gu, n, F, planes, split_npad(n), pend, gelu, xf);
   }
   return hip_check(hipGetLastError(), "swiglu");
 }
@@ -501,11 +502,11 @@ extern "C" int lgmlh_rms_norm(const float *x, int64_t n_rows, int64_t n, float e
   if (out_type == LGMLH_F32)
     hipLaunchKernelGGL(rms_norm_kernel<float>, dim3((unsigned)n_rows), dim3(RMS_THREADS), 0,
                        as_stream(stream), (float *)x, nullptr, n, eps, w, (float *)out, nullptr, 0,
-                       Pending{}, false);
+                       Pending{}, false, (int)XF_SPLIT);
   else
     hipLaunchKernelGGL(rms_norm_kernel<f16>, dim3((unsigned)n_rows), dim3(RMS_THREADS), 0,
                        as_stream(stream), (float *)x, nullptr, n, eps, w, (f16 *)out, nullptr, 0,
-                       Pending{}, false);
+                       Pending{}, false, (int)XF_SPLIT);
   return hip_check(hipGetLastError(), "rms_norm");
 }
 

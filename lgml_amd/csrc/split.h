@@ -73,4 +73,124 @@ __device__ __forceinline__ void split_store_gsum(f16 *__restrict__ planes, int64
   gp[Npad * (K / 32)] = (f16)(s - (float)sh);
 }
 
+// ---- quantized activations ---------------------------------------------------
+// ggml's CPU backend quantizes X to the weight type's vec_dot_type before a
+// quantized product (Q8_K for Q4_K / Q6_K, Q8_0 for Q8_0) and takes integer
+// dots per block. In that mode (lgmlh_model.act = LGMLH_ACT_GGML) a product
+// takes its X as these planes, rows padded to Npad:
+//   q  [Npad][K]       f16 of the int8 q (exact)
+//   bs [Npad][K / 16]  f16 of the Q8_K sums of 16 q (|s| <= 2032, exact)
+//   d  [Npad][K / QB]  f32 block scales: Q8_K d (QB = 256); Q8_0 the f16 d
+//                      widened to f32 (QB = 32)
+// They fit in split_bytes(N, K).
+enum { XF_SPLIT = 0, XF_Q8K = 1, XF_Q80 = 2 };
+
+__host__ __device__ inline int64_t q8_bs_off(int64_t Npad, int64_t K) { return Npad * K; }
+__host__ __device__ inline size_t q8_d_off(int64_t Npad, int64_t K) {  // bytes
+  return (size_t)Npad * K * 2 + (size_t)Npad * (K / 16) * 2;
+}
+
+// quantize_row_q8_K of one 256-value block held by 32 lanes (lane j of the
+// group: values 8j .. 8j + 7). amax = the largest |x|, its first occurrence
+// gives the signed max; iscale = -127 / max; q = min(127, nearest-even(iscale
+// x)); d = 1 / iscale; an all-zero block has q = 0, d = 0. bs: the sum of
+// the 16 q of the lane pair (j & ~1, j | 1).
+__device__ __forceinline__ void q8k_block8(const float (&v)[8], int j, float (&q)[8], float &d,
+                                           float &bs) {
+  float amax = 0.0f, mx = 0.0f;
+  int at = 1 << 30;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const float a = fabsf(v[e]);
+    if (a > amax) {
+      amax = a;
+      mx = v[e];
+      at = 8 * j + e;
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) {
+    const float a2 = __shfl_xor(amax, o), m2 = __shfl_xor(mx, o);
+    const int i2 = __shfl_xor(at, o);
+    if (a2 > amax || (a2 == amax && i2 < at)) {
+      amax = a2;
+      mx = m2;
+      at = i2;
+    }
+  }
+  float s = 0.0f;
+  if (amax == 0.0f) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) q[e] = 0.0f;
+    d = 0.0f;
+  } else {
+    const float iscale = -127.0f / mx;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      q[e] = fminf(127.0f, __builtin_rintf(iscale * v[e]));
+      s += q[e];
+    }
+    d = 1.0f / iscale;
+  }
+  bs = s + __shfl_xor(s, 1);
+}
+
+// quantize_row_q8_0 of one 32-value block held by 4 lanes (lane j: values
+// 8j .. 8j + 7): d = amax / 127, id = d ? 1 / d : 0, q = roundf(x id)
+// (ties away from zero); d is kept as f16 (dh, its bits) and f32(dh).
+__device__ __forceinline__ void q80_block8(const float (&v)[8], float (&q)[8], float &d,
+                                           uint16_t &dh) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  const float dd = amax / 127.0f;
+  const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) q[e] = __builtin_roundf(v[e] * id);
+  const f16 h = (f16)dd;
+  dh = __builtin_bit_cast(uint16_t, h);
+  d = (float)h;
+}
+
+// Stores the 8 values v of row n at columns k0..k0+7 in the form xf. The
+// lanes of a block call it together, in order of k0: 4 for XF_SPLIT and
+// XF_Q80, 32 for XF_Q8K (all of them active).
+__device__ __forceinline__ void act_store8(int xf, f16 *__restrict__ planes, int64_t Npad,
+                                           int64_t K, int64_t n, int64_t k0, const float (&v)[8]) {
+  if (xf == XF_SPLIT) {
+    split_store8(planes, Npad, K, n, k0, v);
+    return;
+  }
+  float q[8], d;
+  f16x8 h;
+  float *dp = (float *)((char *)planes + q8_d_off(Npad, K));
+  if (xf == XF_Q8K) {
+    float bs;
+    q8k_block8(v, (int)((k0 >> 3) & 31), q, d, bs);
+    if ((k0 & 15) == 0) planes[q8_bs_off(Npad, K) + n * (K / 16) + (k0 >> 4)] = (f16)bs;
+    if ((k0 & 255) == 0) dp[n * (K / 256) + (k0 >> 8)] = d;
+  } else {
+    uint16_t dh;
+    q80_block8(v, q, d, dh);
+    if ((k0 & 31) == 0) dp[n * (K / 32) + (k0 >> 5)] = d;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; e++) h[e] = (f16)q[e];
+  *(f16x8 *)(planes + n * K + k0) = h;
+}
+
+// Host side (gemm.hip): the X form of a weight type under an act mode;
+// products on planes; planes from f32 / f16 rows.
+int xf_for(int type, int act);
+int mul_mat_split(int type, const void *w, int64_t M, int64_t K, const f16 *xs, int64_t N,
+                  float *y, int64_t ldy, const float *residual, float *part, size_t part_bytes,
+                  hipStream_t st, Pending *deferred, int xf);
+int mul_mat_grouped(int type, const void *w, int64_t expert_bytes, int64_t M, int64_t K,
+                    const f16 *xs, int64_t Npad, int n_used, int U, const int32_t *sorted,
+                    const int4 *tiles, const int32_t *n_tiles, int max_tiles, int tile_cols,
+                    float *y, hipStream_t st, int xf);
+int split_x(const void *x, int xtype, int64_t N, int64_t K, f16 *xs, hipStream_t st, int xf);
+
 }  // namespace lgmlh

@@ -14,6 +14,7 @@ LIB_PATH = os.path.join(HERE, "liblgml_hip.so")
 F32, F16, Q8_0, Q4_K, Q6_K = 0, 1, 8, 12, 14
 OK, EINVAL, ENOMEM, EHIP, EFULL, ERANGE = 0, -1, -2, -3, -4, -5
 EPI_NONE, EPI_ADD = 0, 1
+ACT_EXACT, ACT_GGML = 0, 1
 
 # Every symbol include/lgml_hip.h declares.
 SYMBOLS = (
@@ -31,7 +32,8 @@ SYMBOLS = (
     "lgmlh_kvpool_longest_kid", "lgmlh_kvpool_set_cap", "lgmlh_kvpool_stats", "lgmlh_block_key",
     "lgmlh_gen_normal", "lgmlh_moe_route", "lgmlh_mul_mat_id_workspace", "lgmlh_mul_mat_id",
     "lgmlh_moe_sum", "lgmlh_plan_ring", "lgmlh_geglu", "lgmlh_softcap",
-    "lgmlh_mul_mat_noalloc_limit", "lgmlh_mul_mat_noalloc",
+    "lgmlh_mul_mat_noalloc_limit", "lgmlh_mul_mat_noalloc", "lgmlh_mul_mat_ggml",
+    "lgmlh_mul_mat_id_ggml", "lgmlh_quantize_act",
 )
 GATING_SOFTMAX, GATING_SIGMOID = 1, 2
 TRACE_ATTN, TRACE_GEMM, TRACE_EXPERTS = 1, 2, 4
@@ -89,7 +91,7 @@ class Model(C.Structure):
                 ("n_cells", C.c_int64), ("layers", C.POINTER(Layer))] + \
                [(n, C.c_int) for n in ("n_expert", "n_used", "n_ff_exp", "gating", "norm_topk")] + \
                [("expert_scale", C.c_float), ("gemma", C.c_int), ("embd_scale", C.c_float),
-                ("softcap", C.c_float), ("ring_cells", C.c_int64)]
+                ("softcap", C.c_float), ("ring_cells", C.c_int64), ("act", C.c_int)]
 
 
 _lib = None
@@ -139,6 +141,8 @@ def _declare(L):
         "lgmlh_dequantize": ([i32, vp, i64, i64, vp, vp], i32),
         "lgmlh_mul_mat_workspace": ([i32, i64, i64, i64], sz),
         "lgmlh_mul_mat": ([i32, vp, i64, i64, vp, i32, i64, vp, i32, vp, vp, sz, vp], i32),
+        "lgmlh_mul_mat_ggml": ([i32, vp, i64, i64, vp, i32, i64, vp, i32, vp, vp, sz, vp], i32),
+        "lgmlh_quantize_act": ([i32, vp, i64, i64, vp, vp, vp, vp], i32),
         "lgmlh_mul_mat_noalloc_limit": ([], sz),
         "lgmlh_mul_mat_noalloc": ([i32, vp, i64, i64, vp, i32, i64, vp, i32, vp, vp], i32),
         "lgmlh_get_rows": ([i32, vp, i64, i64, vp, vp, i64, vp, vp], i32),
@@ -177,6 +181,8 @@ def _declare(L):
         "lgmlh_mul_mat_id_workspace": ([i32, i64, i64, i64, i64, i64, i32], sz),
         "lgmlh_mul_mat_id": ([i32, vp, i64, i64, i64, vp, i32, i64, vp, i64, i32, vp, vp, sz, vp],
                              i32),
+        "lgmlh_mul_mat_id_ggml": ([i32, vp, i64, i64, i64, vp, i32, i64, vp, i64, i32, vp, vp, sz,
+                                   vp], i32),
         "lgmlh_moe_sum": ([vp, vp, i64, i32, i64, vp, vp, vp], i32),
     }
     for name, (args, res) in sig.items():

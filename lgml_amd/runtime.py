@@ -346,6 +346,9 @@ class DeviceModel:
         m.n_cells = self.n_cells
         m.ring_cells = self.ring_cells
         m.layers = self.layers
+        # hp["act_quant"]: the reference CPU path's arithmetic for quantized
+        # weights (X quantized to Q8_K / Q8_0 per block, integer block dots)
+        m.act = hip.ACT_GGML if hp.get("act_quant") else hip.ACT_EXACT
         if gemma:
             m.gemma = 1
             m.embd_scale = hp.get("embd_scale", 0.0)

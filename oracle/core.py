@@ -58,7 +58,7 @@ class Model(C.Structure):
                 ("n_expert", C.c_int), ("n_used", C.c_int), ("n_ff_exp", C.c_int),
                 ("gating", C.c_int), ("norm_topk", C.c_int), ("expert_scale", C.c_float),
                 ("gemma", C.c_int), ("n_swa", C.c_int), ("embd_scale", C.c_float),
-                ("softcap", C.c_float)]
+                ("softcap", C.c_float), ("act_quant", C.c_int)]
 
 
 class Batch(C.Structure):
@@ -94,6 +94,10 @@ def _declare(L):
                                  i32, i32, C.c_float, C.c_float, C.c_float, vp, i32]
     L.orc_set_rows_f16.argtypes = [vp, i64, i64, vp, vp, i64]
     L.orc_mul_mat.argtypes = [i32, vp, i64, i64, vp, i64, vp, i32]
+    L.orc_mul_mat_q8.argtypes = [i32, vp, i64, i64, vp, i64, vp, i32]
+    L.orc_mul_mat_id_q8.argtypes = [i32, vp, i64, i64, i64, vp, i64, vp, i64, i32, vp, i32]
+    L.orc_quantize_q8_K.argtypes = [vp, i64, vp, vp, vp]
+    L.orc_quantize_q8_0_act.argtypes = [vp, i64, vp, vp]
     L.orc_moe_route.argtypes = [vp, i64, i32, i32, i32, i32, C.c_float, vp, vp]
     L.orc_mul_mat_id.argtypes = [i32, vp, i64, i64, i64, vp, i64, vp, i64, i32, vp, i32]
     L.orc_splitmix64.argtypes = [C.POINTER(C.c_uint64)]
@@ -209,6 +213,43 @@ def mul_mat(t, w, M, K, x, nthreads=None):
     return y
 
 
+def mul_mat_q8(t, w, M, K, x, nthreads=None):
+    """ggml's CPU mul_mat for a quantized weight: X quantized per block to the
+    weight type's vec_dot_type (Q8_K / Q8_0), integer block dots."""
+    x = np.ascontiguousarray(x, np.float32)
+    N = x.shape[0]
+    y = np.empty((N, M), np.float32)
+    w = np.ascontiguousarray(w)
+    if lib().orc_mul_mat_q8(t, _p(w), M, K, _p(x), N, _p(y), nthreads or threads()) != 0:
+        raise ValueError("mul_mat_q8 failed")
+    return y
+
+
+def quantize_q8_K(x):
+    """quantize_row_q8_K_ref of each row of x (rows, K): q int8 (rows, K),
+    d f32 (rows, K/256), bsums int16 (rows, K/16)."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, K = x.shape
+    q = np.empty((rows, K), np.int8)
+    d = np.empty((rows, K // 256), np.float32)
+    bs = np.empty((rows, K // 16), np.int16)
+    for r in range(rows):
+        lib().orc_quantize_q8_K(_p(x[r]), K, _p(q[r]), _p(d[r]), _p(bs[r]))
+    return q, d, bs
+
+
+def quantize_q8_0_act(x):
+    """quantize_row_q8_0_ref of each row of x (rows, K): q int8 (rows, K), d
+    f16 bits (rows, K/32)."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, K = x.shape
+    q = np.empty((rows, K), np.int8)
+    d = np.empty((rows, K // 32), np.uint16)
+    for r in range(rows):
+        lib().orc_quantize_q8_0_act(_p(x[r]), K, _p(q[r]), _p(d[r]))
+    return q, d
+
+
 GATING_SOFTMAX, GATING_SIGMOID = 1, 2
 
 
@@ -224,16 +265,18 @@ def moe_route(logits, n_used, gating=GATING_SOFTMAX, norm_topk=True, scale=1.0):
     return ids, w
 
 
-def mul_mat_id(t, w, n_expert, M, K, x, ids, nthreads=None):
-    """y (T, n_used, M): row (t, j) = w[ids[t, j]] x[t, j % U], x (T, U, K)."""
+def mul_mat_id(t, w, n_expert, M, K, x, ids, nthreads=None, act_quant=False):
+    """y (T, n_used, M): row (t, j) = w[ids[t, j]] x[t, j % U], x (T, U, K);
+    act_quant: ggml's CPU arithmetic (mul_mat_q8) per expert."""
     x = np.ascontiguousarray(x, np.float32)
     ids = np.ascontiguousarray(ids, np.int32)
     T, n_used = ids.shape
     U = x.shape[1] if x.ndim == 3 else 1
     y = np.empty((T, n_used, M), np.float32)
     w = np.ascontiguousarray(w)
-    if lib().orc_mul_mat_id(t, _p(w), n_expert, M, K, _p(x), U, _p(ids), T, n_used, _p(y),
-                            nthreads or threads()) != 0:
+    fn = lib().orc_mul_mat_id_q8 if act_quant else lib().orc_mul_mat_id
+    if fn(t, _p(w), n_expert, M, K, _p(x), U, _p(ids), T, n_used, _p(y),
+          nthreads or threads()) != 0:
         raise ValueError("mul_mat_id failed")
     return y
 
@@ -419,6 +462,7 @@ class OracleModel:
         self.c.softcap = float(hp.get("softcap", 0.0))
         self.c.norm_topk = int(bool(hp.get("norm_topk", True)))
         self.c.expert_scale = float(hp.get("expert_scale", 1.0))
+        self.c.act_quant = int(bool(hp.get("act_quant", False)))
 
     def forward(self, kpools, vpools, batch, nthreads=None):
         """kpools/vpools: lists of (cap, Hkv*D) uint16 arrays (f16 bits), updated in place."""

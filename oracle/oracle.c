@@ -561,6 +561,207 @@ orc_mul_mat(int type, const void *w, int64_t M, int64_t K, const float *x, int64
 	return bad ? -1 : 0;
 }
 
+/* ---- ggml's CPU arithmetic for quantized weights ---------------------------
+ * [ggml] mul_mat on the CPU backend (what graph:mul_mat, src/lgml.c:1811-1839,
+ * runs there) first converts each X row to the weight type's vec_dot_type and
+ * then takes integer dot products block by block:
+ *   Q4_K, Q6_K -> Q8_K: 256-value blocks {f32 d; int8 q[256]; int16 bsums[16]}
+ *                 (quantize_row_q8_K_ref): amax = largest |x| (its first
+ *                 occurrence gives the signed max), iscale = -127 / max,
+ *                 q = min(127, nearest(iscale * x)) (round half to even),
+ *                 bsums = sums of 16 q, d = 1 / iscale; an all-zero block
+ *                 has d = 0 and q = 0.
+ *   Q8_0       -> Q8_0: 32-value blocks {f16 d; int8 q[32]}
+ *                 (quantize_row_q8_0_ref): d = amax / 127, id = d ? 1/d : 0,
+ *                 q = roundf(x * id), d stored as f16.
+ * The block dots (ggml_vec_dot_q4_K_q8_K, _q6_K_q8_K, _q8_0_q8_0):
+ *   Q4_K: d_w d_x * sum_g sc_g sum(q x8) - dmin_w d_x * sum_g m_g (bsum_2g + bsum_2g+1)
+ *   Q6_K: d_w d_x * sum_j sc_j sum_16 ((u - 32) x8)
+ *   Q8_0: f16(d_w) f16(d_x) * sum(q_w q_x)
+ * Integer parts are exact (int64 here); the scale products are f32 as in
+ * ggml, and the blocks add in f64. ggml's SIMD variants add the per-block
+ * f32 terms in other orders, so this matches them to f32 rounding, not bit
+ * for bit; parity against ggml itself is unpinned (no fixture holds its
+ * quantized-weight outputs). */
+
+/* nearest(v) = round half to even, as ggml's nearest_int (|v| < 2^22). */
+static int
+nearest_even(float v)
+{
+	return (int)lrintf(v);
+}
+
+void
+orc_quantize_q8_K(const float *x, int64_t K, int8_t *q, float *d, int16_t *bsums)
+{
+	for (int64_t b = 0; b < K / QK_K; b++) {
+		const float *xb = x + b * QK_K;
+		int8_t *qb = q + b * QK_K;
+		float amax = 0, max = 0;
+		for (int j = 0; j < QK_K; j++) {
+			float ax = fabsf(xb[j]);
+			if (ax > amax) {
+				amax = ax;
+				max = xb[j];
+			}
+		}
+		if (amax == 0) {
+			d[b] = 0;
+			memset(qb, 0, QK_K);
+			for (int j = 0; j < 16; j++)
+				bsums[b * 16 + j] = 0;
+			continue;
+		}
+		const float iscale = -127.0f / max;
+		for (int j = 0; j < QK_K; j++) {
+			int v = nearest_even(iscale * xb[j]);
+			qb[j] = (int8_t)(v < 127 ? v : 127);
+		}
+		for (int j = 0; j < 16; j++) {
+			int s = 0;
+			for (int l = 0; l < 16; l++)
+				s += qb[16 * j + l];
+			bsums[b * 16 + j] = (int16_t)s;
+		}
+		d[b] = 1.0f / iscale;
+	}
+}
+
+void
+orc_quantize_q8_0_act(const float *x, int64_t K, int8_t *q, uint16_t *d)
+{
+	for (int64_t b = 0; b < K / 32; b++) {
+		const float *xb = x + b * 32;
+		float amax = 0;
+		for (int j = 0; j < 32; j++)
+			amax = fmaxf(amax, fabsf(xb[j]));
+		const float dd = amax / 127.0f;
+		const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+		d[b] = orc_f32_to_f16(dd);
+		for (int j = 0; j < 32; j++)
+			q[b * 32 + j] = (int8_t)roundf(xb[j] * id);
+	}
+}
+
+/* One X row quantized for weight `type`. */
+typedef struct {
+	int8_t *q;
+	float *d;       /* Q8_K: K/256 d; Q8_0: K/32 f16 d as f32 */
+	int16_t *bsums; /* Q8_K: K/16 */
+} xq_row;
+
+static void
+xq_quantize(int type, const float *x, int64_t K, xq_row *r)
+{
+	if (type == ORC_Q8_0) {
+		uint16_t *h = malloc(sizeof(uint16_t) * (size_t)(K / 32));
+		orc_quantize_q8_0_act(x, K, r->q, h);
+		for (int64_t b = 0; b < K / 32; b++)
+			r->d[b] = orc_f16_to_f32(h[b]);
+		free(h);
+	} else {
+		orc_quantize_q8_K(x, K, r->q, r->d, r->bsums);
+	}
+}
+
+/* sum over K of one weight row (raw blocks) with one quantized X row. */
+static double
+dot_q8(int type, const uint8_t *w, int64_t K, const xq_row *x)
+{
+	double acc = 0;
+
+	if (type == ORC_Q8_0) {
+		for (int64_t b = 0; b < K / 32; b++) {
+			const uint8_t *blk = w + b * Q8_0_BYTES;
+			const int8_t *qw = (const int8_t *)(blk + 2), *qx = x->q + b * 32;
+			int64_t s = 0;
+			for (int l = 0; l < 32; l++)
+				s += (int64_t)qw[l] * qx[l];
+			const float dd = orc_f16_to_f32(rd16(blk)) * x->d[b];
+			acc += (double)dd * (double)s;
+		}
+		return acc;
+	}
+	for (int64_t b = 0; b < K / QK_K; b++) {
+		const int8_t *qx = x->q + b * QK_K;
+		if (type == ORC_Q4_K) {
+			const uint8_t *blk = w + b * Q4K_BYTES, *qs = blk + 16;
+			int64_t I = 0, Mn = 0;
+			for (int g = 0; g < 8; g++) {
+				int sc, mn;
+				q4k_scale_min(g, blk + 4, &sc, &mn);
+				const uint8_t *qq = qs + 32 * (g / 2);
+				int64_t s = 0;
+				for (int l = 0; l < 32; l++) {
+					int qv = (g & 1) ? (qq[l] >> 4) : (qq[l] & 0xF);
+					s += (int64_t)qv * qx[32 * g + l];
+				}
+				I += sc * s;
+				Mn += (int64_t)mn * (x->bsums[b * 16 + 2 * g] + x->bsums[b * 16 + 2 * g + 1]);
+			}
+			const float d = orc_f16_to_f32(rd16(blk)) * x->d[b];
+			const float dm = orc_f16_to_f32(rd16(blk + 2)) * x->d[b];
+			acc += (double)d * (double)I - (double)dm * (double)Mn;
+		} else { /* Q6_K */
+			const uint8_t *blk = w + b * Q6K_BYTES, *ql = blk, *qh = blk + 128;
+			const int8_t *sc = (const int8_t *)(blk + 192);
+			int64_t I = 0;
+			for (int j = 0; j < 16; j++) {
+				int64_t s = 0;
+				for (int l = 0; l < 16; l++) {
+					int v = 16 * j + l, h = v / 128, r = v % 128, t = r / 32, ll = r % 32;
+					int lo = ql[64 * h + ll + 32 * (t & 1)];
+					lo = t < 2 ? (lo & 0xF) : (lo >> 4);
+					int hb = (qh[32 * h + ll] >> (2 * t)) & 3;
+					s += (int64_t)((lo | (hb << 4)) - 32) * qx[v];
+				}
+				I += sc[j] * s;
+			}
+			const float d = orc_f16_to_f32(rd16(blk + 208)) * x->d[b];
+			acc += (double)d * (double)I;
+		}
+	}
+	return acc;
+}
+
+int
+orc_mul_mat_q8(int type, const void *w, int64_t M, int64_t K, const float *x, int64_t N,
+    float *y, int n_threads)
+{
+	int64_t rs = orc_row_size(type, K);
+	int64_t bs = type == ORC_Q8_0 ? 32 : QK_K;
+
+	if (type == ORC_F32)
+		return orc_mul_mat(type, w, M, K, x, N, y, n_threads);
+	if (rs <= 0 || (type != ORC_Q4_K && type != ORC_Q6_K && type != ORC_Q8_0) || K % bs)
+		return -1;
+	int8_t *q = malloc((size_t)(N * K + 1));
+	float *d = malloc(sizeof(float) * (size_t)(N * (K / bs) + 1));
+	int16_t *bsum = malloc(sizeof(int16_t) * (size_t)(N * (K / 16) + 1));
+	if (!q || !d || !bsum) {
+		free(q);
+		free(d);
+		free(bsum);
+		return -1;
+	}
+	for (int64_t n = 0; n < N; n++) {
+		xq_row r = {q + n * K, d + n * (K / bs), bsum + n * (K / 16)};
+		xq_quantize(type, x + n * K, K, &r);
+	}
+#pragma omp parallel for schedule(static) num_threads(nthreads(n_threads))
+	for (int64_t m = 0; m < M; m++) {
+		const uint8_t *wr = (const uint8_t *)w + m * rs;
+		for (int64_t n = 0; n < N; n++) {
+			xq_row r = {q + n * K, d + n * (K / bs), bsum + n * (K / 16)};
+			y[n * M + m] = (float)dot_q8(type, wr, K, &r);
+		}
+	}
+	free(q);
+	free(d);
+	free(bsum);
+	return 0;
+}
+
 /* ggml_rms_norm [ggml] via graph:rms_norm (src/lgml.c:1633): sum of
  * squares in f64, mean rounded to f32, scale = 1/sqrtf(mean + eps). */
 static void
@@ -895,10 +1096,10 @@ orc_moe_route(const float *logits, int64_t n, int n_expert, int n_used, int gati
 
 /* The picks of each expert gathered into one orc_mul_mat call, so each
  * expert row is dequantized once per call. */
-int
-orc_mul_mat_id(int type, const void *w, int64_t n_expert, int64_t M, int64_t K,
+static int
+mul_mat_id_mode(int type, const void *w, int64_t n_expert, int64_t M, int64_t K,
     const float *x, int64_t U, const int32_t *ids, int64_t T, int n_used, float *y,
-    int n_threads)
+    int n_threads, int act)
 {
 	int64_t rs = orc_row_size(type, K), P = T * n_used;
 	int rc = 0;
@@ -926,7 +1127,8 @@ orc_mul_mat_id(int type, const void *w, int64_t n_expert, int64_t M, int64_t K,
 		}
 		if (!c)
 			continue;
-		if (orc_mul_mat(type, (const uint8_t *)w + e * M * rs, M, K, xg, c, yg, n_threads)) {
+		if ((act ? orc_mul_mat_q8 : orc_mul_mat)(type, (const uint8_t *)w + e * M * rs, M, K,
+		    xg, c, yg, n_threads)) {
 			rc = -1;
 			goto done;
 		}
@@ -938,6 +1140,22 @@ done:
 	free(yg);
 	free(which);
 	return rc;
+}
+
+int
+orc_mul_mat_id(int type, const void *w, int64_t n_expert, int64_t M, int64_t K,
+    const float *x, int64_t U, const int32_t *ids, int64_t T, int n_used, float *y,
+    int n_threads)
+{
+	return mul_mat_id_mode(type, w, n_expert, M, K, x, U, ids, T, n_used, y, n_threads, 0);
+}
+
+int
+orc_mul_mat_id_q8(int type, const void *w, int64_t n_expert, int64_t M, int64_t K,
+    const float *x, int64_t U, const int32_t *ids, int64_t T, int n_used, float *y,
+    int n_threads)
+{
+	return mul_mat_id_mode(type, w, n_expert, M, K, x, U, ids, T, n_used, y, n_threads, 1);
 }
 
 int32_t
@@ -963,10 +1181,24 @@ embed_rows(const orc_tensor *t, int64_t E, const int32_t *ids, int64_t N, float 
 		orc_dequantize_row(t->type, (const uint8_t *)t->data + ids[i] * rs, x + i * E, E);
 }
 
+/* A weight product of the forward: with act_quant set, a quantized weight
+ * takes ggml's CPU arithmetic (X in the weight's vec_dot_type, integer
+ * block dots; orc_mul_mat_q8), f32 weights stay exact either way. */
 static int
-mm(const orc_tensor *w, int64_t M, int64_t K, const float *x, int64_t N, float *y, int nt)
+mm(const orc_model *m, const orc_tensor *w, int64_t M, int64_t K, const float *x, int64_t N,
+    float *y, int nt)
 {
+	if (m->act_quant && w->type != ORC_F32)
+		return orc_mul_mat_q8(w->type, w->data, M, K, x, N, y, nt);
 	return orc_mul_mat(w->type, w->data, M, K, x, N, y, nt);
+}
+
+static int
+mm_id(const orc_model *m, int type, const void *w, int64_t NE, int64_t M, int64_t K, const float *x, int64_t U,
+    const int32_t *ids, int64_t T, int n_used, float *y, int nt)
+{
+	return mul_mat_id_mode(type, w, NE, M, K, x, U, ids, T, n_used, y, nt,
+	    m->act_quant && type != ORC_F32);
 }
 
 /* The routed-expert FFN (transformer.lua:2054-2068 with M.moe :1989-2027,
@@ -987,18 +1219,17 @@ moe_ffn(const orc_model *m, const orc_layer *L, const float *h, int64_t N, float
 
 	if (!lg || !ids || !w || !g || !u || !dn)
 		goto done;
-	if (mm(&L->gate_inp, NE, E, h, N, lg, nt) ||
+	if (mm(m, &L->gate_inp, NE, E, h, N, lg, nt) ||
 	    orc_moe_route(lg, N, (int)NE, (int)K, m->gating, m->norm_topk, m->expert_scale, ids, w) ||
-	    orc_mul_mat_id(L->gate_exps.type, L->gate_exps.data, NE, F, E, h, 1, ids, N, (int)K, g,
-	    nt) ||
-	    orc_mul_mat_id(L->up_exps.type, L->up_exps.data, NE, F, E, h, 1, ids, N, (int)K, u, nt))
+	    mm_id(m, L->gate_exps.type, L->gate_exps.data, NE, F, E, h, 1, ids, N, (int)K, g, nt) ||
+	    mm_id(m, L->up_exps.type, L->up_exps.data, NE, F, E, h, 1, ids, N, (int)K, u, nt))
 		goto done;
 	/* swiglu_split: silu(gate) * up */
 	for (int64_t i = 0; i < P * F; i++) {
 		double gv = g[i];
 		g[i] = (float)(gv / (1.0 + exp(-gv)) * (double)u[i]);
 	}
-	if (orc_mul_mat_id(L->down_exps.type, L->down_exps.data, NE, E, F, g, K, ids, N, (int)K, dn,
+	if (mm_id(m, L->down_exps.type, L->down_exps.data, NE, E, F, g, K, ids, N, (int)K, dn,
 	    nt))
 		goto done;
 	/* mul by the weights, then the picks added in order, then x */
@@ -1132,12 +1363,12 @@ orc_forward(const orc_model *m, uint16_t *const *kpool, uint16_t *const *vpool,
 		}
 		for (int64_t t = 0; t < N; t++)
 			rms_norm_row(x + t * E, cur + t * E, E, m->eps, (const float *)L->attn_norm.data);
-		if (mm(&L->wq, H * D, E, cur, N, q, nt) || mm(&L->wk, Hkv * D, E, cur, N, k, nt)) {
+		if (mm(m, &L->wq, H * D, E, cur, N, q, nt) || mm(m, &L->wk, Hkv * D, E, cur, N, k, nt)) {
 			rc = -3;
 			goto done;
 		}
 		if (L->wv.data) {
-			if (mm(&L->wv, Hkv * D, E, cur, N, v, nt)) {
+			if (mm(m, &L->wv, Hkv * D, E, cur, N, v, nt)) {
 				rc = -3;
 				goto done;
 			}
@@ -1168,7 +1399,7 @@ orc_forward(const orc_model *m, uint16_t *const *kpool, uint16_t *const *vpool,
 			rc = -4;
 			goto done;
 		}
-		if (mm(&L->wo, E, H * D, o, N, tmp, nt)) {
+		if (mm(m, &L->wo, E, H * D, o, N, tmp, nt)) {
 			rc = -3;
 			goto done;
 		}
@@ -1186,7 +1417,7 @@ orc_forward(const orc_model *m, uint16_t *const *kpool, uint16_t *const *vpool,
 				goto done;
 			}
 		} else {
-			if (mm(&L->gate, F, E, cur, N, g, nt) || mm(&L->up, F, E, cur, N, u, nt)) {
+			if (mm(m, &L->gate, F, E, cur, N, g, nt) || mm(m, &L->up, F, E, cur, N, u, nt)) {
 				rc = -3;
 				goto done;
 			}
@@ -1195,7 +1426,7 @@ orc_forward(const orc_model *m, uint16_t *const *kpool, uint16_t *const *vpool,
 				double a = m->gemma ? gelu(gv) : gv / (1.0 + exp(-gv));
 				g[i] = (float)(a * (double)u[i]);
 			}
-			if (mm(&L->down, E, F, g, N, tmp, nt)) {
+			if (mm(m, &L->down, E, F, g, N, tmp, nt)) {
 				rc = -3;
 				goto done;
 			}
@@ -1218,7 +1449,7 @@ orc_forward(const orc_model *m, uint16_t *const *kpool, uint16_t *const *vpool,
 		rms_norm_row(x + (int64_t)b->out_rows[r] * E, cur + (int64_t)r * E, E, m->eps,
 		    (const float *)m->output_norm.data);
 	}
-	if (mm(&m->output, V, E, cur, b->n_out, logits, nt)) {
+	if (mm(m, &m->output, V, E, cur, b->n_out, logits, nt)) {
 		rc = -3;
 		goto done;
 	}

@@ -7,8 +7,9 @@
  * only as the checker or the CPU baseline, never as the thing measured.
  *
  * Semantics: fp32 values, f64 reductions, f16 (round to nearest even)
- * KV storage, closed-form Q4_K / Q6_K / Q8_0 dequantization, no
- * activation quantization. Each function cites the reference file:line
+ * KV storage, closed-form Q4_K / Q6_K / Q8_0 dequantization; activations
+ * exact, or (orc_model.act_quant, orc_mul_mat_q8) quantized per block as
+ * ggml's CPU backend does for quantized weights. Each function cites the reference file:line
  * whose behaviour it restates (paths under the lgml tree).
  */
 #ifndef LGML_ORACLE_H
@@ -103,6 +104,10 @@ typedef struct {
 	 * (0 = none); n_swa: the sliding window of swa layers. */
 	int gemma, n_swa;
 	float embd_scale, softcap;
+	/* 0: exact products (f32 activations, f64 sums over dequantized
+	 * weights); 1: ggml's CPU arithmetic for quantized weights (X quantized
+	 * to Q8_K / Q8_0 per block, integer block dots; orc_mul_mat_q8). */
+	int act_quant;
 } orc_model;
 
 /* One ubatch over a paged pool. Sequence s owns tokens
@@ -166,6 +171,19 @@ int orc_set_rows_f16(uint16_t *dst, int64_t dst_rows, int64_t row, const float *
 int orc_mul_mat(int type, const void *w, int64_t M, int64_t K, const float *x, int64_t N,
     float *y, int n_threads);
 
+/* ggml's CPU mul_mat for a quantized weight (src/lgml.c:1811-1839 on the
+ * CPU backend [ggml]): each X row quantized to the weight type's
+ * vec_dot_type (Q8_K for Q4_K / Q6_K, Q8_0 for Q8_0), then integer dot
+ * products per block, scaled by the f32 products of the block scales, the
+ * blocks added in f64. f32 weights: orc_mul_mat. */
+int orc_mul_mat_q8(int type, const void *w, int64_t M, int64_t K, const float *x, int64_t N,
+    float *y, int n_threads);
+/* quantize_row_q8_K_ref [ggml]: per 256 values d (f32), q (int8), 16 sums
+ * of 16 q. K a multiple of 256. */
+void orc_quantize_q8_K(const float *x, int64_t K, int8_t *q, float *d, int16_t *bsums);
+/* quantize_row_q8_0_ref [ggml]: per 32 values d (f16 bits), q (int8). */
+void orc_quantize_q8_0_act(const float *x, int64_t K, int8_t *q, uint16_t *d);
+
 /* The router of M.moe (transformer.lua:1998-2008): probs = soft_max (or
  * sigmoid) of each logits row (n_expert values, f64 sums); ids = the
  * n_used largest, largest first (argsort_top_k, src/ops_nn.c:266-286),
@@ -180,6 +198,10 @@ int orc_moe_route(const float *logits, int64_t n, int n_expert, int n_used, int 
  * w[ids[t][j]] times x[t][j % U] (x is (T, U, K)). f64 accumulation.
  * Returns -1 on an id outside [0, n_expert). */
 int orc_mul_mat_id(int type, const void *w, int64_t n_expert, int64_t M, int64_t K,
+    const float *x, int64_t U, const int32_t *ids, int64_t T, int n_used, float *y,
+    int n_threads);
+/* The same with ggml's CPU arithmetic (orc_mul_mat_q8 per expert). */
+int orc_mul_mat_id_q8(int type, const void *w, int64_t n_expert, int64_t M, int64_t K,
     const float *x, int64_t U, const int32_t *ids, int64_t T, int n_used, float *y,
     int n_threads);
 

@@ -35,7 +35,7 @@ def test_exports_every_declared_symbol(hip):
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing
     assert sorted(hip.SYMBOLS) == names
-    assert L.lgmlh_abi_version() == 6
+    assert L.lgmlh_abi_version() == 7
 
 
 def test_struct_layouts_match_the_header(hip, tmp_path):
