@@ -117,7 +117,9 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
                   int max_blocks, int ring, int window, float *__restrict__ out,
                   f16 *__restrict__ planes, int64_t npad, float *__restrict__ part,
                   const int32_t *__restrict__ order, int n_order) {
-  constexpr int KS = D / 32;   // MFMA k-steps over D
+  // MFMA k-steps over D; a head of 16 takes one step of 32 whose upper
+  // half is zero in K and Q (the lanes of quads 2 and 3 load nothing)
+  constexpr int KS = D >= 32 ? D / 32 : 1;
   constexpr int DT = D / 16;   // d tiles of the output
   __shared__ __align__(16) uint16_t plh[ROWS * P_STRIDE];  // P as f16 hi
   __shared__ __align__(16) uint16_t pll[ROWS * P_STRIDE];  // and lo
@@ -153,11 +155,14 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
   // K rows (A operand of S^T = K Q^T) and V^T columns (A operand of
   // O^T += V^T P^T) of one block, straight from the pool tiles.
   f16x8 kf[4][KS], vf[DT][2];
+  const bool kpart = D >= 32 || quad < 2;  // this lane's k range lies in the head
   auto load_k = [&](const uint16_t *kt) {
 #pragma unroll
     for (int ct = 0; ct < 4; ct++)
 #pragma unroll
-      for (int ks = 0; ks < KS; ks++) kf[ct][ks] = load_f16x8(kt + (ct * 16 + row) * D + ks * 32 + quad * 8);
+      for (int ks = 0; ks < KS; ks++)
+        kf[ct][ks] = kpart ? load_f16x8(kt + (ct * 16 + row) * D + ks * 32 + quad * 8)
+                           : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
   };
   auto load_v = [&](const uint16_t *vt) {
 #pragma unroll
@@ -176,8 +181,8 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
     f32x4 qa[2 * KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
-      qa[2 * ks] = *(const f32x4 *)(qr + ks * 32 + quad * 8);
-      qa[2 * ks + 1] = *(const f32x4 *)(qr + ks * 32 + quad * 8 + 4);
+      qa[2 * ks] = kpart ? *(const f32x4 *)(qr + ks * 32 + quad * 8) : f32x4{0, 0, 0, 0};
+      qa[2 * ks + 1] = kpart ? *(const f32x4 *)(qr + ks * 32 + quad * 8 + 4) : f32x4{0, 0, 0, 0};
     }
     // The first block's tiles go out before the Q pieces are converted,
     // so the two loads overlap. Unconditional, so that the conversion waits
@@ -642,14 +647,15 @@ static void launch_attn(const float *q, int H, int Hkv, float scale_log2, const 
                        (const uint16_t *)vp, ub->items, ub->seq_off, ub->seq_npast, ub->block_tab,
                        ub->max_blocks, ub->ring, ub->window, out, planes, npad, part, ub->order,
                        ub->n_single);
-  // heads of 256 run the shared runs' items with the per-item kernel too
-  else if (const int n1 = D <= 128 ? ub->n_single : ub->n_items; n1 > 0)
+  // heads of 256, and of 32 or less, run the shared runs' items with the
+  // per-item kernel too
+  else if (const int n1 = D <= 128 && D >= 64 ? ub->n_single : ub->n_items; n1 > 0)
     hipLaunchKernelGGL((paged_attn_kernel<D, false>), dim3((uint32_t)n1 * Hkv), dim3(64), 0, st,
                        q, H, Hkv, scale_log2, (const uint16_t *)kp, (const uint16_t *)vp,
                        ub->items, ub->seq_off, ub->seq_npast, ub->block_tab, ub->max_blocks, 0,
                        0, out, planes, npad, part, ub->order, ub->n_single);
   if (ub->ring == 0 && ub->n_shared > 0) {
-    if constexpr (D <= 128)
+    if constexpr (D <= 128 && D >= 64)
       hipLaunchKernelGGL(paged_attn_shared_kernel<D>, dim3(ub->n_shared, Hkv),
                          dim3(64 * SHARED_WAVES), 0, st, q, H, Hkv, scale_log2,
                          (const uint16_t *)kp, (const uint16_t *)vp, ub->items, ub->shared,
@@ -688,14 +694,20 @@ int paged_attention_dev(const float *q, int n_head, int n_head_kv, int head_dim,
     set_error("paged_attention: %d items x %d KV heads in one launch", ub->n_items, n_head_kv);
     return LGMLH_EINVAL;
   }
+  if (planes && head_dim < 32) {
+    set_error("paged_attention: heads of %d write f32 rows only", head_dim);
+    return LGMLH_EINVAL;
+  }
   float sl = scale * LOG2E;
   float *part = (float *)workspace;
   switch (head_dim) {
+    case 16: launch_attn<16>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, planes, npad, part, st); break;
+    case 32: launch_attn<32>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, planes, npad, part, st); break;
     case 64: launch_attn<64>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, planes, npad, part, st); break;
     case 128: launch_attn<128>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, planes, npad, part, st); break;
     case 256: launch_attn<256>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, planes, npad, part, st); break;
     default:
-      set_error("paged_attention: head_dim %d not supported (64, 128, 256)", head_dim);
+      set_error("paged_attention: head_dim %d not supported (16, 32, 64, 128, 256)", head_dim);
       return LGMLH_EINVAL;
   }
   return hip_check(hipGetLastError(), "paged_attention");

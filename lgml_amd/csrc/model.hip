@@ -366,7 +366,7 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
     // a quantized output product takes its X as split planes, written by
     // the attention (and merge) kernels themselves; ggml's Q8 blocks are
     // made from the f32 rows by a kernel of their own
-    const bool oq = isq(L.wo_type), o_split = oq && xfo(L.wo_type) == XF_SPLIT;
+    const bool oq = isq(L.wo_type), o_split = oq && xfo(L.wo_type) == XF_SPLIT && z.D >= 32;
     {
       Span sp(trace, LGMLH_TRACE_ATTN, st);
       LGMLH_TRY(paged_attention_dev(q, (int)z.H, (int)z.Hkv, (int)z.D, scale, L.kpool, L.vpool,

@@ -46,9 +46,19 @@ again, attaches what is still cached of its tokens (pool or RAM store)
 and runs the rest. The reference's E:pool_pressure (:1122-1140) first
 takes the cells of idle slots; here a request that ends gives its blocks
 back at once (keyed ones stay cached and are evicted first), so no idle
-slot holds cells. Paged-pool models only: a sliding-window ring cannot
-be rebuilt from cached blocks (the reference checkpoints it), so there a
-full pool ends the request.
+slot holds cells. A sliding-window ring cannot be rebuilt from cached
+blocks, so a request of a model with rings checkpoints its slot's rings to
+pinned host memory when it lets go (E:checkpoint_slot, :2103-2116) and
+restores them into its new slot when it attaches exactly the tokens it had;
+otherwise it runs again from the start.
+
+The pool can start small (DeviceModel kv_initial) and grow: a reserve that
+finds no free block doubles the pool tensors up to their ceiling before it
+evicts (new_block's grow branch, transformer.lua:934-958, pool_grow
+:831-908).
+
+With prefix_cache, a request that ends publishes the keys of its prompt and
+reply blocks, so a follow-up turn that repeats them attaches them.
 """
 import ctypes as C
 
@@ -78,9 +88,12 @@ class PoolSeqs:
 
     def __init__(self, model, pressure=None):
         self.model = model
-        self.alloc = kvpool.Pool(model.pool_blocks, BLOCK)
+        # blocks up to the model's ceiling, usable up to its present size
+        self.alloc = kvpool.Pool(getattr(model, "max_blocks", model.pool_blocks), BLOCK,
+                                 cap=model.pool_blocks)
         self.pressure = pressure
         self.on_evict = None  # on_evict(block, key, prio), kvpool.lua:149-152
+        self.grows = 0
 
     def evict(self):
         """P:evict (kvpool.lua:139-160), telling on_evict about a keyed block
@@ -94,12 +107,18 @@ class PoolSeqs:
         return self.alloc.evict()
 
     def new_block(self, c, min_):
-        """transformer.lua:934-958 (the pool is allocated whole up front, so
-        the grow branch never runs): a free block, else a cached one, else
-        one that pressure frees for c."""
+        """new_block (transformer.lua:934-958): a free block, else a new one
+        when the pool can grow (the model's pool tensors doubled, up to its
+        ceiling), else a cached one, else one that pressure frees for c."""
         b = self.alloc.take(min_)
         if b is not None:
             return b
+        m = self.model
+        if getattr(m, "max_cells", m.n_cells) > m.n_cells:
+            m.grow_pool()
+            self.alloc.set_cap(m.pool_blocks)
+            self.grows += 1
+            return self.alloc.take(min_)
         b = self.evict()
         if b is None and self.pressure is not None:
             self.pressure(self, c)
@@ -252,6 +271,7 @@ class Request:
         self.started = 0      # submit order (E:victim: the least recently started)
         self.waits = 0        # times it let its cells go
         self.wait_mark = 0    # the engine's count of ended requests when it began to wait
+        self.ring_ckpt = None  # (position, pinned bytes) of its rings while it waits
         # run-ahead engines: sampled tokens of passes not yet read back, the
         # (pass, row) holding the latest one on the device, and whether the
         # request takes part in no further pass
@@ -464,6 +484,17 @@ class Engine:
                 self.infos[k] = (parent, i, list(toks))
 
     def finish(self, req):
+        """A request ends: with prefix_cache, its cells keep the keys of its
+        tokens so far (the prompt and the reply but its last sample: the
+        reference keeps them in the idle slot and publishes its tail when
+        it reuses the slot, engine.lua:1042-1052, E:publish_tail
+        :1906-1918), so a follow-up prompt that repeats them attaches them
+        (E:pick_slot / E:reuse, :1704-1819); then its blocks go back (the
+        keyed ones stay cached until evicted)."""
+        if self.prefix_cache and req.seq is not None and not self.ring_blocks:
+            hist, _ = req.history()
+            if req.seq.n_past == len(hist):
+                self.publish_tail(req, hist)
         self.seqs.free(req.seq)
         self.free_slots.append(req.slot)
         req.done = True
@@ -493,7 +524,7 @@ class Engine:
             v.preempt = True
             return False
         running = sum(1 for q in self.active if not q.preempt and not q.finishing)
-        if running < 2 or self.ring_blocks:
+        if running < 2:
             req.err = str(err)
             return True
         req.preempt = True
@@ -511,12 +542,52 @@ class Engine:
             alloc.publish_part(c.blocks[i], c.keys[i - 1] if i else ROOT_KEY, i + 1,
                                tokens[i * BLOCK:n], c.prio)
 
+    def ring_bytes(self, slot):
+        """The bytes of slot's ring blocks in every sliding layer's K and V
+        ring pools (device uint8 views, in layer order)."""
+        m, R = self.model, self.ring_blocks
+        bb = hip.lib().lgmlh_kv_block_bytes(m.hp["n_head_kv"], m.hp["head_dim"])
+        views = []
+        for il, swa in enumerate(m.swa):
+            if swa:
+                for pool in (m.kpools[il], m.vpools[il]):
+                    views.append(pool[slot * R * bb:(slot + 1) * R * bb])
+        return views
+
+    def checkpoint_ring(self, req):
+        """E:checkpoint_slot (engine.lua:2103-2116, M:snapshot's sliding
+        rings, transformer.lua:1450-1471): the slot's rings, the part of a
+        sequence that cannot be rebuilt from cached blocks, to pinned host
+        memory at the sequence's position."""
+        views = self.ring_bytes(req.slot)
+        buf = torch.empty(sum(v.numel() for v in views), dtype=torch.uint8, pin_memory=True)
+        o = 0
+        for v in views:
+            buf[o:o + v.numel()].copy_(v, non_blocking=True)
+            o += v.numel()
+        torch.cuda.current_stream().synchronize()
+        req.ring_ckpt = (req.seq.n_past, buf)
+
+    def restore_ring(self, req):
+        """M:restore of the rings (transformer.lua:1473-1511) into the new
+        slot's ring blocks: the checkpoint holds the rings at its position,
+        so it serves only a sequence that attached exactly that many tokens."""
+        _, buf = req.ring_ckpt
+        o = 0
+        for v in self.ring_bytes(req.slot):
+            v.copy_(buf[o:o + v.numel()], non_blocking=True)
+            o += v.numel()
+        torch.cuda.current_stream().synchronize()
+
     def let_go(self, req):
         """E:preempt (engine.lua:1193-1243), with no pass of req in flight: it
-        publishes its blocks' keys, lets its cells and slot go and waits;
-        its feed becomes its tokens so far and the rest."""
+        publishes its blocks' keys, checkpoints its rings (a model with
+        sliding layers), lets its cells and slot go and waits; its feed
+        becomes its tokens so far and the rest."""
         hist, rest = req.history()
         assert req.seq.n_past == len(hist), (req.seq.n_past, len(hist))
+        if self.ring_blocks:
+            self.checkpoint_ring(req)
         self.publish_tail(req, hist)
         self.seqs.free(req.seq)
         self.free_slots.append(req.slot)
@@ -551,6 +622,17 @@ class Engine:
             self.active.append(req)
             req.fed = self.attach(req)
             req.seq.n_past = req.fed
+            ck = getattr(req, "ring_ckpt", None)
+            if ck is not None:
+                if req.fed == ck[0]:
+                    self.restore_ring(req)
+                else:
+                    # the rings are at the checkpoint's position: without all
+                    # of its tokens the sequence runs again from the start
+                    self.seqs.free(req.seq)
+                    req.seq = Seq(self.seqs, req.prio)
+                    req.fed = 0
+                req.ring_ckpt = None
 
     def step(self):
         """One pass over every active request; returns the requests that got

@@ -205,20 +205,25 @@ class DeviceModel:
     """A llama / qwen3 / qwen3moe / gemma model on the device with its paged
     KV pool (and, for sliding-window layers, ring pools)."""
 
-    def __init__(self, hp, w, n_cells, ring_cells=0):
+    def __init__(self, hp, w, n_cells, ring_cells=0, kv_initial=0):
         """w: a weights dict of numpy arrays, or a callable source
         w(name, layer, rows, cols) -> (device tensor, type, rows) such as
         generated_weights() (gemma layers then follow workload.gemma_layer).
         ring_cells: cells of each sliding layer's ring pools (a multiple of
-        64; the sequences' ring tables index its blocks)."""
+        64; the sequences' ring tables index its blocks). kv_initial: the
+        paged pool starts at this many cells and grows (grow_pool) up to
+        n_cells, as the reference's pool starts at KV_INITIAL and doubles
+        (engine.lua:49, transformer.lua:831-908); 0: n_cells from the start."""
         from . import workload
         L = hip.lib()
         self.hp = hp
         E, H, Hkv, D = hp["n_embd"], hp["n_head"], hp["n_head_kv"], hp["head_dim"]
         F, V = hp["n_ff"], hp["n_vocab"]
-        self.n_cells = int(n_cells)
+        self.max_cells = int(n_cells)
+        self.n_cells = int(kv_initial) if kv_initial else self.max_cells
         self.ring_cells = int(ring_cells)
         assert self.n_cells % 64 == 0 and self.ring_cells % 64 == 0
+        assert self.max_cells % 64 == 0 and self.n_cells <= self.max_cells
         self._keep = []
         gen = callable(w)
         gemma = bool(hp.get("gemma"))
@@ -316,8 +321,9 @@ class DeviceModel:
                 Ly.wgu, Ly.wgu_type = keep(t).data_ptr(), ty
                 t, ty, _ = repack_concat([mat("down", il, E, F)], F)
                 Ly.wdown, Ly.wdown_type = keep(t).data_ptr(), ty
-            kp = keep(_zeros(kvb_ring if Ly.swa else kvb))
-            vp = keep(_zeros(kvb_ring if Ly.swa else kvb))
+            # the pool tensors live in kpools / vpools (grow_pool replaces them)
+            kp = _zeros(kvb_ring if Ly.swa else kvb)
+            vp = _zeros(kvb_ring if Ly.swa else kvb)
             self.kpools.append(kp)
             self.vpools.append(vp)
             Ly.kpool, Ly.vpool = kp.data_ptr(), vp.data_ptr()
@@ -376,6 +382,43 @@ class DeviceModel:
     @property
     def pool_blocks(self):
         return self.n_cells // 64
+
+    @property
+    def max_blocks(self):
+        return self.max_cells // 64
+
+    def grow_pool(self, cells=None):
+        """pool_grow (transformer.lua:831-908): the paged pool tensors of
+        every layer to `cells` cells (default twice the present, at most
+        max_cells); the new tensors hold the old cells (lgmlh_kv_grow) and
+        zeros after them. Returns the new cell count (unchanged at the
+        ceiling). Sliding layers' rings keep their size."""
+        cells = min(self.max_cells, cells or 2 * self.n_cells)
+        if cells <= self.n_cells:
+            return self.n_cells
+        L, hp = hip.lib(), self.hp
+        Hkv, D = hp["n_head_kv"], hp["head_dim"]
+        nb = L.lgmlh_kv_layer_bytes(cells, Hkv, D)
+        for il in range(hp["n_layer"]):
+            if self.swa[il]:
+                continue
+            for pools, attr in ((self.kpools, "kpool"), (self.vpools, "vpool")):
+                old = pools[il]
+                new = _empty(nb)
+                check(L.lgmlh_kv_grow(old.data_ptr(), self.n_cells, new.data_ptr(), cells, Hkv, D,
+                                      stream()))
+                pools[il] = new
+                setattr(self.layers[il], attr, new.data_ptr())
+        # the old tensors are freed once the copies are done
+        torch.cuda.current_stream().synchronize()
+        self.n_cells = cells
+        self.m.n_cells = cells
+        ptrs = []
+        for il in range(hp["n_layer"]):
+            if not self.swa[il]:
+                ptrs += [self.kpools[il].data_ptr(), self.vpools[il].data_ptr()]
+        self.pools_dev = torch.tensor(ptrs or [0], dtype=torch.int64, device=DEV)
+        return cells
 
     ring_blocks_per_split = 0  # the ring plans' run length (0: as blocks_per_split; 12 for heads of 256)
 

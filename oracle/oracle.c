@@ -220,6 +220,26 @@ orc_f16_to_f32(uint16_t h)
 	return f;
 }
 
+/* orc_f16_to_f32 of every f16 bit pattern, for the attention loops (the
+ * same values, read from a table). Filled once, before parallel regions. */
+static float f16_lut[65536];
+static int f16_lut_ready;
+
+static void
+f16_lut_init(void)
+{
+	if (__atomic_load_n(&f16_lut_ready, __ATOMIC_ACQUIRE))
+		return;
+#pragma omp critical(orc_f16_lut)
+	{
+		if (!f16_lut_ready) {
+			for (uint32_t i = 0; i < 65536; i++)
+				f16_lut[i] = orc_f16_to_f32((uint16_t)i);
+			__atomic_store_n(&f16_lut_ready, 1, __ATOMIC_RELEASE);
+		}
+	}
+}
+
 void
 orc_f32_to_f16_row(const float *x, uint16_t *y, int64_t n)
 {
@@ -525,12 +545,40 @@ nthreads(int n)
 	return n > 0 ? n : 1;
 }
 
+/* sum_k a[k] b[k] in f64: eight f64 lanes (k mod 8) added pairwise at the
+ * end, then the tail in order. */
+typedef double orc_v4d __attribute__((vector_size(32)));
+typedef float orc_v4f __attribute__((vector_size(16)));
+
+static double
+dot_f64(const float *a, const float *b, int64_t K)
+{
+	orc_v4d s0 = {0, 0, 0, 0}, s1 = {0, 0, 0, 0};
+	int64_t k = 0;
+	for (; k + 8 <= K; k += 8) {
+		orc_v4f a0, b0, a1, b1;
+		memcpy(&a0, a + k, 16);
+		memcpy(&b0, b + k, 16);
+		memcpy(&a1, a + k + 4, 16);
+		memcpy(&b1, b + k + 4, 16);
+		s0 += __builtin_convertvector(a0, orc_v4d) * __builtin_convertvector(b0, orc_v4d);
+		s1 += __builtin_convertvector(a1, orc_v4d) * __builtin_convertvector(b1, orc_v4d);
+	}
+	double r = ((s0[0] + s1[0]) + (s0[1] + s1[1])) + ((s0[2] + s1[2]) + (s0[3] + s1[3]));
+	for (; k < K; k++)
+		r += (double)a[k] * (double)b[k];
+	return r;
+}
+
 /* ggml_mul_mat via graph:mul_mat (src/lgml.c:1811-1839): y[n][m] =
  * sum_k w[m][k] * x[n][k]. Each weight row is dequantized once. */
 int
 orc_mul_mat(int type, const void *w, int64_t M, int64_t K, const float *x, int64_t N,
     float *y, int n_threads)
 {
+	/* rows in blocks of RB, dequantized together, so that each X row is
+	 * read once per block (the per-output sums are unchanged) */
+	enum { RB = 8 };
 	int64_t rs = orc_row_size(type, K);
 	int bad = 0;
 
@@ -538,25 +586,23 @@ orc_mul_mat(int type, const void *w, int64_t M, int64_t K, const float *x, int64
 		return -1;
 #pragma omp parallel num_threads(nthreads(n_threads))
 	{
-		float *row = malloc((size_t)K * sizeof(float));
-		if (!row) {
+		float *rows = malloc((size_t)K * RB * sizeof(float));
+		if (!rows) {
 #pragma omp atomic write
 			bad = 1;
 		}
 #pragma omp for schedule(static)
-		for (int64_t m = 0; m < M; m++) {
-			if (!row)
+		for (int64_t m0 = 0; m0 < M; m0 += RB) {
+			if (!rows)
 				continue;
-			orc_dequantize_row(type, (const uint8_t *)w + m * rs, row, K);
-			for (int64_t n = 0; n < N; n++) {
-				const float *xn = x + n * K;
-				double acc = 0;
-				for (int64_t k = 0; k < K; k++)
-					acc += (double)row[k] * (double)xn[k];
-				y[n * M + m] = (float)acc;
-			}
+			int64_t nr = M - m0 < RB ? M - m0 : RB;
+			for (int64_t r = 0; r < nr; r++)
+				orc_dequantize_row(type, (const uint8_t *)w + (m0 + r) * rs, rows + r * K, K);
+			for (int64_t n = 0; n < N; n++)
+				for (int64_t r = 0; r < nr; r++)
+					y[n * M + m0 + r] = (float)dot_f64(rows + r * K, x + n * K, K);
 		}
-		free(row);
+		free(rows);
 	}
 	return bad ? -1 : 0;
 }
@@ -880,6 +926,7 @@ attend(const float *q, const uint16_t *kpool, const uint16_t *vpool, int H, int 
 	int G = H / Hkv;
 	int bad = 0;
 
+	f16_lut_init();
 #pragma omp parallel num_threads(nthreads(n_threads))
 	{
 		int maxp = 0;
@@ -910,7 +957,7 @@ attend(const float *q, const uint16_t *kpool, const uint16_t *vpool, int H, int 
 					const uint16_t *kr = kpool + cell * row + (int64_t)kh * D;
 					double a = 0;
 					for (int d = 0; d < D; d++)
-						a += (double)qh[d] * (double)orc_f16_to_f32(kr[d]);
+						a += (double)qh[d] * (double)f16_lut[kr[d]];
 					sc[j] = a * scale;
 					if (sc[j] > mx)
 						mx = sc[j];
@@ -927,7 +974,7 @@ attend(const float *q, const uint16_t *kpool, const uint16_t *vpool, int H, int 
 					const uint16_t *vr = vpool + cell * row + (int64_t)kh * D;
 					double w = sc[j] / sum;
 					for (int d = 0; d < D; d++)
-						acc[d] += w * (double)orc_f16_to_f32(vr[d]);
+						acc[d] += w * (double)f16_lut[vr[d]];
 				}
 				float *o = out + (t * H + h) * D;
 				for (int d = 0; d < D; d++)
@@ -971,6 +1018,7 @@ orc_flash_attn(const float *q, int H, int T, int D, const uint16_t *k, const uin
 	const int G = H / Hkv;
 	int bad = 0;
 
+	f16_lut_init();
 #pragma omp parallel num_threads(nthreads(n_threads))
 	{
 		double *sc = malloc(sizeof(double) * (size_t)(n_kv + 1));
@@ -999,7 +1047,7 @@ orc_flash_attn(const float *q, int H, int T, int D, const uint16_t *k, const uin
 					const uint16_t *kr = k + (int64_t)kh * k_hs + (int64_t)j * k_rs;
 					double a = 0;
 					for (int d = 0; d < D; d++)
-						a += (double)qh[d] * (double)orc_f16_to_f32(kr[d]);
+						a += (double)qh[d] * (double)f16_lut[kr[d]];
 					a *= scale;
 					if (softcap > 0.0f)
 						a = (double)softcap * tanh(a / softcap);
@@ -1020,7 +1068,7 @@ orc_flash_attn(const float *q, int H, int T, int D, const uint16_t *k, const uin
 					const uint16_t *vr = v + (int64_t)kh * v_hs + (int64_t)j * v_rs;
 					const double w = sc[j] / sum;
 					for (int d = 0; d < D; d++)
-						acc[d] += w * (double)orc_f16_to_f32(vr[d]);
+						acc[d] += w * (double)f16_lut[vr[d]];
 				}
 				float *o = out + ((int64_t)t * H + h) * D;
 				for (int d = 0; d < D; d++)

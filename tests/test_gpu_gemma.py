@@ -90,7 +90,7 @@ RING_CASES = [
 ]
 
 
-@pytest.mark.parametrize("H,Hkv,D", [(8, 4, 256), (32, 8, 128), (4, 2, 64)])
+@pytest.mark.parametrize("H,Hkv,D", [(8, 4, 256), (32, 8, 128), (4, 2, 64), (4, 2, 16)])
 @pytest.mark.parametrize("case", range(len(RING_CASES)))
 def test_ring_attention_matches_oracle(L, H, Hkv, D, case):
     window, R, seqs = RING_CASES[case]

@@ -276,7 +276,8 @@ def gpu_attention(L, q, kpool_rows, vpool_rows, H, Hkv, D, seqs, bt, bps=0, n_ce
     return out.cpu().numpy(), plan
 
 
-@pytest.mark.parametrize("H,Hkv,D", [(32, 8, 128), (4, 2, 64), (8, 4, 256), (16, 16, 64)])
+@pytest.mark.parametrize("H,Hkv,D", [(32, 8, 128), (4, 2, 64), (8, 4, 256), (16, 16, 64),
+                                     (4, 2, 16), (8, 1, 32)])
 def test_paged_attention_parity(L, H, Hkv, D):
     seqs = [(1, 0), (1, 63), (1, 64), (1, 200), (37, 0), (1, 1500), (5, 61), (64, 130), (1, 3000)]
     q, kpool, vpool, bt = make_attn_case(H, Hkv, D, seqs, seed=H + D)
@@ -290,7 +291,8 @@ def test_paged_attention_parity(L, H, Hkv, D):
         assert e < 2e-3 and e < 1e-4, (bps, e)
 
 
-@pytest.mark.parametrize("H,Hkv,D", [(32, 8, 128), (32, 4, 128), (4, 2, 64)])
+@pytest.mark.parametrize("H,Hkv,D", [(32, 8, 128), (32, 4, 128), (4, 2, 64), (4, 2, 16),
+                                     (8, 2, 32)])
 def test_paged_attention_prompt_chunks(L, H, Hkv, D):
     """Prompt chunks run in shared sets of 8 query groups (one workgroup
     reads each K / V block once for the set, lgmlh_plan): a 512-token chunk
