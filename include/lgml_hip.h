@@ -452,6 +452,12 @@ typedef struct {
 	const float *post_attn_norm, *post_ffn_norm;
 	float out_scale, rope_base;
 	const float *rope_freqs;
+	/* This layer's head size, KV heads and rotated dimensions (0 = the
+	 * model's; n_rot 0 with head_dim set = head_dim): gemma's sliding and
+	 * global layers differ (transformer.lua:215-235). The plan a layer
+	 * attends through (the ring plan for a sliding layer) must be made for
+	 * its KV heads; its pool tensors hold rows of n_head_kv x head_dim. */
+	int head_dim, n_head_kv, n_rot;
 } lgmlh_layer;
 
 typedef struct {

@@ -65,6 +65,22 @@ struct Sizes {
 
 static bool isq(int type) { return type != LGMLH_F32; }
 
+// A layer's attention shape: its own head size, KV heads and rotated
+// dimensions where it sets them (gemma's sliding and global layers differ,
+// transformer.lua:215-235), else the model's; W = the row width of [q|k|v].
+struct LDims {
+  int D, Hkv, n_rot;
+  int64_t W;
+};
+static LDims dims_of(const lgmlh_model *m, const lgmlh_layer &L) {
+  LDims d;
+  d.D = L.head_dim > 0 ? L.head_dim : m->head_dim;
+  d.Hkv = L.n_head_kv > 0 ? L.n_head_kv : m->n_head_kv;
+  d.n_rot = L.n_rot > 0 ? L.n_rot : L.head_dim > 0 ? L.head_dim : m->n_rot;
+  d.W = (int64_t)(m->n_head + 2 * d.Hkv) * d.D;
+  return d;
+}
+
 // The V product of layer L takes its X planes apart from the q|k product's.
 static bool v_own_planes(const lgmlh_model *m, const lgmlh_layer &L) {
   return L.wv && isq(L.wv_type) && isq(L.wqkv_type) &&
@@ -82,7 +98,17 @@ static Sizes sizes_of(const lgmlh_model *m, int64_t n_tokens, int64_t n_items, i
   z.D = m->head_dim;
   z.F = m->n_ff;
   z.V = m->n_vocab;
-  z.W = (z.H + 2 * z.Hkv) * z.D;
+  // the widest layer sizes the buffers (z.D: the largest head, z.W the
+  // widest [q|k|v] row)
+  z.W = 0;
+  size_t attn_unit = 0;  // floats of an item's partial state per KV head set
+  for (int il = 0; il < m->n_layer; il++) {
+    const LDims d = dims_of(m, m->layers[il]);
+    if (d.W > z.W) z.W = d.W;
+    if (d.D > z.D) z.D = d.D;
+    const size_t u = (size_t)d.Hkv * (16 * d.D + 32);
+    if (u > attn_unit) attn_unit = u;
+  }
   z.n_out = n_out;
   size_t g = 0, gv = 0;
   auto upd = [&](int t, int64_t M, int64_t K, int64_t N) {
@@ -98,13 +124,14 @@ static Sizes sizes_of(const lgmlh_model *m, int64_t n_tokens, int64_t n_items, i
   z.tc = z.moe ? moe_tile_cols(z.P, z.NE) : 16;
   for (int il = 0; il < m->n_layer; il++) {
     const lgmlh_layer &L = m->layers[il];
+    const LDims d = dims_of(m, L);
     upd(L.wqkv_type, L.wqkv_rows, z.E, z.N);
     if (L.wv) {
       // pending beside the [q|k] partials: a region of its own
-      size_t w = partial_bytes(L.wv_type, z.W - L.wqkv_rows, z.E, z.N);
+      size_t w = partial_bytes(L.wv_type, d.W - L.wqkv_rows, z.E, z.N);
       if (w > gv) gv = w;
     }
-    upd(L.wo_type, z.E, z.H * z.D, z.N);
+    upd(L.wo_type, z.E, z.H * d.D, z.N);
     if (!L.gate_inp) {
       upd(L.wgu_type, 2 * z.F, z.E, z.N);
       upd(L.wdown_type, z.E, z.F, z.N);
@@ -119,7 +146,7 @@ static Sizes sizes_of(const lgmlh_model *m, int64_t n_tokens, int64_t n_items, i
   int64_t rmax = z.N > n_out ? z.N : n_out;
   if (z.P > rmax) rmax = z.P;  // the expert activations of the picks
   z.split_ws = split_bytes(rmax, kmax);
-  z.attn_ws = (size_t)n_items * z.Hkv * (16 * z.D + 32) * sizeof(float);
+  z.attn_ws = (size_t)n_items * attn_unit * sizeof(float);
   return z;
 }
 
@@ -213,8 +240,7 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
                              const lgmlh_ubatch *ub_ring, const int32_t *out_rows, int n_out,
                              float *logits, void *workspace, size_t ws_bytes, lgmlh_trace *trace,
                              void *stream) {
-  if (!m || !ub || !logits || !workspace || !m->layers || m->n_layer <= 0 ||
-      m->n_head_kv != ub->n_head_kv) {
+  if (!m || !ub || !logits || !workspace || !m->layers || m->n_layer <= 0) {
     set_error("forward: bad arguments");
     return LGMLH_EINVAL;
   }
@@ -222,12 +248,20 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
     set_error("forward: act %d is neither LGMLH_ACT_EXACT nor LGMLH_ACT_GGML", m->act);
     return LGMLH_EINVAL;
   }
-  for (int il = 0; il < m->n_layer; il++)
-    if (m->layers[il].swa && (!ub_ring || ub_ring->ring <= 0 || ub_ring->n_tokens != ub->n_tokens ||
-                              ub_ring->n_head_kv != ub->n_head_kv)) {
+  for (int il = 0; il < m->n_layer; il++) {
+    const lgmlh_layer &L = m->layers[il];
+    if (L.swa && (!ub_ring || ub_ring->ring <= 0 || ub_ring->n_tokens != ub->n_tokens)) {
       set_error("forward: layer %d slides and needs the pass's ring plan", il);
       return LGMLH_EINVAL;
     }
+    // each plan is made for the KV heads of the layers that attend through it
+    const int hkv = dims_of(m, L).Hkv;
+    if ((L.swa ? ub_ring : ub)->n_head_kv != hkv) {
+      set_error("forward: layer %d has %d KV heads; its plan was made for %d", il, hkv,
+                (L.swa ? ub_ring : ub)->n_head_kv);
+      return LGMLH_EINVAL;
+    }
+  }
   if (!out_rows) {
     out_rows = ub->logit_rows;
     n_out = ub->n_seq;
@@ -274,7 +308,7 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
     set_error("forward: workspace carve failed");
     return LGMLH_ENOMEM;
   }
-  const float scale = m->attn_scale > 0 ? m->attn_scale : 1.0f / sqrtf((float)z.D);
+
 
   // The X form of a quantized product (split planes, or ggml's Q8_K / Q8_0
   // blocks under LGMLH_ACT_GGML).
@@ -321,6 +355,8 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
                          m->embd_scale));
   for (int il = 0; il < m->n_layer; il++) {
     const lgmlh_layer &L = m->layers[il];
+    const LDims d = dims_of(m, L);
+    const float scale = m->attn_scale > 0 ? m->attn_scale : 1.0f / sqrtf((float)d.D);
     const bool v_sep = L.wv != nullptr;
     const bool v_own = v_own_planes(m, L);
     const bool qin_q = isq(L.wqkv_type) || (v_sep && isq(L.wv_type));
@@ -340,24 +376,24 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
     if (sd) {
       LGMLH_TRY(hip_check(hipEventRecord(sd->fork, st), "forward: fork"));
       LGMLH_TRY(hip_check(hipStreamWaitEvent(sd->s, sd->fork, 0), "forward: fork"));
-      LGMLH_TRY(gemm_on(sd->s, L.wv_type, L.wv, z.W - L.wqkv_rows, z.E, xn, z.N,
-                        qkv + L.wqkv_rows, z.W, nullptr, gws_v, z.gemm_ws_v, p_v,
+      LGMLH_TRY(gemm_on(sd->s, L.wv_type, L.wv, d.W - L.wqkv_rows, z.E, xn, z.N,
+                        qkv + L.wqkv_rows, d.W, nullptr, gws_v, z.gemm_ws_v, p_v,
                         v_own ? xs_v : nullptr));
       LGMLH_TRY(hip_check(hipEventRecord(sd->join, sd->s), "forward: join"));
     }
-    LGMLH_TRY(gemm(L.wqkv_type, L.wqkv, L.wqkv_rows, z.E, xn, z.N, qkv, z.W, nullptr, gws,
+    LGMLH_TRY(gemm(L.wqkv_type, L.wqkv, L.wqkv_rows, z.E, xn, z.N, qkv, d.W, nullptr, gws,
                    z.gemm_ws, p_qk));
     if (sd) {
       LGMLH_TRY(hip_check(hipStreamWaitEvent(st, sd->join, 0), "forward: join"));
     } else if (v_sep) {
-      LGMLH_TRY(gemm_on(st, L.wv_type, L.wv, z.W - L.wqkv_rows, z.E, xn, z.N, qkv + L.wqkv_rows,
-                        z.W, nullptr, gws_v, z.gemm_ws_v, p_v, v_own ? xs_v : nullptr));
+      LGMLH_TRY(gemm_on(st, L.wv_type, L.wv, d.W - L.wqkv_rows, z.E, xn, z.N, qkv + L.wqkv_rows,
+                        d.W, nullptr, gws_v, z.gemm_ws_v, p_v, v_own ? xs_v : nullptr));
     }
     // a sliding layer keeps its K / V in the sequences' rings (rows_swa,
     // transformer.lua:2469-2476) and attends through the ring plan
     const lgmlh_ubatch *lub = L.swa ? ub_ring : ub;
     const int vmode = (L.v_from_k ? QKV_V_FROM_K : 0) | (m->gemma ? QKV_V_NORM : 0);
-    LGMLH_TRY(qkv_rope_store_dev(qkv, z.N, (int)z.H, (int)z.Hkv, (int)z.D, m->n_rot,
+    LGMLH_TRY(qkv_rope_store_dev(qkv, z.N, (int)z.H, d.Hkv, d.D, d.n_rot,
                                  m->rope_neox, L.rope_base > 0 ? L.rope_base : m->rope_base,
                                  L.rope_freqs ? L.rope_freqs : m->rope_freqs, L.q_norm, L.k_norm,
                                  m->eps, ub->pos, L.kpool, L.vpool,
@@ -366,16 +402,16 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
     // a quantized output product takes its X as split planes, written by
     // the attention (and merge) kernels themselves; ggml's Q8 blocks are
     // made from the f32 rows by a kernel of their own
-    const bool oq = isq(L.wo_type), o_split = oq && xfo(L.wo_type) == XF_SPLIT && z.D >= 32;
+    const bool oq = isq(L.wo_type), o_split = oq && xfo(L.wo_type) == XF_SPLIT && d.D >= 32;
     {
       Span sp(trace, LGMLH_TRACE_ATTN, st);
-      LGMLH_TRY(paged_attention_dev(q, (int)z.H, (int)z.Hkv, (int)z.D, scale, L.kpool, L.vpool,
+      LGMLH_TRY(paged_attention_dev(q, (int)z.H, d.Hkv, d.D, scale, L.kpool, L.vpool,
                                     lub, o_split ? nullptr : att, o_split ? xs : nullptr,
                                     split_npad(z.N), aws, z.attn_ws, st));
     }
     if (oq && !o_split)
-      LGMLH_TRY(split_x(att, LGMLH_F32, z.N, z.H * z.D, xs, st, xfo(L.wo_type)));
-    LGMLH_TRY(out_product(L.wo_type, L.wo, z.H * z.D, att, L.post_attn_norm, 0.0f, p_o));
+      LGMLH_TRY(split_x(att, LGMLH_F32, z.N, z.H * d.D, xs, st, xfo(L.wo_type)));
+    LGMLH_TRY(out_product(L.wo_type, L.wo, z.H * d.D, att, L.post_attn_norm, 0.0f, p_o));
     if (L.gate_inp) {
       // routed experts (transformer.lua:2054-2068, M.moe :1989-2027): x +=
       // attention out, then ffn_norm for the router (f32) and the experts

@@ -143,11 +143,13 @@ class PoolSeqs:
 
     def copy_block(self, src, dst, n):
         """M.copy_block (transformer.lua:989-1007) on the device, every layer."""
-        hp = self.model.hp
-        for kp, vp in zip(self.model.kpools, self.model.vpools):
-            check(hip.lib().lgmlh_kv_copy_block(kp.data_ptr(), vp.data_ptr(), self.model.n_cells,
-                                                hp["n_head_kv"], hp["head_dim"], src, dst, n,
-                                                stream()))
+        m = self.model
+        D, Hkv = getattr(m, "paged_dims", (m.hp["head_dim"], m.hp["n_head_kv"]))
+        for il, (kp, vp) in enumerate(zip(m.kpools, m.vpools)):
+            if getattr(m, "swa", None) and m.swa[il]:
+                continue  # ring pools hold no pool blocks
+            check(hip.lib().lgmlh_kv_copy_block(kp.data_ptr(), vp.data_ptr(), m.n_cells, Hkv, D,
+                                                src, dst, n, stream()))
 
     def truncate(self, c, n):
         """transformer.lua:1084-1108."""
@@ -388,7 +390,7 @@ class Engine:
     def block_host(self, b, buf, out):
         m = self.model
         check(hip.lib().lgmlh_kv_block_host(m.pools_dev.data_ptr(), m.n_pools, m.n_cells,
-                                            m.hp["n_head_kv"], m.hp["head_dim"], b, buf.data_ptr(),
+                                            m.paged_dims[1], m.paged_dims[0], b, buf.data_ptr(),
                                             1 if out else 0, stream()))
 
     def spill_block(self, b, key, prio):
@@ -546,7 +548,7 @@ class Engine:
         """The bytes of slot's ring blocks in every sliding layer's K and V
         ring pools (device uint8 views, in layer order)."""
         m, R = self.model, self.ring_blocks
-        bb = hip.lib().lgmlh_kv_block_bytes(m.hp["n_head_kv"], m.hp["head_dim"])
+        bb = hip.lib().lgmlh_kv_block_bytes(m.ring_dims[1], m.ring_dims[0])
         views = []
         for il, swa in enumerate(m.swa):
             if swa:

@@ -74,7 +74,8 @@ class Layer(C.Structure):
                 ("exp_gu_type", C.c_int), ("exp_down_type", C.c_int), ("exp_gu", C.c_void_p),
                 ("exp_down", C.c_void_p), ("swa", C.c_int), ("v_from_k", C.c_int),
                 ("post_attn_norm", C.c_void_p), ("post_ffn_norm", C.c_void_p),
-                ("out_scale", C.c_float), ("rope_base", C.c_float), ("rope_freqs", C.c_void_p)]
+                ("out_scale", C.c_float), ("rope_base", C.c_float), ("rope_freqs", C.c_void_p),
+                ("head_dim", C.c_int), ("n_head_kv", C.c_int), ("n_rot", C.c_int)]
 
 
 class Trace(C.Structure):

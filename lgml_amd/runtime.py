@@ -254,27 +254,27 @@ class DeviceModel:
             arr = w["layers"][layer][name][0] if layer is not None else w[name][0]
             return keep(_dev(np.asarray(arr, np.float32))).data_ptr()
 
-        kvb = L.lgmlh_kv_layer_bytes(self.n_cells, Hkv, D)
-        kvb_ring = L.lgmlh_kv_layer_bytes(self.ring_cells, Hkv, D)
         self.kpools, self.vpools = [], []
         self.layers = (hip.Layer * hp["n_layer"])()
         qk_norm = hp["arch"] in ("qwen3", "qwen3moe", "gemma4")
         NE = hp.get("n_expert", 0)
         self.swa = []
+        self.dims = []  # (head_dim, n_head_kv) per layer
         for il in range(hp["n_layer"]):
             Ly = self.layers[il]
             g = layer_info(il)
-            if not gen:
-                lw = w["layers"][il]
-                if lw.get("head_dim", D) != D or lw.get("n_head_kv", Hkv) != Hkv:
-                    raise ValueError("layer %d: head size %s / %s KV heads; the device forward "
-                                     "takes one head size and KV head count for every layer"
-                                     % (il, lw.get("head_dim"), lw.get("n_head_kv")))
+            # this layer's head size and KV heads (gemma's sliding and global
+            # layers differ, transformer.lua:215-235)
+            lw = w["layers"][il] if not gen else {}
+            Dl, Hl = int(lw.get("head_dim") or D), int(lw.get("n_head_kv") or Hkv)
+            Ly.head_dim, Ly.n_head_kv = Dl, Hl
+            Ly.n_rot = int(lw.get("n_rot") or 0)
+            self.dims.append((Dl, Hl))
             Ly.attn_norm = vec("attn_norm", il, E)
             Ly.ffn_norm = vec("ffn_norm", il, E)
             for nm in ("q_norm", "k_norm"):
                 if (gen and qk_norm) or (not gen and w["layers"][il].get(nm) is not None):
-                    setattr(Ly, nm, vec(nm, il, D))
+                    setattr(Ly, nm, vec(nm, il, Dl))
             if gemma:
                 for nm in ("post_attn_norm", "post_ffn_norm"):
                     if gen or w["layers"][il].get(nm) is not None:
@@ -288,8 +288,8 @@ class DeviceModel:
             if Ly.swa and self.ring_cells <= 0:
                 raise ValueError("layer %d slides: the model needs ring_cells" % il)
             has_wv = g.get("has_wv", True) if gen else "wv" in w["layers"][il]
-            wq, wk = mat("wq", il, H * D, E), mat("wk", il, Hkv * D, E)
-            wv = mat("wv", il, Hkv * D, E) if has_wv else None
+            wq, wk = mat("wq", il, H * Dl, E), mat("wk", il, Hl * Dl, E)
+            wv = mat("wv", il, Hl * Dl, E) if has_wv else None
             if wv is None:
                 # V is the raw K (transformer.lua:1779): wqkv holds [wq | wk]
                 t, ty, M = repack_concat([wq, wk], E)
@@ -303,7 +303,7 @@ class DeviceModel:
                 Ly.wv, Ly.wv_type = keep(tv).data_ptr(), tyv
             Ly.wqkv, Ly.wqkv_type, Ly.wqkv_rows = keep(t).data_ptr(), ty, M
             del wq, wk, wv
-            t, ty, _ = repack_concat([mat("wo", il, E, H * D)], H * D)
+            t, ty, _ = repack_concat([mat("wo", il, E, H * Dl)], H * Dl)
             Ly.wo, Ly.wo_type = keep(t).data_ptr(), ty
             if NE:
                 # routed experts: the router stays f32 (convert.lua:135-137)
@@ -322,11 +322,22 @@ class DeviceModel:
                 t, ty, _ = repack_concat([mat("down", il, E, F)], F)
                 Ly.wdown, Ly.wdown_type = keep(t).data_ptr(), ty
             # the pool tensors live in kpools / vpools (grow_pool replaces them)
-            kp = _zeros(kvb_ring if Ly.swa else kvb)
-            vp = _zeros(kvb_ring if Ly.swa else kvb)
+            kvb_l = L.lgmlh_kv_layer_bytes(self.ring_cells if Ly.swa else self.n_cells, Hl, Dl)
+            kp = _zeros(kvb_l)
+            vp = _zeros(kvb_l)
             self.kpools.append(kp)
             self.vpools.append(vp)
             Ly.kpool, Ly.vpool = kp.data_ptr(), vp.data_ptr()
+        # the paged layers share one head shape, and so do the sliding ones:
+        # each kind attends through one plan (made for its KV heads), and
+        # the block copies take one row layout per pool kind
+        kinds = {sw: {d for d, s_ in zip(self.dims, self.swa) if s_ == sw} for sw in (False, True)}
+        for sw, ds in kinds.items():
+            if len(ds) > 1:
+                raise ValueError("%s layers with head shapes %s: one (head_dim, n_head_kv) per kind"
+                                 % ("sliding" if sw else "paged", sorted(ds)))
+        self.paged_dims = next(iter(kinds[False])) if kinds[False] else (D, Hkv)
+        self.ring_dims = next(iter(kinds[True])) if kinds[True] else (D, Hkv)
         m = hip.Model()
         for k in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "n_ff", "n_vocab",
                   "n_rot", "rope_neox"):
@@ -377,7 +388,8 @@ class DeviceModel:
                 ptrs += [self.kpools[il].data_ptr(), self.vpools[il].data_ptr()]
         self.n_pools = len(ptrs)
         self.pools_dev = torch.tensor(ptrs or [0], dtype=torch.int64, device=DEV)
-        self.block_bytes_all = self.n_pools * L.lgmlh_kv_block_bytes(Hkv, D)
+        self.block_bytes_all = self.n_pools * L.lgmlh_kv_block_bytes(self.paged_dims[1],
+                                                                     self.paged_dims[0])
 
     @property
     def pool_blocks(self):
@@ -397,7 +409,7 @@ class DeviceModel:
         if cells <= self.n_cells:
             return self.n_cells
         L, hp = hip.lib(), self.hp
-        Hkv, D = hp["n_head_kv"], hp["head_dim"]
+        D, Hkv = self.paged_dims
         nb = L.lgmlh_kv_layer_bytes(cells, Hkv, D)
         for il in range(hp["n_layer"]):
             if self.swa[il]:
@@ -444,13 +456,13 @@ class DeviceModel:
             blocks_per_split = 12
         if len(ids) and (ids.min() < 0 or ids.max() >= self.hp["n_vocab"]):
             raise ValueError("token id out of range [0, %d)" % self.hp["n_vocab"])
-        p = Plan(seq_n, seq_npast, block_tab, ids, self.hp["n_head"], self.hp["n_head_kv"],
+        p = Plan(seq_n, seq_npast, block_tab, ids, self.hp["n_head"], self.paged_dims[1],
                  self.pool_blocks, blocks_per_split)
         if any(self.swa):
             if ring_tab is None:
                 raise ValueError("the model has sliding-window layers: pass ring_tab")
             p.ring = Plan(seq_n, seq_npast, ring_tab, ids, self.hp["n_head"],
-                          self.hp["n_head_kv"], self.ring_cells // 64, ring_bps,
+                          self.ring_dims[1], self.ring_cells // 64, ring_bps,
                           ring_tab=ring_tab, window=self.hp["n_swa"])
         return p
 
@@ -495,11 +507,10 @@ class DeviceModel:
         (ring cells for a sliding layer)."""
         cells = np.ascontiguousarray(cells, np.int64)
         dc = torch.from_numpy(cells).to(DEV)
-        out = torch.empty((len(cells), self.hp["n_head_kv"] * self.hp["head_dim"]),
-                          dtype=torch.int16, device=DEV)
+        D, Hkv = self.dims[layer]
+        out = torch.empty((len(cells), Hkv * D), dtype=torch.int16, device=DEV)
         pool = (self.kpools if which == 0 else self.vpools)[layer]
         n = self.ring_cells if self.swa[layer] else self.n_cells
-        check(hip.lib().lgmlh_kv_gather(pool.data_ptr(), which, n,
-                                        self.hp["n_head_kv"], self.hp["head_dim"],
+        check(hip.lib().lgmlh_kv_gather(pool.data_ptr(), which, n, Hkv, D,
                                         dc.data_ptr(), len(cells), out.data_ptr(), stream()))
         return out.cpu().numpy().view(np.uint16)

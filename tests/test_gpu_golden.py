@@ -58,3 +58,40 @@ def test_hip_path_matches_llama_cpp_rows(arch):
     assert err < d["tol"], "max logit error %.3g" % err
     _, _, orows = run_rows(arch)
     assert rel_err(np.array(rows), np.array(orows)) < 1e-4
+
+
+GOLDEN_G4 = os.path.join(os.path.dirname(__file__), "golden", "ref_gemma4.json")
+
+
+def test_hip_path_matches_gemma4_rows():
+    """REF.dense of test/test_gemma4.lua:192-224 on the GPU: the tiny gemma4
+    model (test_gemma4.lua:38-174) with a sliding layer (window 6, heads of
+    16, 2 KV heads, through a ring) and a global one (heads of 32, 1 KV
+    head, V = the raw K, proportional rope), post norms, GeGLU, output
+    scales, tied output and a logit softcap; every token's logits at the
+    golden indices within 2e-3 of llama.cpp and the argmax of every row."""
+    from lgml_amd import runtime
+    from tests.test_oracle_golden import run_gemma4_rows
+    hp, w = models.ref_tiny_gemma4()
+    gm = runtime.DeviceModel(hp, w, 128, ring_cells=64)
+    d = json.load(open(GOLDEN_G4))
+    ref = d["rows"]["dense"]
+    nb = sum(len(b) for b in d["batches"])
+    passes = d["batches"] + [[r["id"]] for r in ref[nb:]]
+    rows, npast = [], 0
+    for ids in passes:
+        ids = np.array(ids, np.int32)
+        plan = gm.plan([len(ids)], [npast], np.array([[0, 1]], np.int32), ids,
+                       ring_tab=np.array([[0]], np.int32))
+        rows.extend(gm.forward(plan, out_rows=np.arange(len(ids))).cpu().numpy())
+        npast += len(ids)
+    idx = [i - 1 for i in d["idx_1based"]]
+    assert len(rows) == len(ref) == 31
+    err = 0.0
+    for r, got in zip(ref, rows):
+        err = max(err, max(abs(float(got[i]) - v) for i, v in zip(idx, r["v"])))
+        assert int(np.argmax(got)) == r["best"], "argmax differs from llama.cpp"
+    print("gemma4 dense: max |logit - llama.cpp| %.3g (tol %g)" % (err, d["tol"]), flush=True)
+    assert err < d["tol"], "max logit error %.3g" % err
+    _, _, orows = run_gemma4_rows()
+    assert rel_err(np.array(rows), np.array(orows)) < 1e-4
