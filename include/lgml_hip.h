@@ -511,11 +511,19 @@ typedef struct {
  * matrix has a type of its own runs that product on a side stream beside
  * the q|k product (not while tracing): the first such pass on a host
  * thread and device creates that stream (non-blocking, default priority)
- * and two events, kept until the process ends; if creating them fails,
- * the pass runs on the caller's stream alone. */
+ * and two events, kept until lgmlh_forward_release or the process
+ * ends; if creating them fails, the pass runs on the caller's stream
+ * alone. */
 int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub, const lgmlh_ubatch *ub_ring,
     const int32_t *out_rows, int n_out, float *logits, void *workspace, size_t ws_bytes,
     lgmlh_trace *trace, void *stream);
+/* Destroy the side stream and the two events that lgmlh_forward made for
+ * the calling thread on the current device (after the work queued on that
+ * stream ends); nothing to do when it made none. A later pass makes them
+ * again. For hosts that tear a thread's device context down (the
+ * counterpart of backend:close / the backend's last release,
+ * src/lgml.c:50-66,535-545). */
+int lgmlh_forward_release(void);
 
 #ifdef __cplusplus
 }

@@ -216,11 +216,12 @@ struct Side {
   hipEvent_t fork = nullptr, join = nullptr;
   bool failed = false;
 };
+constexpr int SIDE_MAX_DEV = 16;
+thread_local Side sides[SIDE_MAX_DEV];
+
 Side *side_of() {
-  constexpr int MAX_DEV = 16;
-  static thread_local Side sides[MAX_DEV];
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return nullptr;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= SIDE_MAX_DEV) return nullptr;
   Side &sd = sides[dev];
   if (sd.failed) return nullptr;
   if (!sd.s) {
@@ -235,6 +236,31 @@ Side *side_of() {
   return &sd;
 }
 }  // namespace
+
+// The calling thread's side stream and events on the current device, made
+// by its first pass with a V product of its own type, are destroyed (after
+// the work queued on the stream ends); a later pass makes them again.
+extern "C" int lgmlh_forward_release(void) {
+  int dev = 0;
+  LGMLH_TRY(hip_check(hipGetDevice(&dev), "forward_release: device"));
+  if (dev < 0 || dev >= SIDE_MAX_DEV) return LGMLH_OK;
+  Side &sd = sides[dev];
+  if (sd.s) {
+    LGMLH_TRY(hip_check(hipStreamSynchronize(sd.s), "forward_release: sync"));
+    LGMLH_TRY(hip_check(hipStreamDestroy(sd.s), "forward_release: stream"));
+    sd.s = nullptr;
+  }
+  if (sd.fork) {
+    LGMLH_TRY(hip_check(hipEventDestroy(sd.fork), "forward_release: event"));
+    sd.fork = nullptr;
+  }
+  if (sd.join) {
+    LGMLH_TRY(hip_check(hipEventDestroy(sd.join), "forward_release: event"));
+    sd.join = nullptr;
+  }
+  sd.failed = false;
+  return LGMLH_OK;
+}
 
 extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
                              const lgmlh_ubatch *ub_ring, const int32_t *out_rows, int n_out,

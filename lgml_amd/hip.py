@@ -33,7 +33,7 @@ SYMBOLS = (
     "lgmlh_gen_normal", "lgmlh_moe_route", "lgmlh_mul_mat_id_workspace", "lgmlh_mul_mat_id",
     "lgmlh_moe_sum", "lgmlh_plan_ring", "lgmlh_geglu", "lgmlh_softcap",
     "lgmlh_mul_mat_noalloc_limit", "lgmlh_mul_mat_noalloc", "lgmlh_mul_mat_ggml",
-    "lgmlh_mul_mat_id_ggml", "lgmlh_quantize_act",
+    "lgmlh_mul_mat_id_ggml", "lgmlh_quantize_act", "lgmlh_forward_release",
 )
 GATING_SOFTMAX, GATING_SIGMOID = 1, 2
 TRACE_ATTN, TRACE_GEMM, TRACE_EXPERTS = 1, 2, 4
@@ -158,6 +158,7 @@ def _declare(L):
                                      i32], sz),
         "lgmlh_forward": ([C.POINTER(Model), C.POINTER(Ubatch), C.POINTER(Ubatch), vp, i32, vp,
                            vp, sz, C.POINTER(Trace), vp], i32),
+        "lgmlh_forward_release": ([], i32),
         "lgmlh_kvpool_bytes": ([C.c_int32, C.c_int32], sz),
         "lgmlh_kvpool_init": ([vp, sz, C.c_int32, C.c_int32, C.c_int32], i32),
         "lgmlh_kvpool_take": ([vp, C.c_int32], C.c_int32),

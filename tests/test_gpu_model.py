@@ -113,3 +113,26 @@ def test_batched_pass_equals_lone_pass():
         la2 = gm_a.forward(gm_a.plan([1], [len(prompts[s])], bt[s:s + 1],
                                      np.array([nxt[s]], np.int32))).cpu().numpy()
         assert np.array_equal(la2[0].view(np.uint32), lb2[s].view(np.uint32))
+
+
+def test_forward_release_then_forward_again():
+    """lgmlh_forward_release destroys the side stream and events of the
+    calling thread (made by a pass whose V product has its own type, as in
+    the Q4_K_M mix); a pass after it makes them again and gives the same
+    bits. A release with nothing made returns 0."""
+    from lgml_amd import hip, runtime
+    hp, w = models.build("c2", seed=5, n_layer=2, init="normal")
+    gm = runtime.DeviceModel(hp, w, 1024)
+    prompts = [lcg_ints(5000 + i, n, 0, hp["n_vocab"]) for i, n in enumerate([7, 30])]
+    sch = Schedule(16, 2)
+    for s, p in enumerate(prompts):
+        sch.grow(s, len(p))
+    bt = sch.table([0, 1])
+    ids = np.concatenate([np.array(p, np.int32) for p in prompts])
+    a = gm.forward(gm.plan([7, 30], [0, 0], bt, ids)).cpu().numpy()
+    torch.cuda.synchronize()
+    hip.check(hip.lib().lgmlh_forward_release())
+    hip.check(hip.lib().lgmlh_forward_release())
+    b = gm.forward(gm.plan([7, 30], [0, 0], bt, ids)).cpu().numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    hip.check(hip.lib().lgmlh_forward_release())
