@@ -304,9 +304,13 @@ struct WFrag<LGMLH_Q8_0> {
 // group ahead. A split writes its partial sums; a second kernel adds the
 // splits in order (no inter-workgroup sync).
 // One column tile of Q4_K / Q6_K (the grouped expert products; plain
-// products of at most 16 columns): registers capped at 128 so that two
-// workgroups share a CU, twice the weight loads in flight (C5's expert
-// products 5.18 -> 4.42 ms per step). Q8_0 would spill under the cap.
+// products of at most 16 columns): registers capped at 128 (4 waves per
+// SIMD) so that two workgroups share a CU, twice the weight loads in
+// flight (C5's expert products 5.18 -> 4.42 ms per step). Q8_0 would spill
+// under the cap, and so does Q6_K on ggml's X (its two exact parts per
+// group): capped at 256 it takes 149 and runs 3 waves per SIMD (the V
+// product of C2's mix, 1024 x 4096 at 64 columns, 19.1 -> 17.5 us with its
+// reduction; 4096 x 14336 at 16 columns 31.4 -> 26.1 us).
 // Q4_K with 64-column tiles: workgroups of 4 waves (128 rows) with one X
 // buffer (66 KB of LDS), so that two share a CU; one's waits for its next
 // K step (the X loads, the barriers) are filled by the other's products
@@ -330,7 +334,8 @@ __host__ __device__ constexpr int gemm_waves(int type, int nct) {
 // 4-wave Q4_K workgroups keep two X buffers.
 template <int TYPE, int NCT, bool GATHER, bool Q8>
 __global__ void __launch_bounds__(gemm_waves(TYPE, NCT) * 64,
-                                  NCT == 1 && TYPE != LGMLH_Q8_0   ? 4
+                                  NCT == 1 && TYPE == LGMLH_Q6_K && Q8 ? 2
+                                  : NCT == 1 && TYPE != LGMLH_Q8_0   ? 4
                                   : NCT == 4 && TYPE == LGMLH_Q4_K ? 2
                                                                    : 1)
 qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__restrict__ xs,
@@ -347,11 +352,11 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   constexpr int DX_SLOTS = !Q8 ? 1 : TYPE == LGMLH_Q8_0 ? 128 : 16;
   __shared__ __align__(16) u32x4 xh0_[X_SLOTS], xh1_[ONEBUF ? 1 : X_SLOTS];
   __shared__ __align__(16) u32x4 xl0_[XL_SLOTS], xl1_[ONEBUF ? 1 : XL_SLOTS];
-  // Q4_K group sums, 8 f16 per row: hi and lo (Q8: the 16 sums of 16 q,
-  // 0..7 and 8..15)
-  __shared__ __align__(16) u32x4 gh0_[64], gh1_[64];
-  __shared__ __align__(16) u32x4 gl0_[64], gl1_[64];
-  __shared__ __align__(16) u32x4 gz_[1];              // zeros for lanes c >= 2
+  // Q4_K group sums, 8 f16 per row: hi at slots 0..63, lo at 64..127 (Q8:
+  // the 16 sums of 16 q, 0..7 and 8..15), slot 128 zeros for lanes c >= 2.
+  // One LDS object per buffer: the compiler then knows that reads of one
+  // buffer need not wait for the loads in flight into the other.
+  __shared__ __align__(16) u32x4 gs0_[129], gs1_[129];
   __shared__ __align__(16) u32x4 dx0_[DX_SLOTS], dx1_[DX_SLOTS];
   // Q8_0: the 256-byte headers of every wave's chunks (wave w, tile a at
   // slots 32 w + 16 a .. + 15)
@@ -359,13 +364,15 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
   __shared__ __align__(16) u32x4 hd0_[HD_SLOTS], hd1_[HD_SLOTS];
   auto XH = [&](int b) { return b && !ONEBUF ? xh1_ : xh0_; };
   auto XL = [&](int b) { return b && !ONEBUF ? xl1_ : xl0_; };
-  auto GH = [&](int b) { return b && !ONEBUF ? gh1_ : gh0_; };
-  auto GL = [&](int b) { return b && !ONEBUF ? gl1_ : gl0_; };
+  auto GS = [&](int b) { return b && !ONEBUF ? gs1_ : gs0_; };
   auto HD = [&](int b) { return b ? hd1_ : hd0_; };
   auto DX = [&](int b) { return (const float *)(b ? dx1_ : dx0_); };
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-  if (tid == 0) gz_[0] = u32x4{0, 0, 0, 0};  // read after the prologue's barrier
+  if (tid == 0) {  // read after the prologue's barrier
+    gs0_[128] = u32x4{0, 0, 0, 0};
+    gs1_[128] = u32x4{0, 0, 0, 0};
+  }
   const int64_t NSB = K / QK_K;
   const int64_t MT = (M + 15) / 16;
   // Tile order for the wide tiles: the dispatcher deals workgroups round-
@@ -472,12 +479,12 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
       if (wave < 2)  // wave 0: hi sums, wave 1: lo sums
         __builtin_amdgcn_global_load_lds(
             (const void *)((wave == 0 ? ghi : glo) + goff + kstep * 8),
-            (lds_t *)(wave == 0 ? GH(buf) : GL(buf)), 16, 0, 0);
+            (lds_t *)(GS(buf) + 64 * wave), 16, 0, 0);
     }
     if constexpr (TYPE == LGMLH_Q4_K && Q8) {
       if (wave < 2)  // wave 0: sums 0..7 of 16 q, wave 1: sums 8..15
         __builtin_amdgcn_global_load_lds((const void *)(bsp + goff + kstep * 16 + 8 * wave),
-                                         (lds_t *)(wave == 0 ? GH(buf) : GL(buf)), 16, 0, 0);
+                                         (lds_t *)(GS(buf) + 64 * wave), 16, 0, 0);
     }
     if constexpr (Q8 && TYPE != LGMLH_Q8_0) {
       if (wave == 2)  // the d of each column (lane)
@@ -516,8 +523,8 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
     if constexpr (TYPE == LGMLH_Q4_K && !Q8) {
       // lanes c >= 2 (k past the 8 groups) read zeros: no branch per step
       const bool gs = c < 2;
-      const f16 *gh = gs ? (const f16 *)GH(buf) + r16 * 8 + 4 * c : (const f16 *)gz_;
-      const f16 *gl = gs ? (const f16 *)GL(buf) + r16 * 8 + 4 * c : (const f16 *)gz_;
+      const f16 *gh = (const f16 *)GS(buf) + (gs ? r16 * 8 + 4 * c : 128 * 8);
+      const f16 *gl = gh + (gs ? 64 * 8 : 0);
       const int cstride = gs ? 16 * 8 : 0;
 #pragma unroll
       for (int ct = 0; ct < NCT; ct++) {
@@ -527,7 +534,7 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
     }
     if constexpr (TYPE == LGMLH_Q4_K && Q8) {
       // the 16 sums of 16 q: lane c holds sums 4c .. 4c + 3 of its column
-      const f16 *gs = (const f16 *)(c < 2 ? GH(buf) : GL(buf)) + r16 * 8 + 4 * (c & 1);
+      const f16 *gs = (const f16 *)GS(buf) + (c < 2 ? 0 : 64 * 8) + r16 * 8 + 4 * (c & 1);
 #pragma unroll
       for (int ct = 0; ct < NCT; ct++) sh4[ct] = *(const f16x4 *)(gs + ct * 16 * 8);
     }
