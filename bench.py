@@ -93,6 +93,10 @@ def parse():
                     help="arithmetic of the quantized weight products: ggml (the reference CPU "
                          "path's: X quantized to Q8_K / Q8_0 per block, integer block dots; "
                          "default) or exact (f32-accurate X as f16 hi + lo halves)")
+    ap.add_argument("--graph-probe", action="store_true",
+                    help="only time one decode pass of the workload's model at 64 contexts "
+                         "U[128, 4000] three ways: eager, as a captured HIP graph replayed "
+                         "(same plan), and the capture itself; prints the three")
     ap.add_argument("--product", default="", metavar="TYPE:MxK:N",
                     help="only run one weight product (q4 / q6 / q8, M x K weights, N rows), "
                          "5 times after 2 untimed calls: the subject of the products' counter "
@@ -327,8 +331,84 @@ def read_probe(nbytes):
     return 0
 
 
+def graph_probe(args):
+    """What a captured graph of the decode pass would save: the pass run
+    eagerly (lgmlh_forward launches kernel after kernel), a capture of the
+    same call replayed (every replay checked equal to the eager logits, with
+    eager passes between replays), and the wall time of capturing and
+    instantiating it. A plan changes every step (lengths, work items, grid
+    sizes), so a graph would be captured again per pass."""
+    import numpy as np
+    import torch
+
+    from lgml_amd import runtime, workload
+    wl = WORKLOADS[args.workload]
+    hp = dict(workload.SHAPES[wl["shape"]])
+    if hp.get("gemma"):
+        print("--graph-probe runs the paged-only workloads (c2, c3, c5)", file=sys.stderr)
+        return 2
+    hp["act_quant"] = args.act == "ggml"
+    S, nbk = 64, (4000 + 64 + 63) // 64
+    model = runtime.DeviceModel(hp, runtime.generated_weights(
+        hp, args.seed, workload.policy(hp["wtype"], hp["n_layer"])), S * nbk * 64)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(args.seed)
+    for t in model.kpools + model.vpools:
+        t.view(torch.float16).uniform_(-1.0, 1.0, generator=g)
+    rng = workload.Lcg(args.seed)
+    npast = [rng.int(128, 4000) for _ in range(S)]
+    ids = np.array([rng.int(0, hp["n_vocab"] - 1) for _ in range(S)], np.int32)
+    bt = (np.arange(S, dtype=np.int32)[:, None] * nbk + np.arange(nbk, dtype=np.int32)[None, :])
+    plan = model.plan([1] * S, npast, bt, ids)
+    out = torch.empty((S, hp["n_vocab"]), dtype=torch.float32, device="cuda")
+    for _ in range(3):
+        model.forward(plan, logits=out)
+    torch.cuda.synchronize()
+    ref = out.clone()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn, n=20):
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    eager = timed(lambda: model.forward(plan, logits=out))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    caps = []
+    for _ in range(3):
+        graph = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with torch.cuda.graph(graph, stream=side):
+            model.forward(plan, logits=out)
+        torch.cuda.synchronize()
+        caps.append((time.perf_counter() - t0) * 1e3)
+    for i in range(4):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(out, ref):
+            print("replay %d differs from the eager pass" % i, file=sys.stderr)
+            return 1
+        model.forward(plan, logits=out)
+    replay = timed(graph.replay)
+    if not torch.equal(out, ref):
+        print("the timed replays differ from the eager pass", file=sys.stderr)
+        return 1
+    print("%s decode pass, 64 sequences: eager %.3f ms, graph replay %.3f ms (%.3f ms less), "
+          "capture + instantiate %s ms" % (args.workload, eager, replay, eager - replay,
+                                            " / ".join("%.2f" % c for c in caps)))
+    return 0
+
+
 def main():
     args = parse()
+    if args.graph_probe:
+        return graph_probe(args)
     if args.read_probe:
         return read_probe(args.read_probe)
     if args.calibrate_copy:
