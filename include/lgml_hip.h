@@ -7,9 +7,10 @@
  * longjmps, and never allocates device or host memory: callers pass
  * buffers and workspaces whose sizes the *_bytes / *_workspace functions
  * report. (One exception, stated at lgmlh_forward: a side stream and two
- * events, made once per host thread and device.) Device pointers are HIP device addresses; `stream` is a
- * hipStream_t (NULL = the null stream). Calls on one stream are ordered;
- * calls on different streams that share a workspace race.
+ * events per host thread, device and caller stream, made once and released
+ * by lgmlh_forward_release.) Device pointers are HIP device addresses;
+ * `stream` is a hipStream_t (NULL = the null stream). Calls on one stream
+ * are ordered; calls on different streams that share a workspace race.
  *
  * Reference citations are paths under the lgml tree (mischief/lgml).
  */
@@ -510,15 +511,17 @@ typedef struct {
  * a layer slides (NULL otherwise). trace may be NULL. A layer whose V
  * matrix has a type of its own runs that product on a side stream beside
  * the q|k product (not while tracing): the first such pass on a host
- * thread and device creates that stream (non-blocking, default priority)
- * and two events, kept until lgmlh_forward_release or the process
- * ends; if creating them fails, the pass runs on the caller's stream
- * alone. */
+ * thread, device and caller stream creates that side stream (non-blocking,
+ * default priority) and two events, kept until lgmlh_forward_release or
+ * the process ends; passes on different caller streams (up to 4 per
+ * thread and device) get side streams of their own, so that neither's side
+ * products queue behind the other's. If creating them fails, or a fifth
+ * caller stream asks, the pass runs on the caller's stream alone. */
 int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub, const lgmlh_ubatch *ub_ring,
     const int32_t *out_rows, int n_out, float *logits, void *workspace, size_t ws_bytes,
     lgmlh_trace *trace, void *stream);
-/* Destroy the side stream and the two events that lgmlh_forward made for
- * the calling thread on the current device (after the work queued on that
+/* Destroy the side streams and events that lgmlh_forward made for the
+ * calling thread on the current device (after the work queued on each
  * stream ends); nothing to do when it made none. A later pass makes them
  * again. For hosts that tear a thread's device context down (the
  * counterpart of backend:close / the backend's last release,

@@ -208,57 +208,70 @@ struct Span {
   }
 };
 
-// A side stream (default priority) and two events per host thread and
-// device, for a product that runs beside another product of the same pass;
-// null when any of them cannot be made (the caller stays on its stream).
+// A side stream (default priority) and two events per host thread, device
+// and caller stream (up to SIDE_PER_DEV caller streams), for a product that
+// runs beside another product of the same pass; null when none can be made
+// (the caller stays on its stream). Passes on different caller streams get
+// different side streams, so that one's side products never queue behind
+// another's.
 struct Side {
+  hipStream_t caller = nullptr;
   hipStream_t s = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
   bool failed = false;
 };
-constexpr int SIDE_MAX_DEV = 16;
-thread_local Side sides[SIDE_MAX_DEV];
+constexpr int SIDE_MAX_DEV = 16, SIDE_PER_DEV = 4;
+thread_local Side sides[SIDE_MAX_DEV][SIDE_PER_DEV];
 
-Side *side_of() {
+Side *side_of(hipStream_t caller) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= SIDE_MAX_DEV) return nullptr;
-  Side &sd = sides[dev];
-  if (sd.failed) return nullptr;
-  if (!sd.s) {
-    if (hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&sd.join, hipEventDisableTiming) != hipSuccess) {
-      (void)hipGetLastError();
-      sd.failed = true;
-      return nullptr;
-    }
+  Side *free_slot = nullptr;
+  for (Side &sd : sides[dev]) {
+    if ((sd.s || sd.failed) && sd.caller == caller) return sd.failed ? nullptr : &sd;
+    if (!sd.s && !sd.failed && !free_slot) free_slot = &sd;
+  }
+  if (!free_slot) return nullptr;
+  Side &sd = *free_slot;
+  sd.caller = caller;
+  if (hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&sd.join, hipEventDisableTiming) != hipSuccess) {
+    (void)hipGetLastError();
+    if (sd.s) (void)hipStreamDestroy(sd.s);
+    if (sd.fork) (void)hipEventDestroy(sd.fork);
+    sd.s = nullptr;
+    sd.fork = sd.join = nullptr;
+    sd.failed = true;
+    return nullptr;
   }
   return &sd;
 }
 }  // namespace
 
-// The calling thread's side stream and events on the current device, made
-// by its first pass with a V product of its own type, are destroyed (after
-// the work queued on the stream ends); a later pass makes them again.
+// The calling thread's side streams and events on the current device, made
+// by its passes with a V product of its own type, are destroyed (after the
+// work queued on each stream ends); later passes make them again.
 extern "C" int lgmlh_forward_release(void) {
   int dev = 0;
   LGMLH_TRY(hip_check(hipGetDevice(&dev), "forward_release: device"));
   if (dev < 0 || dev >= SIDE_MAX_DEV) return LGMLH_OK;
-  Side &sd = sides[dev];
-  if (sd.s) {
-    LGMLH_TRY(hip_check(hipStreamSynchronize(sd.s), "forward_release: sync"));
-    LGMLH_TRY(hip_check(hipStreamDestroy(sd.s), "forward_release: stream"));
-    sd.s = nullptr;
+  for (Side &sd : sides[dev]) {
+    if (sd.s) {
+      LGMLH_TRY(hip_check(hipStreamSynchronize(sd.s), "forward_release: sync"));
+      LGMLH_TRY(hip_check(hipStreamDestroy(sd.s), "forward_release: stream"));
+      sd.s = nullptr;
+    }
+    if (sd.fork) {
+      LGMLH_TRY(hip_check(hipEventDestroy(sd.fork), "forward_release: event"));
+      sd.fork = nullptr;
+    }
+    if (sd.join) {
+      LGMLH_TRY(hip_check(hipEventDestroy(sd.join), "forward_release: event"));
+      sd.join = nullptr;
+    }
+    sd = Side{};
   }
-  if (sd.fork) {
-    LGMLH_TRY(hip_check(hipEventDestroy(sd.fork), "forward_release: event"));
-    sd.fork = nullptr;
-  }
-  if (sd.join) {
-    LGMLH_TRY(hip_check(hipEventDestroy(sd.join), "forward_release: event"));
-    sd.join = nullptr;
-  }
-  sd.failed = false;
   return LGMLH_OK;
 }
 
@@ -398,7 +411,7 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
     // product that leaves most CUs idle: it runs on a side stream beside
     // the q|k product (not while tracing, whose events time one stream).
     p_v = Pending{};
-    Side *sd = v_sep && !trace ? side_of() : nullptr;
+    Side *sd = v_sep && !trace ? side_of(st) : nullptr;
     if (sd) {
       LGMLH_TRY(hip_check(hipEventRecord(sd->fork, st), "forward: fork"));
       LGMLH_TRY(hip_check(hipStreamWaitEvent(sd->s, sd->fork, 0), "forward: fork"));

@@ -113,7 +113,8 @@ def generated_weights(hp, seed, policy):
 
 def load_gguf(path, n_cells, ring_cells=0):
     """A DeviceModel from a gguf file (lgml_amd.gguf.load: llama, qwen3,
-    qwen3moe, gemma4 with one head size for every layer)."""
+    qwen3moe, gemma4; a gemma4 model's sliding and global layers keep their
+    own head sizes and KV head counts)."""
     from . import gguf
     hp, w = gguf.load(path)
     return DeviceModel(hp, w, n_cells, ring_cells)

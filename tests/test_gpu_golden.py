@@ -9,6 +9,8 @@ the reference's LCG and draw order, run on the GPU over the golden passes
 tolerance, test_qwen_moe.lua:378-400) and the argmax of every row equal to
 the reference's `best`. These rows come from llama.cpp, so parity here does
 not pass through this build's oracle; the oracle's rows are compared too.
+The same models written as gguf files in the reference's layout and read
+back by runtime.load_gguf meet the same rows on the device.
 """
 import json
 import os
@@ -26,10 +28,11 @@ torch = pytest.importorskip("torch")
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "ref_logits.json")
 
 
-def gpu_rows(arch):
+def gpu_rows(arch, gm=None):
     from lgml_amd import runtime
-    hp, w = models.ref_tiny(arch)
-    gm = runtime.DeviceModel(hp, w, 128)
+    if gm is None:
+        hp, w = models.ref_tiny(arch)
+        gm = runtime.DeviceModel(hp, w, 128)
     d = json.load(open(GOLDEN))
     ref = d["rows"][arch]
     nb = sum(len(b) for b in d["batches"])
@@ -44,10 +47,7 @@ def gpu_rows(arch):
     return d, ref, rows
 
 
-@pytest.mark.parametrize("arch", ["llama", "qwen3", "qwen3moe"])
-def test_hip_path_matches_llama_cpp_rows(arch):
-    from tests.test_oracle_golden import run_rows
-    d, ref, rows = gpu_rows(arch)
+def check_rows(arch, d, ref, rows):
     idx = [i - 1 for i in d["idx_1based"]]
     assert len(rows) == len(ref) == 14
     err = 0.0
@@ -56,8 +56,31 @@ def test_hip_path_matches_llama_cpp_rows(arch):
         assert int(np.argmax(got)) == r["best"], "argmax differs from llama.cpp"
     print("%s: max |logit - llama.cpp| %.3g (tol %g)" % (arch, err, d["tol"]), flush=True)
     assert err < d["tol"], "max logit error %.3g" % err
+
+
+@pytest.mark.parametrize("arch", ["llama", "qwen3", "qwen3moe"])
+def test_hip_path_matches_llama_cpp_rows(arch):
+    from tests.test_oracle_golden import run_rows
+    d, ref, rows = gpu_rows(arch)
+    check_rows(arch, d, ref, rows)
     _, _, orows = run_rows(arch)
     assert rel_err(np.array(rows), np.array(orows)) < 1e-4
+
+
+@pytest.mark.parametrize("arch", ["llama", "qwen3", "qwen3moe"])
+def test_gguf_loaded_models_match_llama_cpp_rows(tmp_path, arch):
+    """§8(f) row 3 end to end on the device: the tiny models written as gguf
+    files with the reference's key-values and tensor names
+    (test/test_qwen_moe.lua:65-200), read by runtime.load_gguf into a
+    DeviceModel, meet the same llama.cpp rows."""
+    from lgml_amd import runtime
+    from tests import gguf_util as gw
+    from tests.test_gguf_loader import kv_qwen, tensors_of
+    hp, w = models.ref_tiny(arch)
+    path = str(tmp_path / ("%s.gguf" % arch))
+    gw.write(path, kv_qwen(arch, hp), tensors_of(arch, hp, w))
+    d, ref, rows = gpu_rows(arch, runtime.load_gguf(path, 128))
+    check_rows(arch, d, ref, rows)
 
 
 GOLDEN_G4 = os.path.join(os.path.dirname(__file__), "golden", "ref_gemma4.json")
@@ -73,7 +96,26 @@ def test_hip_path_matches_gemma4_rows():
     from lgml_amd import runtime
     from tests.test_oracle_golden import run_gemma4_rows
     hp, w = models.ref_tiny_gemma4()
-    gm = runtime.DeviceModel(hp, w, 128, ring_cells=64)
+    rows = gemma4_rows(runtime.DeviceModel(hp, w, 128, ring_cells=64))
+    _, _, orows = run_gemma4_rows()
+    assert rel_err(np.array(rows), np.array(orows)) < 1e-4
+
+
+def test_gguf_loaded_gemma4_matches_llama_cpp_rows(tmp_path):
+    """The tiny gemma4 model as a gguf file (test/test_gemma4.lua:84-174:
+    per-layer KV head counts, head sizes of 16 and 32, no attn_v on the
+    global layer, tied output), read by runtime.load_gguf, meets REF.dense
+    on the device."""
+    from lgml_amd import runtime
+    from tests import gguf_util as gw
+    from tests.test_gguf_loader import kv_gemma4, tensors_of
+    hp, w = models.ref_tiny_gemma4()
+    path = str(tmp_path / "gemma4.gguf")
+    gw.write(path, kv_gemma4(hp, w), tensors_of("gemma4", hp, w, gemma=True))
+    gemma4_rows(runtime.load_gguf(path, 128, ring_cells=64))
+
+
+def gemma4_rows(gm):
     d = json.load(open(GOLDEN_G4))
     ref = d["rows"]["dense"]
     nb = sum(len(b) for b in d["batches"])
@@ -93,5 +135,4 @@ def test_hip_path_matches_gemma4_rows():
         assert int(np.argmax(got)) == r["best"], "argmax differs from llama.cpp"
     print("gemma4 dense: max |logit - llama.cpp| %.3g (tol %g)" % (err, d["tol"]), flush=True)
     assert err < d["tol"], "max logit error %.3g" % err
-    _, _, orows = run_gemma4_rows()
-    assert rel_err(np.array(rows), np.array(orows)) < 1e-4
+    return rows
