@@ -13,6 +13,18 @@ Every cell a pass reads holds the same random f16 K / V on both sides (the
 device pools are written through lgmlh_kv_store from the oracle's f16
 values, exact). Logits must be within 2e-3 max relative error of the
 oracle's and the greedy ids identical.
+
+The same passes in ggml's arithmetic (X quantized per block, what bench.py
+runs by default) cannot be held to 2e-3: ggml's arithmetic is not
+continuous in X, and the GPU's attention (within 1e-4 of the oracle's)
+puts some of its outputs on the other side of a rounding boundary of the
+next product's Q8_K blocks. They are held to what shows that the GPU runs
+ggml's arithmetic: its distance to the exact oracle equals the ggml
+oracle's within 10% (it carries the same quantization), its distance to
+the ggml oracle is at most a quarter of the quantization's own effect
+(F - E), and every greedy id is the ggml oracle's. (Measured: C2 G-F 0.0048
+against F-E 0.0225, C5 0.0040 against 0.0626; the oracle with every norm
+vector one ulp up moves by 0.0028 and 0.0017.)
 """
 import numpy as np
 import pytest
@@ -61,9 +73,14 @@ def fill_both(L, gm, kp, vp, layer, cells, rng, ring):
     torch.cuda.synchronize()
 
 
-def decode_pass(hp, w, contexts, seed, ring_blocks=0):
+def decode_pass(hp, w, contexts, seed, ring_blocks=0, ggml=False):
+    """The GPU's logits and the oracle's; ggml: the GPU and the oracle in
+    ggml's arithmetic, and also {"E": exact oracle, "P": ggml oracle with
+    the ggml oracle with every norm vector one ulp up}."""
     from lgml_amd import hip, runtime
     L = hip.lib()
+    if ggml:
+        hp = dict(hp, act_quant=True)
     S = len(contexts)
     nbs = [(c + 1 + 63) // 64 for c in contexts]
     n_cells = sum(nbs) * 64
@@ -102,7 +119,23 @@ def decode_pass(hp, w, contexts, seed, ring_blocks=0):
     lg = gm.forward(plan).cpu().numpy()
     b = core.BatchDesc([1] * S, contexts, bt, 64, ids, plan.logit_rows, ring_tab=rt)
     lo = om.forward(kp, vp, b)
-    return lg, lo
+    if not ggml:
+        return lg, lo
+    print("oracle F done", flush=True)
+    more = {"E": core.OracleModel(dict(hp, act_quant=False), w).forward(kp, vp, b)}
+    print("oracle E done", flush=True)
+    # every norm vector one ulp up (each layer's attn_norm and ffn_norm, the
+    # output norm): each input that ggml's arithmetic quantizes after a norm
+    # moves by about an ulp, as the GPU's own f32 rounding moves them all
+    def up(v):
+        a, t = v
+        return ((a * np.float32(1 + 2**-23)).astype(np.float32), t)
+    wp = dict(w, layers=[dict(Lw) for Lw in w["layers"]], output_norm=up(w["output_norm"]))
+    for Lw in wp["layers"]:
+        Lw["attn_norm"], Lw["ffn_norm"] = up(Lw["attn_norm"]), up(Lw["ffn_norm"])
+    more["P"] = core.OracleModel(hp, wp).forward(kp, vp, b)
+    print("oracle P done", flush=True)
+    return lg, lo, more
 
 
 def check(lg, lo, name):
@@ -139,3 +172,39 @@ def test_c4_bench_shape_decode_pass():
     R = workload.ring_blocks(hp, 1)
     lg, lo = decode_pass(hp, w, ctx, 62, ring_blocks=R)
     check(lg, lo, "c4 width, 32 slots, sliding + global")
+
+
+def check_ggml(lg, lf, more, name):
+    rms = lambda x: float(np.sqrt(np.mean(np.square(x, dtype=np.float64))))
+    den = rms(more["E"])
+    r = dict(gf=rms(lg - lf) / den, ge=rms(lg - more["E"]) / den,
+             fe=rms(lf - more["E"]) / den, pf=rms(more["P"] - lf) / den)
+    same = sum(int(np.argmax(g)) == core.argmax(f) for g, f in zip(lg, lf))
+    print("%s (ggml): G-F %.3g  P-F %.3g  G-E %.3g  F-E %.3g; greedy ids equal %d / %d" % (
+        name, r["gf"], r["pf"], r["ge"], r["fe"], same, len(lg)), flush=True)
+    assert abs(r["ge"] - r["fe"]) <= 0.1 * r["fe"], r
+    assert r["gf"] <= 0.25 * r["fe"], r
+    assert same == len(lg)
+
+
+def test_c2_bench_shape_decode_pass_ggml():
+    hp, w = models.build("c2", seed=41, n_layer=1, init="normal")
+    ctx = bench_contexts(20261201, 64, 128, 4096, hp["n_vocab"])
+    check_ggml(*decode_pass(hp, w, ctx, 42, ggml=True), "c2 width, 64 slots")
+
+
+def test_c5_bench_shape_decode_pass_ggml():
+    hp, w = models.build("c5", seed=51, n_layer=1, init="normal")
+    ctx = bench_contexts(20261201, 64, 256, 8192, hp["n_vocab"])
+    check_ggml(*decode_pass(hp, w, ctx, 52, ggml=True), "c5 width, 64 slots")
+
+
+def test_c4_bench_shape_decode_pass_ggml():
+    from lgml_amd import workload
+    shape = dict(models.SHAPES["c4"], swa_period=2)
+    hp, w = models.build(shape, seed=61, n_layer=2, init="normal")
+    hp["n_swa"] = shape["n_swa"]
+    ctx = bench_contexts(20261201, 32, 1024, 16384, hp["n_vocab"])
+    R = workload.ring_blocks(hp, 1)
+    check_ggml(*decode_pass(hp, w, ctx, 62, ring_blocks=R, ggml=True),
+               "c4 width, 32 slots, sliding + global")
