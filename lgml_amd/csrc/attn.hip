@@ -51,20 +51,87 @@ struct Partial {
   static constexpr int floats = ROWS * D + 2 * ROWS;
 };
 
+// The Q8_K blocks of the output product's X (ggml's arithmetic) from the
+// rows of an item in one run: a block (256 values) is 256 / D heads of one
+// token, rows row .. of one row group and all four quads: value
+// (row % HB) D + 16 dt + 4 quad + i of the block. The same steps as
+// q8k_block8 (largest |x| and its first occurrence, iscale = -127 / max,
+// q = min(127, nearest-even(iscale x)), d = 1 / iscale, the 16 sums of 16
+// q); every lane takes part in the reductions, lanes of rows past the
+// item's store nothing.
+template <int D>
+__device__ __forceinline__ void finish_q8k(const f32x4 (&o)[D / 16], float l, bool rvalid,
+                                           int64_t n, int rhead, int H, int row, int quad,
+                                           f16 *__restrict__ planes, int64_t npad) {
+  constexpr int DT = D / 16, HB = 256 / D;
+  const int64_t K = (int64_t)H * D;
+  f32x4 y[DT];
+  float amax = 0.0f, mx = 0.0f;
+  int at = 1 << 30;
+  const int kb = (row % HB) * D + quad * 4;
+#pragma unroll
+  for (int dt = 0; dt < DT; dt++) {
+    y[dt] = o[dt] / l;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float a = fabsf(y[dt][i]);
+      if (a > amax) {
+        amax = a;
+        mx = y[dt][i];
+        at = kb + dt * 16 + i;
+      }
+    }
+  }
+#pragma unroll
+  for (int s = 1; s < HB; s <<= 1) q8k_amax_step(amax, mx, at, s);
+  q8k_amax_step(amax, mx, at, 16);
+  q8k_amax_step(amax, mx, at, 32);
+  const float iscale = amax == 0.0f ? 0.0f : -127.0f / mx;
+  const int64_t col = (int64_t)rhead * D + quad * 4;
+  f16 *qrow = planes + n * K;
+  f16 *bsrow = planes + q8_bs_off(npad, K) + n * (K / 16);
+#pragma unroll
+  for (int dt = 0; dt < DT; dt++) {
+    float qv[4], s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      qv[i] = amax == 0.0f ? 0.0f : fminf(127.0f, __builtin_rintf(iscale * y[dt][i]));
+      s += qv[i];
+    }
+    s += __shfl_xor(s, 16);
+    s += __shfl_xor(s, 32);
+    if (rvalid) {
+      *(f16x4 *)(qrow + col + dt * 16) = f16x4{(f16)qv[0], (f16)qv[1], (f16)qv[2], (f16)qv[3]};
+      if (quad == 0) bsrow[(col + dt * 16) >> 4] = (f16)s;
+    }
+  }
+  if (rvalid && quad == 0 && row % HB == 0) {
+    float *dp = (float *)((char *)planes + q8_d_off(npad, K));
+    dp[n * (K / 256) + (int64_t)rhead * D / 256] = amax == 0.0f ? 0.0f : 1.0f / iscale;
+  }
+}
+
 // The end of a work item: lane holds O^T[d = dt*16 + quad*4 + i][row].
 // A group in one run writes o / l (as the merge divides: a token's output
 // does not depend on whether its group was split) to out or, with planes,
-// to the split planes of the output product's X; a run of a split group
-// writes its partial state (rows in use only) for the merge.
+// to the output product's X in the form xf (split planes, or Q8_K blocks);
+// a run of a split group writes its partial state (rows in use only) for
+// the merge.
 template <int D>
 __device__ __forceinline__ void finish_item(const f32x4 (&o)[D / 16], float m, float l, int mg,
                                             bool rvalid, int tok0, int rtok, int rhead, int ntok,
                                             int G, int row, int quad, int item, int kvh, int Hkv,
                                             int H, float *__restrict__ out,
-                                            f16 *__restrict__ planes, int64_t npad,
+                                            f16 *__restrict__ planes, int64_t npad, int xf,
                                             float *__restrict__ part) {
   constexpr int DT = D / 16;
   if (mg < 0) {
+    if constexpr (D >= 64) {
+      if (planes && xf == XF_Q8K) {  // wave-uniform
+        finish_q8k<D>(o, l, rvalid, tok0 + rtok, rhead, H, row, quad, planes, npad);
+        return;
+      }
+    }
     if (rvalid) {
       const int64_t n = tok0 + rtok;
       if (planes) {
@@ -115,7 +182,7 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
                   const int32_t *__restrict__ items, const int32_t *__restrict__ seq_off,
                   const int32_t *__restrict__ seq_npast, const int32_t *__restrict__ block_tab,
                   int max_blocks, int ring, int window, float *__restrict__ out,
-                  f16 *__restrict__ planes, int64_t npad, float *__restrict__ part,
+                  f16 *__restrict__ planes, int64_t npad, int xf, float *__restrict__ part,
                   const int32_t *__restrict__ order, int n_order) {
   // MFMA k-steps over D; a head of 16 takes one step of 32 whose upper
   // half is zero in K and Q (the lanes of quads 2 and 3 load nothing)
@@ -313,7 +380,7 @@ paged_attn_kernel(const float *__restrict__ q, int H, int Hkv, float scale_log2,
     if (blo < bhi) block(bhi - 1, std::false_type{});
 
   finish_item<D>(o, m, l, mg, rvalid, tok0, rtok, rhead, ntok, G, row, quad, item, kvh, Hkv, H,
-                 out, planes, npad, part);
+                 out, planes, npad, xf, part);
 }
 
 // Shared runs (a prompt chunk's query groups in sets, lgmlh_plan): one
@@ -345,7 +412,7 @@ paged_attn_shared_kernel(const float *__restrict__ q, int H, int Hkv, float scal
                          const int32_t *__restrict__ seq_off, const int32_t *__restrict__ seq_npast,
                          const int32_t *__restrict__ block_tab, int max_blocks,
                          float *__restrict__ out, f16 *__restrict__ planes, int64_t npad,
-                         float *__restrict__ part) {
+                         int xf, float *__restrict__ part) {
   constexpr int KS = D / 32, DT = D / 16;
   constexpr int TILE = 64 * D;             // f16 of one K (or V) tile
   constexpr int KC = D / 8;                // 16-byte chunks per K row
@@ -517,7 +584,7 @@ paged_attn_shared_kernel(const float *__restrict__ q, int H, int Hkv, float scal
   }
   if (!active) return;
   finish_item<D>(o, m, l, mg, rvalid, tok0, rtok, rhead, ntok, G, row, quad, item, kvh, Hkv, H,
-                 out, planes, npad, part);
+                 out, planes, npad, xf, part);
 }
 
 // Fixed-order merge of the splits of one token group (merge group: first
@@ -528,7 +595,7 @@ paged_attn_shared_kernel(const float *__restrict__ q, int H, int Hkv, float scal
 template <int D>
 __global__ void __launch_bounds__(64)
 merge_kernel(const int32_t *__restrict__ merge, int H, int Hkv, const float *__restrict__ part,
-             float *__restrict__ out, f16 *__restrict__ planes, int64_t npad) {
+             float *__restrict__ out, f16 *__restrict__ planes, int64_t npad, int xf) {
   constexpr int WMAX = 64;  // splits whose weights are kept in LDS
   __shared__ float wsh[WMAX * ROWS], lsh[2 * ROWS];
   const int lane = threadIdx.x, mg = blockIdx.x, kvh = blockIdx.y;
@@ -609,7 +676,39 @@ merge_kernel(const int32_t *__restrict__ merge, int H, int Hkv, const float *__r
       const int r = rr[jj], d0 = dd[jj];
       const f32x4 y = acc[jj] / lsh[r];
       const int64_t n = tok0 + r / G, k = (int64_t)(kvh * G + r % G) * D + d0;
-      if (planes) {
+      if (planes && xf == XF_Q8K) {
+        // the 64 lanes hold one Q8_K block (whole chunks: G D % 256 == 0),
+        // value 4 lane + i of the block; the steps of finish_q8k
+        const int64_t K = (int64_t)H * D;
+        float amax = 0.0f, mx = 0.0f;
+        int at = 1 << 30;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float a = fabsf(y[i]);
+          if (a > amax) {
+            amax = a;
+            mx = y[i];
+            at = 4 * lane + i;
+          }
+        }
+#pragma unroll
+        for (int s = 1; s < 64; s <<= 1) q8k_amax_step(amax, mx, at, s);
+        const float iscale = amax == 0.0f ? 0.0f : -127.0f / mx;
+        float qv[4], s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          qv[i] = amax == 0.0f ? 0.0f : fminf(127.0f, __builtin_rintf(iscale * y[i]));
+          s += qv[i];
+        }
+        s += __shfl_xor(s, 1);
+        s += __shfl_xor(s, 2);
+        *(f16x4 *)(planes + n * K + k) = f16x4{(f16)qv[0], (f16)qv[1], (f16)qv[2], (f16)qv[3]};
+        if ((lane & 3) == 0) planes[q8_bs_off(npad, K) + n * (K / 16) + (k >> 4)] = (f16)s;
+        if (lane == 0) {
+          float *dp = (float *)((char *)planes + q8_d_off(npad, K));
+          dp[n * (K / 256) + (k >> 8)] = amax == 0.0f ? 0.0f : 1.0f / iscale;
+        }
+      } else if (planes) {
         // 8 lanes hold a 32-value group
         const int64_t K = (int64_t)H * D;
         const float v[4] = {y[0], y[1], y[2], y[3]};
@@ -638,42 +737,49 @@ extern "C" size_t lgmlh_attention_workspace(const lgmlh_plan_info *info, int hea
 template <int D>
 static void launch_attn(const float *q, int H, int Hkv, float scale_log2, const void *kp,
                         const void *vp, const lgmlh_ubatch *ub, float *out, f16 *planes,
-                        int64_t npad, float *part, hipStream_t st) {
+                        int64_t npad, int xf, float *part, hipStream_t st) {
   // one workgroup per (item, KV head), the items on their own in the
   // plan's order
   if (ub->ring > 0)
     hipLaunchKernelGGL((paged_attn_kernel<D, true>), dim3((uint32_t)ub->n_single * Hkv),
                        dim3(64), 0, st, q, H, Hkv, scale_log2, (const uint16_t *)kp,
                        (const uint16_t *)vp, ub->items, ub->seq_off, ub->seq_npast, ub->block_tab,
-                       ub->max_blocks, ub->ring, ub->window, out, planes, npad, part, ub->order,
-                       ub->n_single);
+                       ub->max_blocks, ub->ring, ub->window, out, planes, npad, xf, part,
+                       ub->order, ub->n_single);
   // heads of 256, and of 32 or less, run the shared runs' items with the
   // per-item kernel too
   else if (const int n1 = D <= 128 && D >= 64 ? ub->n_single : ub->n_items; n1 > 0)
     hipLaunchKernelGGL((paged_attn_kernel<D, false>), dim3((uint32_t)n1 * Hkv), dim3(64), 0, st,
                        q, H, Hkv, scale_log2, (const uint16_t *)kp, (const uint16_t *)vp,
                        ub->items, ub->seq_off, ub->seq_npast, ub->block_tab, ub->max_blocks, 0,
-                       0, out, planes, npad, part, ub->order, ub->n_single);
+                       0, out, planes, npad, xf, part, ub->order, ub->n_single);
   if (ub->ring == 0 && ub->n_shared > 0) {
     if constexpr (D <= 128 && D >= 64)
       hipLaunchKernelGGL(paged_attn_shared_kernel<D>, dim3(ub->n_shared, Hkv),
                          dim3(64 * SHARED_WAVES), 0, st, q, H, Hkv, scale_log2,
                          (const uint16_t *)kp, (const uint16_t *)vp, ub->items, ub->shared,
                          ub->seq_off, ub->seq_npast, ub->block_tab, ub->max_blocks, out, planes,
-                         npad, part);
+                         npad, xf, part);
   }
   if (ub->n_merge > 0)
     hipLaunchKernelGGL(merge_kernel<D>, dim3(ub->n_merge, Hkv), dim3(64), 0, st, ub->merge, H,
-                       Hkv, part, out, planes, npad);
+                       Hkv, part, out, planes, npad, xf);
 }
 
 namespace lgmlh {
-// The attention output as f32 rows (out) or, with planes set, as the split
-// planes (rows padded to npad) of the output product's X.
+// The attention output as f32 rows (out) or, with planes set, as the
+// output product's X in the form xf (rows padded to npad): XF_SPLIT split
+// planes (heads of 32 or more), or XF_Q8K blocks when a block's 256 / D
+// heads are of one KV head's group (heads of 64 or more, G % (256 / D) ==
+// 0: attn_q8k_fits).
+bool attn_q8k_fits(int head_dim, int G) {
+  return head_dim >= 64 && head_dim <= 256 && G % (256 / head_dim) == 0;
+}
+
 int paged_attention_dev(const float *q, int n_head, int n_head_kv, int head_dim, float scale,
                         const void *kpool, const void *vpool, const lgmlh_ubatch *ub, float *out,
                         f16 *planes, int64_t npad, void *workspace, size_t workspace_bytes,
-                        hipStream_t st) {
+                        hipStream_t st, int xf) {
   if (!q || !kpool || !vpool || !ub || !(out || planes) || n_head_kv <= 0 ||
       n_head % n_head_kv) {
     set_error("paged_attention: bad arguments");
@@ -694,18 +800,20 @@ int paged_attention_dev(const float *q, int n_head, int n_head_kv, int head_dim,
     set_error("paged_attention: %d items x %d KV heads in one launch", ub->n_items, n_head_kv);
     return LGMLH_EINVAL;
   }
-  if (planes && head_dim < 32) {
-    set_error("paged_attention: heads of %d write f32 rows only", head_dim);
+  if (planes && (xf == XF_SPLIT ? head_dim < 32
+                                : xf != XF_Q8K || !attn_q8k_fits(head_dim, G))) {
+    set_error("paged_attention: heads of %d (%d per KV head) cannot write X form %d", head_dim,
+              G, xf);
     return LGMLH_EINVAL;
   }
   float sl = scale * LOG2E;
   float *part = (float *)workspace;
   switch (head_dim) {
-    case 16: launch_attn<16>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, planes, npad, part, st); break;
-    case 32: launch_attn<32>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, planes, npad, part, st); break;
-    case 64: launch_attn<64>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, planes, npad, part, st); break;
-    case 128: launch_attn<128>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, planes, npad, part, st); break;
-    case 256: launch_attn<256>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, planes, npad, part, st); break;
+    case 16: launch_attn<16>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, planes, npad, xf, part, st); break;
+    case 32: launch_attn<32>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, planes, npad, xf, part, st); break;
+    case 64: launch_attn<64>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, planes, npad, xf, part, st); break;
+    case 128: launch_attn<128>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, planes, npad, xf, part, st); break;
+    case 256: launch_attn<256>(q, n_head, n_head_kv, sl, kpool, vpool, ub, out, planes, npad, xf, part, st); break;
     default:
       set_error("paged_attention: head_dim %d not supported (16, 32, 64, 128, 256)", head_dim);
       return LGMLH_EINVAL;
@@ -723,5 +831,5 @@ extern "C" int lgmlh_paged_attention(const float *q, int n_head, int n_head_kv, 
     return LGMLH_EINVAL;
   }
   return paged_attention_dev(q, n_head, n_head_kv, head_dim, scale, kpool, vpool, ub, out,
-                             nullptr, 0, workspace, workspace_bytes, as_stream(stream));
+                             nullptr, 0, workspace, workspace_bytes, as_stream(stream), XF_SPLIT);
 }

@@ -17,7 +17,8 @@ int mul_mat_f32(const float *w, int64_t M, int64_t K, const float *x, int64_t N,
 int paged_attention_dev(const float *q, int n_head, int n_head_kv, int head_dim, float scale,
                         const void *kpool, const void *vpool, const lgmlh_ubatch *ub, float *out,
                         f16 *planes, int64_t npad, void *workspace, size_t workspace_bytes,
-                        hipStream_t st);
+                        hipStream_t st, int xf);
+bool attn_q8k_fits(int head_dim, int G);
 int rms_norm_dev(float *x, const int32_t *rows, int64_t n_rows, int64_t n, float eps,
                  const float *w, float *out, f16 *planes, hipStream_t st, Pending pend,
                  bool writeback, int xf);
@@ -438,15 +439,19 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
                                  m->eps, ub->pos, L.kpool, L.vpool,
                                  L.swa ? m->ring_cells : m->n_cells, lub->cells, q, st, p_qk, p_v,
                                  vmode));
-    // a quantized output product takes its X as split planes, written by
-    // the attention (and merge) kernels themselves; ggml's Q8 blocks are
-    // made from the f32 rows by a kernel of their own
-    const bool oq = isq(L.wo_type), o_split = oq && xfo(L.wo_type) == XF_SPLIT && d.D >= 32;
+    // a quantized output product takes its X (split planes, or ggml's Q8_K
+    // blocks when a block's heads are of one KV head's group) from the
+    // attention (and merge) kernels themselves; other forms are made from
+    // the f32 rows by a kernel of their own
+    const int xo = xfo(L.wo_type);
+    const bool oq = isq(L.wo_type),
+               o_split = oq && (xo == XF_SPLIT ? d.D >= 32
+                                               : xo == XF_Q8K && attn_q8k_fits(d.D, (int)z.H / d.Hkv));
     {
       Span sp(trace, LGMLH_TRACE_ATTN, st);
       LGMLH_TRY(paged_attention_dev(q, (int)z.H, d.Hkv, d.D, scale, L.kpool, L.vpool,
                                     lub, o_split ? nullptr : att, o_split ? xs : nullptr,
-                                    split_npad(z.N), aws, z.attn_ws, st));
+                                    split_npad(z.N), aws, z.attn_ws, st, xo));
     }
     if (oq && !o_split)
       LGMLH_TRY(split_x(att, LGMLH_F32, z.N, z.H * d.D, xs, st, xfo(L.wo_type)));

@@ -90,6 +90,19 @@ __host__ __device__ inline size_t q8_d_off(int64_t Npad, int64_t K) {  // bytes
   return (size_t)Npad * K * 2 + (size_t)Npad * (K / 16) * 2;
 }
 
+// One step of a Q8_K block's maximum across lanes (quantize_row_q8_K: the
+// value of largest |x|, ties to its first occurrence in the block): amax,
+// the signed value and its index in the block, merged with lane ^ o.
+__device__ __forceinline__ void q8k_amax_step(float &amax, float &mx, int &at, int o) {
+  const float a2 = __shfl_xor(amax, o), m2 = __shfl_xor(mx, o);
+  const int i2 = __shfl_xor(at, o);
+  if (a2 > amax || (a2 == amax && i2 < at)) {
+    amax = a2;
+    mx = m2;
+    at = i2;
+  }
+}
+
 // quantize_row_q8_K of one 256-value block held by 32 lanes (lane j of the
 // group: values 8j .. 8j + 7). amax = the largest |x|, its first occurrence
 // gives the signed max; iscale = -127 / max; q = min(127, nearest-even(iscale
@@ -109,15 +122,7 @@ __device__ __forceinline__ void q8k_block8(const float (&v)[8], int j, float (&q
     }
   }
 #pragma unroll
-  for (int o = 1; o < 32; o <<= 1) {
-    const float a2 = __shfl_xor(amax, o), m2 = __shfl_xor(mx, o);
-    const int i2 = __shfl_xor(at, o);
-    if (a2 > amax || (a2 == amax && i2 < at)) {
-      amax = a2;
-      mx = m2;
-      at = i2;
-    }
-  }
+  for (int o = 1; o < 32; o <<= 1) q8k_amax_step(amax, mx, at, o);
   float s = 0.0f;
   if (amax == 0.0f) {
 #pragma unroll
