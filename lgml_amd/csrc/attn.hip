@@ -111,6 +111,42 @@ __device__ __forceinline__ void finish_q8k(const f32x4 (&o)[D / 16], float l, bo
   }
 }
 
+// The Q8_0 blocks of the output product's X (ggml's arithmetic, a Q8_0
+// output matrix) from the rows of an item in one run: block g of a head is
+// its d tiles 2g and 2g + 1, held by the row's four quads; the steps of
+// q80_block8 (d = amax / 127, q = roundf(x / d), d kept as f16).
+template <int D>
+__device__ __forceinline__ void finish_q80(const f32x4 (&o)[D / 16], float l, bool rvalid,
+                                           int64_t n, int rhead, int H, int quad,
+                                           f16 *__restrict__ planes, int64_t npad) {
+  constexpr int DT = D / 16;
+  const int64_t K = (int64_t)H * D;
+  float *dp = (float *)((char *)planes + q8_d_off(npad, K));
+#pragma unroll
+  for (int g = 0; g < DT / 2; g++) {
+    const f32x4 y0 = o[2 * g] / l, y1 = o[2 * g + 1] / l;
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) amax = fmaxf(amax, fmaxf(fabsf(y0[i]), fabsf(y1[i])));
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    const float dd = amax / 127.0f;
+    const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+    if (rvalid) {
+      const int64_t col = (int64_t)rhead * D + 32 * g + quad * 4;
+      f16x4 h0, h1;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        h0[i] = (f16)__builtin_roundf(y0[i] * id);
+        h1[i] = (f16)__builtin_roundf(y1[i] * id);
+      }
+      *(f16x4 *)(planes + n * K + col) = h0;
+      *(f16x4 *)(planes + n * K + col + 16) = h1;
+      if (quad == 0) dp[n * (K / 32) + (col >> 5)] = (float)(f16)dd;
+    }
+  }
+}
+
 // The end of a work item: lane holds O^T[d = dt*16 + quad*4 + i][row].
 // A group in one run writes o / l (as the merge divides: a token's output
 // does not depend on whether its group was split) to out or, with planes,
@@ -129,6 +165,12 @@ __device__ __forceinline__ void finish_item(const f32x4 (&o)[D / 16], float m, f
     if constexpr (D >= 64) {
       if (planes && xf == XF_Q8K) {  // wave-uniform
         finish_q8k<D>(o, l, rvalid, tok0 + rtok, rhead, H, row, quad, planes, npad);
+        return;
+      }
+    }
+    if constexpr (D >= 32) {
+      if (planes && xf == XF_Q80) {
+        finish_q80<D>(o, l, rvalid, tok0 + rtok, rhead, H, quad, planes, npad);
         return;
       }
     }
@@ -708,6 +750,22 @@ merge_kernel(const int32_t *__restrict__ merge, int H, int Hkv, const float *__r
           float *dp = (float *)((char *)planes + q8_d_off(npad, K));
           dp[n * (K / 256) + (k >> 8)] = amax == 0.0f ? 0.0f : 1.0f / iscale;
         }
+      } else if (planes && xf == XF_Q80) {
+        // 8 lanes hold a Q8_0 block (32 values); the steps of q80_block8
+        const int64_t K = (int64_t)H * D;
+        float amax = fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3])));
+        amax = fmaxf(amax, __shfl_xor(amax, 1));
+        amax = fmaxf(amax, __shfl_xor(amax, 2));
+        amax = fmaxf(amax, __shfl_xor(amax, 4));
+        const float dd = amax / 127.0f;
+        const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+        *(f16x4 *)(planes + n * K + k) =
+            f16x4{(f16)__builtin_roundf(y[0] * id), (f16)__builtin_roundf(y[1] * id),
+                  (f16)__builtin_roundf(y[2] * id), (f16)__builtin_roundf(y[3] * id)};
+        if ((e4 & 7) == 0) {
+          float *dp = (float *)((char *)planes + q8_d_off(npad, K));
+          dp[n * (K / 32) + (k >> 5)] = (float)(f16)dd;
+        }
       } else if (planes) {
         // 8 lanes hold a 32-value group
         const int64_t K = (int64_t)H * D;
@@ -769,9 +827,9 @@ static void launch_attn(const float *q, int H, int Hkv, float scale_log2, const 
 namespace lgmlh {
 // The attention output as f32 rows (out) or, with planes set, as the
 // output product's X in the form xf (rows padded to npad): XF_SPLIT split
-// planes (heads of 32 or more), or XF_Q8K blocks when a block's 256 / D
-// heads are of one KV head's group (heads of 64 or more, G % (256 / D) ==
-// 0: attn_q8k_fits).
+// planes or XF_Q80 blocks (heads of 32 or more), or XF_Q8K blocks when a
+// block's 256 / D heads are of one KV head's group (heads of 64 or more,
+// G % (256 / D) == 0: attn_q8k_fits).
 bool attn_q8k_fits(int head_dim, int G) {
   return head_dim >= 64 && head_dim <= 256 && G % (256 / head_dim) == 0;
 }
@@ -800,8 +858,7 @@ int paged_attention_dev(const float *q, int n_head, int n_head_kv, int head_dim,
     set_error("paged_attention: %d items x %d KV heads in one launch", ub->n_items, n_head_kv);
     return LGMLH_EINVAL;
   }
-  if (planes && (xf == XF_SPLIT ? head_dim < 32
-                                : xf != XF_Q8K || !attn_q8k_fits(head_dim, G))) {
+  if (planes && (xf == XF_Q8K ? !attn_q8k_fits(head_dim, G) : head_dim < 32)) {
     set_error("paged_attention: heads of %d (%d per KV head) cannot write X form %d", head_dim,
               G, xf);
     return LGMLH_EINVAL;

@@ -439,14 +439,13 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
                                  m->eps, ub->pos, L.kpool, L.vpool,
                                  L.swa ? m->ring_cells : m->n_cells, lub->cells, q, st, p_qk, p_v,
                                  vmode));
-    // a quantized output product takes its X (split planes, or ggml's Q8_K
-    // blocks when a block's heads are of one KV head's group) from the
-    // attention (and merge) kernels themselves; other forms are made from
-    // the f32 rows by a kernel of their own
+    // a quantized output product takes its X (split planes, ggml's Q8_0
+    // blocks, or its Q8_K blocks when a block's heads are of one KV head's
+    // group) from the attention (and merge) kernels themselves; heads too
+    // small for that have theirs made from the f32 rows
     const int xo = xfo(L.wo_type);
     const bool oq = isq(L.wo_type),
-               o_split = oq && (xo == XF_SPLIT ? d.D >= 32
-                                               : xo == XF_Q8K && attn_q8k_fits(d.D, (int)z.H / d.Hkv));
+               o_split = oq && (xo == XF_Q8K ? attn_q8k_fits(d.D, (int)z.H / d.Hkv) : d.D >= 32);
     {
       Span sp(trace, LGMLH_TRACE_ATTN, st);
       LGMLH_TRY(paged_attention_dev(q, (int)z.H, d.Hkv, d.D, scale, L.kpool, L.vpool,
