@@ -815,6 +815,413 @@ qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__r
     emit(out, ld_out, false, nz == 1 && residual);
 }
 
+// ---- decode-sized products: the weights stream through LDS ----------------------
+// At N <= 64 columns in ggml arithmetic, qstream_kernel keeps two K steps of
+// weights in flight per wave at all times: they travel by global-to-LDS
+// loads (no registers held) into a ring of two LDS stages per wave; at each
+// step boundary a wave reads the next step's weights from the ring into
+// registers and sends the loads of the step after next into the stage it
+// just read. X is double-buffered in LDS as in qgemm_kernel. A wave waits
+// for its own loads of the next step only (s_waitcnt vmcnt leaving the
+// younger loads of the step after in flight), then one barrier publishes
+// the next step's X. (qgemm_kernel waits for every load in flight at each
+// step, the next step's weights included.)
+//
+// One workgroup of 8 waves per CU, one 16-row tile per wave (LDS at 64
+// columns: Q4_K 106.5 KB, Q6_K 117 KB, Q8_0 136 KB). Measured on the
+// MI355X, the kernel is bound by issue, not by its bytes: a copy with its
+// loads taken out runs as long, and the fragment builds and scale flushes
+// (about 4.5 VALU instructions per MFMA) co-issue with the MFMAs only in
+// part. Each 16-row tile takes the fragments, MFMAs, K steps, split ranges
+// and scale flushes of qgemm_kernel's ggml mode in the same order, so a
+// product gives the same bits through either kernel.
+// Workgroup shape: WV waves of R row tiles each.
+__host__ __device__ constexpr int qs_waves(int type) { return 8; }
+__host__ __device__ constexpr int qs_rt(int type) { return 1; }
+// One wave's stage: the chunk headers of its tiles (16-byte slots), then
+// each tile's lane data as planes of 64 x 16 B (plane p holds bytes 16 p ..
+// 16 p + 15 of every lane's record, so a lane's 16-byte read of a plane is
+// conflict-free).
+__host__ __device__ constexpr int qs_hslots(int type) { return chunk_hdr(type) / 16; }
+__host__ __device__ constexpr int qs_planes(int type) { return lane_bytes(type) / 16; }
+__host__ __device__ constexpr int qs_stage_slots(int type, int R) {
+  return R * (qs_hslots(type) + 64 * qs_planes(type));
+}
+
+// s_waitcnt with only the vector-memory counter (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt and lgkmcnt at their maxima).
+#define LGMLH_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+// A workgroup barrier that waits for nothing itself: __syncthreads()'s
+// fence would wait for every load in flight (vmcnt(0)), the younger
+// weight loads included. The global-to-LDS loads a barrier publishes are
+// waited for before it with LGMLH_WAIT_VMCNT; the empty asm statements
+// keep the compiler from moving memory operations across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Global-to-LDS loads of 16 (4) bytes per lane into lds + 16 (4) * lane,
+// issued as inline assembly. The compiler's wait insertion tells such
+// loads' targets apart only for a few LDS objects with precise alias
+// information; here, where it cannot, it would wait for every load in
+// flight before each LDS read. qstream_kernel waits for its loads itself
+// (LGMLH_WAIT_VMCNT, then a barrier), and the compiler's own waits for
+// other memory operations stay correct: these loads only add to the
+// counter it waits on.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const void *g, const void *lds) {
+  const uint32_t l = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)lds;
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(g), "s"(l) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma4(const void *g, const void *lds) {
+  const uint32_t l = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)lds;
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(g), "s"(l) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// A wave's weights of one K step for R row tiles (chunks at wt[a] + ko)
+// into its stage region `mine`: the R * HS header slots (64 per load), then
+// R * NP planes. stage_loads() global-to-LDS loads per wave.
+template <int TYPE, int R>
+__host__ __device__ constexpr int stage_loads() {
+  return (R * qs_hslots(TYPE) + 63) / 64 + R * qs_planes(TYPE);
+}
+template <int TYPE, int R>
+__device__ __forceinline__ void stage_w(const uint8_t *const (&wt)[R], uint32_t ko, u32x4 *mine,
+                                        int lane) {
+  constexpr int HS = qs_hslots(TYPE), NP = qs_planes(TYPE), NHI = (R * HS + 63) / 64;
+#pragma unroll
+  for (int h = 0; h < NHI; h++) {
+    const int sl = 64 * h + lane;
+    if (sl < R * HS) {
+      const int a = R == 1 ? 0 : sl / HS;
+      lds_dma16(wt[a] + ko + 16 * (sl - a * HS), mine + 64 * h);
+    }
+  }
+#pragma unroll
+  for (int a = 0; a < R; a++)
+#pragma unroll
+    for (int p = 0; p < NP; p++)
+      lds_dma16(wt[a] + ko + chunk_hdr(TYPE) + lane * lane_bytes(TYPE) + 16 * p,
+                mine + R * HS + (a * NP + p) * 64);
+}
+// The WFrag fields of R tiles from a stage region (Q8_0 also the d of the
+// lane's rows, 8 blocks: bytes 64 c .. 64 c + 63 of the header, into q8d).
+template <int TYPE, int R>
+__device__ __forceinline__ void read_stage(const u32x4 *mine, int lane, WFrag<TYPE> (&cur)[R],
+                                           u32x4 (&q8d)[R][4]) {
+  constexpr int HS = qs_hslots(TYPE), NP = qs_planes(TYPE);
+  const int c = lane >> 4, r16 = lane & 15;
+#pragma unroll
+  for (int a = 0; a < R; a++) {
+    const u32x4 *hdr = mine + a * HS, *pl = mine + R * HS + a * NP * 64 + lane;
+    if constexpr (TYPE == LGMLH_Q4_K) {
+      cur[a].dm = hdr[c];
+      const uint32_t *sp = (const uint32_t *)hdr + 16 + 3 * r16;
+      cur[a].s0 = sp[0];
+      cur[a].s1 = sp[1];
+      cur[a].s2 = sp[2];
+      cur[a].qs[0] = pl[0];
+      cur[a].qs[1] = pl[64];
+    } else if constexpr (TYPE == LGMLH_Q6_K) {
+      cur[a].d4 = ((const u32x2 *)hdr)[c];
+      cur[a].scl = hdr[2 + r16];
+      cur[a].ql[0] = pl[0];
+      cur[a].ql[1] = pl[64];
+      cur[a].qh = pl[128];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        cur[a].qs[i] = pl[64 * i];
+        q8d[a][i] = hdr[4 * c + i];
+      }
+    }
+  }
+}
+
+template <int TYPE, int NCT, int WV, int R>
+__global__ void __launch_bounds__(WV * 64, 1)
+qstream_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__restrict__ xs,
+               int64_t Npad, int64_t N, float *__restrict__ y, int64_t ldy,
+               const float *__restrict__ residual, int nz, int sb_per_split,
+               float *__restrict__ part) {
+  constexpr int SS = qs_stage_slots(TYPE, R);  // slots of one wave's stage
+  constexpr int COLS = NCT * 16, X_SLOTS = COLS * 32;
+  constexpr int DX_SLOTS = TYPE == LGMLH_Q8_0 ? 128 : 16;
+  constexpr int GS_SLOTS = TYPE == LGMLH_Q4_K ? 128 : 1;
+  // Two weight stages and two X buffers, each of the latter holding the q
+  // slots, then (Q4_K) the sums of 16 q, then the d.
+  constexpr int XB_SLOTS = X_SLOTS + GS_SLOTS + DX_SLOTS;
+  __shared__ __align__(16) u32x4 ws0_[WV * SS], ws1_[WV * SS];
+  __shared__ __align__(16) u32x4 x0_[XB_SLOTS], x1_[XB_SLOTS];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane >> 4, r16 = lane & 15;
+  const int64_t NSB = K / QK_K, MT = (M + 15) / 16;
+  const int z = (int)blockIdx.y;
+  const int64_t sb_lo = (int64_t)z * sb_per_split;
+  const int64_t sb_hi = sb_lo + sb_per_split < NSB ? sb_lo + sb_per_split : NSB;
+  const uint32_t nsteps = (uint32_t)(sb_hi - sb_lo);
+  const int64_t rt0 = ((int64_t)blockIdx.x * WV + wave) * R;
+  const uint8_t *wt[R];
+#pragma unroll
+  for (int a = 0; a < R; a++) {
+    const int64_t rt = rt0 + a < MT ? rt0 + a : MT - 1;  // computed, never stored
+    wt[a] = w + (rt * NSB + sb_lo) * chunk_bytes(TYPE);
+  }
+  // X: the plane slots as qgemm_kernel stages them (piece kp of column n at
+  // slot n * 32 + (kp ^ (n & 15))), XJ loads of 64 slots per wave
+  // (with fewer slots than lanes, the first X_SLOTS / 64 waves load one each)
+  constexpr int XJ = X_SLOTS >= WV * 64 ? X_SLOTS / (WV * 64) : 1;
+  static_assert(X_SLOTS >= WV * 64 ? XJ * WV * 64 == X_SLOTS : X_SLOTS % 64 == 0,
+                "X slots per wave");
+  const f16 *xq = xs + sb_lo * QK_K;
+  constexpr int QB = TYPE == LGMLH_Q8_0 ? 32 : QK_K;
+  const f16 *bsp = xs + q8_bs_off(Npad, K) + sb_lo * 16;
+  const float *dxp =
+      (const float *)((const char *)xs + q8_d_off(Npad, K)) + sb_lo * (QK_K / QB);
+  uint32_t xoff[XJ];
+#pragma unroll
+  for (int j = 0; j < XJ; j++) {
+    const int sl = (wave * XJ + j) * 64 + lane, n = sl >> 5, kp = (sl & 31) ^ (n & 15);
+    xoff[j] = (uint32_t)(n * K + kp * 8) * 2u;
+  }
+  const int64_t xr_lane = lane < COLS ? lane : 0;  // gs / d: lane = column
+  const uint32_t goff = (uint32_t)(xr_lane * (K / 16)), doff = (uint32_t)(xr_lane * (K / QB));
+
+  auto load_x = [&](uint32_t kstep, u32x4 *xb) __attribute__((always_inline)) {
+    u32x4 *gb = xb + X_SLOTS, *db = xb + X_SLOTS + GS_SLOTS;
+#pragma unroll
+    for (int j = 0; j < XJ; j++)
+      if (X_SLOTS >= WV * 64 || wave < X_SLOTS / 64)
+        lds_dma16((const uint8_t *)(xq + kstep * QK_K) + xoff[j], &xb[(wave * XJ + j) * 64]);
+    if constexpr (TYPE == LGMLH_Q4_K) {
+      if (wave < 2)  // the 16 sums of 16 q: wave 0 sums 0..7, wave 1 8..15
+        lds_dma16(bsp + goff + kstep * 16 + 8 * wave, gb + 64 * wave);
+    }
+    if constexpr (TYPE != LGMLH_Q8_0) {
+      if (wave == 2)  // the Q8_K d of each column
+        lds_dma4(dxp + doff + kstep, db);
+    } else {
+      if (wave < 2)  // the d of blocks 4 wave .. 4 wave + 3 of each column
+        lds_dma16(dxp + doff + kstep * 8 + 4 * wave, db + 64 * wave);
+    }
+  };
+  constexpr int NWI = stage_loads<TYPE, R>();  // weight loads per wave and step
+  auto load_w = [&](uint32_t kstep, u32x4 *stage) __attribute__((always_inline)) {
+    stage_w<TYPE, R>(wt, kstep * (uint32_t)chunk_bytes(TYPE), stage + wave * SS, lane);
+  };
+  // Registers of the step being computed.
+  WFrag<TYPE> cur[R];
+  u32x4 q8d[R][4];
+  auto read_w = [&](const u32x4 *stage) __attribute__((always_inline)) {
+    read_stage<TYPE, R>(stage + wave * SS, lane, cur, q8d);
+  };
+
+  f32x4 acc[R][NCT];
+#pragma unroll
+  for (int a = 0; a < R; a++)
+#pragma unroll
+    for (int b = 0; b < NCT; b++) acc[a][b] = f32x4{0, 0, 0, 0};
+  const uint32_t sh6 = 8u * (uint32_t)(c >> 1);
+
+  // One K step on registers cur and the X buffers (qgemm_kernel's ggml
+  // mode: one MFMA per group and tile on the integer q; Q6_K the two exact
+  // parts; Q8_0 a flush per block; Q4_K / Q6_K the scales per step).
+  auto compute = [&](const u32x4 *xb) __attribute__((always_inline)) {
+    const u32x4 *gb = xb + X_SLOTS, *db = xb + X_SLOTS + GS_SLOTS;
+    const float *dxf = (const float *)db;
+    f32x4 cm[R][NCT];
+    f16x4 sh4[NCT];
+    if constexpr (TYPE == LGMLH_Q4_K) {
+      const f16 *gsr = (const f16 *)gb + (c < 2 ? 0 : 64 * 8) + r16 * 8 + 4 * (c & 1);
+#pragma unroll
+      for (int ct = 0; ct < NCT; ct++) sh4[ct] = *(const f16x4 *)(gsr + ct * 16 * 8);
+    }
+    uint32_t scb[R][2];
+    if constexpr (TYPE == LGMLH_Q4_K) {
+#pragma unroll
+      for (int a = 0; a < R; a++) {
+        scb[a][0] = cur[a].sc03();
+        scb[a][1] = cur[a].sc47();
+      }
+    }
+    f16x8 bh[NCT];
+    auto read_bh = [&](int g) __attribute__((always_inline)) {
+      const int slot = r16 * 32 + ((4 * g + c) ^ r16);
+#pragma unroll
+      for (int ct = 0; ct < NCT; ct++) bh[ct] = __builtin_bit_cast(f16x8, xb[ct * 16 * 32 + slot]);
+    };
+    read_bh(0);
+    f16x2 sp[R], cp[R];
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+      f16x8 af[R], af2[R], afr[R];
+      if constexpr (TYPE == LGMLH_Q4_K) {
+        if ((g & 1) == 0) {
+#pragma unroll
+          for (int a = 0; a < R; a++) cur[a].pair(g >> 1, scb[a][g >> 2], sp[a], cp[a]);
+        }
+      }
+#pragma unroll
+      for (int a = 0; a < R; a++) {
+        if constexpr (TYPE == LGMLH_Q4_K)
+          af[a] = cur[a].frag(g, sp[a], cp[a]);
+        else if constexpr (TYPE == LGMLH_Q6_K)
+          cur[a].frag(g, sh6, af[a], af2[a], afr[a]);  // afr unused
+        else
+          af[a] = cur[a].frag(g);
+      }
+#pragma unroll
+      for (int a = 0; a < R; a++)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ct++) {
+          const f32x4 c0 = (g == 0 || TYPE == LGMLH_Q8_0) ? f32x4{0, 0, 0, 0} : cm[a][ct];
+          cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bh[ct], c0, 0, 0, 0);
+        }
+      if constexpr (TYPE == LGMLH_Q6_K) {
+#pragma unroll
+        for (int a = 0; a < R; a++)
+#pragma unroll
+          for (int ct = 0; ct < NCT; ct++)
+            cm[a][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af2[a], bh[ct], cm[a][ct], 0, 0, 0);
+      }
+      if (g < 7) read_bh(g + 1);
+      if constexpr (TYPE == LGMLH_Q8_0) {
+        float dxg[NCT];
+#pragma unroll
+        for (int ct = 0; ct < NCT; ct++)
+          dxg[ct] = dxf[(g >> 2) * 256 + (ct * 16 + r16) * 4 + (g & 3)];
+#pragma unroll
+        for (int a = 0; a < R; a++) {
+          const uint32_t dlo = q8d[a][g >> 1][2 * (g & 1)], dhi = q8d[a][g >> 1][2 * (g & 1) + 1];
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const float d = h2f((uint16_t)((i < 2 ? dlo : dhi) >> (16 * (i & 1))));
+#pragma unroll
+            for (int ct = 0; ct < NCT; ct++)
+              acc[a][ct][i] = fmaf(d * dxg[ct], cm[a][ct][i], acc[a][ct][i]);
+          }
+        }
+#pragma unroll
+        for (int a = 0; a < R; a++)
+#pragma unroll
+          for (int ct = 0; ct < NCT; ct++) asm volatile("" : "+v"(acc[a][ct]));
+      }
+    }
+    if constexpr (TYPE != LGMLH_Q8_0) {
+      float dxs[NCT];
+#pragma unroll
+      for (int ct = 0; ct < NCT; ct++) dxs[ct] = dxf[ct * 16 + r16];
+      if constexpr (TYPE == LGMLH_Q4_K) {
+#pragma unroll
+        for (int a = 0; a < R; a++) {
+          const f16x4 am = cur[a].mins16(c);
+          float dd[4], dm[4];
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            dd[i] = h2f((uint16_t)cur[a].dm[i]);
+            dm[i] = h2f((uint16_t)(cur[a].dm[i] >> 16));
+          }
+#pragma unroll
+          for (int ct = 0; ct < NCT; ct++) {
+            const f32x4 mn =
+                __builtin_amdgcn_mfma_f32_16x16x16f16(am, sh4[ct], f32x4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+              acc[a][ct][i] = fmaf(dxs[ct], fmaf(dd[i], cm[a][ct][i], -(dm[i] * mn[i])),
+                                   acc[a][ct][i]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int a = 0; a < R; a++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const float d4 = 4.0f * h2f((uint16_t)(cur[a].d4[i >> 1] >> (16 * (i & 1))));
+#pragma unroll
+            for (int ct = 0; ct < NCT; ct++)
+              acc[a][ct][i] = fmaf(d4 * dxs[ct], cm[a][ct][i], acc[a][ct][i]);
+          }
+      }
+    }
+  };
+
+  // Step k (buffers of parity P = k % 2): compute on cur; then wait for this
+  // wave's loads of step k + 1 (the loads of k + 2 stay in flight), a
+  // barrier (everyone's X of k + 1 has landed, everyone is done with the X
+  // of k), read the weights of k + 1, and send the loads of X k + 2 and of
+  // the weights of k + 3 (into the stage just read).
+  auto step = [&](uint32_t k, int P) __attribute__((always_inline)) {
+    u32x4 *xb = P ? x1_ : x0_;
+    u32x4 *wn = P ? ws0_ : ws1_;  // the stage of k + 1 (and k + 3)
+    compute(xb);
+    if (k + 1 >= nsteps) return;
+    if (k + 2 < nsteps) {
+      LGMLH_WAIT_VMCNT(NWI);
+    } else {
+      LGMLH_WAIT_VMCNT(0);
+    }
+    lds_barrier();
+    read_w(wn);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the stage is read before it is reloaded
+    if (k + 2 < nsteps) load_x(k + 2, xb);
+    if (k + 3 < nsteps) load_w(k + 3, wn);
+  };
+  if (nsteps > 0) {
+    load_x(0, x0_);
+    load_w(0, ws0_);
+    if (nsteps > 1) {
+      load_w(1, ws1_);
+      LGMLH_WAIT_VMCNT(NWI);
+    } else {
+      LGMLH_WAIT_VMCNT(0);
+    }
+    lds_barrier();
+    read_w(ws0_);
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    if (nsteps > 1) load_x(1, x1_);
+    if (nsteps > 2) load_w(2, ws0_);
+  }
+  for (uint32_t k = 0; k < nsteps; k += 2) {
+    step(k, 0);
+    if (k + 1 < nsteps) step(k + 1, 1);
+  }
+
+  // acc[a][ct][i] = Y[ct * 16 + r16][(rt0 + a) * 16 + 4 c + i]
+  float *const out = nz == 1 ? y : part + (int64_t)z * N * M;
+  const int64_t ld = nz == 1 ? ldy : M;
+  const bool res = nz == 1 && residual;
+  const bool vec = (ld & 3) == 0 && ((uintptr_t)out & 15) == 0 &&
+                   (!res || ((ldy & 3) == 0 && ((uintptr_t)residual & 15) == 0));
+#pragma unroll
+  for (int a = 0; a < R; a++)
+#pragma unroll
+    for (int ct = 0; ct < NCT; ct++) {
+      const int64_t n = ct * 16 + r16, m = (rt0 + a) * 16 + 4 * c;
+      if (n >= N) continue;
+      if (vec && m + 3 < M) {
+        f32x4 v = acc[a][ct];
+        if (res) v += *(const f32x4 *)(residual + n * ldy + m);
+        *(f32x4 *)(out + n * ld + m) = v;
+        continue;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        if (m + i < M) {
+          float v = acc[a][ct][i];
+          if (res) v += residual[n * ldy + m + i];
+          out[n * ld + m + i] = v;
+        }
+    }
+}
+
 // The partial sums of a split-K product, added in the canonical order
 // (Pending::sum): pairs of splits, then the pairs in order, then the
 // residual.
@@ -886,12 +1293,13 @@ f32gemm_kernel(const float *__restrict__ w, int64_t M, int64_t K, const float *_
 // then the pairs in order, so that a workgroup may run both splits of a
 // pair itself (see launch_q) with the same result.
 constexpr int SPLIT_PAIR = 2;
+constexpr int SPLIT_ROWS = 128;  // the row unit of the split count
 int splits_for(int64_t M, int64_t K, int64_t N, int *sb_per_split = nullptr) {
   (void)N;
   const int64_t NSB = K / QK_K;
-  const int64_t tiles = (M + WG_ROWS - 1) / WG_ROWS;
-  // About one workgroup per CU (256) at 64 columns, at least 2 K steps per
-  // split so the pipeline has a step to overlap.
+  const int64_t tiles = (M + SPLIT_ROWS - 1) / SPLIT_ROWS;
+  // About one workgroup of SPLIT_ROWS rows per CU (256), at least 2 K steps
+  // per split so the pipeline has a step to overlap.
   int64_t want = (256 + tiles / 2) / tiles;
   const int64_t maxs = NSB / 2 > 1 ? NSB / 2 : 1;
   if (want > maxs) want = maxs;
@@ -925,6 +1333,32 @@ static int launch_q(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t 
   int spb = 0;
   const int splits = splits_for(M, K, N, &spb);
   const int64_t Npad = split_npad(N);
+  if constexpr (Q8) {
+    if (N <= 64) {  // decode-sized: the streamed-weight kernel, unfolded splits
+      constexpr int WV = qs_waves(TYPE), R = qs_rt(TYPE);
+      const int wrows = WV * R * 16;
+      dim3 grid((unsigned)((M + wrows - 1) / wrows), (unsigned)splits);
+#define LGMLH_STREAM(NCT_)                                                                  \
+  hipLaunchKernelGGL((qstream_kernel<TYPE, NCT_, WV, R>), grid, dim3(WV * 64), 0, st,       \
+                     (const uint8_t *)w, M, K, xs, Npad, N, y, ldy, res, splits, spb, part)
+      if (N <= 16)
+        LGMLH_STREAM(1);
+      else if (N <= 32)
+        LGMLH_STREAM(2);
+      else
+        LGMLH_STREAM(4);
+#undef LGMLH_STREAM
+      *group = SPLIT_PAIR;
+      if (splits > 1 && !defer) {
+        int64_t total = N * M;
+        unsigned blocks = (unsigned)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
+        Pending pd{part, splits, N, M};
+        pd.group = SPLIT_PAIR;
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, st, pd, y, ldy, res);
+      }
+      return splits > 1 ? splits : 0;
+    }
+  }
   // Column tiles of 64, or of 16 / 32 for a batch that small (the same sums
   // per element: only the columns a workgroup carries change). A decode-
   // sized product (N <= 64) with fewer than 200 workgroups of rows and
