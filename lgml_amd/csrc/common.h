@@ -79,6 +79,27 @@ struct Pending {
       const float *p = part + n * cols + m0;
       const int64_t zs = rows * cols;
       int z = 0;
+      // eight partials in flight at once (all loads before the adds)
+      for (; z + 8 <= splits; z += 8, p += 8 * zs) {
+        f4 ai[8], bi[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          ai[i] = *(const f4 *)(p + i * zs);
+          bi[i] = *(const f4 *)(p + i * zs + 4);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+          if (group == 2) {
+            a += ai[i] + ai[i + 1];
+            b += bi[i] + bi[i + 1];
+          } else {
+            a += ai[i];
+            b += bi[i];
+            a += ai[i + 1];
+            b += bi[i + 1];
+          }
+        }
+      }
       if (group == 2) {
         for (; z + 4 <= splits; z += 4, p += 4 * zs) {
           const f4 a0 = *(const f4 *)p, b0 = *(const f4 *)(p + 4);
@@ -135,6 +156,21 @@ struct Pending {
       const float *p = part + n * cols + m0;
       const int64_t zs = rows * cols;
       int z = 0;
+      // eight partials in flight at once (all loads before the adds)
+      for (; z + 8 <= splits; z += 8, p += 8 * zs) {
+        f4 ai[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) ai[i] = *(const f4 *)(p + i * zs);
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+          if (group == 2) {
+            a += ai[i] + ai[i + 1];
+          } else {
+            a += ai[i];
+            a += ai[i + 1];
+          }
+        }
+      }
       if (group == 2) {
         for (; z + 2 <= splits; z += 2, p += 2 * zs) {
           const f4 a0 = *(const f4 *)p, a1 = *(const f4 *)(p + zs);
