@@ -630,16 +630,17 @@ paged_attn_shared_kernel(const float *__restrict__ q, int H, int Hkv, float scal
 }
 
 // Fixed-order merge of the splits of one token group (merge group: first
-// item, splits, first token, tokens), one wave per (group, KV head). Lane
-// r < rows finds its row's max M, the split weights w = exp2(m - M) and
-// L = sum l w; then every lane adds the split outputs of 4 columns at a
-// time (up to 4 such positions per round), weighted, in split order.
+// item, splits, first token, tokens), one wave per (group, KV head). Each
+// lane holds up to 4 positions of 4 output columns per round; for each it
+// loads, in one go per 8 splits, the split outputs with the m and l of the
+// position's row, and finds the row's max M, the split weights w = exp2(m -
+// M) and L = sum l w itself (the lanes of a row agree), adding the outputs
+// weighted, in split order. A merge of up to 8 splits is one round trip.
 template <int D>
 __global__ void __launch_bounds__(64)
 merge_kernel(const int32_t *__restrict__ merge, int H, int Hkv, const float *__restrict__ part,
              float *__restrict__ out, f16 *__restrict__ planes, int64_t npad, int xf) {
-  constexpr int WMAX = 64;  // splits whose weights are kept in LDS
-  __shared__ float wsh[WMAX * ROWS], lsh[2 * ROWS];
+  constexpr int SC = 8;  // splits per load round
   const int lane = threadIdx.x, mg = blockIdx.x, kvh = blockIdx.y;
   const int first = merge[4 * mg + 0], ns = merge[4 * mg + 1];
   const int tok0 = merge[4 * mg + 2], ntok = merge[4 * mg + 3] & 0xff;
@@ -647,76 +648,66 @@ merge_kernel(const int32_t *__restrict__ merge, int H, int Hkv, const float *__r
   const int G = H / Hkv, nrows = ntok * G;
   const float *p0 = part + ((int64_t)first * Hkv + kvh) * Partial<D>::floats;
   const int64_t pstride = (int64_t)stride * Hkv * Partial<D>::floats;
-  // Loads go out in rounds: the m and l of 8 splits, then 4 splits of 4
-  // output positions per lane (addresses clamped into range; the values
-  // past the last split are dropped), so a merge takes a few round trips.
-  if (lane < nrows) {
-    const float *ml = p0 + ROWS * D + lane;
-    float M = -INFINITY;
-    for (int s0 = 0; s0 < ns; s0 += 8) {
-      float mv[8];
-#pragma unroll
-      for (int i = 0; i < 8; i++) mv[i] = ml[(int64_t)min(s0 + i, ns - 1) * pstride];
-#pragma unroll
-      for (int i = 0; i < 8; i++) M = fmaxf(M, mv[i]);  // repeats of the last split: same max
-    }
-    float L = 0.0f;
-    for (int s0 = 0; s0 < ns; s0 += 8) {
-      float mv[8], lv[8];
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const int64_t o = (int64_t)min(s0 + i, ns - 1) * pstride;
-        mv[i] = ml[o];
-        lv[i] = ml[o + ROWS];
-      }
-#pragma unroll
-      for (int i = 0; i < 8; i++)
-        if (s0 + i < ns) {
-          const float w = exp2f(mv[i] - M);  // 0 for a split that saw no cell
-          L += lv[i] * w;
-          if (s0 + i < WMAX) wsh[(s0 + i) * ROWS + lane] = w;
-        }
-    }
-    lsh[lane] = L;
-    lsh[ROWS + lane] = M;
-  }
-  __syncthreads();
+  const float *ml = p0 + ROWS * D;  // m of row r at ml[r], l at ml[ROWS + r]
   const int n4 = nrows * (D / 4);
   for (int base = 0; base < n4; base += 4 * 64) {
+    const int nj = min(4, (n4 - base + 63) / 64);  // wave-uniform
     int rr[4], dd[4];
     f32x4 acc[4];
+    float M[4], L[4];
 #pragma unroll
     for (int jj = 0; jj < 4; jj++) {
       const int e4 = min(base + lane + 64 * jj, n4 - 1);
       rr[jj] = e4 / (D / 4);
       dd[jj] = 4 * (e4 % (D / 4));
       acc[jj] = f32x4{0, 0, 0, 0};
+      M[jj] = -INFINITY;
+      L[jj] = 0.0f;
     }
-    for (int sp = 0; sp < ns; sp += 4) {
-      f32x4 a[4][4];
+    // More than SC splits: the maxima first, over every split's m.
+    if (ns > SC)
+      for (int s0 = 0; s0 < ns; s0 += SC) {
 #pragma unroll
-      for (int jj = 0; jj < 4; jj++)
+        for (int jj = 0; jj < 4; jj++)
+          if (jj < nj) {
+            float mv[SC];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-          a[jj][i] = *(const f32x4 *)(p0 + (int64_t)min(sp + i, ns - 1) * pstride + rr[jj] * D +
-                                      dd[jj]);
+            for (int i = 0; i < SC; i++) mv[i] = ml[(int64_t)min(s0 + i, ns - 1) * pstride + rr[jj]];
 #pragma unroll
-      for (int jj = 0; jj < 4; jj++)
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-          if (sp + i < ns) {
-            const int z = sp + i, r = rr[jj];
-            const float w = z < WMAX ? wsh[z * ROWS + r]
-                                     : exp2f(p0[z * pstride + ROWS * D + r] - lsh[ROWS + r]);
-            acc[jj] += a[jj][i] * w;
+            for (int i = 0; i < SC; i++) M[jj] = fmaxf(M[jj], mv[i]);  // repeats: same max
           }
+      }
+    for (int s0 = 0; s0 < ns; s0 += SC) {
+#pragma unroll
+      for (int jj = 0; jj < 4; jj++)
+        if (jj < nj) {
+          f32x4 a[SC];
+          float mv[SC], lv[SC];
+#pragma unroll
+          for (int i = 0; i < SC; i++) {
+            const int64_t o = (int64_t)min(s0 + i, ns - 1) * pstride;
+            a[i] = *(const f32x4 *)(p0 + o + rr[jj] * D + dd[jj]);
+            mv[i] = ml[o + rr[jj]];
+            lv[i] = ml[o + ROWS + rr[jj]];
+          }
+          if (ns <= SC)
+#pragma unroll
+            for (int i = 0; i < SC; i++) M[jj] = fmaxf(M[jj], mv[i]);
+#pragma unroll
+          for (int i = 0; i < SC; i++)
+            if (s0 + i < ns) {
+              const float w = exp2f(mv[i] - M[jj]);  // 0 for a split that saw no cell
+              L[jj] += lv[i] * w;
+              acc[jj] += a[i] * w;
+            }
+        }
     }
 #pragma unroll
     for (int jj = 0; jj < 4; jj++) {
       const int e4 = base + lane + 64 * jj;
-      if (e4 >= n4) continue;  // groups of 8 lanes (D / 4 is a multiple of 8) leave together
+      if (jj >= nj || e4 >= n4) continue;  // groups of 8 lanes (D / 4 is a multiple of 8) leave together
       const int r = rr[jj], d0 = dd[jj];
-      const f32x4 y = acc[jj] / lsh[r];
+      const f32x4 y = acc[jj] / L[jj];
       const int64_t n = tok0 + r / G, k = (int64_t)(kvh * G + r % G) * D + d0;
       if (planes && xf == XF_Q8K) {
         // the 64 lanes hold one Q8_K block (whole chunks: G D % 256 == 0),

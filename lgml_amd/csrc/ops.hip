@@ -77,7 +77,8 @@ __global__ void rms_norm_kernel(float *__restrict__ x, const int32_t *__restrict
   };
   // The row stays in registers: thread tid holds pieces tid + RMS_THREADS j
   // of 8 values (n % 8 == 0 and n <= 8 * RMS_THREADS * RMS_PIECES).
-  f32x4 v[RMS_PIECES][2], t[RMS_PIECES][2];
+  // The weight's pieces are loaded with the row's, not after the sum.
+  f32x4 v[RMS_PIECES][2], t[RMS_PIECES][2], wv[RMS_PIECES][2], pw[RMS_PIECES][2];
   double st = 0;
 #pragma unroll
   for (int j = 0; j < RMS_PIECES; j++) {
@@ -86,6 +87,14 @@ __global__ void rms_norm_kernel(float *__restrict__ x, const int32_t *__restrict
       const f32x4 *src = (const f32x4 *)(xr + 8 * pc);
       v[j][0] = src[0];
       v[j][1] = src[1];
+      if (w) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) wv[j][e >> 2][e & 3] = w[8 * pc + e];
+      }
+      if (pend.splits && pend.post) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) pw[j][e >> 2][e & 3] = pend.post[8 * pc + e];
+      }
       if (pend.splits) {
         // the pending product: its split sums in order
         float ps[8];
@@ -112,7 +121,7 @@ __global__ void rms_norm_kernel(float *__restrict__ x, const int32_t *__restrict
       if (pc < n / 8)
 #pragma unroll
         for (int e = 0; e < 8; e++)
-          v[j][e >> 2][e & 3] = t[j][e >> 2][e & 3] * sc_t * pend.post[8 * pc + e] + v[j][e >> 2][e & 3];
+          v[j][e >> 2][e & 3] = t[j][e >> 2][e & 3] * sc_t * pw[j][e >> 2][e & 3] + v[j][e >> 2][e & 3];
     }
   }
   double s = 0;
@@ -145,7 +154,7 @@ __global__ void rms_norm_kernel(float *__restrict__ x, const int32_t *__restrict
 #pragma unroll
       for (int e = 0; e < 8; e++) {
         y[e] = v[j][e >> 2][e & 3] * scale;
-        if (w) y[e] = y[e] * w[8 * pc + e];
+        if (w) y[e] = y[e] * wv[j][e >> 2][e & 3];
       }
       if (out)
 #pragma unroll
