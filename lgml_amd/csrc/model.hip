@@ -29,7 +29,9 @@ int qkv_rope_store_dev(float *qkv, int64_t n, int n_head, int n_head_kv, int hea
                        int neox, float freq_base, const float *freq_factors, const float *q_norm,
                        const float *k_norm, float eps, const int32_t *pos, void *kpool,
                        void *vpool, int64_t n_cells, const int64_t *cells, float *q_out,
-                       void *stream, Pending pa, Pending pb, int vmode);
+                       void *stream, Pending pa, Pending pb, int vmode, const float *table);
+int rope_table_dev(const int32_t *pos, int64_t n, int n_rot, float freq_base,
+                   const float *freq_factors, float *table, hipStream_t st);
 size_t partial_bytes(int type, int64_t M, int64_t K, int64_t N);
 int get_rows_dev(int type, const void *table, int64_t n_cols, const int32_t *ids, int64_t n,
                  float *out, hipStream_t st, float scale);
@@ -62,9 +64,22 @@ struct Sizes {
   bool moe;
   int NE, NU, tc;
   int64_t FX, P;
+  // rope angle tables of the pass: distinct settings, the widest n_rot
+  int n_rope, rot;
 };
 
 static bool isq(int type) { return type != LGMLH_F32; }
+
+// A layer's rope setting (rotated dimensions, base, frequency factors).
+struct RopeKey {
+  int n_rot;
+  float base;
+  const float *ff;
+  bool operator==(const RopeKey &o) const {
+    return n_rot == o.n_rot && base == o.base && ff == o.ff;
+  }
+};
+constexpr int MAX_ROPE = 8;  // distinct settings with a table of their own
 
 // A layer's attention shape: its own head size, KV heads and rotated
 // dimensions where it sets them (gemma's sliding and global layers differ,
@@ -80,6 +95,24 @@ static LDims dims_of(const lgmlh_model *m, const lgmlh_layer &L) {
   d.n_rot = L.n_rot > 0 ? L.n_rot : L.head_dim > 0 ? L.head_dim : m->n_rot;
   d.W = (int64_t)(m->n_head + 2 * d.Hkv) * d.D;
   return d;
+}
+
+static RopeKey rope_key(const lgmlh_model *m, const lgmlh_layer &L) {
+  return RopeKey{dims_of(m, L).n_rot, L.rope_base > 0 ? L.rope_base : m->rope_base,
+                 L.rope_freqs ? L.rope_freqs : m->rope_freqs};
+}
+
+// The distinct rope settings of the model's layers, in layer order (at most
+// MAX_ROPE: further ones make their angles in the layer's own kernel).
+static int rope_keys(const lgmlh_model *m, RopeKey (&keys)[MAX_ROPE]) {
+  int n = 0;
+  for (int il = 0; il < m->n_layer; il++) {
+    const RopeKey k = rope_key(m, m->layers[il]);
+    bool seen = false;
+    for (int j = 0; j < n; j++) seen = seen || keys[j] == k;
+    if (!seen && n < MAX_ROPE) keys[n++] = k;
+  }
+  return n;
 }
 
 // The V product of layer L takes its X planes apart from the q|k product's.
@@ -148,6 +181,11 @@ static Sizes sizes_of(const lgmlh_model *m, int64_t n_tokens, int64_t n_items, i
   if (z.P > rmax) rmax = z.P;  // the expert activations of the picks
   z.split_ws = split_bytes(rmax, kmax);
   z.attn_ws = (size_t)n_items * attn_unit * sizeof(float);
+  RopeKey keys[MAX_ROPE];
+  z.n_rope = rope_keys(m, keys);
+  z.rot = 0;
+  for (int j = 0; j < z.n_rope; j++)
+    if (keys[j].n_rot > z.rot) z.rot = keys[j].n_rot;
   return z;
 }
 
@@ -166,6 +204,7 @@ static size_t ws_bytes_of(const Sizes &z) {
   add(z.split_ws);           // X planes of the current product
   if (z.v_own) add(split_bytes(z.N, z.E));  // X planes of a V product of its own form
   add(z.attn_ws);
+  add((size_t)z.n_rope * z.N * z.rot * 4);  // rope angle tables
   add(z.gemm_ws);
   add(z.gemm_ws_v);
   if (z.moe) {
@@ -329,6 +368,7 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
   f16 *xs = (f16 *)cv.take(z.split_ws);
   f16 *xs_v = z.v_own ? (f16 *)cv.take(split_bytes(z.N, z.E)) : nullptr;
   void *aws = cv.take(z.attn_ws);
+  float *rtab = (float *)cv.take((size_t)z.n_rope * z.N * z.rot * 4);
   float *gws = (float *)cv.take(z.gemm_ws);
   float *gws_v = (float *)cv.take(z.gemm_ws_v);
   float *rpart = nullptr, *mwts = nullptr, *gu_e = nullptr, *act_e = nullptr, *y_e = nullptr;
@@ -393,6 +433,12 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
   // was made.
   LGMLH_TRY(get_rows_dev(m->tok_embd_type, m->tok_embd, z.E, ub->ids, z.N, x, st,
                          m->embd_scale));
+  // the rope angles of every token, once per setting for all its layers
+  RopeKey rkeys[MAX_ROPE];
+  const int n_rope = rope_keys(m, rkeys);
+  for (int j = 0; j < n_rope; j++)
+    LGMLH_TRY(rope_table_dev(ub->pos, z.N, rkeys[j].n_rot, rkeys[j].base, rkeys[j].ff,
+                             rtab + (size_t)j * z.N * z.rot, st));
   for (int il = 0; il < m->n_layer; il++) {
     const lgmlh_layer &L = m->layers[il];
     const LDims d = dims_of(m, L);
@@ -433,12 +479,14 @@ extern "C" int lgmlh_forward(const lgmlh_model *m, const lgmlh_ubatch *ub,
     // transformer.lua:2469-2476) and attends through the ring plan
     const lgmlh_ubatch *lub = L.swa ? ub_ring : ub;
     const int vmode = (L.v_from_k ? QKV_V_FROM_K : 0) | (m->gemma ? QKV_V_NORM : 0);
-    LGMLH_TRY(qkv_rope_store_dev(qkv, z.N, (int)z.H, d.Hkv, d.D, d.n_rot,
-                                 m->rope_neox, L.rope_base > 0 ? L.rope_base : m->rope_base,
-                                 L.rope_freqs ? L.rope_freqs : m->rope_freqs, L.q_norm, L.k_norm,
-                                 m->eps, ub->pos, L.kpool, L.vpool,
+    const RopeKey rk = rope_key(m, L);
+    const float *tab = nullptr;
+    for (int j = 0; j < n_rope; j++)
+      if (rkeys[j] == rk) tab = rtab + (size_t)j * z.N * z.rot;
+    LGMLH_TRY(qkv_rope_store_dev(qkv, z.N, (int)z.H, d.Hkv, d.D, d.n_rot, m->rope_neox, rk.base,
+                                 rk.ff, L.q_norm, L.k_norm, m->eps, ub->pos, L.kpool, L.vpool,
                                  L.swa ? m->ring_cells : m->n_cells, lub->cells, q, st, p_qk, p_v,
-                                 vmode));
+                                 vmode, tab));
     // a quantized output product takes its X (split planes, ggml's Q8_0
     // blocks, or its Q8_K blocks when a block's heads are of one KV head's
     // group) from the attention (and merge) kernels themselves; heads too

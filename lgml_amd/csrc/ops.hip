@@ -178,6 +178,29 @@ __device__ void head_rms_norm(float *v, int D, float eps, const float *w) {
   for (int i = lane; i < D; i += 64) v[i] = w ? (v[i] * scale) * w[i] : v[i] * scale;
 }
 
+// The rotation of pair i at position p: theta_0 = p, theta_{i+1} = theta_i
+// * base^(-2/n_rot) (a running f32 product, as the CPU reference's rope
+// cache), divided by the frequency factor; its cos and sin.
+__device__ __forceinline__ void rope_angle(int p, int i, float theta_scale,
+                                           const float *__restrict__ ff, float &c, float &s) {
+  float theta = (float)p;
+  for (int j = 0; j < i; j++) theta *= theta_scale;
+  const float tt = theta / (ff ? ff[i] : 1.0f);
+  c = cosf(tt);
+  s = sinf(tt);
+}
+
+// The angle table of a pass for one rope setting: row t (n_rot floats) holds
+// the cos of pairs 0 .. n_rot / 2 - 1 at position pos[t], then their sin.
+// Every layer with that setting reads it instead of making its own.
+__global__ void rope_table_kernel(const int32_t *__restrict__ pos, int n_rot, float theta_scale,
+                                  const float *__restrict__ ff, float *__restrict__ table) {
+  const int64_t t = blockIdx.x;
+  const int half = n_rot / 2, p = pos[t];
+  for (int i = threadIdx.x; i < half; i += blockDim.x)
+    rope_angle(p, i, theta_scale, ff, table[t * n_rot + i], table[t * n_rot + half + i]);
+}
+
 // One workgroup per (token, 8 heads) and one wave per head of [q | k | v]:
 // the head's values (with the pending split sums) go to LDS, then its norm
 // (q_norm / k_norm; on gemma the V norm without a weight, :1782-1784),
@@ -191,7 +214,7 @@ qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int Hkv, int D, int 
                       float eps, const int32_t *__restrict__ pos, uint16_t *__restrict__ kp,
                       uint16_t *__restrict__ vp, const int64_t *__restrict__ cells,
                       int64_t n_cells, float *__restrict__ q_out, Pending pa, Pending pb,
-                      int vmode) {
+                      int vmode, const float *__restrict__ table) {
   extern __shared__ float lds[];
   const int64_t t = blockIdx.x;
   const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -201,9 +224,8 @@ qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int Hkv, int D, int 
   float *cs_ = lds, *sn_ = lds + half, *v = lds + n_rot + wv * D;
   const bool has = h < NH;  // wave-uniform
   const bool is_q = h < H, is_k = !is_q && h < H + Hkv, is_v = h >= H + Hkv;
-  // One angle per rotated pair i, shared by every head: theta_0 = pos,
-  // theta_{i+1} = theta_i * base^(-2/n_rot) (a running f32 product, as the
-  // CPU reference's rope cache), divided by the frequency factor.
+  // One angle per rotated pair i, shared by every head (rope_angle), from
+  // the pass's table when one is given.
   // Columns of the head: [0, pa.cols) may come from pending partials pa,
   // the rest from pb; pieces of 4 (W, pa.cols, pb.cols multiples of 8).
   // A lane's first piece is loaded before the angles are made, so that the
@@ -223,13 +245,14 @@ qkv_rope_store_kernel(const float *__restrict__ qkv, int H, int Hkv, int D, int 
   float x0[4];
   const bool first = has && lane < D / 4;
   if (first) piece(lane, x0);
-  const int p = pos[t];
-  for (int i = threadIdx.x; i < half; i += blockDim.x) {
-    float theta = (float)p;
-    for (int j = 0; j < i; j++) theta *= theta_scale;
-    const float tt = theta / (ff ? ff[i] : 1.0f);
-    cs_[i] = cosf(tt);
-    sn_[i] = sinf(tt);
+  if (table) {  // the pass's angle table (rope_table_kernel): cos, then sin
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+      cs_[i] = table[t * n_rot + i];
+      sn_[i] = table[t * n_rot + half + i];
+    }
+  } else {
+    const int p = pos[t];
+    for (int i = threadIdx.x; i < half; i += blockDim.x) rope_angle(p, i, theta_scale, ff, cs_[i], sn_[i]);
   }
   if (first)
 #pragma unroll
@@ -520,13 +543,18 @@ extern "C" int lgmlh_rms_norm(const float *x, int64_t n_rows, int64_t n, float e
 }
 
 namespace lgmlh {
+// base^(-2/n_rot) rounded to f32 on the host, as the CPU reference does.
+static float rope_theta_scale(float freq_base, int n_rot) {
+  return powf(freq_base, -2.0f / (float)n_rot);
+}
+
 int qkv_rope_store_dev(float *qkv, int64_t n, int n_head, int n_head_kv,
                                     int head_dim, int n_rot, int neox, float freq_base,
                                     const float *freq_factors, const float *q_norm,
                                     const float *k_norm, float eps, const int32_t *pos,
                                     void *kpool, void *vpool, int64_t n_cells,
                                     const int64_t *cells, float *q_out, void *stream, Pending pa,
-                       Pending pb, int vmode) {
+                       Pending pb, int vmode, const float *table) {
   if (!qkv || !pos || !kpool || !vpool || !cells || !q_out || n < 0 || n_head <= 0 ||
       n_head_kv <= 0 || head_dim <= 0 || head_dim % 8 || head_dim > 1024 || n_rot <= 0 ||
       n_rot > head_dim ||
@@ -535,16 +563,23 @@ int qkv_rope_store_dev(float *qkv, int64_t n, int n_head, int n_head_kv,
     return LGMLH_EINVAL;
   }
   if (n == 0) return LGMLH_OK;
-  // base^(-2/n_rot) rounded to f32 on the host, as the CPU reference does.
-  float theta_scale = powf(freq_base, -2.0f / (float)n_rot);
+  const float theta_scale = rope_theta_scale(freq_base, n_rot);
   const size_t lds = ((size_t)QKV_HEADS * head_dim + n_rot) * sizeof(float);
   const int groups = (n_head + 2 * n_head_kv + QKV_HEADS - 1) / QKV_HEADS;
   hipLaunchKernelGGL(qkv_rope_store_kernel, dim3((unsigned)n, (unsigned)groups),
                      dim3(64 * QKV_HEADS), lds,
                      as_stream(stream), qkv, n_head, n_head_kv, head_dim, n_rot, neox,
                      theta_scale, freq_factors, q_norm, k_norm, eps, pos, (uint16_t *)kpool,
-                     (uint16_t *)vpool, cells, n_cells, q_out, pa, pb, vmode);
+                     (uint16_t *)vpool, cells, n_cells, q_out, pa, pb, vmode, table);
   return hip_check(hipGetLastError(), "qkv_rope_store");
+}
+
+int rope_table_dev(const int32_t *pos, int64_t n, int n_rot, float freq_base,
+                   const float *freq_factors, float *table, hipStream_t st) {
+  if (n == 0) return LGMLH_OK;
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)n), dim3(64), 0, st, pos, n_rot,
+                     rope_theta_scale(freq_base, n_rot), freq_factors, table);
+  return hip_check(hipGetLastError(), "rope_table");
 }
 }  // namespace lgmlh
 
@@ -556,7 +591,7 @@ extern "C" int lgmlh_qkv_rope_store(float *qkv, int64_t n, int n_head, int n_hea
                                     const int64_t *cells, float *q_out, void *stream) {
   return qkv_rope_store_dev(qkv, n, n_head, n_head_kv, head_dim, n_rot, neox, freq_base,
                             freq_factors, q_norm, k_norm, eps, pos, kpool, vpool, n_cells, cells,
-                            q_out, stream, Pending{}, Pending{}, 0);
+                            q_out, stream, Pending{}, Pending{}, 0, nullptr);
 }
 
 extern "C" int lgmlh_swiglu(const float *gu, int64_t n, int64_t F, void *out, int out_type,
