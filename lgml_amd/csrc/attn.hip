@@ -713,19 +713,12 @@ merge_kernel(const int32_t *__restrict__ merge, int H, int Hkv, const float *__r
         // the 64 lanes hold one Q8_K block (whole chunks: G D % 256 == 0),
         // value 4 lane + i of the block; the steps of finish_q8k
         const int64_t K = (int64_t)H * D;
-        float amax = 0.0f, mx = 0.0f;
-        int at = 1 << 30;
+        float amax = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const float a = fabsf(y[i]);
-          if (a > amax) {
-            amax = a;
-            mx = y[i];
-            at = 4 * lane + i;
-          }
-        }
-#pragma unroll
-        for (int s = 1; s < 64; s <<= 1) q8k_amax_step(amax, mx, at, s);
+        for (int i = 0; i < 4; i++) amax = fmaxf(amax, fabsf(y[i]));
+        amax = group_max<64>(amax);
+        const float yv[4] = {y[0], y[1], y[2], y[3]};
+        const float mx = group_first_abs<64, 4>(yv, amax);
         const float iscale = amax == 0.0f ? 0.0f : -127.0f / mx;
         float qv[4], s = 0.0f;
 #pragma unroll
@@ -733,8 +726,8 @@ merge_kernel(const int32_t *__restrict__ merge, int H, int Hkv, const float *__r
           qv[i] = amax == 0.0f ? 0.0f : fminf(127.0f, __builtin_rintf(iscale * y[i]));
           s += qv[i];
         }
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
+        s += dpp_f<DPP_XOR1>(s);
+        s += dpp_f<DPP_XOR2>(s);
         *(f16x4 *)(planes + n * K + k) = f16x4{(f16)qv[0], (f16)qv[1], (f16)qv[2], (f16)qv[3]};
         if ((lane & 3) == 0) planes[q8_bs_off(npad, K) + n * (K / 16) + (k >> 4)] = (f16)s;
         if (lane == 0) {
@@ -745,9 +738,7 @@ merge_kernel(const int32_t *__restrict__ merge, int H, int Hkv, const float *__r
         // 8 lanes hold a Q8_0 block (32 values); the steps of q80_block8
         const int64_t K = (int64_t)H * D;
         float amax = fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3])));
-        amax = fmaxf(amax, __shfl_xor(amax, 1));
-        amax = fmaxf(amax, __shfl_xor(amax, 2));
-        amax = fmaxf(amax, __shfl_xor(amax, 4));
+        amax = group_max<8>(amax);
         const float dd = amax / 127.0f;
         const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
         *(f16x4 *)(planes + n * K + k) =
@@ -763,8 +754,8 @@ merge_kernel(const int32_t *__restrict__ merge, int H, int Hkv, const float *__r
         const float v[4] = {y[0], y[1], y[2], y[3]};
         split_store4(planes, npad, K, n, k, v);
         float s = v[0] + v[1] + v[2] + v[3];
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
+        s += dpp_f<DPP_XOR1>(s);
+        s += dpp_f<DPP_XOR2>(s);
         s += __shfl_xor(s, 4);
         if ((e4 & 7) == 0) split_store_gsum(planes, npad, K, n, k >> 5, s);
       } else {

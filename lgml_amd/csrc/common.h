@@ -205,20 +205,55 @@ __device__ __forceinline__ uint16_t f2h(float f) {
   return __builtin_bit_cast(uint16_t, (f16)f);  // round to nearest even
 }
 
-// Wave64 reductions within groups of 16 lanes (lanes l, l^1, l^2, ...).
-__device__ __forceinline__ float max16(float v) {
-  v = fmaxf(v, __shfl_xor(v, 1));
-  v = fmaxf(v, __shfl_xor(v, 2));
-  v = fmaxf(v, __shfl_xor(v, 4));
-  v = fmaxf(v, __shfl_xor(v, 8));
+// A lane reads another lane's value of its row of 16 by a DPP modifier on a
+// VALU move (no trip through the LDS unit, as a shuffle takes). gfx9
+// encodings: quad_perm [1,0,3,2] = lane ^ 1, [2,3,0,1] = lane ^ 2 (the
+// same lanes as those shuffles, so sums keep their order and bits);
+// row_half_mirror (lane 7 - i of its 8) and row_mirror (15 - i of its 16)
+// pair other lanes, for reductions whose result does not depend on the
+// order (max, exact integer sums).
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// The largest v over aligned groups of W lanes (W = 2 .. 64, a power of
+// two): after the quad steps every lane holds its quad's max, the mirrors
+// pair the quads of 8 and the halves of 16, shuffles the rest.
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+  static_assert(W >= 2 && W <= 64 && (W & (W - 1)) == 0, "group width");
+  v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+  if constexpr (W > 2) v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+  if constexpr (W > 4) v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+  if constexpr (W > 8) v = fmaxf(v, dpp_f<DPP_MIRROR>(v));
+  if constexpr (W > 16) v = fmaxf(v, __shfl_xor(v, 16));
+  if constexpr (W > 32) v = fmaxf(v, __shfl_xor(v, 32));
   return v;
 }
-__device__ __forceinline__ float sum16(float v) {
-  v += __shfl_xor(v, 1);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 4);
-  v += __shfl_xor(v, 8);
-  return v;
+
+// The signed value of the first element, in order of (lane, index), of an
+// aligned group of W lanes holding E values each whose |value| is amax (the
+// group's largest |value|, > 0; with amax = 0 the result is 0 or a zero of
+// either sign). Every lane of the group gets it.
+template <int W, int E>
+__device__ __forceinline__ float group_first_abs(const float (&v)[E], float amax) {
+  float mine = 0.0f;
+  bool has = false;
+#pragma unroll
+  for (int e = E - 1; e >= 0; e--)
+    if (fabsf(v[e]) == amax) {
+      mine = v[e];
+      has = true;
+    }
+  const int lane = __lane_id();
+  const int base = lane & ~(W - 1);
+  const unsigned long long bal = __ballot(has);
+  const unsigned long long grp = W == 64 ? bal : (bal >> base) & ((1ull << W) - 1);
+  const int src = base + (grp ? __builtin_ctzll(grp) : 0);
+  return __shfl(mine, src);
 }
 
 }  // namespace lgmlh

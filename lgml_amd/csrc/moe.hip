@@ -159,14 +159,9 @@ __device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
 }
 
 // Reductions over the 16 lanes of a lane group (one DPP row) by a butterfly
-// of row permutes: lane ^ 1, lane ^ 2 (quad permutes), then the mirrors
-// within 8 and within 16 lanes. Every lane ends with the same result.
-constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
-                                                                0xF, 0xF, false));
-}
+// of row permutes (dpp_f, common.h): lane ^ 1, lane ^ 2 (quad permutes),
+// then the mirrors within 8 and within 16 lanes. Every lane ends with the
+// same result.
 template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);

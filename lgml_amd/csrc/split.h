@@ -110,19 +110,12 @@ __device__ __forceinline__ void q8k_amax_step(float &amax, float &mx, int &at, i
 // the 16 q of the lane pair (j & ~1, j | 1).
 __device__ __forceinline__ void q8k_block8(const float (&v)[8], int j, float (&q)[8], float &d,
                                            float &bs) {
-  float amax = 0.0f, mx = 0.0f;
-  int at = 1 << 30;
+  (void)j;  // the lanes of a block are 32 aligned lanes, lane j holding values 8j ..
+  float amax = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 8; e++) {
-    const float a = fabsf(v[e]);
-    if (a > amax) {
-      amax = a;
-      mx = v[e];
-      at = 8 * j + e;
-    }
-  }
-#pragma unroll
-  for (int o = 1; o < 32; o <<= 1) q8k_amax_step(amax, mx, at, o);
+  for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));  // NaN never counts
+  amax = group_max<32>(amax);
+  const float mx = group_first_abs<32, 8>(v, amax);
   float s = 0.0f;
   if (amax == 0.0f) {
 #pragma unroll
@@ -137,7 +130,7 @@ __device__ __forceinline__ void q8k_block8(const float (&v)[8], int j, float (&q
     }
     d = 1.0f / iscale;
   }
-  bs = s + __shfl_xor(s, 1);
+  bs = s + dpp_f<DPP_XOR1>(s);
 }
 
 // quantize_row_q8_0 of one 32-value block held by 4 lanes (lane j: values
@@ -148,8 +141,7 @@ __device__ __forceinline__ void q80_block8(const float (&v)[8], float (&q)[8], f
   float amax = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));
-  amax = fmaxf(amax, __shfl_xor(amax, 1));
-  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  amax = group_max<4>(amax);
   const float dd = amax / 127.0f;
   const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
 #pragma unroll
