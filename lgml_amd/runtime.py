@@ -261,6 +261,7 @@ class DeviceModel:
         NE = hp.get("n_expert", 0)
         self.swa = []
         self.dims = []  # (head_dim, n_head_kv) per layer
+        rope_dev = {}  # the bytes of a layer's rope factors -> their device copy
         for il in range(hp["n_layer"]):
             Ly = self.layers[il]
             g = layer_info(il)
@@ -283,7 +284,13 @@ class DeviceModel:
                 Ly.out_scale = g.get("out_scale", 0.0)
                 Ly.rope_base = g.get("rope_base", 0.0)
                 if g.get("rope_freqs") is not None:
-                    Ly.rope_freqs = keep(_dev(np.asarray(g["rope_freqs"], np.float32))).data_ptr()
+                    # layers with the same factors share one device copy (and
+                    # so one rope angle table per pass)
+                    rf = np.ascontiguousarray(g["rope_freqs"], np.float32)
+                    key = rf.tobytes()
+                    if key not in rope_dev:
+                        rope_dev[key] = keep(_dev(rf)).data_ptr()
+                    Ly.rope_freqs = rope_dev[key]
             Ly.swa = int(g.get("swa", 0))
             self.swa.append(bool(Ly.swa))
             if Ly.swa and self.ring_cells <= 0:
