@@ -630,18 +630,20 @@ paged_attn_shared_kernel(const float *__restrict__ q, int H, int Hkv, float scal
 }
 
 // Fixed-order merge of the splits of one token group (merge group: first
-// item, splits, first token, tokens), one wave per (group, KV head). Each
-// lane holds up to 4 positions of 4 output columns per round; for each it
-// loads, in one go per 8 splits, the split outputs with the m and l of the
-// position's row, and finds the row's max M, the split weights w = exp2(m -
-// M) and L = sum l w itself (the lanes of a row agree), adding the outputs
-// weighted, in split order. A merge of up to 8 splits is one round trip.
+// item, splits, first token, tokens), one workgroup of MERGE_THREADS per
+// (group, KV head). Each thread holds a position of 4 output columns (up to
+// 4 per round); for each it loads, in one go per SC splits, the split
+// outputs with the m and l of the position's row, and finds the row's max
+// M, the split weights w = exp2(m - M) and L = sum l w itself (the threads
+// of a row agree), adding the outputs weighted, in split order. A merge of
+// up to SC splits is one round trip.
+constexpr int MERGE_THREADS = 256;
 template <int D>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(MERGE_THREADS)
 merge_kernel(const int32_t *__restrict__ merge, int H, int Hkv, const float *__restrict__ part,
              float *__restrict__ out, f16 *__restrict__ planes, int64_t npad, int xf) {
-  constexpr int SC = 8;  // splits per load round
-  const int lane = threadIdx.x, mg = blockIdx.x, kvh = blockIdx.y;
+  constexpr int SC = 16, MT = MERGE_THREADS;  // splits per load round
+  const int tid = threadIdx.x, lane = tid & 63, mg = blockIdx.x, kvh = blockIdx.y;
   const int first = merge[4 * mg + 0], ns = merge[4 * mg + 1];
   const int tok0 = merge[4 * mg + 2], ntok = merge[4 * mg + 3] & 0xff;
   const int stride = merge[4 * mg + 3] >> 8;  // items from one split to the next
@@ -650,14 +652,14 @@ merge_kernel(const int32_t *__restrict__ merge, int H, int Hkv, const float *__r
   const int64_t pstride = (int64_t)stride * Hkv * Partial<D>::floats;
   const float *ml = p0 + ROWS * D;  // m of row r at ml[r], l at ml[ROWS + r]
   const int n4 = nrows * (D / 4);
-  for (int base = 0; base < n4; base += 4 * 64) {
-    const int nj = min(4, (n4 - base + 63) / 64);  // wave-uniform
+  for (int base = 0; base < n4; base += 4 * MT) {
+    const int nj = min(4, (n4 - base + MT - 1) / MT);  // workgroup-uniform
     int rr[4], dd[4];
     f32x4 acc[4];
     float M[4], L[4];
 #pragma unroll
     for (int jj = 0; jj < 4; jj++) {
-      const int e4 = min(base + lane + 64 * jj, n4 - 1);
+      const int e4 = min(base + tid + MT * jj, n4 - 1);
       rr[jj] = e4 / (D / 4);
       dd[jj] = 4 * (e4 % (D / 4));
       acc[jj] = f32x4{0, 0, 0, 0};
@@ -704,8 +706,10 @@ merge_kernel(const int32_t *__restrict__ merge, int H, int Hkv, const float *__r
     }
 #pragma unroll
     for (int jj = 0; jj < 4; jj++) {
-      const int e4 = base + lane + 64 * jj;
-      if (jj >= nj || e4 >= n4) continue;  // groups of 8 lanes (D / 4 is a multiple of 8) leave together
+      const int e4 = base + tid + MT * jj;
+      // groups of 8 lanes (D / 4 is a multiple of 8) leave together, and
+      // whole waves where a wave holds a Q8_K block (n4 a multiple of 64)
+      if (jj >= nj || e4 >= n4) continue;
       const int r = rr[jj], d0 = dd[jj];
       const f32x4 y = acc[jj] / L[jj];
       const int64_t n = tok0 + r / G, k = (int64_t)(kvh * G + r % G) * D + d0;
@@ -802,7 +806,7 @@ static void launch_attn(const float *q, int H, int Hkv, float scale_log2, const 
                          npad, xf, part);
   }
   if (ub->n_merge > 0)
-    hipLaunchKernelGGL(merge_kernel<D>, dim3(ub->n_merge, Hkv), dim3(64), 0, st, ub->merge, H,
+    hipLaunchKernelGGL(merge_kernel<D>, dim3(ub->n_merge, Hkv), dim3(MERGE_THREADS), 0, st, ub->merge, H,
                        Hkv, part, out, planes, npad, xf);
 }
 
