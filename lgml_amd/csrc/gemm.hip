@@ -1651,7 +1651,7 @@ __global__ void act_quant_kernel(const float *__restrict__ x, int64_t N, int64_t
   for (int e = 0; e < 8; e++) v[e] = x[n * K + k0 + e];
   if (xf == XF_Q8K) {
     float bs;
-    q8k_block8(v, (int)((k0 >> 3) & 31), qv, dd, bs);
+    q8k_block8(v, qv, dd, bs);
     if ((k0 & 15) == 0) bsums[n * (K / 16) + (k0 >> 4)] = (int16_t)bs;
     if ((k0 & 255) == 0) ((float *)d)[n * (K / 256) + (k0 >> 8)] = dd;
   } else {

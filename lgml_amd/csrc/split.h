@@ -103,14 +103,13 @@ __device__ __forceinline__ void q8k_amax_step(float &amax, float &mx, int &at, i
   }
 }
 
-// quantize_row_q8_K of one 256-value block held by 32 lanes (lane j of the
-// group: values 8j .. 8j + 7). amax = the largest |x|, its first occurrence
-// gives the signed max; iscale = -127 / max; q = min(127, nearest-even(iscale
-// x)); d = 1 / iscale; an all-zero block has q = 0, d = 0. bs: the sum of
-// the 16 q of the lane pair (j & ~1, j | 1).
-__device__ __forceinline__ void q8k_block8(const float (&v)[8], int j, float (&q)[8], float &d,
+// quantize_row_q8_K of one 256-value block held by 32 aligned lanes (lane j
+// of the group: values 8j .. 8j + 7). amax = the largest |x|, its first
+// occurrence gives the signed max; iscale = -127 / max; q = min(127,
+// nearest-even(iscale x)); d = 1 / iscale; an all-zero block has q = 0, d =
+// 0. bs: the sum of the 16 q of the lane pair (j & ~1, j | 1).
+__device__ __forceinline__ void q8k_block8(const float (&v)[8], float (&q)[8], float &d,
                                            float &bs) {
-  (void)j;  // the lanes of a block are 32 aligned lanes, lane j holding values 8j ..
   float amax = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));  // NaN never counts
@@ -165,7 +164,7 @@ __device__ __forceinline__ void act_store8(int xf, f16 *__restrict__ planes, int
   float *dp = (float *)((char *)planes + q8_d_off(Npad, K));
   if (xf == XF_Q8K) {
     float bs;
-    q8k_block8(v, (int)((k0 >> 3) & 31), q, d, bs);
+    q8k_block8(v, q, d, bs);
     if ((k0 & 15) == 0) planes[q8_bs_off(Npad, K) + n * (K / 16) + (k0 >> 4)] = (f16)bs;
     if ((k0 & 255) == 0) dp[n * (K / 256) + (k0 >> 8)] = d;
   } else {
