@@ -92,14 +92,19 @@ def test_mul_mat_ggml_parity_and_batch_invariance(L, ty, MK):
     wf = core.fill_normal(M * K, 0, 0.02, 7).reshape(M, K)
     w = core.quantize(ty, wf)
     x = act_rows(K, 130, 8)
+    ys = {}
     for N in ((17, 32, 64, 130) if big else (1, 3, 17, 32, 64, 70, 130)):
-        y = run_mul_mat_ggml(L, ty, w, M, K, x[:N])
+        y = ys[N] = run_mul_mat_ggml(L, ty, w, M, K, x[:N])
         want = core.mul_mat_q8(ty, w, M, K, x[:N])
         assert rel_err(y, want) < 1e-5, (N, rel_err(y, want))
         if N in (32, 130):
             for j in ((0, 63, 64, 129) if N == 130 else (0, 16, 31)):
                 alone = run_mul_mat_ggml(L, ty, w, M, K, x[j:j + 1])
                 assert np.array_equal(alone[0].view(np.uint32), y[j].view(np.uint32)), j
+    # every batch size (the decode kernels at N <= 64, the wide one above)
+    # gives each row the same bits
+    for N, y in ys.items():
+        assert np.array_equal(y.view(np.uint32), ys[130][:N].view(np.uint32)), N
 
 
 @pytest.mark.parametrize("ty", [core.Q4_K, core.Q6_K])
