@@ -93,7 +93,7 @@ def test_mul_mat_ggml_parity_and_batch_invariance(L, ty, MK):
     w = core.quantize(ty, wf)
     x = act_rows(K, 130, 8)
     ys = {}
-    for N in ((17, 32, 64, 130) if big else (1, 3, 17, 32, 64, 70, 130)):
+    for N in ((17, 32, 64, 130) if big else (1, 3, 17, 32, 40, 64, 70, 130)):
         y = ys[N] = run_mul_mat_ggml(L, ty, w, M, K, x[:N])
         want = core.mul_mat_q8(ty, w, M, K, x[:N])
         assert rel_err(y, want) < 1e-5, (N, rel_err(y, want))
