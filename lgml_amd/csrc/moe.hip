@@ -96,47 +96,62 @@ router_part_kernel(const float *__restrict__ w, int NE, int64_t K, const float *
 }
 
 // The same partials for a prefill-sized batch: a workgroup takes 64
-// experts x 64 tokens of one K chunk, thread t experts t % 16 + 16 i and
-// tokens t / 16 + 16 j (i, j < 4), so each K fragment read from LDS feeds
-// four products. Each sum is the same fmaf chain in k order.
+// experts x ROUTER_TT tokens of one K chunk, thread t experts t % 16 + 16 i
+// (i < 4) and tokens t / 16 + 16 j (j < ROUTER_TT / 16), so each K fragment
+// read from LDS feeds several products. Each sum is the same fmaf chain in
+// k order.
+constexpr int ROUTER_TT = 64;
 __global__ void __launch_bounds__(256)
 router_tile_kernel(const float *__restrict__ w, int NE, int64_t K, const float *__restrict__ x,
                    int64_t N, float *__restrict__ part) {
-  constexpr int TE = 64, TT = 64, Q = ROUTER_KC / 4;
+  constexpr int TE = 64, TT = ROUTER_TT, TJ = TT / 16, Q = ROUTER_KC / 4;
   __shared__ __align__(16) float ws_[TE * ROUTER_LD];
   __shared__ __align__(16) float xs_[TT * ROUTER_LD];
   const int t = threadIdx.x, ei = t & 15, ti = t >> 4;
   const int64_t e0 = (int64_t)blockIdx.x * TE, n0 = (int64_t)blockIdx.z * TT;
   const int64_t k0 = (int64_t)blockIdx.y * ROUTER_KC;
-  for (int i = t; i < TE * Q; i += 256) {
-    const int r = i / Q, c4 = 4 * (i % Q);
-    f32x4 v = f32x4{0, 0, 0, 0};
-    if (e0 + r < NE && k0 + c4 < K) v = *(const f32x4 *)(w + (e0 + r) * K + k0 + c4);
-    *(f32x4 *)&ws_[r * ROUTER_LD + c4] = v;
+  // 16-byte loads, all issued before the first LDS store
+  constexpr int WJ = TE * Q / 256, XJ = TT * Q / 256;
+  f32x4 wv_[WJ], xv_[XJ];
+#pragma unroll
+  for (int j = 0; j < WJ; j++) {
+    const int i = t + 256 * j, r = i / Q, c4 = 4 * (i % Q);
+    wv_[j] = f32x4{0, 0, 0, 0};
+    if (e0 + r < NE && k0 + c4 < K) wv_[j] = *(const f32x4 *)(w + (e0 + r) * K + k0 + c4);
   }
-  for (int i = t; i < TT * Q; i += 256) {
-    const int r = i / Q, c4 = 4 * (i % Q);
-    f32x4 v = f32x4{0, 0, 0, 0};
-    if (n0 + r < N && k0 + c4 < K) v = *(const f32x4 *)(x + (n0 + r) * K + k0 + c4);
-    *(f32x4 *)&xs_[r * ROUTER_LD + c4] = v;
+#pragma unroll
+  for (int j = 0; j < XJ; j++) {
+    const int i = t + 256 * j, r = i / Q, c4 = 4 * (i % Q);
+    xv_[j] = f32x4{0, 0, 0, 0};
+    if (n0 + r < N && k0 + c4 < K) xv_[j] = *(const f32x4 *)(x + (n0 + r) * K + k0 + c4);
+  }
+#pragma unroll
+  for (int j = 0; j < WJ; j++) {
+    const int i = t + 256 * j;
+    *(f32x4 *)&ws_[(i / Q) * ROUTER_LD + 4 * (i % Q)] = wv_[j];
+  }
+#pragma unroll
+  for (int j = 0; j < XJ; j++) {
+    const int i = t + 256 * j;
+    *(f32x4 *)&xs_[(i / Q) * ROUTER_LD + 4 * (i % Q)] = xv_[j];
   }
   __syncthreads();
-  float acc[4][4];
+  float acc[4][TJ];
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) acc[i][j] = 0.0f;
+    for (int j = 0; j < TJ; j++) acc[i][j] = 0.0f;
 #pragma unroll 2
   for (int c = 0; c < ROUTER_KC; c += 4) {
-    f32x4 wv[4], xv[4];
+    f32x4 wv[4], xv[TJ];
 #pragma unroll
     for (int i = 0; i < 4; i++) wv[i] = *(const f32x4 *)(ws_ + (ei + 16 * i) * ROUTER_LD + c);
 #pragma unroll
-    for (int j = 0; j < 4; j++) xv[j] = *(const f32x4 *)(xs_ + (ti + 16 * j) * ROUTER_LD + c);
+    for (int j = 0; j < TJ; j++) xv[j] = *(const f32x4 *)(xs_ + (ti + 16 * j) * ROUTER_LD + c);
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
+      for (int j = 0; j < TJ; j++) {
         acc[i][j] = fmaf(wv[i][0], xv[j][0], acc[i][j]);
         acc[i][j] = fmaf(wv[i][1], xv[j][1], acc[i][j]);
         acc[i][j] = fmaf(wv[i][2], xv[j][2], acc[i][j]);
@@ -146,7 +161,7 @@ router_tile_kernel(const float *__restrict__ w, int NE, int64_t K, const float *
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int j = 0; j < TJ; j++) {
       const int64_t e = e0 + ei + 16 * i, n = n0 + ti + 16 * j;
       if (e < NE && n < N) part[((int64_t)blockIdx.y * N + n) * NE + e] = acc[i][j];
     }
@@ -654,7 +669,8 @@ int router_logits(const float *w, int NE, int64_t K, const float *x, int64_t T, 
     return LGMLH_EINVAL;
   }
   if (T > 64 && NE >= 64) {  // prefill-sized: 64 x 64 tiles
-    dim3 grid((unsigned)((NE + 63) / 64), (unsigned)router_splits(K), (unsigned)((T + 63) / 64));
+    dim3 grid((unsigned)((NE + 63) / 64), (unsigned)router_splits(K),
+              (unsigned)((T + ROUTER_TT - 1) / ROUTER_TT));
     hipLaunchKernelGGL(router_tile_kernel, grid, dim3(256), 0, st, w, NE, K, x, T, part);
     return hip_check(hipGetLastError(), "moe router");
   }
