@@ -1373,17 +1373,19 @@ static int launch_q(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t 
   const int64_t small_wg = TYPE == LGMLH_Q4_K ? 100 : 200;
   if (N <= 64 && (int64_t)((M + WG_ROWS - 1) / WG_ROWS) * splits < small_wg) nct = 1;
   const int cols = 16 * nct;
-  const int64_t tiles = ((N + cols - 1) / cols) * ((M + WG_ROWS - 1) / WG_ROWS);
-  // With workgroups to spare (two rounds of CUs or more), a workgroup runs
-  // both splits of a pair: half the partial sums (none for a product of
-  // two splits) to write and read back. Same sums either way.
-  const int fold = splits > 1 && nct == 4 && TYPE != LGMLH_Q8_0 &&
-                           tiles * ((splits + 1) / SPLIT_PAIR) >= 512
-                       ? SPLIT_PAIR
-                       : 1;
+  const int wrows = gemm_waves(TYPE, nct) * RT_PER_WAVE * 16;  // rows per workgroup
+  const int64_t tiles = ((N + cols - 1) / cols) * ((M + wrows - 1) / wrows);
+  // With 8192 workgroups or more (16 rounds of two per CU), a workgroup
+  // runs both splits of a pair: half the partial sums (none for a product
+  // of two splits) to write and read back. Same sums either way. Below
+  // that, one split per workgroup finishes sooner, and that outweighs the
+  // consumers' reads of twice the partials (C2's 512-token prefill pass:
+  // products 16.1 -> 15.2 ms, the rms_norm and rope consumers 1.85 ->
+  // 2.29 ms, the pass 0.4 ms shorter than with pairs from 512 tiles).
+  const int fold =
+      splits > 1 && nct == 4 && TYPE != LGMLH_Q8_0 && tiles * splits >= 8192 ? SPLIT_PAIR : 1;
   const int nz = (splits + fold - 1) / fold;
   *group = fold == 1 ? SPLIT_PAIR : 1;
-  const int wrows = gemm_waves(TYPE, nct) * RT_PER_WAVE * 16;  // rows per workgroup
   dim3 grid((unsigned)((N + cols - 1) / cols), (unsigned)((M + wrows - 1) / wrows),
             (unsigned)nz);
 #define LGMLH_PLAIN(NCT_)                                                                  \

@@ -82,7 +82,7 @@ def run_mul_mat_ggml(L, ty, w, M, K, x):
 
 # The shapes of test_gpu_kernels' product test: 16-, 32- and 64-column
 # kernels, split and unsplit K, 4- and 8-wave workgroups; and (4096, 4096)
-# at N = 576, where a workgroup runs both splits of a pair.
+# at N = 4096, where a workgroup runs both splits of a pair.
 @pytest.mark.parametrize("ty", [core.Q4_K, core.Q6_K, core.Q8_0])
 @pytest.mark.parametrize("MK", [(512, 1024), (256, 4096), (48, 768), (25600, 1024),
                                 (51200, 256), (12800, 1024)])
@@ -109,7 +109,9 @@ def test_mul_mat_ggml_parity_and_batch_invariance(L, ty, MK):
 
 @pytest.mark.parametrize("ty", [core.Q4_K, core.Q6_K])
 def test_mul_mat_ggml_folded_pairs(L, ty):
-    M, K, N = 4096, 4096, 576
+    # N = 4096: 8192 workgroups of single splits or more (Q4_K 16384, Q6_K
+    # 8192), so a workgroup runs both splits of a pair
+    M, K, N = 4096, 4096, 4096
     w = core.quantize(ty, core.fill_normal(M * K, 0, 0.02, 17).reshape(M, K))
     x = core.fill_normal(N * K, 0, 1, 18).reshape(N, K)
     y = run_mul_mat_ggml(L, ty, w, M, K, x)

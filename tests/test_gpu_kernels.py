@@ -162,18 +162,25 @@ def test_mul_mat_parity_and_batch_invariance(L, ty, MK):
                 assert np.array_equal(alone[0].view(np.uint32), y[j].view(np.uint32)), j
 
 
-# At prefill sizes a workgroup runs both K splits of a pair (gemm.hip
-# launch_q: Q4_K / Q6_K with 64-column tiles and at least 512 workgroups of
-# pairs); its sums are the same as with one workgroup per split, bit for
-# bit. (4096, 4096): 8 splits, 4 pairs; (4096, 3584): 7 splits, the last
-# pair a single split; (16384, 1024): 2 splits, one pair, written straight
-# to y (and, with the residual, over it in place).
+# At large batches a workgroup runs both K splits of a pair (gemm.hip
+# launch_q: Q4_K / Q6_K with 64-column tiles and at least 8192 workgroups
+# of single splits: column tiles x row blocks of 128 (Q4_K) or 256 (Q6_K)
+# rows x splits); its sums are the same as with one workgroup per split,
+# bit for bit. (4096, 4096): 8 splits, 4 pairs; (4096, 3584): 7 splits,
+# the last pair a single split; (16384, 1024): 2 splits, one pair, written
+# straight to y (and, with the residual, over it in place). N is the
+# smallest multiple of 64 that reaches 8192 workgroups.
+FOLD_N = {(core.Q4_K, (4096, 4096)): 2048, (core.Q4_K, (4096, 3584)): 2368,
+          (core.Q4_K, (16384, 1024)): 2048, (core.Q6_K, (4096, 4096)): 4096,
+          (core.Q6_K, (4096, 3584)): 4736, (core.Q6_K, (16384, 1024)): 4096}
+
+
 @pytest.mark.parametrize("ty", [core.Q4_K, core.Q6_K])
 @pytest.mark.parametrize("MK", [(4096, 4096), (4096, 3584), (16384, 1024)])
 def test_mul_mat_folded_split_pairs(L, ty, MK):
     from lgml_amd import hip
     M, K = MK
-    N = 576
+    N = FOLD_N[(ty, MK)]
     wf = core.fill_normal(M * K, 0, 0.02, 17).reshape(M, K)
     w = core.quantize(ty, wf)
     x = core.fill_normal(N * K, 0, 1, 18).reshape(N, K)
