@@ -29,7 +29,7 @@
 
 namespace lgmlh {
 
-constexpr int GEMM_WAVES = 8;      // waves per workgroup (4 for Q4_K wide tiles: gemm_waves)
+constexpr int GEMM_WAVES = 8;      // waves per workgroup (4 for Q4_K / Q6_K wide tiles: gemm_waves)
 constexpr int RT_PER_WAVE = 2;     // 16-row tiles per wave
 // Rows of an 8-wave workgroup: the unit in which the K-split count and the
 // tiling rules count row tiles (fixed, so the splits do not depend on N).
@@ -315,11 +315,12 @@ struct WFrag<LGMLH_Q8_0> {
 // buffer (66 KB of LDS), so that two share a CU; one's waits for its next
 // K step (the X loads, the barriers) are filled by the other's products
 // (C2's Q4_K shapes at N = 576: 4-15% faster, gate|up at N = 64 6%; the
-// mixed phase 3228 -> 3397 tok/s). A tile's sums do not depend on the
-// workgroup shape: each 16-row tile takes the same fragments in the same
-// K steps.
-__host__ __device__ constexpr int gemm_waves(int type, int nct) {
-  return nct == 4 && type == LGMLH_Q4_K ? 4 : GEMM_WAVES;
+// mixed phase 3228 -> 3397 tok/s). Q6_K on ggml's X the same, with two X
+// buffers (70 KB): C2's Q6_K down products at a 512-token prefill pass 4.21
+// -> 3.27 ms. A tile's sums do not depend on the workgroup shape: each
+// 16-row tile takes the same fragments in the same K steps.
+__host__ __device__ constexpr int gemm_waves(int type, int nct, bool q8) {
+  return nct == 4 && (type == LGMLH_Q4_K || (type == LGMLH_Q6_K && q8)) ? 4 : GEMM_WAVES;
 }
 //
 // Q8: X as ggml's quantized activations (split.h: Q8_K for Q4_K / Q6_K,
@@ -331,18 +332,18 @@ __host__ __device__ constexpr int gemm_waves(int type, int nct) {
 // MFMA of the mins against the 16 sums of 16 q, and the block scales go on
 // in f32: Q4_K d_x (d_w I - dmin_w Mn), Q6_K (d_w d_x) I, Q8_0 per 32-value
 // block (d_w d_x) I. X is half the bytes to stage (no lo plane), so the
-// 4-wave Q4_K workgroups keep two X buffers.
+// 4-wave Q4_K / Q6_K workgroups keep two X buffers.
 template <int TYPE, int NCT, bool GATHER, bool Q8>
-__global__ void __launch_bounds__(gemm_waves(TYPE, NCT) * 64,
+__global__ void __launch_bounds__(gemm_waves(TYPE, NCT, Q8) * 64,
                                   NCT == 1 && TYPE == LGMLH_Q6_K && Q8 ? 2
                                   : NCT == 1 && TYPE != LGMLH_Q8_0   ? 4
-                                  : NCT == 4 && TYPE == LGMLH_Q4_K ? 2
+                                  : gemm_waves(TYPE, NCT, Q8) == 4 ? 2
                                                                    : 1)
 qgemm_kernel(const uint8_t *__restrict__ w, int64_t M, int64_t K, const f16 *__restrict__ xs,
              int64_t Npad, int64_t N, float *__restrict__ y, int64_t ldy,
              const float *__restrict__ residual, int nz, int sb_per_split, int fold,
              float *__restrict__ part, Gather gt) {
-  constexpr int WVS = gemm_waves(TYPE, NCT);  // waves per workgroup
+  constexpr int WVS = gemm_waves(TYPE, NCT, Q8);  // waves per workgroup
   constexpr bool ONEBUF = WVS < GEMM_WAVES && !Q8;  // one X buffer
   constexpr int COLS = NCT * 16;            // N columns per workgroup
   constexpr int X_SLOTS = COLS * 32;
@@ -1373,7 +1374,7 @@ static int launch_q(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t 
   const int64_t small_wg = TYPE == LGMLH_Q4_K ? 100 : 200;
   if (N <= 64 && (int64_t)((M + WG_ROWS - 1) / WG_ROWS) * splits < small_wg) nct = 1;
   const int cols = 16 * nct;
-  const int wrows = gemm_waves(TYPE, nct) * RT_PER_WAVE * 16;  // rows per workgroup
+  const int wrows = gemm_waves(TYPE, nct, Q8) * RT_PER_WAVE * 16;  // rows per workgroup
   const int64_t tiles = ((N + cols - 1) / cols) * ((M + wrows - 1) / wrows);
   // With 8192 workgroups or more (16 rounds of two per CU), a workgroup
   // runs both splits of a pair: half the partial sums (none for a product
@@ -1389,7 +1390,7 @@ static int launch_q(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t 
   dim3 grid((unsigned)((N + cols - 1) / cols), (unsigned)((M + wrows - 1) / wrows),
             (unsigned)nz);
 #define LGMLH_PLAIN(NCT_)                                                                  \
-  hipLaunchKernelGGL((qgemm_kernel<TYPE, NCT_, false, Q8>), grid, dim3(gemm_waves(TYPE, NCT_) * 64), \
+  hipLaunchKernelGGL((qgemm_kernel<TYPE, NCT_, false, Q8>), grid, dim3(gemm_waves(TYPE, NCT_, Q8) * 64), \
                      0, st,                                                                \
                      (const uint8_t *)w, M, K, xs, Npad, N, y, ldy, res, nz, spb, fold,    \
                      part, Gather{})
@@ -1467,9 +1468,9 @@ template <int TYPE, int NCT, bool Q8>
 static void launch_grouped(const void *w, int64_t M, int64_t K, const f16 *xs, int64_t Npad,
                            const Gather &gt, int max_tiles, float *y, hipStream_t st) {
   const int NSB = (int)(K / QK_K);
-  const int wrows = gemm_waves(TYPE, NCT) * RT_PER_WAVE * 16;
+  const int wrows = gemm_waves(TYPE, NCT, Q8) * RT_PER_WAVE * 16;
   dim3 grid((unsigned)max_tiles, (unsigned)((M + wrows - 1) / wrows), 1);
-  hipLaunchKernelGGL((qgemm_kernel<TYPE, NCT, true, Q8>), grid, dim3(gemm_waves(TYPE, NCT) * 64), 0, st,
+  hipLaunchKernelGGL((qgemm_kernel<TYPE, NCT, true, Q8>), grid, dim3(gemm_waves(TYPE, NCT, Q8) * 64), 0, st,
                      (const uint8_t *)w, M, K, xs, Npad, (int64_t)0, y, M, (const float *)nullptr,
                      1, NSB, 1, (float *)nullptr, gt);
 }
