@@ -132,9 +132,9 @@ def test_set_rows_f16_bit_exact(L):
 
 
 @pytest.mark.parametrize("n", [4096, 2560, 2048, 64])
-def test_rms_norm_f32_and_f16(L, n):
+@pytest.mark.parametrize("rows", [37, 600])  # past 512 rows: n / 8 threads per row
+def test_rms_norm_f32_and_f16(L, n, rows):
     from lgml_amd import hip
-    rows = 37
     rng = np.random.default_rng(n)
     x = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
     w = rng.uniform(0.5, 1.5, n).astype(np.float32)
@@ -145,6 +145,11 @@ def test_rms_norm_f32_and_f16(L, n):
                                hip.F32, st()))
     got = out.cpu().numpy()
     assert rel_err(got, want) < 1e-6
+    # a row gives the same bits in either launch shape
+    few = torch.empty((3, n), dtype=torch.float32, device="cuda")
+    hip.check(L.lgmlh_rms_norm(dx.data_ptr(), 3, n, 1e-6, dw.data_ptr(), few.data_ptr(), hip.F32,
+                               st()))
+    assert np.array_equal(few.cpu().numpy().view(np.uint32), got[:3].view(np.uint32))
     o16 = torch.empty((rows, n), dtype=torch.float16, device="cuda")
     hip.check(L.lgmlh_rms_norm(dx.data_ptr(), rows, n, 1e-6, dw.data_ptr(), o16.data_ptr(),
                                hip.F16, st()))
